@@ -1,0 +1,183 @@
+/*
+ * mx_qlinear.h -- C ABI of the MI355X (gfx950) quantized DiT linear path.
+ *
+ * One shared library, libmx_qlinear.so, built by hipcc for gfx950 only. Every entry
+ * point takes raw device pointers, element counts and a hipStream_t passed as void*,
+ * enqueues its kernels on that stream and returns without synchronising. Nothing
+ * allocates device memory except mxq_w4a8_codebook_gemm's caller-provided workspace
+ * contract (the caller allocates it). Return value: MXQ_OK (0) or a negative error
+ * code; mxq_last_error() then describes the failure (thread-local string).
+ *
+ * Reference paths are relative to the reference tree; CK stands for
+ * backends/turbo/vendor/comfy_kitchen. Numerics follow the reference's eager
+ * PyTorch path (CK/backends/eager/quantization.py), which is the semantics the
+ * parity tests hold these kernels to.
+ */
+#ifndef MX_QLINEAR_H
+#define MX_QLINEAR_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MXQ_ABI_VERSION 1
+
+/* Return codes. */
+#define MXQ_OK 0
+#define MXQ_ERR_INVALID (-1)     /* bad argument (reference: ValueError / std::runtime_error) */
+#define MXQ_ERR_UNSUPPORTED (-2) /* valid request outside this build (reference launchers return false) */
+#define MXQ_ERR_HIP (-3)         /* HIP runtime or launch failure */
+
+/* dtype codes: CK/backends/eager/quantization.py:34-42 (DTYPE_CODE_TO_DTYPE). */
+#define MXQ_DTYPE_F32 0
+#define MXQ_DTYPE_F16 1
+#define MXQ_DTYPE_BF16 2
+#define MXQ_DTYPE_E4M3 5
+
+/* Pre-quantization activation codes: CK/backends/_activations.py:19-24. */
+#define MXQ_ACT_NONE 0
+#define MXQ_ACT_GELU_TANH 1
+
+/* Thread-local description of the last failure in this thread ("" if none). */
+const char* mxq_last_error(void);
+
+/* MXQ_ABI_VERSION of the loaded library. */
+int mxq_abi_version(void);
+
+/*
+ * Per-row (per-token) symmetric INT8 quantization.
+ *   x      [rows, cols] of x_dtype (bf16, fp16 or fp32), row-major, contiguous
+ *   q      [rows, cols] int8 out;  scales [rows] fp32 out
+ *   input_act  MXQ_ACT_NONE or MXQ_ACT_GELU_TANH (bf16 only): apply tanh-GELU to x first
+ * Semantics: CK/backends/eager/quantization.py:857-875.
+ * Replaces: launch_quantize_int8_rowwise_kernel, CK/backends/cuda/ops/int8_linear.cu:1035-1084
+ * (stochastic rounding, off by default there, is not provided).
+ */
+int mxq_quantize_int8_rowwise(const void* x, int x_dtype, int8_t* q, float* scales,
+                              int64_t rows, int64_t cols, int input_act, void* stream);
+
+/*
+ * The same quantizer for bf16 rows whose absmax is already known (row_absmax[r] must
+ * equal max |x[r, :]|, e.g. accumulated by mxq_int8_gemm_dequant_gelu_absmax). One
+ * streaming pass over x. Second half of the FFN chain's per-token re-quantization.
+ */
+int mxq_quantize_int8_rowwise_absmax(const void* x_bf16, const float* row_absmax, int8_t* q,
+                                     float* scales, int64_t rows, int64_t cols, void* stream);
+
+/*
+ * adaLN: layer_norm(x, no affine, eps) * (1 + scale) + shift, bf16 in and out.
+ *   scale, shift  [rows / scale_group, cols] and [rows / shift_group, cols] bf16: row r uses
+ *                 modulation row r / scale_group (r / shift_group); a single [cols] vector
+ *                 is scale_group = shift_group = rows.
+ * Semantics: CK/backends/eager/adaln.py:11-14 (four bf16 roundings).
+ * Replaces: launch_adaln_kernel, CK/backends/cuda/ops/adaln.cu:256-313 (subtract_mean=true).
+ */
+int mxq_adaln(const void* x, const void* scale, const void* shift, void* out, int64_t rows,
+              int64_t cols, int64_t scale_group, int64_t shift_group, float eps, void* stream);
+
+/*
+ * adaLN fused with the per-row INT8 quantizer: q, scales = quantize(adaln(x, ...)).
+ * y_out (bf16 [rows, cols]) optionally receives the modulated rows; pass NULL to skip.
+ * Replaces the launch_adaln_kernel + launch_quantize_int8_rowwise_kernel pair that feeds
+ * the QKV projection (CK/backends/cuda/ops/adaln.cu:256-313, int8_linear.cu:1035-1084).
+ */
+int mxq_adaln_quantize_int8(const void* x, const void* scale, const void* shift,
+                            int64_t scale_group, int64_t shift_group, float eps, int8_t* q,
+                            float* scales, void* y_out, int64_t rows, int64_t cols,
+                            void* stream);
+
+/*
+ * Raw INT8 GEMM: C[m, n] = sum_k A[m, k] * B[n, k] in int32.
+ *   a [M, K] int8 row-major; b [N, K] int8 row-major (the checkpoint's [out, in] layout);
+ *   c [M, ldc] int32. K must be a multiple of 16.
+ * Replaces: torch._int_mm in _int8_matmul_accumulate, CK/backends/eager/quantization.py:749-782.
+ */
+int mxq_int8_gemm_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M, int64_t N,
+                      int64_t K, int64_t ldc, void* stream);
+
+/*
+ * INT8 GEMM with the fused dequant epilogue:
+ *   D[m, n] = out(fp32(acc) * (xs[m] * ws[n]));  D[m, n] = out(D[m, n] + bias[n])
+ *   xs [M] fp32; ws [ws_numel] fp32 with ws_numel 1 (tensorwise) or N (per channel);
+ *   bias [N] of out_dtype or NULL; d [M, ldd] of out_dtype (fp32, fp16 or bf16).
+ * Semantics: CK/backends/eager/quantization.py:1031-1054.
+ * Replaces: launch_cutlass_int8_dequant / launch_cutlass_int8_dequant_strided,
+ * CK/backends/cuda/ops/cutlass_gemm_int8.cu:613-665 (there bias is fp32 and the bias add is
+ * fused before one rounding; here it follows the eager two-rounding recipe).
+ */
+int mxq_int8_gemm_dequant(const int8_t* a, const int8_t* b, const float* xs, const float* ws,
+                          int64_t ws_numel, const void* bias, void* d, int64_t M, int64_t N,
+                          int64_t K, int64_t ldd, int out_dtype, void* stream);
+
+/*
+ * fc1 of the INT8 FFN chain: the bf16 dequant epilogue above, then tanh-GELU in bf16,
+ *   h[m, n] = bf16(gelu(bf16(bf16(acc * (xs*ws)) + bias)))
+ * and row_absmax[m] = max(row_absmax[m], max_n |h[m, n]|) by atomics. row_absmax must hold
+ * zeros (or earlier partial maxima) on entry; mxq_fill_f32 clears it on the stream.
+ * Replaces the reference's fc1 int8_linear + apply_input_act("gelu_tanh") + the absmax half of
+ * fc2's quantizer (CK/backends/eager/quantization.py:971-1056, CK/backends/_activations.py:40-53).
+ */
+int mxq_int8_gemm_dequant_gelu_absmax(const int8_t* a, const int8_t* b, const float* xs,
+                                      const float* ws, int64_t ws_numel, const void* bias_bf16,
+                                      void* h_bf16, float* row_absmax, int64_t M, int64_t N,
+                                      int64_t K, int64_t ldh, void* stream);
+
+/*
+ * y[i] = gelu_tanh(x[i]) for n bf16 values, bit-identical to torch's CPU
+ * gelu(approximate="tanh") on bfloat16 (x and y may alias).
+ * Replaces: apply_input_act(x, "gelu_tanh"), CK/backends/_activations.py:40-53.
+ */
+int mxq_gelu_tanh_bf16(const void* x, void* y, int64_t n, void* stream);
+
+/* p[0..n) = value on the stream (a kernel, so it is safe inside captured graphs). */
+int mxq_fill_f32(float* p, float value, int64_t n, void* stream);
+
+/*
+ * Grouped int4 -> int8 weight decode:
+ *   w8[n, k] = clamp(rne(v * s_rel[n, k / G]), -127, 127), v = codebook[c] or c - 8,
+ *   c = low nibble of qdata[n, k/2] for even k, high nibble for odd k.
+ *   qdata [N, K/2] int8; s_rel [N, K/G] fp32 (s_rel_dtype 0) or float8_e4m3fn bits (5);
+ *   codebook [16] fp32 or NULL; out [N, K] int8.
+ * Semantics: CK/backends/eager/w4a8_int8.py:344-363.
+ * Replaces: launch_dequant_int4_grouped_to_int8 / _e4m3, CK/backends/cuda/ops/w4a8_gemm.cu:93-121.
+ */
+int mxq_dequant_int4_grouped_to_int8(const int8_t* qdata, const void* s_rel, int s_rel_dtype,
+                                     const float* codebook, int8_t* out, int64_t N, int64_t K,
+                                     int64_t group_size, void* stream);
+
+/*
+ * Reference-format W4A8 linear on an already quantized activation: decode the packed weight
+ * chunk by chunk into `workspace` ([chunk_cols, K] int8) and run the dequant GEMM with
+ * ws = s_channel. Arguments as mxq_dequant_int4_grouped_to_int8 and mxq_int8_gemm_dequant;
+ * out [M, N] of out_dtype, bias [N] of out_dtype or NULL.
+ * Replaces: launch_w4a8_codebook_gemm_chunked, CK/backends/cuda/ops/w4a8_gemm.cu:133-164.
+ */
+int mxq_w4a8_codebook_gemm(const int8_t* xq, const int8_t* qdata, const void* s_rel,
+                           int s_rel_dtype, const float* codebook, const float* s_channel,
+                           const float* xs, const void* bias, int8_t* workspace, void* out,
+                           int64_t M, int64_t N, int64_t K, int64_t group_size,
+                           int64_t chunk_cols, int out_dtype, void* stream);
+
+/*
+ * Grouped-scale W4A8 GEMM (int4 weights with one fp16 scale per K-group and output channel):
+ *   P_g[m, n] = sum_{k in group g} A[m, k] * (c[n, k] - 8)      (exact int32)
+ *   acc       = fma-accumulated over g = 0, 1, ... of fp32(P_g) * fp32(scale[g, n])
+ *   D[m, n]   = out(acc * xs[m]);  then D = out(D + bias[n]) if bias
+ *   a [M, K] int8; xs [M] fp32; qdata [N, K/2] int8 (offset-8 nibbles packed as in
+ *   CK/backends/eager/w4a8_int8.py:200-202); group_scale [K/G, N] fp16; G = group_size
+ *   (a multiple of 128 here); d [M, ldd] of out_dtype.
+ * The reference has no kernel for this layout (its W4A8 folds group scales into the int8
+ * grid, w4a8_gemm.cu:4-18); unpacking follows CK/backends/eager/w4a8_int8.py:351-355.
+ */
+int mxq_w4a8_gemm_grouped(const int8_t* a, const float* xs, const int8_t* qdata,
+                          const uint16_t* group_scale, const void* bias, void* d, int64_t M,
+                          int64_t N, int64_t K, int64_t group_size, int64_t ldd, int out_dtype,
+                          void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MX_QLINEAR_H */

@@ -1,0 +1,126 @@
+"""torch-CPU restatement of the reference's eager op sequence.
+
+Test infrastructure only (see the package docstring). It replays, op for op, the
+PyTorch CPU path the reference runs when no GPU backend is present, so that
+``bench.py`` can time it as the CPU baseline and the tests can cross-check it
+against the numpy restatement in ``eager_np``. Paths are relative to the
+reference tree; ``CK`` = ``backends/turbo/vendor/comfy_kitchen``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+
+def quantize_int8_rowwise(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """CK/backends/eager/quantization.py:857-875 (+815-818, 821-826)."""
+    abs_max = x.abs().amax(dim=-1, keepdim=True)
+    scale = (abs_max.float() / 127.0).clamp(min=1e-30)
+    s = scale.to(dtype=x.dtype)
+    s = torch.where(s == 0, torch.full_like(s, torch.finfo(x.dtype).tiny), s)
+    q = (x / s).round_().clamp_(-128.0, 127.0).to(torch.int8)
+    return q, scale
+
+
+def int8_matmul(a: torch.Tensor, w_nk: torch.Tensor) -> torch.Tensor:
+    """``torch._int_mm`` with the K padding of quantization.py:749-782."""
+    b = w_nk.t().contiguous()
+    k = a.shape[1]
+    pk = (k + 7) // 8 * 8
+    if pk != k:
+        a = torch.cat((a, a.new_zeros(a.shape[0], pk - k)), dim=1)
+        b = torch.cat((b, b.new_zeros(pk - k, b.shape[1])), dim=0)
+    n = b.shape[1]
+    pn = (n + 7) // 8 * 8
+    if pn != n:
+        b = torch.cat((b, b.new_zeros(b.shape[0], pn - n)), dim=1)
+    out = torch._int_mm(a, b)
+    return out[:, :n] if pn != n else out
+
+
+def dequant(result: torch.Tensor, x_scale: torch.Tensor, weight_scale: torch.Tensor,
+            bias: torch.Tensor | None, out_dtype: torch.dtype) -> torch.Tensor:
+    """Chunked dequant and bias add of quantization.py:1031-1054."""
+    m, n = result.shape
+    chunk_size = max(1, min(m, 256 * 1024 * 1024 // (n * 4)))
+    ws = weight_scale.to(torch.float32).reshape(1, -1)
+    parts = []
+    for i in range(0, m, chunk_size):
+        e = min(i + chunk_size, m)
+        chunk = result[i:e].float()
+        parts.append((chunk * (x_scale[i:e].to(torch.float32) * ws)).to(out_dtype))
+    out = torch.cat(parts, dim=0)
+    if bias is not None:
+        out = out + bias.to(dtype=out.dtype).reshape(1, -1)
+    return out
+
+
+def apply_input_act(x: torch.Tensor, input_act: str | None) -> torch.Tensor:
+    """CK/backends/_activations.py:40-53 (gelu_tanh only; swiglu is out of this path)."""
+    if input_act in (None, "none"):
+        return x
+    if input_act == "gelu_tanh":
+        return torch.nn.functional.gelu(x, approximate="tanh")
+    raise ValueError(f"unsupported input_act: {input_act!r}")
+
+
+def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+                bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
+                input_act: str | None = None) -> torch.Tensor:
+    """CK/backends/eager/quantization.py:971-1056 with convrot=False."""
+    x = apply_input_act(x, input_act)
+    weight_scale = weight_scale.to(torch.float32).reshape(-1)
+    x2 = x.reshape(-1, x.shape[-1])
+    q, s = quantize_int8_rowwise(x2)
+    acc = int8_matmul(q, weight)
+    out = dequant(acc, s, weight_scale, bias, out_dtype)
+    return out.reshape(*x.shape[:-1], weight.shape[0])
+
+
+def adaln(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """CK/backends/eager/adaln.py:11-14."""
+    normalized = torch.nn.functional.layer_norm(x, x.shape[-1:], eps=eps)
+    return normalized * (1 + scale) + shift
+
+
+def dequant_int4_grouped_to_int8(qdata, s_rel, codebook, group_size):
+    """CK/backends/eager/w4a8_int8.py:344-363."""
+    n, k_half = qdata.shape
+    k = k_half * 2
+    packed = qdata.to(torch.int32) & 0xFF
+    codes = torch.empty(n, k, dtype=torch.int32)
+    codes[:, 0::2] = packed & 0xF
+    codes[:, 1::2] = (packed >> 4) & 0xF
+    values = codebook.float()[codes] if codebook is not None else codes.float() - 8.0
+    values = values.view(n, k // group_size, group_size) * s_rel.float().unsqueeze(-1)
+    return values.view(n, k).round().clamp_(-127, 127).to(torch.int8)
+
+
+def w4a8_grouped_linear(a: torch.Tensor, x_scale: torch.Tensor, qdata: torch.Tensor,
+                        group_scale: torch.Tensor, group_size: int,
+                        out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """Grouped-scale W4A8: per-group ``torch._int_mm`` partials, fp32 group scaling.
+
+    There is no reference implementation of this format; this is the eager
+    composition of reference ops (w4a8_int8.py:351-355 unpacking, ``_int_mm``)
+    that the CPU baseline times.
+    """
+    n, k_half = qdata.shape
+    k = k_half * 2
+    packed = qdata.to(torch.int32) & 0xFF
+    codes = torch.empty(n, k, dtype=torch.int8)
+    codes[:, 0::2] = ((packed & 0xF) - 8).to(torch.int8)
+    codes[:, 1::2] = (((packed >> 4) & 0xF) - 8).to(torch.int8)
+    acc = torch.zeros(a.shape[0], n, dtype=torch.float32)
+    gs = group_scale.float()
+    for g in range(k // group_size):
+        sl = slice(g * group_size, (g + 1) * group_size)
+        part = int8_matmul(a[:, sl].contiguous(), codes[:, sl].contiguous())
+        acc.addcmul_(part.float(), gs[g].reshape(1, -1))
+    return (acc * x_scale.reshape(-1, 1).float()).to(out_dtype)
+
+
+def ffn_gelu_int8(x, w1, s1, b1, w2, s2, b2):
+    """fc1 -> tanh-GELU (as fc2's input_act) -> fc2, two eager int8_linear calls."""
+    h = int8_linear(x, w1, s1, b1)
+    return int8_linear(h, w2, s2, b2, input_act="gelu_tanh")

@@ -1,0 +1,160 @@
+"""GPU parity: INT8 GEMM (int32), fused dequant epilogues, int8_linear and the FFN chain.
+
+Bar: int32 accumulators bit-exact; bf16/fp16/fp32 outputs bit-exact against the oracle's
+restatement of the eager recipe (which is within 1 bf16 ulp of any other rounding order).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import mx_qlinear._lib as L
+from _util import activations, bf16_vec, bits, gen, int8_weight
+from oracle import eager_np
+from oracle.bf16 import bf16_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _mx():
+    import mx_qlinear
+
+    return mx_qlinear
+
+
+def _i8(shape, seed, lo=-128, hi=128):
+    return torch.randint(lo, hi, shape, generator=gen(seed), dtype=torch.int8)
+
+
+@pytest.mark.parametrize(
+    "m,n,k",
+    [(1, 1, 16), (256, 256, 128), (257, 384, 3072), (300, 200, 144), (64, 1000, 4096), (513, 257, 1040)],
+)
+def test_gemm_i32_exact(dev, m, n, k):
+    print(f"gemm i32 m={m} n={n} k={k}", flush=True)
+    a, w = _i8((m, k), m + k), _i8((n, k), n * 3 + k)
+    c = _mx().mm_int8(a.to(dev), w.to(dev).t())
+    assert np.array_equal(c.cpu().numpy(), eager_np.int8_matmul(a.numpy(), w.numpy()))
+
+
+def test_gemm_i32_bruteforce_small(dev):
+    a, w = _i8((19, 48), 1), _i8((23, 48), 2)
+    c = _mx().mm_int8(a.to(dev), w.to(dev).t())
+    assert np.array_equal(c.cpu().numpy(), eager_np.int8_matmul_bruteforce(a.numpy(), w.numpy()))
+
+
+def test_gemm_extremes_and_structure(dev):
+    """Saturation-free extremes, identity and permutation weights."""
+    k = 20480
+    a = torch.full((3, k), -128, dtype=torch.int8)
+    a[1] = 127
+    w = torch.full((2, k), -128, dtype=torch.int8)
+    c = _mx().mm_int8(a.to(dev), w.to(dev).t()).cpu()
+    assert c[0, 0] == k * 128 * 128 and c[1, 0] == -k * 127 * 128
+    k = 512
+    a = _i8((300, k), 5)
+    eye = torch.eye(k, dtype=torch.int8)
+    assert torch.equal(_mx().mm_int8(a.to(dev), eye.to(dev)).cpu(), a.to(torch.int32))
+    perm = torch.randperm(k, generator=gen(6))
+    c = _mx().mm_int8(a.to(dev), eye[:, perm].contiguous().to(dev)).cpu()
+    assert torch.equal(c, a[:, perm].to(torch.int32))
+
+
+def test_gemm_i32_strided_output(dev):
+    m, n, k, ldc = 100, 300, 256, 512
+    a, w = _i8((m, k), 8), _i8((n, k), 9)
+    c = torch.full((m, ldc), 7, dtype=torch.int32, device=dev)
+    from mx_qlinear.ops import _p, _stream
+
+    ad, wd = a.to(dev), w.to(dev)
+    L.call("mxq_int8_gemm_i32", _p(ad), _p(wd), _p(c), m, n, k, ldc, _stream(dev))
+    c = c.cpu().numpy()
+    assert np.array_equal(c[:, :n], eager_np.int8_matmul(a.numpy(), w.numpy()))
+    assert np.all(c[:, n:] == 7)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("with_bias", [False, True])
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_dequant_epilogue_matches_oracle(dev, out_dtype, with_bias, per_channel):
+    m, n, k = 260, 520, 1024
+    x = activations(m, k, 41)
+    w, ws = int8_weight(n, k, 42)
+    if not per_channel:
+        ws = ws[:1].clone()
+    bias = bf16_vec(n, 43, 0.01) if with_bias else None
+    y = _mx().int8_linear(x.to(dev), w.to(dev), ws.to(dev), None if bias is None else bias.to(dev),
+                          out_dtype=out_dtype)
+    name = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[out_dtype]
+    # a bf16 bias is cast to the output dtype before the add (bias.to(result.dtype))
+    ref = eager_np.int8_linear(bits(x), w.numpy(), ws.numpy(), None if bias is None else bits(bias), name)
+    got = y.float().cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.astype(np.float32).view(np.uint32))
+
+
+def test_int8_linear_config1(dev):
+    """W8A8 single linear, X [1024, 3072] with 0.5% outlier channels, W [3072, 3072]."""
+    m, k, n = 1024, 3072, 3072
+    x = activations(m, k, 20261201)
+    w, ws = int8_weight(n, k, 20261202)
+    bias = bf16_vec(n, 20261203, 0.01)
+    y = _mx().int8_linear(x.to(dev), w.to(dev), ws.reshape(n, 1).to(dev), bias.to(dev))
+    ref = eager_np.int8_linear(bits(x), w.numpy(), ws.numpy(), bits(bias), "bf16")
+    assert np.array_equal(bits(y), bf16_bits(ref))
+
+
+def test_int8_linear_leading_dims_and_empty(dev):
+    x = activations(2 * 3 * 5, 256, 3).reshape(2, 3, 5, 256)
+    w, ws = int8_weight(64, 256, 4)
+    y = _mx().int8_linear(x.to(dev), w.to(dev), ws.to(dev))
+    assert y.shape == (2, 3, 5, 64)
+    ref = eager_np.int8_linear(bits(x), w.numpy(), ws.numpy(), None, "bf16")
+    assert np.array_equal(bits(y), bf16_bits(ref))
+    e = _mx().int8_linear(x[:0].to(dev), w.to(dev), ws.to(dev))
+    assert e.shape == (0, 3, 5, 64)
+
+
+def test_int8_linear_k_not_multiple_of_16(dev):
+    x = activations(40, 100, 12)
+    w, ws = int8_weight(48, 100, 13)
+    y = _mx().int8_linear(x.to(dev), w.to(dev), ws.to(dev))
+    ref = eager_np.int8_linear(bits(x), w.numpy(), ws.numpy(), None, "bf16")
+    assert np.array_equal(bits(y), bf16_bits(ref))
+
+
+def test_int8_linear_gelu_input_act(dev):
+    x = (torch.randn(96, 512, generator=gen(21)) * 2).to(torch.bfloat16)
+    w, ws = int8_weight(256, 512, 22)
+    y = _mx().int8_linear(x.to(dev), w.to(dev), ws.to(dev), input_act="gelu_tanh")
+    ref = eager_np.int8_linear(bits(x), w.numpy(), ws.numpy(), None, "bf16", input_act="gelu_tanh")
+    assert np.array_equal(bits(y), bf16_bits(ref))
+
+
+def test_int8_linear_rejects_bad_arguments(dev):
+    x = activations(4, 64, 1).to(dev)
+    w, ws = int8_weight(8, 64, 2)
+    with pytest.raises(ValueError):
+        _mx().int8_linear(x, w[:, :32].contiguous().to(dev), ws.to(dev))
+    with pytest.raises(ValueError):
+        _mx().int8_linear(x, w.to(dev), ws[:3].to(dev))
+    with pytest.raises(ValueError):
+        _mx().int8_linear(x, w.to(dev), ws.to(dev), input_act="relu")
+
+
+@pytest.mark.parametrize("m,k,hidden,n", [(300, 256, 1024, 256), (64, 512, 2048, 384)])
+def test_ffn_chain_matches_oracle(dev, m, k, hidden, n):
+    print(f"ffn m={m} k={k} hidden={hidden} n={n}", flush=True)
+    x = activations(m, k, 500 + m)
+    w1, s1 = int8_weight(hidden, k, 501)
+    w2, s2 = int8_weight(n, hidden, 502)
+    b1, b2 = bf16_vec(hidden, 503, 0.01), bf16_vec(n, 504, 0.01)
+    out, h = _mx().int8_ffn_gelu(x.to(dev), w1.to(dev), s1.to(dev), b1.to(dev), w2.to(dev), s2.to(dev),
+                                 b2.to(dev), return_hidden=True)
+    ref_out, ref_h = eager_np.ffn_gelu_int8(bits(x), w1.numpy(), s1.numpy(), bits(b1), w2.numpy(),
+                                            s2.numpy(), bits(b2))
+    assert np.array_equal(bits(h), bf16_bits(ref_h))
+    assert np.array_equal(bits(out), bf16_bits(ref_out))
+    # same result as the unfused two-call composition of the public API
+    y1 = _mx().int8_linear(x.to(dev), w1.to(dev), s1.to(dev), b1.to(dev))
+    y2 = _mx().int8_linear(y1, w2.to(dev), s2.to(dev), b2.to(dev), input_act="gelu_tanh")
+    assert torch.equal(y2, out)

@@ -1,0 +1,165 @@
+"""GPU parity: per-token quantizers, tanh-GELU and adaLN against the CPU oracle.
+
+Bar: quantized int8 values and fp32 scales bit-exact; GELU bit-exact against torch's CPU GELU
+table; adaLN's modulated bf16 output within the bound stated in test_adaln_matches_oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from _util import activations, bf16_vec, bits, from_bits, gen
+from oracle import eager_np, eager_torch
+from oracle.bf16 import bf16_bits, bf16_to_f32, bf16_ulp
+
+pytestmark = pytest.mark.gpu
+
+
+def _mx():
+    import mx_qlinear
+
+    return mx_qlinear
+
+
+@pytest.mark.parametrize(
+    "m,k",
+    [(1, 64), (3, 8), (7, 3072), (64, 520), (257, 5120), (33, 20480), (5, 100), (2, 24), (9, 6152)],
+)
+def test_quant_bf16_matches_oracle(dev, m, k):
+    print(f"quant bf16 m={m} k={k}", flush=True)
+    x = activations(m, k, seed=20261201 + m * 7 + k)
+    q, s = _mx().quantize_int8_rowwise(x.to(dev))
+    q_ref, s_ref = eager_np.quantize_int8_rowwise(bits(x))
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+
+
+def test_quant_known_answers(dev):
+    """Rows whose result is fixed by hand: constant, zero, one-hot, exact ties, -128."""
+    k = 64
+    rows = []
+    rows.append(np.full(k, 1.0, np.float32))                      # q = 127 everywhere
+    rows.append(np.full(k, 3.0, np.float32))                      # bf16(s) rounds up: q = 126
+    rows.append(np.zeros(k, np.float32))                          # s = 1e-30, q = 0
+    r = np.zeros(k, np.float32); r[5] = -2.5; rows.append(r)      # one-hot: q[5] = -127
+    # s = bf16(127/127) = 1 -> x/s = x exactly: ties 0.5 -> 0, 1.5 -> 2, 2.5 -> 2, -3.5 -> -4
+    r = np.zeros(k, np.float32); r[:6] = [127.0, 0.5, 1.5, 2.5, -3.5, 126.5]; rows.append(r)
+    # amax 42.5 -> s = 0.334646, bf16(s) = 0.333984 (rounded down) -> -42.5 / bf16(s) =
+    # -127.2515 -> bf16 -127.5 -> half-to-even -128, kept by the [-128, 127] clamp;
+    # 1 / bf16(s) = 2.9942 -> bf16 2.9921875 -> 3; +42.5 would give 128 -> clamp 127.
+    r = np.zeros(k, np.float32); r[:3] = [-42.5, 1.0, 42.5]; rows.append(r)
+    xb = np.stack([np.asarray(b) for b in (bf16_bits(r) for r in rows)])
+    q, s = _mx().quantize_int8_rowwise(from_bits(xb).to(dev))
+    q = q.cpu().numpy()
+    s = s.cpu().numpy().reshape(-1)
+    assert np.all(q[0] == 127) and np.all(q[1] == 126)
+    assert s[2] == np.float32(1e-30) and np.all(q[2] == 0)
+    assert q[3, 5] == -127 and np.count_nonzero(q[3]) == 1
+    assert list(q[4, :6]) == [127, 0, 2, 2, -4, 126]
+    assert list(q[5, :3]) == [-128, 3, 127]
+    q_ref, s_ref = eager_np.quantize_int8_rowwise(xb)
+    assert np.array_equal(q, q_ref) and np.array_equal(s, s_ref.reshape(-1))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_quant_fp16_fp32_match_eager(dev, dtype):
+    x = (torch.randn(37, 1000, generator=gen(5)) * 3).to(dtype)
+    x[3] = 0
+    x[4, :] = 1e-6
+    q, s = _mx().quantize_int8_rowwise(x.to(dev))
+    q_ref, s_ref = eager_torch.quantize_int8_rowwise(x)
+    assert torch.equal(q.cpu(), q_ref)
+    assert torch.equal(s.cpu(), s_ref)
+
+
+def test_quant_row_slices_are_independent(dev):
+    """Quantizing a row range equals the same rows of the full result (per-token scales)."""
+    x = activations(300, 3072, seed=11).to(dev)
+    q, s = _mx().quantize_int8_rowwise(x)
+    q2, s2 = _mx().quantize_int8_rowwise(x[101:233])
+    assert torch.equal(q[101:233], q2) and torch.equal(s[101:233], s2)
+
+
+def test_gelu_exhaustive_matches_torch_table(dev):
+    golden = np.load(__import__("pathlib").Path(__file__).parent / "golden" / "gelu_tanh_bf16.npy")
+    allbits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    y = _mx().apply_input_act(from_bits(allbits).to(dev), "gelu_tanh")
+    yb = bits(y)
+    finite = (allbits & 0x7F80) != 0x7F80
+    assert np.array_equal(yb[finite], golden[finite])
+    assert yb[0x7F80] == golden[0x7F80]  # +inf
+    # odd length, unaligned tail path
+    y2 = _mx().apply_input_act(from_bits(allbits[3:1003]).to(dev), "gelu_tanh")
+    assert np.array_equal(bits(y2), golden[3:1003])
+
+
+def test_quant_gelu_input_act_matches_oracle(dev):
+    x = (torch.randn(65, 3072, generator=gen(3)) * 2).to(torch.bfloat16)
+    q, s = _mx().quantize_int8_rowwise(x.to(dev), input_act="gelu_tanh")
+    q_ref, s_ref = eager_np.quantize_int8_rowwise(eager_np.gelu_tanh_bf16(bits(x)))
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+
+
+def test_quant_with_known_absmax(dev):
+    import mx_qlinear._lib as L
+    from mx_qlinear.ops import _p, _stream
+
+    x = activations(129, 2048, seed=9)
+    amax = np.max(np.abs(bf16_to_f32(bits(x))), axis=1).astype(np.float32)
+    xd = x.to(dev)
+    a = torch.from_numpy(amax).to(dev)
+    q = torch.empty(129, 2048, dtype=torch.int8, device=dev)
+    s = torch.empty(129, dtype=torch.float32, device=dev)
+    L.call("mxq_quantize_int8_rowwise_absmax", _p(xd), _p(a), _p(q), _p(s), 129, 2048, _stream(dev))
+    q_ref, s_ref = eager_np.quantize_int8_rowwise(bits(x))
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy(), s_ref.reshape(-1))
+
+
+def _adaln_inputs(m, d, seed):
+    x = activations(m, d, seed)
+    sc = bf16_vec(d, seed + 1, 0.1)
+    sh = bf16_vec(d, seed + 2, 0.1)
+    return x, sc, sh
+
+
+@pytest.mark.parametrize("m,d", [(64, 5120), (33, 1024), (7, 8192)])
+def test_adaln_matches_oracle(dev, m, d):
+    """Modulated bf16 within max(1 ulp of y, 1 ulp of the product term) of the oracle.
+
+    LayerNorm statistics are reductions whose order differs from torch's CPU kernel, so the
+    normalised value can differ by one bf16 ulp; the product with bf16(1 + scale) and the
+    shift add can carry that ulp into y. The int8 quantization of the kernel's own modulated
+    rows must be bit-exact.
+    """
+    print(f"adaln m={m} d={d}", flush=True)
+    x, sc, sh = _adaln_inputs(m, d, 100 + m)
+    q, s, y = _mx().adaln_quantize_int8(x.to(dev), sc.to(dev), sh.to(dev), 1e-6, return_modulated=True)
+    y_ref = eager_np.adaln(bits(x), bits(sc), bits(sh), 1e-6)
+    yv, rv = bf16_to_f32(bits(y)), bf16_to_f32(y_ref)
+    n_ref = eager_np.layer_norm_f64(bits(x))
+    t = bf16_to_f32(bf16_bits(np.float32(1.0) + bf16_to_f32(bits(sc))))
+    prod = np.abs(n_ref * t)
+    tol = np.maximum(bf16_ulp(np.maximum(np.abs(rv), np.abs(yv))), bf16_ulp(prod))
+    assert np.all(np.abs(yv - rv) <= tol)
+    mismatch = np.mean(bits(y) != y_ref)
+    print(f"adaLN bf16 mismatch rate vs torch CPU: {mismatch:.2e}")
+    assert mismatch < 1e-2
+    q_ref, s_ref = eager_np.quantize_int8_rowwise(bits(y))
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+    y2 = _mx().adaln(x.to(dev), sc.to(dev), sh.to(dev), 1e-6)
+    assert torch.equal(y2, y)
+
+
+def test_adaln_modulation_groups(dev):
+    """scale/shift with one row per group of 4 consecutive x rows."""
+    m, d = 16, 512
+    x = activations(m, d, 77)
+    sc = (torch.randn(4, d, generator=gen(1)) * 0.1).to(torch.bfloat16)
+    sh = (torch.randn(4, d, generator=gen(2)) * 0.1).to(torch.bfloat16)
+    y = _mx().adaln(x.to(dev), sc.to(dev), sh.to(dev))
+    for g in range(4):
+        yg = _mx().adaln(x[4 * g:4 * g + 4].to(dev), sc[g].to(dev), sh[g].to(dev))
+        assert torch.equal(y[4 * g:4 * g + 4], yg)

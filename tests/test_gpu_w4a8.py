@@ -1,0 +1,124 @@
+"""GPU parity: int4 grouped decode, reference-format W4A8 linear and group-scaled W4A8 GEMM.
+
+Bar: decoded int8 weights bit-exact; outputs bit-exact against the oracle's restatement of the
+same summation order; the group-scaled GEMM additionally within its float32 error bound of the
+float64 value and exact where the arithmetic is exact (unit / power-of-two scales).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from _util import activations, bf16_vec, bits, gen, group_scales, packed_int4
+from oracle import eager_np
+from oracle.bf16 import bf16_bits, bf16_ulp
+
+pytestmark = pytest.mark.gpu
+
+
+def _mx():
+    import mx_qlinear
+
+    return mx_qlinear
+
+
+@pytest.mark.parametrize("g", [4, 16, 32, 128])
+@pytest.mark.parametrize("e4m3", [False, True])
+@pytest.mark.parametrize("codebook", [False, True])
+def test_decode_matches_oracle(dev, g, e4m3, codebook):
+    n, k = 96, 512
+    qd = packed_int4(n, k, 7 + g)
+    s = torch.rand(n, k // g, generator=gen(g)) * 30
+    if e4m3:
+        s = s.to(torch.float8_e4m3fn)
+    cb = torch.linspace(-7.5, 7.5, 16) if codebook else None
+    w8 = _mx().dequantize_int4_grouped_to_int8(qd.to(dev), s.to(dev), None if cb is None else cb.to(dev), g)
+    s_np = s.view(torch.uint8).numpy() if e4m3 else s.numpy()
+    ref = eager_np.dequant_int4_grouped_to_int8(qd.numpy(), s_np, None if cb is None else cb.numpy(), g,
+                                                s_rel_is_e4m3=e4m3)
+    assert np.array_equal(w8.cpu().numpy(), ref)
+
+
+def test_decode_unit_scale_is_code_minus_8(dev):
+    n, k = 16, 64
+    codes = np.arange(n * k).reshape(n, k) % 16
+    qd = torch.from_numpy(eager_np.pack_int4(codes))
+    w8 = _mx().dequantize_int4_grouped_to_int8(qd.to(dev), torch.ones(n, k // 16, device=dev), None, 16)
+    assert np.array_equal(w8.cpu().numpy(), codes - 8)
+
+
+def test_w4a8_reference_format_linear(dev):
+    m, n, k, g = 200, 300, 1024, 16
+    x = activations(m, k, 31)
+    qd = packed_int4(n, k, 32)
+    s_rel = (torch.rand(n, k // g, generator=gen(33)) * 15 + 1).to(torch.float8_e4m3fn)
+    s_ch = torch.rand(n, generator=gen(34)) * 1e-3
+    cb = torch.linspace(-7.5, 7.5, 16)
+    bias = bf16_vec(n, 35, 0.01)
+    y = _mx().w4a8_int8_linear(x.to(dev), qd.to(dev), s_rel.to(dev), s_ch.to(dev), codebook=cb.to(dev),
+                               bias=bias.to(dev), group_size=g, convrot_groupsize=0)
+    ref = eager_np.w4a8_reference_linear(bits(x), qd.numpy(), s_rel.view(torch.uint8).numpy(), s_ch.numpy(),
+                                         cb.numpy(), g, bits(bias), "bf16", s_rel_is_e4m3=True)
+    assert np.array_equal(bits(y), bf16_bits(ref))
+
+
+def _int_input(m, k, seed):
+    return torch.randint(-128, 128, (m, k), generator=gen(seed), dtype=torch.int8)
+
+
+@pytest.mark.parametrize("m", [64, 2048])
+def test_grouped_unit_scales_are_exact(dev, m):
+    """scale = 1, xs = 1, fp32 out: the output is the exact integer sum of A * (c - 8)."""
+    n, k, g = 384, 1024, 128
+    a = _int_input(m, k, m)
+    qd = packed_int4(n, k, m + 1)
+    gs = torch.ones(k // g, n, dtype=torch.float16)
+    y = _mx().w4a8_grouped_linear(a.to(dev), qd.to(dev), gs.to(dev), g, out_dtype=torch.float32,
+                                  x_scale=torch.ones(m, device=dev))
+    w = eager_np.unpack_int4(qd.numpy()) - 8
+    exact = a.numpy().astype(np.int64) @ w.astype(np.int64).T
+    assert np.array_equal(y.cpu().numpy(), exact.astype(np.float32))
+
+
+def test_grouped_power_of_two_scales_are_exact(dev):
+    """Per-group scales 2^-(g % 5): every fp32 step is exact, so the group indexing is pinned."""
+    m, n, k, g = 96, 256, 2048, 128
+    a = _int_input(m, k, 3)
+    qd = packed_int4(n, k, 4)
+    gs = torch.tensor([2.0 ** -(i % 5) for i in range(k // g)], dtype=torch.float16)[:, None].repeat(1, n)
+    gs[:, 7] = 4.0
+    y = _mx().w4a8_grouped_linear(a.to(dev), qd.to(dev), gs.to(dev), g, out_dtype=torch.float32,
+                                  x_scale=torch.ones(m, device=dev))
+    p = eager_np.w4a8_group_partials(a.numpy(), qd.numpy(), g).astype(np.float64)
+    exact = (p * gs.double().numpy()[:, None, :]).sum(axis=0)
+    assert np.array_equal(y.cpu().numpy().astype(np.float64), exact)
+
+
+@pytest.mark.parametrize("m,n,k,g", [(512, 1024, 5120, 128), (2048, 640, 1024, 128), (100, 200, 1024, 256),
+                                     (33, 70, 512, 128)])
+def test_grouped_matches_oracle(dev, m, n, k, g):
+    print(f"w4a8 grouped m={m} n={n} k={k} g={g}", flush=True)
+    x = activations(m, k, 1000 + m, outlier_frac=0.0)
+    qd = packed_int4(n, k, 1001 + n)
+    gs = group_scales(k, n, g, 1002)
+    y = _mx().w4a8_grouped_linear(x.to(dev), qd.to(dev), gs.to(dev), g)
+    a, xs = eager_np.quantize_int8_rowwise(bits(x))
+    ref = eager_np.w4a8_grouped_linear(a, xs, qd.numpy(), gs.numpy(), g)
+    assert np.array_equal(bits(y), bf16_bits(ref))
+    # independent float64 pin: |y - exact| <= 1 ulp(y) + fp32 accumulation bound
+    exact, mag = eager_np.w4a8_grouped_linear_f64(a, xs, qd.numpy(), gs.numpy(), g)
+    yv = y.float().cpu().numpy().astype(np.float64)
+    bound = bf16_ulp(np.abs(exact).astype(np.float32)).astype(np.float64) + (k // g + 2) * 2.0 ** -24 * mag
+    assert np.all(np.abs(yv - exact) <= bound)
+
+
+def test_grouped_with_bias(dev):
+    m, n, k, g = 64, 256, 512, 128
+    x = activations(m, k, 70)
+    qd = packed_int4(n, k, 71)
+    gs = group_scales(k, n, g, 72)
+    bias = bf16_vec(n, 73, 0.01)
+    y = _mx().w4a8_grouped_linear(x.to(dev), qd.to(dev), gs.to(dev), g, bias=bias.to(dev))
+    a, xs = eager_np.quantize_int8_rowwise(bits(x))
+    ref = eager_np.w4a8_grouped_linear(a, xs, qd.numpy(), gs.numpy(), g, bits(bias))
+    assert np.array_equal(bits(y), bf16_bits(ref))

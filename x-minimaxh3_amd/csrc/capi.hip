@@ -1,0 +1,26 @@
+// Error reporting shared by every C-ABI entry point of libmx_qlinear.so.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "mxq_common.h"
+
+static thread_local char g_last_error[512] = "";
+
+int mxq_set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int mxq_check_launch(const char* what) {
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess)
+    return mxq_set_error(MXQ_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(err));
+  return MXQ_OK;
+}
+
+extern "C" const char* mxq_last_error(void) { return g_last_error; }
+
+extern "C" int mxq_abi_version(void) { return MXQ_ABI_VERSION; }

@@ -1,0 +1,171 @@
+// Shared device helpers for the gfx950 quantized-linear kernels.
+//
+// Number formats follow the reference's eager PyTorch semantics
+// (backends/turbo/vendor/comfy_kitchen/backends/eager/quantization.py):
+// every float operation is one IEEE-754 fp32 operation with round-to-nearest-even,
+// bfloat16/float16 results are rounded from fp32 with round-to-nearest-even.
+// All HIP sources are compiled with -ffp-contract=off so that no multiply-add
+// is fused unless written as fmaf() explicitly.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mx_qlinear.h"
+
+#define MXQ_DEVICE __device__ __forceinline__
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+
+namespace mxq {
+
+constexpr int kWave = 64;
+
+// ---- bfloat16 / float16 -------------------------------------------------------
+
+MXQ_DEVICE float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// Materialise an fp32 value before it is narrowed. The reference rounds every product to
+// fp32 first and then to the output type (two roundings); without this barrier the backend
+// folds fptrunc(fmul) into v_fma_mixlo_f16, a single rounding that differs on fp16 ties.
+MXQ_DEVICE float fp32_barrier(float f) {
+  __asm__ volatile("" : "+v"(f));
+  return f;
+}
+
+// fp32 -> bf16 bits, round-to-nearest-even (v_cvt_pk_bf16_f32 under the default rounding
+// mode). NaN inputs give a quiet NaN; their bit pattern is not part of the contract.
+MXQ_DEVICE uint32_t f32_to_bf16_bits(float f) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)fp32_barrier(f));
+}
+
+// Two fp32 -> packed bf16 pair (lo in bits 0..15), one v_cvt_pk_bf16_f32.
+MXQ_DEVICE uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  const f2 v = {fp32_barrier(lo), fp32_barrier(hi)};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2));
+}
+
+MXQ_DEVICE float round_bf16(float f) { return bf16_to_f32(f32_to_bf16_bits(f)); }
+
+MXQ_DEVICE float f16_to_f32(uint32_t bits16) {
+  _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits16);
+  return (float)h;
+}
+
+MXQ_DEVICE uint32_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)fp32_barrier(f);  // v_cvt_f16_f32, round-to-nearest-even
+  return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+MXQ_DEVICE float round_f16(float f) { return f16_to_f32(f32_to_f16_bits(f)); }
+
+// Output element types, by the reference's dtype codes
+// (backends/eager/quantization.py:34-42): 0 fp32, 1 fp16, 2 bf16.
+template <int kCode> struct OutT;
+template <> struct OutT<0> {
+  typedef float T;
+  static MXQ_DEVICE float round(float f) { return f; }
+  static MXQ_DEVICE float load(const float* p) { return *p; }
+};
+template <> struct OutT<1> {
+  typedef uint16_t T;
+  static MXQ_DEVICE float round(float f) { return round_f16(f); }
+  static MXQ_DEVICE float load(const uint16_t* p) { return f16_to_f32(*p); }
+};
+template <> struct OutT<2> {
+  typedef uint16_t T;
+  static MXQ_DEVICE float round(float f) { return round_bf16(f); }
+  static MXQ_DEVICE float load(const uint16_t* p) { return bf16_to_f32(*p); }
+};
+
+template <int kCode> MXQ_DEVICE void store_out(typename OutT<kCode>::T* p, float v);
+template <> MXQ_DEVICE void store_out<0>(float* p, float v) { *p = v; }
+template <> MXQ_DEVICE void store_out<1>(uint16_t* p, float v) { *p = (uint16_t)f32_to_f16_bits(v); }
+template <> MXQ_DEVICE void store_out<2>(uint16_t* p, float v) { *p = (uint16_t)f32_to_bf16_bits(v); }
+
+// ---- quantizer pieces -----------------------------------------------------------
+
+// Eager scale: max(fp32(amax) / 127, 1e-30) (quantization.py:872-873).
+MXQ_DEVICE float row_scale_from_absmax(float amax) {
+  float s = amax / 127.0f;
+  return (s != s) ? s : fmaxf(s, 1e-30f);
+}
+
+// Round a float holding a bf16/fp16/fp32 quotient to int8 with the eager rule:
+// round-half-to-even, clamp to [-128, 127]; NaN -> 0.
+MXQ_DEVICE int quant_round_clamp(float qf) {
+  float r = __builtin_rintf(qf);
+  r = fminf(fmaxf(r, -128.0f), 127.0f);
+  return (qf != qf) ? 0 : (int)r;
+}
+
+// ---- tanh-GELU on bfloat16 ----------------------------------------------------------
+// Bit-exact torch CPU gelu(approximate="tanh") on a bfloat16 input (the routine the reference
+// applies, backends/turbo/vendor/comfy_kitchen/backends/_activations.py:47-48). The function
+// depends on the 16 input bits only: inputs with biased exponent below MXQ_GELU_E_LO map to
+// bf16(x / 2), finite inputs at or above MXQ_GELU_E_HI to x (x > 0) or -0.0 (x < 0); the
+// 3072 inputs in between are looked up in a table generated from torch by gen_gelu_table.py,
+// which verifies each rule against all 65,536 torch outputs.
+#define MXQ_GELU_TABLE_DECL static __constant__ uint16_t kGeluTable[3072]
+#include "gelu_tanh_bf16_table.inc"
+#undef MXQ_GELU_TABLE_DECL
+
+MXQ_DEVICE uint32_t gelu_table_index(uint32_t b) {
+  const int e = (int)((b >> 7) & 0xFFu);
+  const int ei = min(max(e - MXQ_GELU_E_LO, 0), MXQ_GELU_E_HI - MXQ_GELU_E_LO - 1);
+  return ((b >> 15) * (MXQ_GELU_E_HI - MXQ_GELU_E_LO) + ei) * 128u + (b & 0x7Fu);
+}
+
+// Result for inputs outside the table range; `looked_up` is table[gelu_table_index(b)].
+MXQ_DEVICE uint32_t gelu_bf16_finish(uint32_t b, uint32_t looked_up) {
+  const uint32_t e = (b >> 7) & 0xFFu, sign = b & 0x8000u, mag = b & 0x7FFFu;
+  const uint32_t v = mag & 0xFFu;
+  const uint32_t half_sub = (v >> 1) + ((v & 1u) & ((v >> 1) & 1u));
+  const uint32_t half = sign | (e >= 2 ? mag - 0x80u : half_sub);
+  const uint32_t big = sign ? 0x8000u : b;
+  const uint32_t special = (b == 0x7F80u) ? 0x7F80u : MXQ_GELU_NAN;
+  return e < MXQ_GELU_E_LO ? half : e < MXQ_GELU_E_HI ? looked_up : e < 255u ? big : special;
+}
+
+// GELU of one bf16 (bits) using the table in constant memory.
+MXQ_DEVICE uint32_t gelu_bf16(uint32_t b) {
+  return gelu_bf16_finish(b, kGeluTable[gelu_table_index(b)]);
+}
+
+// ---- wave reductions --------------------------------------------------------------
+
+MXQ_DEVICE float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+MXQ_DEVICE float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// max over the 32 lanes of each half-wave (lanes sharing l / 32).
+MXQ_DEVICE float halfwave_max(float v) {
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Non-negative floats order like their bit patterns; NaN (0x7FC00000) sorts above +inf.
+MXQ_DEVICE void atomic_max_nonneg(float* addr, float v) {
+  atomicMax(reinterpret_cast<unsigned int*>(addr), __float_as_uint(v));
+}
+
+}  // namespace mxq
+
+// ---- host-side error plumbing (defined in capi.hip) -------------------------------
+int mxq_set_error(int code, const char* fmt, ...);
+int mxq_check_launch(const char* what);

@@ -1,0 +1,422 @@
+// Per-token INT8 quantizers and adaLN for gfx950.
+//
+// Row quantizer semantics (backends/turbo/vendor/comfy_kitchen/backends/eager/quantization.py:857-875):
+//   amax = max |x|;  s = max(fp32(amax) / 127, 1e-30);  q = clamp(rne(T(x / T(s))), -128, 127)
+// where T is the input dtype (bf16 / fp16 / fp32) and the division is one fp32 division rounded
+// to T. For bf16 the quotient of two bf16 values is never within 2^-17 (relative) of a bf16
+// rounding midpoint unless it is exactly representable, so bf16(x * rn(1/s)) == bf16(x / s)
+// for every pair; the bf16 kernels therefore take one reciprocal per row and multiply.
+// (The identity is checked exhaustively over all bf16 pairs by the CPU test suite.)
+//
+// Layout: one wavefront per row; each lane owns 16-byte chunks lane, lane+64, ... of the row,
+// held in registers between the absmax reduction and the quantize pass, so x is read from HBM
+// exactly once and q written once (the memory-bound roofline: 2 B read + 1 B written / element).
+
+#include "mxq_common.h"
+
+namespace mxq {
+
+constexpr int kQuantBlock = 256;               // 4 waves, one row each
+constexpr int kRowsPerBlock = kQuantBlock / kWave;
+
+MXQ_DEVICE float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+MXQ_DEVICE float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+MXQ_DEVICE uint32_t pack_q4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) |
+         ((uint32_t)(d & 0xFF) << 24);
+}
+
+// Quantize 8 bf16 values (4 packed words) with reciprocal r; returns 8 int8 in two words.
+MXQ_DEVICE v2u quant8_bf16(v4u w, float r) {
+  int q[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    q[2 * i] = quant_round_clamp(round_bf16(bf16_lo(w[i]) * r));
+    q[2 * i + 1] = quant_round_clamp(round_bf16(bf16_hi(w[i]) * r));
+  }
+  v2u o;
+  o[0] = pack_q4(q[0], q[1], q[2], q[3]);
+  o[1] = pack_q4(q[4], q[5], q[6], q[7]);
+  return o;
+}
+
+MXQ_DEVICE uint32_t gelu_pair(uint32_t w) {
+  return gelu_bf16(w & 0xFFFFu) | (gelu_bf16(w >> 16) << 16);
+}
+
+MXQ_DEVICE float absmax_pair(uint32_t w) {
+  return fmaxf(fabsf(bf16_lo(w)), fabsf(bf16_hi(w)));
+}
+
+// bf16 rows, cols % 8 == 0, cols <= 512 * NCH: row held in registers.
+template <int NCH, bool kGelu>
+__global__ __launch_bounds__(kQuantBlock) void quant_rows_bf16_reg(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scales,
+    int64_t rows, int cols) {
+  const int lane = threadIdx.x % kWave;
+  const int nchunk = cols / 8;
+  for (int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave; row < rows;
+       row += (int64_t)gridDim.x * kRowsPerBlock) {
+    const v4u* src = reinterpret_cast<const v4u*>(x + row * cols);
+    v4u v[NCH];
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = lane + j * kWave;
+      if (c < nchunk) {
+        v[j] = __builtin_nontemporal_load(src + c);
+        if (kGelu) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[j][i] = gelu_pair(v[j][i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m = fmaxf(m, absmax_pair(v[j][i]));
+      }
+    }
+    const float amax = wave_max(m);
+    const float s = row_scale_from_absmax(amax);
+    const float r = 1.0f / round_bf16(s);
+    v2u* dst = reinterpret_cast<v2u*>(q + row * cols);
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = lane + j * kWave;
+      if (c < nchunk) __builtin_nontemporal_store(quant8_bf16(v[j], r), dst + c);
+    }
+    if (lane == 0) scales[row] = s;
+  }
+}
+
+// Any dtype, any cols: two passes over the row with scalar loads (second pass hits cache).
+template <int kDtype, bool kGelu>
+__global__ __launch_bounds__(kQuantBlock) void quant_rows_generic(
+    const void* __restrict__ xv, int8_t* __restrict__ q, float* __restrict__ scales,
+    int64_t rows, int64_t cols) {
+  const int lane = threadIdx.x % kWave;
+  for (int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave; row < rows;
+       row += (int64_t)gridDim.x * kRowsPerBlock) {
+    auto load = [&](int64_t i) -> float {
+      float f;
+      if (kDtype == MXQ_DTYPE_F32) {
+        f = reinterpret_cast<const float*>(xv)[row * cols + i];
+      } else {
+        const uint16_t b = reinterpret_cast<const uint16_t*>(xv)[row * cols + i];
+        f = (kDtype == MXQ_DTYPE_BF16) ? bf16_to_f32(b) : f16_to_f32(b);
+      }
+      if (kGelu) f = bf16_to_f32(gelu_bf16(f32_to_bf16_bits(f)));
+      return f;
+    };
+    float m = 0.0f;
+    for (int64_t i = lane; i < cols; i += kWave) m = fmaxf(m, fabsf(load(i)));
+    const float amax = wave_max(m);
+    const float s = row_scale_from_absmax(amax);
+    float s_math;
+    if (kDtype == MXQ_DTYPE_BF16) {
+      s_math = round_bf16(s);
+    } else if (kDtype == MXQ_DTYPE_F16) {
+      s_math = round_f16(s);
+      if (s_math == 0.0f) s_math = 6.103515625e-05f;  // torch.finfo(float16).tiny
+    } else {
+      s_math = s;
+    }
+    for (int64_t i = lane; i < cols; i += kWave) {
+      const float f = load(i);
+      float qf = f / s_math;
+      if (kDtype == MXQ_DTYPE_BF16) qf = round_bf16(qf);
+      if (kDtype == MXQ_DTYPE_F16) qf = round_f16(qf);
+      q[row * cols + i] = (int8_t)quant_round_clamp(qf);
+    }
+    if (lane == 0) scales[row] = s;
+  }
+}
+
+// Streaming quantizer with a known row absmax; each thread handles one 8-element chunk.
+__global__ __launch_bounds__(256) void quant_rows_bf16_absmax(
+    const uint16_t* __restrict__ x, const float* __restrict__ row_absmax,
+    int8_t* __restrict__ q, float* __restrict__ scales, int64_t total_chunks,
+    int64_t chunks_per_row) {
+  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < total_chunks;
+       c += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = c / chunks_per_row;
+    const float s = row_scale_from_absmax(row_absmax[row]);
+    const float r = 1.0f / round_bf16(s);
+    const v4u w = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(x) + c);
+    __builtin_nontemporal_store(quant8_bf16(w, r), reinterpret_cast<v2u*>(q) + c);
+    if (c == row * chunks_per_row) scales[row] = s;
+  }
+}
+
+// ---- adaLN ------------------------------------------------------------------------
+// y = bf16(bf16(bf16(n) * bf16(1 + scale)) + shift), n = (x - mean) * rstd in fp32,
+// rstd = 1 / sqrt(var + eps), var the biased variance (CK/backends/eager/adaln.py:11-14 on
+// torch's CPU layer_norm). Statistics are two-pass over the register-resident row.
+
+MXQ_DEVICE uint32_t modulate(float xv, float mean, float rstd, uint32_t sc, uint32_t sh) {
+  const float n = round_bf16((xv - mean) * rstd);
+  const float t = round_bf16(1.0f + bf16_to_f32(sc));
+  const float p = round_bf16(n * t);
+  return f32_to_bf16_bits(p + bf16_to_f32(sh));
+}
+
+template <int NCH, bool kQuant>
+__global__ __launch_bounds__(kQuantBlock) void adaln_rows_reg(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ scale,
+    const uint16_t* __restrict__ shift, int64_t scale_group, int64_t shift_group, float eps,
+    int8_t* __restrict__ q, float* __restrict__ scales, uint16_t* __restrict__ y_out,
+    int64_t rows, int cols) {
+  const int lane = threadIdx.x % kWave;
+  const int nchunk = cols / 8;
+  for (int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave; row < rows;
+       row += (int64_t)gridDim.x * kRowsPerBlock) {
+    const v4u* src = reinterpret_cast<const v4u*>(x + row * cols);
+    const v4u* scv = reinterpret_cast<const v4u*>(scale + (row / scale_group) * cols);
+    const v4u* shv = reinterpret_cast<const v4u*>(shift + (row / shift_group) * cols);
+    v4u v[NCH];
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = lane + j * kWave;
+      if (c < nchunk) {
+        v[j] = __builtin_nontemporal_load(src + c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sum += bf16_lo(v[j][i]) + bf16_hi(v[j][i]);
+      }
+    }
+    const float mean = wave_sum(sum) / (float)cols;
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = lane + j * kWave;
+      if (c < nchunk) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float a = bf16_lo(v[j][i]) - mean, b = bf16_hi(v[j][i]) - mean;
+          ss += a * a;
+          ss += b * b;
+        }
+      }
+    }
+    const float var = wave_sum(ss) / (float)cols;
+    const float rstd = 1.0f / sqrtf(var + eps);
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = lane + j * kWave;
+      if (c < nchunk) {
+        const v4u sc = scv[c], sh = shv[c];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t lo = modulate(bf16_lo(v[j][i]), mean, rstd, sc[i] & 0xFFFF, sh[i] & 0xFFFF);
+          const uint32_t hi = modulate(bf16_hi(v[j][i]), mean, rstd, sc[i] >> 16, sh[i] >> 16);
+          v[j][i] = lo | (hi << 16);
+          m = fmaxf(m, absmax_pair(v[j][i]));
+        }
+        if (y_out != nullptr) reinterpret_cast<v4u*>(y_out + row * cols)[c] = v[j];
+      }
+    }
+    if (kQuant) {
+      const float amax = wave_max(m);
+      const float s = row_scale_from_absmax(amax);
+      const float r = 1.0f / round_bf16(s);
+      v2u* dst = reinterpret_cast<v2u*>(q + row * cols);
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int c = lane + j * kWave;
+        if (c < nchunk) __builtin_nontemporal_store(quant8_bf16(v[j], r), dst + c);
+      }
+      if (lane == 0) scales[row] = s;
+    }
+  }
+}
+
+// Elementwise tanh-GELU on bf16 (8 elements per thread when 16-byte aligned).
+__global__ __launch_bounds__(256) void gelu_bf16_kernel(const uint16_t* __restrict__ x,
+                                                        uint16_t* __restrict__ y, int64_t n,
+                                                        int vec) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  if (vec) {
+    const int64_t nv = n / 8;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nv; i += stride) {
+      v4u w = reinterpret_cast<const v4u*>(x)[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[j] = gelu_pair(w[j]);
+      reinterpret_cast<v4u*>(y)[i] = w;
+    }
+    for (int64_t i = nv * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+      y[i] = (uint16_t)gelu_bf16(x[i]);
+  } else {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+      y[i] = (uint16_t)gelu_bf16(x[i]);
+  }
+}
+
+__global__ void fill_f32_kernel(float* __restrict__ p, float value, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = value;
+}
+
+static unsigned row_grid(int64_t rows) {
+  const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  return (unsigned)(blocks < 65536 * 4 ? blocks : 65536 * 4);
+}
+
+// Smallest register-chunk count covering cols (chunks of 8 elements per lane, 64 lanes).
+static int pick_nch(int64_t cols) {
+  const int64_t need = (cols / 8 + kWave - 1) / kWave;
+  const int options[] = {1, 2, 4, 8, 12, 16, 24, 32, 40};
+  for (int o : options)
+    if (need <= o) return o;
+  return 0;
+}
+
+}  // namespace mxq
+
+using namespace mxq;
+
+#define MXQ_NCH_SWITCH(nch, BODY) \
+  switch (nch) {                  \
+    case 1: { constexpr int N_ = 1; BODY; } break;   \
+    case 2: { constexpr int N_ = 2; BODY; } break;   \
+    case 4: { constexpr int N_ = 4; BODY; } break;   \
+    case 8: { constexpr int N_ = 8; BODY; } break;   \
+    case 12: { constexpr int N_ = 12; BODY; } break; \
+    case 16: { constexpr int N_ = 16; BODY; } break; \
+    case 24: { constexpr int N_ = 24; BODY; } break; \
+    case 32: { constexpr int N_ = 32; BODY; } break; \
+    case 40: { constexpr int N_ = 40; BODY; } break; \
+    default: break;                                  \
+  }
+
+#define MXQ_NCH_SWITCH_16(nch, BODY) \
+  switch (nch) {                     \
+    case 1: { constexpr int N_ = 1; BODY; } break;   \
+    case 2: { constexpr int N_ = 2; BODY; } break;   \
+    case 4: { constexpr int N_ = 4; BODY; } break;   \
+    case 8: { constexpr int N_ = 8; BODY; } break;   \
+    case 12: { constexpr int N_ = 12; BODY; } break; \
+    case 16: { constexpr int N_ = 16; BODY; } break; \
+    default: break;                                  \
+  }
+
+extern "C" int mxq_quantize_int8_rowwise(const void* x, int x_dtype, int8_t* q, float* scales,
+                                         int64_t rows, int64_t cols, int input_act,
+                                         void* stream) {
+  if (rows < 0 || cols < 0) return mxq_set_error(MXQ_ERR_INVALID, "negative shape");
+  if (rows == 0) return MXQ_OK;
+  if (cols == 0) return mxq_set_error(MXQ_ERR_INVALID, "quantize_int8_rowwise needs cols > 0");
+  if (!x || !q || !scales) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  if (x_dtype != MXQ_DTYPE_BF16 && x_dtype != MXQ_DTYPE_F16 && x_dtype != MXQ_DTYPE_F32)
+    return mxq_set_error(MXQ_ERR_UNSUPPORTED, "input dtype code %d", x_dtype);
+  if (input_act != MXQ_ACT_NONE && input_act != MXQ_ACT_GELU_TANH)
+    return mxq_set_error(MXQ_ERR_INVALID, "unsupported input_act code %d", input_act);
+  if (input_act == MXQ_ACT_GELU_TANH && x_dtype != MXQ_DTYPE_BF16)
+    return mxq_set_error(MXQ_ERR_UNSUPPORTED, "gelu_tanh input_act needs bf16 input");
+  hipStream_t st = (hipStream_t)stream;
+  const bool gelu = input_act == MXQ_ACT_GELU_TANH;
+  const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 8 == 0);
+  const int nch = pick_nch(cols);
+  if (x_dtype == MXQ_DTYPE_BF16 && cols % 8 == 0 && aligned && nch > 0 && cols <= INT32_MAX) {
+    if (gelu) {
+      MXQ_NCH_SWITCH(nch, (quant_rows_bf16_reg<N_, true><<<row_grid(rows), kQuantBlock, 0, st>>>(
+                               (const uint16_t*)x, q, scales, rows, (int)cols)));
+    } else {
+      MXQ_NCH_SWITCH(nch, (quant_rows_bf16_reg<N_, false><<<row_grid(rows), kQuantBlock, 0, st>>>(
+                               (const uint16_t*)x, q, scales, rows, (int)cols)));
+    }
+    return mxq_check_launch("quant_rows_bf16_reg");
+  }
+  if (x_dtype == MXQ_DTYPE_BF16) {
+    if (gelu)
+      quant_rows_generic<MXQ_DTYPE_BF16, true><<<row_grid(rows), kQuantBlock, 0, st>>>(x, q, scales, rows, cols);
+    else
+      quant_rows_generic<MXQ_DTYPE_BF16, false><<<row_grid(rows), kQuantBlock, 0, st>>>(x, q, scales, rows, cols);
+  } else if (x_dtype == MXQ_DTYPE_F16) {
+    quant_rows_generic<MXQ_DTYPE_F16, false><<<row_grid(rows), kQuantBlock, 0, st>>>(x, q, scales, rows, cols);
+  } else {
+    quant_rows_generic<MXQ_DTYPE_F32, false><<<row_grid(rows), kQuantBlock, 0, st>>>(x, q, scales, rows, cols);
+  }
+  return mxq_check_launch("quant_rows_generic");
+}
+
+extern "C" int mxq_quantize_int8_rowwise_absmax(const void* x_bf16, const float* row_absmax,
+                                                int8_t* q, float* scales, int64_t rows,
+                                                int64_t cols, void* stream) {
+  if (rows < 0 || cols <= 0) return mxq_set_error(MXQ_ERR_INVALID, "bad shape [%lld, %lld]", (long long)rows, (long long)cols);
+  if (rows == 0) return MXQ_OK;
+  if (!x_bf16 || !row_absmax || !q || !scales) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  if (cols % 8 != 0 || (uintptr_t)x_bf16 % 16 != 0 || (uintptr_t)q % 8 != 0)
+    return mxq_set_error(MXQ_ERR_UNSUPPORTED, "absmax quantizer needs cols %% 8 == 0 and aligned rows");
+  const int64_t cpr = cols / 8, total = rows * cpr;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 256 * 1024) blocks = 256 * 1024;
+  quant_rows_bf16_absmax<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)x_bf16, row_absmax, q, scales, total, cpr);
+  return mxq_check_launch("quant_rows_bf16_absmax");
+}
+
+static int adaln_launch(const void* x, const void* scale, const void* shift, int64_t scale_group,
+                        int64_t shift_group, float eps, int8_t* q, float* scales, void* y_out,
+                        int64_t rows, int64_t cols, void* stream, bool quant) {
+  if (rows < 0 || cols <= 0) return mxq_set_error(MXQ_ERR_INVALID, "bad shape");
+  if (rows == 0) return MXQ_OK;
+  if (!x || !scale || !shift) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  if (scale_group <= 0 || shift_group <= 0)
+    return mxq_set_error(MXQ_ERR_INVALID, "modulation groups must be positive");
+  if (quant && (!q || !scales)) return mxq_set_error(MXQ_ERR_INVALID, "null output");
+  const int nch = pick_nch(cols);
+  if (cols % 8 != 0 || nch == 0 || nch > 16 || (uintptr_t)x % 16 || (uintptr_t)scale % 16 ||
+      (uintptr_t)shift % 16 || (y_out && (uintptr_t)y_out % 16) || (q && (uintptr_t)q % 8))
+    return mxq_set_error(MXQ_ERR_UNSUPPORTED,
+                         "adaLN needs cols %% 8 == 0, cols <= 8192 and 16-byte aligned rows");
+  hipStream_t st = (hipStream_t)stream;
+  if (quant) {
+    MXQ_NCH_SWITCH_16(nch, (adaln_rows_reg<N_, true><<<row_grid(rows), kQuantBlock, 0, st>>>(
+                             (const uint16_t*)x, (const uint16_t*)scale, (const uint16_t*)shift,
+                             scale_group, shift_group, eps, q, scales, (uint16_t*)y_out, rows,
+                             (int)cols)));
+  } else {
+    MXQ_NCH_SWITCH_16(nch, (adaln_rows_reg<N_, false><<<row_grid(rows), kQuantBlock, 0, st>>>(
+                             (const uint16_t*)x, (const uint16_t*)scale, (const uint16_t*)shift,
+                             scale_group, shift_group, eps, nullptr, nullptr, (uint16_t*)y_out,
+                             rows, (int)cols)));
+  }
+  return mxq_check_launch("adaln_rows_reg");
+}
+
+extern "C" int mxq_adaln(const void* x, const void* scale, const void* shift, void* out,
+                         int64_t rows, int64_t cols, int64_t scale_group, int64_t shift_group,
+                         float eps, void* stream) {
+  if (!out) return mxq_set_error(MXQ_ERR_INVALID, "null output");
+  return adaln_launch(x, scale, shift, scale_group, shift_group, eps, nullptr, nullptr, out, rows,
+                      cols, stream, false);
+}
+
+extern "C" int mxq_adaln_quantize_int8(const void* x, const void* scale, const void* shift,
+                                       int64_t scale_group, int64_t shift_group, float eps,
+                                       int8_t* q, float* scales, void* y_out, int64_t rows,
+                                       int64_t cols, void* stream) {
+  return adaln_launch(x, scale, shift, scale_group, shift_group, eps, q, scales, y_out, rows, cols,
+                      stream, true);
+}
+
+extern "C" int mxq_fill_f32(float* p, float value, int64_t n, void* stream) {
+  if (n < 0) return mxq_set_error(MXQ_ERR_INVALID, "negative length");
+  if (n == 0) return MXQ_OK;
+  if (!p) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  fill_f32_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(p, value, n);
+  return mxq_check_launch("fill_f32");
+}
+
+extern "C" int mxq_gelu_tanh_bf16(const void* x, void* y, int64_t n, void* stream) {
+  if (n < 0) return mxq_set_error(MXQ_ERR_INVALID, "negative length");
+  if (n == 0) return MXQ_OK;
+  if (!x || !y) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  const int vec = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0);
+  int64_t blocks = (n / 8 + 255) / 256 + 1;
+  if (blocks > 65536) blocks = 65536;
+  gelu_bf16_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>((const uint16_t*)x, (uint16_t*)y, n, vec);
+  return mxq_check_launch("gelu_bf16_kernel");
+}

@@ -1,0 +1,35 @@
+"""mx_qlinear: the MI355X (gfx950) quantized DiT linear path.
+
+Per-token INT8 activation quantization (optionally fused with adaLN), INT8 x INT8 -> INT32
+GEMMs on CDNA4 matrix cores with fused dequant / bias / tanh-GELU / re-quant epilogues, and
+W4A8 GEMMs, behind the reference's Comfy-Kitchen function names and its quantized-linear
+module contract. All compute runs in hand-written HIP kernels (libmx_qlinear.so, C ABI in
+include/mx_qlinear.h); there is no CPU path.
+"""
+
+from .ops import (  # noqa: F401
+    FfnWorkspace,
+    adaln,
+    adaln_quantize_int8,
+    apply_input_act,
+    dequantize_int4_grouped_to_int8,
+    int8_ffn_gelu,
+    int8_linear,
+    int8_linear_prequantized,
+    mm_int8,
+    quantize_int8_rowwise,
+    w4a8_grouped_linear,
+    w4a8_int8_linear,
+)
+from .modules import (  # noqa: F401
+    ComfyQuantSpec,
+    ConvRotInt8Linear,
+    ConvRotW4A8Linear,
+    PreparedConvRotInt8Input,
+    W4A8QuantSpec,
+    inspect_quantized_layers,
+    int8_kernel,
+    w4a8_kernel,
+)
+
+__version__ = "0.1.0"

@@ -1,0 +1,477 @@
+"""Torch-facing functions of the quantized linear path.
+
+Names, argument order, defaults and error behaviour mirror the reference's Comfy-Kitchen API
+(backends/turbo/vendor/comfy_kitchen/__init__.py:110-127, 702-764 and
+comfy_kitchen/tensor/w4a8_int8.py:89-115; CK below stands for
+backends/turbo/vendor/comfy_kitchen). Every function runs the HIP kernels of libmx_qlinear.so
+on the tensors' GPU and current stream; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import call
+
+_OUT_CODES = {torch.float32: _lib.DTYPE_F32, torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16}
+_ACT_CODES = {None: _lib.ACT_NONE, "none": _lib.ACT_NONE, "gelu_tanh": _lib.ACT_GELU_TANH}
+
+
+def _p(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_gpu(*tensors: torch.Tensor | None) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError("mx_qlinear runs on the GPU only; got a tensor on " + str(t.device))
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _act_code(input_act: str | None) -> int:
+    try:
+        return _ACT_CODES[input_act]
+    except KeyError:
+        raise ValueError(
+            f"unsupported input_act: {input_act!r} (expected one of ['gelu_tanh', 'none'])"
+        ) from None
+
+
+def _out_code(dtype: torch.dtype) -> int:
+    try:
+        return _OUT_CODES[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported output dtype {dtype}") from None
+
+
+# ---------------------------------------------------------------------------------------
+# quantizers and adaLN
+# ---------------------------------------------------------------------------------------
+
+def quantize_int8_rowwise(x: torch.Tensor, stochastic_rounding: int | None = 0,
+                          input_act: str | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row INT8 quantization: ``(q int8 [..., K], scale fp32 [..., 1])``.
+
+    CK/__init__.py:702-709 / CK/backends/eager/quantization.py:857-875. Stochastic rounding
+    is not provided (the reference default, 0, is). ``input_act='gelu_tanh'`` applies the
+    activation to a bf16 input first (CK/backends/_activations.py:40-53).
+    """
+    if stochastic_rounding:
+        raise NotImplementedError("stochastic rounding is not provided by mx_qlinear")
+    dev = _require_gpu(x)
+    if x.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise ValueError(f"unsupported input dtype {x.dtype}")
+    k = x.shape[-1]
+    if k == 0:
+        raise ValueError("quantize_int8_rowwise needs a non-empty last dimension")
+    x2 = x.reshape(-1, k).contiguous()
+    m = x2.shape[0]
+    q = torch.empty((m, k), dtype=torch.int8, device=dev)
+    s = torch.empty((m, 1), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        call("mxq_quantize_int8_rowwise", _p(x2), _OUT_CODES[x.dtype], _p(q), _p(s), m, k,
+             _act_code(input_act), _stream(dev))
+    return q.reshape(x.shape), s.reshape(*x.shape[:-1], 1)
+
+
+def apply_input_act(x: torch.Tensor, input_act: str | None) -> torch.Tensor:
+    """The pre-quantization activation (CK/backends/_activations.py:40-53) for bf16 inputs.
+
+    ``gelu_tanh`` is bit-identical to torch's CPU ``gelu(approximate='tanh')`` on bfloat16.
+    """
+    code = _act_code(input_act)
+    if code == _lib.ACT_NONE:
+        return x
+    dev = _require_gpu(x)
+    if x.dtype != torch.bfloat16:
+        raise NotImplementedError("gelu_tanh is provided for bfloat16 tensors")
+    xc = x.contiguous()
+    y = torch.empty_like(xc)
+    with torch.cuda.device(dev):
+        call("mxq_gelu_tanh_bf16", _p(xc), _p(y), xc.numel(), _stream(dev))
+    return y
+
+
+def _modulation(t: torch.Tensor, rows: int, cols: int, dev, name: str):
+    t = t.to(device=dev, dtype=torch.bfloat16)
+    if t.shape[-1] != cols:
+        raise ValueError(f"{name} last dimension {t.shape[-1]} != {cols}")
+    t2 = t.reshape(-1, cols).contiguous()
+    g = t2.shape[0]
+    if g == 0 or rows % g != 0:
+        raise ValueError(f"{name} with {g} rows does not broadcast over {rows} rows")
+    return t2, rows // g
+
+
+def adaln(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """``layer_norm(x) * (1 + scale) + shift`` in bf16 (CK/__init__.py:110-127, eager adaln.py:11-14).
+
+    ``scale`` / ``shift`` are ``[D]`` or one row per consecutive group of x rows
+    (``[G, D]`` with G dividing the number of rows), as the reference's CUDA launcher's
+    scale_group / shift_group (CK/backends/cuda/ops/adaln.cu:256-313).
+    """
+    dev = _require_gpu(x)
+    if x.dtype != torch.bfloat16:
+        raise NotImplementedError("mx_qlinear.adaln supports bfloat16 inputs")
+    d = x.shape[-1]
+    x2 = x.reshape(-1, d).contiguous()
+    rows = x2.shape[0]
+    out = torch.empty_like(x2)
+    if rows == 0:
+        return out.reshape(x.shape)
+    sc, sg = _modulation(scale, rows, d, dev, "scale")
+    sh, hg = _modulation(shift, rows, d, dev, "shift")
+    with torch.cuda.device(dev):
+        call("mxq_adaln", _p(x2), _p(sc), _p(sh), _p(out), rows, d, sg, hg, float(eps), _stream(dev))
+    return out.reshape(x.shape)
+
+
+def adaln_quantize_int8(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
+                        eps: float = 1e-6, return_modulated: bool = False):
+    """``quantize_int8_rowwise(adaln(x, scale, shift, eps))`` in one pass over x.
+
+    Returns ``(q, x_scale)`` or ``(q, x_scale, modulated_bf16)`` when ``return_modulated``.
+    """
+    dev = _require_gpu(x)
+    if x.dtype != torch.bfloat16:
+        raise NotImplementedError("adaln_quantize_int8 supports bfloat16 inputs")
+    d = x.shape[-1]
+    x2 = x.reshape(-1, d).contiguous()
+    rows = x2.shape[0]
+    q = torch.empty((rows, d), dtype=torch.int8, device=dev)
+    s = torch.empty((rows, 1), dtype=torch.float32, device=dev)
+    y = torch.empty_like(x2) if return_modulated else None
+    if rows:
+        sc, sg = _modulation(scale, rows, d, dev, "scale")
+        sh, hg = _modulation(shift, rows, d, dev, "shift")
+        with torch.cuda.device(dev):
+            call("mxq_adaln_quantize_int8", _p(x2), _p(sc), _p(sh), sg, hg, float(eps), _p(q), _p(s),
+                 _p(y), rows, d, _stream(dev))
+    out = (q.reshape(x.shape), s.reshape(*x.shape[:-1], 1))
+    return out + (y.reshape(x.shape),) if return_modulated else out
+
+
+# ---------------------------------------------------------------------------------------
+# INT8 GEMMs
+# ---------------------------------------------------------------------------------------
+
+def _pad_k(q: torch.Tensor, w: torch.Tensor):
+    """Zero-pad K to a multiple of 16 (zero terms leave the int32 sums unchanged,
+    as the reference's own K padding, CK/backends/eager/quantization.py:770-775)."""
+    k = q.shape[1]
+    kp = (k + 15) // 16 * 16
+    if kp == k:
+        return q, w, k
+    qp = torch.zeros((q.shape[0], kp), dtype=torch.int8, device=q.device)
+    qp[:, :k] = q
+    wp = torch.zeros((w.shape[0], kp), dtype=torch.int8, device=w.device)
+    wp[:, :k] = w
+    return qp, wp, kp
+
+
+def mm_int8(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """``C[M, N] = A[M, K] @ B[K, N]`` in int32 (CK/__init__.py:717-719, eager quantization.py:785-800)."""
+    if a.dtype != torch.int8 or b.dtype != torch.int8 or a.dim() != 2 or b.dim() != 2:
+        raise ValueError("mm_int8 expects two 2-D int8 tensors")
+    if a.shape[1] != b.shape[0]:
+        raise ValueError(f"K mismatch: {a.shape[1]} vs {b.shape[0]}")
+    dev = _require_gpu(a, b)
+    m, n = a.shape[0], b.shape[1]
+    out = torch.empty((m, n), dtype=torch.int32, device=dev)
+    if m == 0 or n == 0:
+        return out
+    if a.shape[1] == 0:
+        return out.zero_()
+    a2, w2, k = _pad_k(a.contiguous(), b.t().contiguous())
+    with torch.cuda.device(dev):
+        call("mxq_int8_gemm_i32", _p(a2), _p(w2), _p(out), m, n, k, n, _stream(dev))
+    return out
+
+
+def _weight_scale(weight_scale: torch.Tensor, n: int, dev) -> torch.Tensor:
+    ws = torch.as_tensor(weight_scale).to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+    if ws.numel() not in (1, n):
+        raise ValueError(
+            f"INT8 weight scale must be scalar or per-output-channel, got {tuple(weight_scale.shape)} "
+            f"for {n} output channels"
+        )
+    return ws
+
+
+def _bias(bias: torch.Tensor | None, n: int, dtype: torch.dtype, dev):
+    if bias is None:
+        return None
+    b = bias.to(device=dev, dtype=dtype).reshape(-1).contiguous()
+    if b.numel() != n:
+        raise ValueError(f"bias has {b.numel()} entries, expected {n}")
+    return b
+
+
+def int8_linear_prequantized(x_qdata: torch.Tensor, x_scale: torch.Tensor, weight: torch.Tensor,
+                             weight_scale: torch.Tensor, bias: torch.Tensor | None = None,
+                             out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """INT8 GEMM + dequant epilogue from an already quantized 2-D activation.
+
+    CK/backends/cuda/__init__.py:1934-1957 (``int8_linear_prequantized``).
+    """
+    if x_qdata.dim() != 2 or x_qdata.dtype != torch.int8:
+        raise ValueError("x_qdata must be a 2-D int8 tensor")
+    if weight.dim() != 2 or weight.dtype != torch.int8:
+        raise ValueError("weight must be a 2-D int8 tensor")
+    if x_qdata.shape[1] != weight.shape[1]:
+        raise ValueError(
+            f"Input and weight inner dimensions must match, got {x_qdata.shape[1]} and {weight.shape[1]}"
+        )
+    dev = _require_gpu(x_qdata, weight)
+    m, n = x_qdata.shape[0], weight.shape[0]
+    code = _out_code(out_dtype)
+    ws = _weight_scale(weight_scale, n, dev)
+    b = _bias(bias, n, out_dtype, dev)
+    xs = x_scale.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+    if xs.numel() != m:
+        raise ValueError(f"x_scale has {xs.numel()} entries, expected {m}")
+    out = torch.empty((m, n), dtype=out_dtype, device=dev)
+    if m == 0 or n == 0:
+        return out
+    q2, w2, k = _pad_k(x_qdata.contiguous(), weight.contiguous())
+    with torch.cuda.device(dev):
+        call("mxq_int8_gemm_dequant", _p(q2), _p(w2), _p(xs), _p(ws), ws.numel(), _p(b), _p(out),
+             m, n, k, n, code, _stream(dev))
+    return out
+
+
+def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+                bias: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+                convrot: bool = False, convrot_groupsize: int = 256,
+                input_act: str | None = None) -> torch.Tensor:
+    """Dynamically quantized INT8 linear (CK/__init__.py:722-764, eager quantization.py:971-1056).
+
+    x [..., K] (bf16 / fp16 / fp32); weight int8 [N, K]; weight_scale scalar or [N] (any
+    shape with that many elements); bias [N] or None. Returns [..., N] of ``out_dtype``
+    (default bf16). ``input_act='gelu_tanh'`` is folded into the quantizer.
+    """
+    if out_dtype is None:
+        out_dtype = torch.bfloat16
+    act = _act_code(input_act)
+    if x.shape[-1] != weight.shape[-1]:
+        raise ValueError(
+            f"Input and weight inner dimensions must match, got {x.shape[-1]} and {weight.shape[-1]}"
+        )
+    if convrot:
+        raise NotImplementedError("ConvRot rotation is not provided by this build of mx_qlinear")
+    dev = _require_gpu(x, weight)
+    n = weight.shape[0]
+    _weight_scale(weight_scale, n, dev)  # validate before launching anything
+    if act and x.dtype != torch.bfloat16:
+        raise NotImplementedError("input_act='gelu_tanh' needs a bfloat16 input")
+    lead = x.shape[:-1]
+    if x.numel() == 0:
+        return torch.empty((*lead, n), dtype=out_dtype, device=dev)
+    q, s = quantize_int8_rowwise(x.reshape(-1, x.shape[-1]), input_act=input_act)
+    out = int8_linear_prequantized(q, s, weight, weight_scale, bias, out_dtype)
+    return out.reshape(*lead, n)
+
+
+# ---------------------------------------------------------------------------------------
+# The INT8 FFN chain: fc1 -> tanh-GELU -> per-token re-quant -> fc2
+# ---------------------------------------------------------------------------------------
+
+class FfnWorkspace:
+    """Reusable device buffers of :func:`int8_ffn_gelu` for a given (M, K, hidden) shape."""
+
+    def __init__(self, m: int, k: int, hidden: int, device):
+        self.shape = (m, k, hidden)
+        self.xq = torch.empty((m, k), dtype=torch.int8, device=device)
+        self.xs = torch.empty((m, 1), dtype=torch.float32, device=device)
+        self.h = torch.empty((m, hidden), dtype=torch.bfloat16, device=device)
+        self.hmax = torch.empty((m,), dtype=torch.float32, device=device)
+        self.hq = torch.empty((m, hidden), dtype=torch.int8, device=device)
+        self.hs = torch.empty((m, 1), dtype=torch.float32, device=device)
+
+
+def int8_ffn_gelu(x: torch.Tensor, fc1_weight: torch.Tensor, fc1_scale: torch.Tensor,
+                  fc1_bias: torch.Tensor | None, fc2_weight: torch.Tensor, fc2_scale: torch.Tensor,
+                  fc2_bias: torch.Tensor | None, workspace: FfnWorkspace | None = None,
+                  return_hidden: bool = False):
+    """``int8_linear(int8_linear(x, fc1), fc2, input_act='gelu_tanh')`` in four launches.
+
+    The reference composes two ``int8_linear`` calls with the activation applied before the
+    second quantizer (CK/backends/eager/quantization.py:971-1056,
+    CK/backends/_activations.py:40-53). Here fc1's epilogue applies GELU and accumulates each
+    row's absmax, so the intermediate is read once by a single-pass quantizer. Results are
+    identical to the two-call composition. bf16 in and out.
+    """
+    if x.dtype != torch.bfloat16:
+        raise NotImplementedError("int8_ffn_gelu takes a bfloat16 input")
+    dev = _require_gpu(x, fc1_weight, fc2_weight)
+    k = x.shape[-1]
+    hidden, n = fc1_weight.shape[0], fc2_weight.shape[0]
+    if fc1_weight.shape[1] != k or fc2_weight.shape[1] != hidden:
+        raise ValueError("FFN weight shapes do not chain")
+    if k % 16 or hidden % 16:
+        raise NotImplementedError("int8_ffn_gelu needs K and the hidden width to be multiples of 16")
+    x2 = x.reshape(-1, k).contiguous()
+    m = x2.shape[0]
+    s1 = _weight_scale(fc1_scale, hidden, dev)
+    s2 = _weight_scale(fc2_scale, n, dev)
+    b1 = _bias(fc1_bias, hidden, torch.bfloat16, dev)
+    b2 = _bias(fc2_bias, n, torch.bfloat16, dev)
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    if m == 0:
+        return out.reshape(*x.shape[:-1], n)
+    ws = workspace if workspace is not None and workspace.shape == (m, k, hidden) else FfnWorkspace(m, k, hidden, dev)
+    w1 = fc1_weight.contiguous()
+    w2 = fc2_weight.contiguous()
+    st = _stream(dev)
+    with torch.cuda.device(dev):
+        call("mxq_quantize_int8_rowwise", _p(x2), _lib.DTYPE_BF16, _p(ws.xq), _p(ws.xs), m, k,
+             _lib.ACT_NONE, st)
+        call("mxq_fill_f32", _p(ws.hmax), 0.0, m, st)
+        call("mxq_int8_gemm_dequant_gelu_absmax", _p(ws.xq), _p(w1), _p(ws.xs), _p(s1), s1.numel(),
+             _p(b1), _p(ws.h), _p(ws.hmax), m, hidden, k, hidden, st)
+        call("mxq_quantize_int8_rowwise_absmax", _p(ws.h), _p(ws.hmax), _p(ws.hq), _p(ws.hs), m,
+             hidden, st)
+        call("mxq_int8_gemm_dequant", _p(ws.hq), _p(w2), _p(ws.hs), _p(s2), s2.numel(), _p(b2),
+             _p(out), m, n, hidden, n, _lib.DTYPE_BF16, st)
+    out = out.reshape(*x.shape[:-1], n)
+    return (out, ws.h.reshape(*x.shape[:-1], hidden)) if return_hidden else out
+
+
+# ---------------------------------------------------------------------------------------
+# W4A8
+# ---------------------------------------------------------------------------------------
+
+def _srel_code(s_rel: torch.Tensor) -> tuple[torch.Tensor, int]:
+    if s_rel.dtype == torch.float8_e4m3fn:
+        return s_rel.contiguous().view(torch.uint8), _lib.DTYPE_E4M3
+    return s_rel.to(torch.float32).contiguous(), _lib.DTYPE_F32
+
+
+def dequantize_int4_grouped_to_int8(qdata: torch.Tensor, s_rel: torch.Tensor,
+                                    codebook: torch.Tensor | None, group_size: int) -> torch.Tensor:
+    """Decode packed int4 to the int8 grid (CK/backends/eager/w4a8_int8.py:344-363)."""
+    if qdata.dim() != 2 or qdata.dtype != torch.int8:
+        raise ValueError("packed weight must be a 2D int8 tensor")
+    dev = _require_gpu(qdata)
+    n, kh = qdata.shape
+    k = kh * 2
+    if group_size <= 0 or k % group_size:
+        raise ValueError(f"K={k} must be divisible by group_size={group_size}")
+    if tuple(s_rel.shape) != (n, k // group_size):
+        raise ValueError(f"s_rel must have shape {(n, k // group_size)}, got {tuple(s_rel.shape)}")
+    sr, code = _srel_code(s_rel.to(dev))
+    cb = None if codebook is None else codebook.to(device=dev, dtype=torch.float32).contiguous()
+    out = torch.empty((n, k), dtype=torch.int8, device=dev)
+    with torch.cuda.device(dev):
+        call("mxq_dequant_int4_grouped_to_int8", _p(qdata.contiguous()), _p(sr), code, _p(cb), _p(out),
+             n, k, group_size, _stream(dev))
+    return out
+
+
+def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, s_channel: torch.Tensor,
+                     codebook: torch.Tensor | None = None, correction: torch.Tensor | None = None,
+                     bias: torch.Tensor | None = None, group_size: int = 16,
+                     convrot_groupsize: int = 256, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """Reference-format W4A8 linear (CK/tensor/w4a8_int8.py:89-115, eager w4a8_int8.py:457-508).
+
+    The reference always rotates activations with ConvRot before quantizing; that rotation is
+    not part of this build, so only ``convrot_groupsize=0`` (no rotation) is accepted.
+    """
+    if convrot_groupsize:
+        raise NotImplementedError("ConvRot rotation is not provided by this build of mx_qlinear; "
+                                  "pass convrot_groupsize=0 for unrotated weights")
+    if correction is not None:
+        raise NotImplementedError("the W4A8 correction term is not provided by this build")
+    if qdata.dim() != 2 or qdata.dtype != torch.int8:
+        raise ValueError("packed weight must be a 2D int8 tensor")
+    n, kh = qdata.shape
+    k = kh * 2
+    if x.shape[-1] != k:
+        raise ValueError(f"Input K={x.shape[-1]} does not match qdata K={k}")
+    if (group_size < 4 or k % 16 != 0 or k % group_size != 0
+            or (16 % group_size != 0 and group_size % 16 != 0)):
+        raise ValueError(
+            f"K={k} must be divisible by 16, group_size={group_size}; group_size must be >=4 "
+            "and divide 16 or be a multiple of 16"
+        )
+    if tuple(s_rel.shape) != (n, k // group_size):
+        raise ValueError(f"s_rel must have shape {(n, k // group_size)}, got {tuple(s_rel.shape)}")
+    if tuple(s_channel.shape) != (n,):
+        raise ValueError(f"s_channel must have shape {(n,)}, got {tuple(s_channel.shape)}")
+    if codebook is not None and tuple(codebook.shape) != (16,):
+        raise ValueError(f"codebook must have shape (16,), got {tuple(codebook.shape)}")
+    dev = _require_gpu(x, qdata)
+    code = _out_code(out_dtype)
+    lead = x.shape[:-1]
+    xq, xs = quantize_int8_rowwise(x.reshape(-1, k))
+    m = xq.shape[0]
+    out = torch.empty((m, n), dtype=out_dtype, device=dev)
+    if m == 0:
+        return out.reshape(*lead, n)
+    sr, scode = _srel_code(s_rel.to(dev))
+    cb = None if codebook is None else codebook.to(device=dev, dtype=torch.float32).contiguous()
+    sch = s_channel.to(device=dev, dtype=torch.float32).contiguous()
+    b = _bias(bias, n, out_dtype, dev)
+    chunk = min(n, 4096)
+    work = torch.empty((chunk, k), dtype=torch.int8, device=dev)
+    with torch.cuda.device(dev):
+        call("mxq_w4a8_codebook_gemm", _p(xq), _p(qdata.contiguous()), _p(sr), scode, _p(cb), _p(sch),
+             _p(xs), _p(b), _p(work), _p(out), m, n, k, group_size, chunk, code, _stream(dev))
+    return out.reshape(*lead, n)
+
+
+def w4a8_grouped_linear(x: torch.Tensor, qdata: torch.Tensor, group_scale: torch.Tensor,
+                        group_size: int = 128, bias: torch.Tensor | None = None,
+                        out_dtype: torch.dtype = torch.bfloat16,
+                        x_scale: torch.Tensor | None = None) -> torch.Tensor:
+    """Group-scaled int4 weights x per-token int8 activations.
+
+    ``x`` is bf16/fp16/fp32 ``[..., K]`` (quantized per token here) or int8 ``[M, K]`` with its
+    ``x_scale``; ``qdata`` int8 ``[N, K/2]`` packs offset-8 codes two per byte, even k in the
+    low nibble (CK/backends/eager/w4a8_int8.py:200-202); ``group_scale`` fp16 ``[K/G, N]``.
+    y = out(xs[m] * sum_g fp32(scale[g, n]) * P_g[m, n]), P_g the exact int32 partial of group g.
+    """
+    if qdata.dim() != 2 or qdata.dtype != torch.int8:
+        raise ValueError("packed weight must be a 2D int8 tensor")
+    n, kh = qdata.shape
+    k = kh * 2
+    if x.shape[-1] != k:
+        raise ValueError(f"Input K={x.shape[-1]} does not match qdata K={k}")
+    if group_size <= 0 or k % group_size:
+        raise ValueError(f"K={k} must be divisible by group_size={group_size}")
+    if tuple(group_scale.shape) != (k // group_size, n):
+        raise ValueError(f"group_scale must have shape {(k // group_size, n)}, got {tuple(group_scale.shape)}")
+    dev = _require_gpu(x, qdata, group_scale)
+    code = _out_code(out_dtype)
+    if x.dtype == torch.int8:
+        if x_scale is None:
+            raise ValueError("an int8 input needs x_scale")
+        xq = x.reshape(-1, k).contiguous()
+        xs = x_scale.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+    else:
+        xq, xs = quantize_int8_rowwise(x.reshape(-1, k))
+    lead = x.shape[:-1]
+    m = xq.shape[0]
+    out = torch.empty((m, n), dtype=out_dtype, device=dev)
+    if m == 0:
+        return out.reshape(*lead, n)
+    gs = group_scale.to(device=dev, dtype=torch.float16).contiguous()
+    b = _bias(bias, n, out_dtype, dev)
+    with torch.cuda.device(dev):
+        call("mxq_w4a8_gemm_grouped", _p(xq), _p(xs), _p(qdata.contiguous()), _p(gs), _p(b), _p(out),
+             m, n, k, group_size, n, code, _stream(dev))
+    return out.reshape(*lead, n)
