@@ -1,0 +1,396 @@
+"""Benchmark of the quantized DiT linear path on one MI355X.
+
+Default workload (the headline "DiT FFN tokens/s at 720p"): the full INT8 FFN chain at
+720p x 5 s, M = 75600 tokens (21 latent frames x 45 x 80 patches), d_model 5120, d_ff 20480:
+per-token int8 quant -> fc1 int8 GEMM + bias + tanh-GELU (+ row absmax) -> per-token re-quant
+-> fc2 int8 GEMM + bias -> bf16. One step = one pass over the 75600 tokens with all inputs
+resident in HBM. Synthetic data: X ~ N(0, 1) with 0.5% outlier channels x20, weights
+N(0, 0.02) row-quantized to int8 with fp32 per-channel scales, biases N(0, 0.01), seeded.
+
+Prints one JSON line. `roofline` is for the dominant kernel (the int8 GEMM: fc1 and fc2 are
+launches of the same kernel), timed live with HIP events on the stream it runs on;
+`cpu_baseline` is the reference's eager PyTorch CPU composition (the oracle's torch
+restatement) timed on this host on a bounded row sample.
+
+Other workloads (--workload): qkv_adaln (fused adaLN + quant + QKV GEMM, M=75600, N=15360),
+w4a8_gemm (8192 x 5120 x 5120, group 128), w4a8_skinny (512 x 10240 x 5120), linear_c1
+(1024 x 3072 x 3072).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "x-minimaxh3_amd"))
+
+import mx_qlinear  # noqa: E402
+from mx_qlinear import _lib  # noqa: E402
+from mx_qlinear.ops import _p, _stream  # noqa: E402
+
+INT8_PEAK_TOPS = 5000.0   # MI355X dense INT8 MFMA
+HBM_PEAK_GBS = 8000.0     # MI355X HBM3E
+SEED = 20261201
+
+
+def _gen(dev, i):
+    return torch.Generator(device=dev).manual_seed(SEED + i)
+
+
+def make_activations(m, k, dev, i):
+    g = _gen(dev, i)
+    x = torch.randn(m, k, generator=g, device=dev, dtype=torch.float32)
+    n_out = -(-k * 5 // 1000)
+    idx = torch.randperm(k, generator=g, device=dev)[:n_out]
+    x[:, idx] *= 20.0
+    return x.to(torch.bfloat16)
+
+
+def make_int8_weight(n, k, dev, i):
+    wf = (torch.randn(n, k, generator=_gen(dev, i), device=dev) * 0.02).to(torch.bfloat16)
+    q, s = mx_qlinear.quantize_int8_rowwise(wf)
+    return q, s.reshape(-1)
+
+
+def make_bias(n, dev, i):
+    return (torch.randn(n, generator=_gen(dev, i), device=dev) * 0.01).to(torch.bfloat16)
+
+
+class Timer:
+    """HIP events around selected launches, on the current stream."""
+
+    def __init__(self):
+        self.spans = {}
+
+    def span(self, name):
+        timer = self
+
+        class _S:
+            def __enter__(self):
+                self.a = torch.cuda.Event(enable_timing=True)
+                self.b = torch.cuda.Event(enable_timing=True)
+                self.a.record()
+
+            def __exit__(self, *exc):
+                self.b.record()
+                timer.spans.setdefault(name, []).append((self.a, self.b))
+
+        return _S()
+
+    def mean_ms(self, name):
+        ev = self.spans.get(name, [])
+        return sum(a.elapsed_time(b) for a, b in ev) / max(len(ev), 1)
+
+
+# ----------------------------------------------------------------------------------------
+# workloads
+# ----------------------------------------------------------------------------------------
+
+class FfnWorkload:
+    name = "int8_ffn_gelu_720p"
+
+    def __init__(self, dev, m=75600, k=5120, hidden=20480):
+        self.m, self.k, self.hidden = m, k, hidden
+        self.x = make_activations(m, k, dev, 0)
+        self.w1, self.s1 = make_int8_weight(hidden, k, dev, 1)
+        self.w2, self.s2 = make_int8_weight(k, hidden, dev, 2)
+        self.b1, self.b2 = make_bias(hidden, dev, 3), make_bias(k, dev, 4)
+        self.ws = mx_qlinear.FfnWorkspace(m, k, hidden, dev)
+        self.out = torch.empty(m, k, dtype=torch.bfloat16, device=dev)
+        self.dev = dev
+
+    def step(self, timer=None):
+        ws, m, k, h = self.ws, self.m, self.k, self.hidden
+        st = _stream(self.dev)
+        t = timer.span if timer else (lambda name: _Null())
+        with t("quant_x"):
+            _lib.call("mxq_quantize_int8_rowwise", _p(self.x), _lib.DTYPE_BF16, _p(ws.xq), _p(ws.xs), m, k,
+                      _lib.ACT_NONE, st)
+        _lib.call("mxq_fill_f32", _p(ws.hmax), 0.0, m, st)
+        with t("fc1_gemm"):
+            _lib.call("mxq_int8_gemm_dequant_gelu_absmax", _p(ws.xq), _p(self.w1), _p(ws.xs), _p(self.s1),
+                      h, _p(self.b1), _p(ws.h), _p(ws.hmax), m, h, k, h, st)
+        with t("requant"):
+            _lib.call("mxq_quantize_int8_rowwise_absmax", _p(ws.h), _p(ws.hmax), _p(ws.hq), _p(ws.hs), m, h, st)
+        with t("fc2_gemm"):
+            _lib.call("mxq_int8_gemm_dequant", _p(ws.hq), _p(self.w2), _p(ws.hs), _p(self.s2), k, _p(self.b2),
+                      _p(self.out), m, k, h, k, _lib.DTYPE_BF16, st)
+
+    def ops_per_step(self):
+        return 2 * 2 * self.m * self.k * self.hidden
+
+    def units_per_step(self):
+        return self.m
+
+    def dominant(self, timer):
+        """(kernel label, ops per launch, mean launch ms) of the slower GEMM launch."""
+        cands = [("fc1_gemm", timer.mean_ms("fc1_gemm")), ("fc2_gemm", timer.mean_ms("fc2_gemm"))]
+        name, ms = max(cands, key=lambda c: c[1])
+        return ("gemm_i8_kernel (" + name + ")", 2 * self.m * self.k * self.hidden, ms)
+
+    def config(self):
+        return {"workload": self.name, "tokens": self.m, "d_model": self.k, "d_ff": self.hidden,
+                "act": "gelu_tanh", "weights": "int8 per-channel", "activations": "int8 per-token"}
+
+    def cpu_baseline(self, budget_s):
+        from oracle import eager_torch
+
+        w1, s1, b1 = self.w1.cpu(), self.s1.cpu(), self.b1.cpu()
+        w2, s2, b2 = self.w2.cpu(), self.s2.cpu(), self.b2.cpu()
+
+        def run(rows):
+            x = self.x[:rows].cpu()
+            t0 = time.perf_counter()
+            eager_torch.ffn_gelu_int8(x, w1, s1, b1, w2, s2, b2)
+            return time.perf_counter() - t0
+
+        return _cpu_sample(run, budget_s, self.m, "tokens/s", "first {rows} of the 75600 tokens through "
+                           "the eager fc1 -> gelu_tanh -> fc2 int8_linear composition")
+
+
+class _Null:
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *e):
+        return False
+
+
+class QkvWorkload:
+    name = "qkv_adaln_720p"
+
+    def __init__(self, dev, m=75600, k=5120, n=15360):
+        self.m, self.k, self.n = m, k, n
+        self.x = make_activations(m, k, dev, 10)
+        self.sc = (torch.randn(k, generator=_gen(dev, 11), device=dev) * 0.1).to(torch.bfloat16)
+        self.sh = (torch.randn(k, generator=_gen(dev, 12), device=dev) * 0.1).to(torch.bfloat16)
+        self.w, self.s = make_int8_weight(n, k, dev, 13)
+        self.b = make_bias(n, dev, 14)
+        self.xq = torch.empty(m, k, dtype=torch.int8, device=dev)
+        self.xs = torch.empty(m, dtype=torch.float32, device=dev)
+        self.out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        self.dev = dev
+
+    def step(self, timer=None):
+        st = _stream(self.dev)
+        t = timer.span if timer else (lambda name: _Null())
+        with t("adaln_quant"):
+            _lib.call("mxq_adaln_quantize_int8", _p(self.x), _p(self.sc), _p(self.sh), self.m, self.m, 1e-6,
+                      _p(self.xq), _p(self.xs), None, self.m, self.k, st)
+        with t("qkv_gemm"):
+            _lib.call("mxq_int8_gemm_dequant", _p(self.xq), _p(self.w), _p(self.xs), _p(self.s), self.n,
+                      _p(self.b), _p(self.out), self.m, self.n, self.k, self.n, _lib.DTYPE_BF16, st)
+
+    def ops_per_step(self):
+        return 2 * self.m * self.n * self.k
+
+    def units_per_step(self):
+        return self.m
+
+    def dominant(self, timer):
+        return ("gemm_i8_kernel (qkv)", self.ops_per_step(), timer.mean_ms("qkv_gemm"))
+
+    def config(self):
+        return {"workload": self.name, "tokens": self.m, "d_model": self.k, "qkv_out": self.n,
+                "norm": "layernorm eps 1e-6 + (1+scale)*x+shift"}
+
+    def cpu_baseline(self, budget_s):
+        from oracle import eager_torch
+
+        sc, sh, w, s, b = self.sc.cpu(), self.sh.cpu(), self.w.cpu(), self.s.cpu(), self.b.cpu()
+
+        def run(rows):
+            x = self.x[:rows].cpu()
+            t0 = time.perf_counter()
+            eager_torch.int8_linear(eager_torch.adaln(x, sc, sh), w, s, b)
+            return time.perf_counter() - t0
+
+        return _cpu_sample(run, budget_s, self.m, "tokens/s", "first {rows} tokens through eager adaln -> int8_linear")
+
+
+class W4A8Workload:
+    def __init__(self, dev, m, n, k, g=128, name="w4a8_gemm"):
+        self.name = name
+        self.m, self.n, self.k, self.g = m, n, k, g
+        x = make_activations(m, k, dev, 20)
+        self.xq, xs = mx_qlinear.quantize_int8_rowwise(x)
+        self.xs = xs.reshape(-1)
+        self.x = x
+        self.w = torch.randint(-128, 128, (n, k // 2), generator=_gen(dev, 21), device=dev, dtype=torch.int8)
+        self.gs = (torch.randn(k // g, n, generator=_gen(dev, 22), device=dev).abs() * 0.01).to(torch.float16)
+        self.out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        self.dev = dev
+
+    def step(self, timer=None):
+        st = _stream(self.dev)
+        t = timer.span if timer else (lambda name: _Null())
+        with t("w4a8_gemm"):
+            _lib.call("mxq_w4a8_gemm_grouped", _p(self.xq), _p(self.xs), _p(self.w), _p(self.gs), None,
+                      _p(self.out), self.m, self.n, self.k, self.g, self.n, _lib.DTYPE_BF16, st)
+
+    def ops_per_step(self):
+        return 2 * self.m * self.n * self.k
+
+    def units_per_step(self):
+        return self.m
+
+    def alg_bytes(self):
+        return self.m * self.k + self.n * self.k // 2 + (self.k // self.g) * self.n * 2 + self.m * 4 + self.m * self.n * 2
+
+    def dominant(self, timer):
+        return ("w4a8_grouped_kernel", self.ops_per_step(), timer.mean_ms("w4a8_gemm"))
+
+    def config(self):
+        return {"workload": self.name, "m": self.m, "n": self.n, "k": self.k, "group": self.g,
+                "weights": "int4 offset-8 packed, fp16 group scales"}
+
+    def cpu_baseline(self, budget_s):
+        from oracle import eager_torch
+
+        w, gs = self.w.cpu(), self.gs.cpu()
+
+        def run(rows):
+            a, xs = self.xq[:rows].cpu(), self.xs[:rows].cpu()
+            t0 = time.perf_counter()
+            eager_torch.w4a8_grouped_linear(a, xs, w, gs, self.g)
+            return time.perf_counter() - t0
+
+        return _cpu_sample(run, budget_s, self.m, "tokens/s", "first {rows} rows through eager per-group _int_mm")
+
+
+class LinearC1Workload:
+    name = "int8_linear_1024x3072x3072"
+
+    def __init__(self, dev):
+        self.m = self.k = 3072
+        self.m = 1024
+        self.n = 3072
+        self.x = make_activations(self.m, self.k, dev, 30)
+        self.w, self.s = make_int8_weight(self.n, self.k, dev, 31)
+        self.b = make_bias(self.n, dev, 32)
+        self.dev = dev
+
+    def step(self, timer=None):
+        t = timer.span if timer else (lambda name: _Null())
+        with t("linear"):
+            mx_qlinear.int8_linear(self.x, self.w, self.s, self.b)
+
+    def ops_per_step(self):
+        return 2 * self.m * self.n * self.k
+
+    def units_per_step(self):
+        return self.m
+
+    def dominant(self, timer):
+        return ("int8_linear (quant + gemm)", self.ops_per_step(), timer.mean_ms("linear"))
+
+    def config(self):
+        return {"workload": self.name, "m": self.m, "n": self.n, "k": self.k}
+
+    def cpu_baseline(self, budget_s):
+        from oracle import eager_torch
+
+        w, s, b = self.w.cpu(), self.s.cpu(), self.b.cpu()
+
+        def run(rows):
+            x = self.x[:rows].cpu()
+            t0 = time.perf_counter()
+            eager_torch.int8_linear(x, w, s, b)
+            return time.perf_counter() - t0
+
+        return _cpu_sample(run, budget_s, self.m, "tokens/s", "first {rows} of 1024 rows through eager int8_linear")
+
+
+def _cpu_sample(run, budget_s, max_rows, unit, what):
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    rows = 16
+    elapsed = run(rows)
+    while elapsed < budget_s / 4 and rows < max_rows:
+        rows = min(max_rows, rows * 4)
+        elapsed = run(rows)
+    if elapsed < budget_s / 2 and rows < max_rows:
+        rows = min(max_rows, int(rows * budget_s / 2 / max(elapsed, 1e-3)))
+        elapsed = run(rows)
+    return {"value": rows / elapsed, "unit": unit, "cores": threads, "kind": "port",
+            "sample": what.format(rows=rows) + f" ({elapsed:.1f} s, torch {torch.__version__} CPU)"}
+
+
+WORKLOADS = {
+    "ffn": lambda dev: FfnWorkload(dev),
+    "qkv_adaln": lambda dev: QkvWorkload(dev),
+    "w4a8_gemm": lambda dev: W4A8Workload(dev, 8192, 5120, 5120, name="w4a8_gemm_8192x5120x5120"),
+    "w4a8_skinny": lambda dev: W4A8Workload(dev, 512, 10240, 5120, name="w4a8_skinny_512x10240x5120"),
+    "linear_c1": lambda dev: LinearC1Workload(dev),
+}
+
+METRICS = {
+    "ffn": ("DiT FFN tokens/s at 720p (INT8 fc1 -> GELU -> re-quant -> fc2)", "tokens/s"),
+    "qkv_adaln": ("QKV projection with fused adaLN, tokens/s at 720p", "tokens/s"),
+    "w4a8_gemm": ("W4A8 GEMM TOPS", "TOPS"),
+    "w4a8_skinny": ("W4A8 skinny projection HBM GB/s", "GB/s"),
+    "linear_c1": ("W8A8 linear TOPS", "TOPS"),
+}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="ffn", choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work (0: skip)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (the path shards over "
+              "tokens with no communication; see the design notes)", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = WORKLOADS[args.workload](dev)
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        wl.step()
+    torch.cuda.synchronize()
+    timer = Timer()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        wl.step(timer)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = wall * 1e3 / args.steps
+    units = wl.units_per_step() * args.steps / wall
+    metric, unit = METRICS[args.workload]
+    if unit == "TOPS":
+        value = wl.ops_per_step() * args.steps / wall / 1e12
+    elif unit == "GB/s":
+        value = wl.alg_bytes() * args.steps / wall / 1e9
+    else:
+        value = units
+    kname, kops, kms = wl.dominant(timer)
+    achieved = kops / (kms * 1e-3) / 1e12
+    line = {
+        "metric": metric, "value": round(value, 3), "unit": unit, "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic (seeded N(0,1) activations with 0.5% x20 "
+        "outlier channels; N(0,0.02) weights row-quantized)",
+        "config": wl.config(),
+        "tops_per_step": round(wl.ops_per_step() / (ms * 1e-3) / 1e12, 2),
+        "int8_peak_frac_per_step": round(wl.ops_per_step() / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+        "kernel_ms": {k: round(timer.mean_ms(k), 4) for k in timer.spans},
+        "roofline": {"bound": "mfma", "kernel": kname, "achieved": round(achieved, 2), "peak": INT8_PEAK_TOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": None},
+    }
+    if args.cpu_budget > 0:
+        line["cpu_baseline"] = wl.cpu_baseline(args.cpu_budget)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -6,22 +6,20 @@
 //
 // Main loop: a 256-thread workgroup (4 wave64s, 2 x 2) owns a 256 x 256 output tile; each wave
 // owns 128 x 128 as a 4 x 4 grid of v_mfma_i32_32x32x32_i8 blocks (256 int32 accumulators per
-// lane, held in AGPRs). K advances 128 bytes per stage; A and B stages (32 KB each) are
-// double-buffered in LDS. Global loads for stage k+1 are issued before the MFMAs of stage k and
-// written to LDS after them, so one barrier per stage suffices.
+// lane, held in AGPRs). K advances 64 bytes per stage; a stage (A 16 KB + B 16 KB) is fetched
+// with gfx950's direct-to-LDS 16-byte loads into one of four LDS buffers, three stages ahead of
+// the MFMAs, so global latency hides behind two stages of matrix work and no VGPRs stage data.
+// Waits and barriers are issued by hand (s_waitcnt vmcnt + s_barrier) so that the prefetches
+// stay in flight across the barrier that publishes the next stage.
 //
-// LDS operand layout: a tile row is 128 bytes = eight 16-byte chunks; chunk c of row r sits at
-// slot c ^ (r & 7) ^ ((r >> 3) & 1). Eight consecutive rows then hit eight distinct 16-byte slots
-// of a 128-byte bank sweep and sixteen consecutive rows distinct slots of a 256-byte sweep, so
-// the MFMA operand reads (ds_read_b128, one row per lane) and the stage writes are conflict-free.
-//
-// Epilogue: each wave converts its accumulators in place (MFMA layout) and writes them to an
-// LDS copy of the output tile; the workgroup then streams that tile to HBM row by row with
-// 16-byte stores (2-byte outputs: the whole tile at once; 4-byte outputs: two halves).
+// Epilogue: the MFMAs run with the weights as first operand, so each lane's accumulators are
+// one output row in four runs of four consecutive columns. Every output type is converted in
+// registers and stored as 8- or 16-byte runs (lanes l and l + 32 cover adjacent runs); the
+// per-row scale is one register per 32-row block and row reductions stay inside lane pairs.
 //   kEpiI32     raw int32 accumulators.
 //   kEpiDequant y = out(fp32(acc) * (xs[m] * ws[n])); y = out(y + bias[n])
 //               (backends/eager/quantization.py:1031-1054; single IEEE ops, -ffp-contract=off).
-//   kEpiGelu    bf16 dequant as above, then h = gelu_tanh(y) in bf16 while streaming out, and the
+//   kEpiGelu    bf16 dequant as above, then h = gelu_tanh(y) in bf16 (table in LDS), and the
 //               per-row absmax of h folded into row_absmax[m] with atomics (it feeds the next
 //               layer's quantizer, backends/_activations.py:40-53 + quantization.py:857-875).
 
@@ -29,25 +27,14 @@
 
 namespace mxq {
 
-constexpr int kBM = 256, kBN = 256, kBK = 128;
+constexpr int kBM = 256, kBN = 256, kBK = 64;
 constexpr int kGemmThreads = 256;
 constexpr int kWaveM = 128, kWaveN = 128;
-constexpr int kStageA = kBM * kBK, kStageB = kBN * kBK;
+constexpr int kNS = 4;                                  // LDS pipeline stages
+constexpr int kStageA = kBM * kBK, kStageB = kBN * kBK; // 16 KB each
 constexpr int kStageBytes = kStageA + kStageB;
+constexpr int kLoadsPerStage = 8;                       // direct-to-LDS loads per wave per stage
 constexpr int kGroupM = 8;
-
-// Epilogue LDS map: output tile rows padded by 16 bytes (rows r and r+4, written by the two
-// half-waves of one store, then land in different banks).
-template <int kElem> struct EpiLayout {
-  static constexpr int kRows = kElem == 2 ? kBM : kBM / 2;   // rows per pass
-  static constexpr int kPitch = kBN * kElem + 16;
-  static constexpr int kTile = kRows * kPitch;
-  static constexpr int kFactors = kTile;                     // xs[256], ws[256], bias[256] floats
-  static constexpr int kBytes = kTile + 3 * 256 * 4;
-};
-constexpr int kLdsBytes = EpiLayout<4>::kBytes > 2 * kStageBytes
-                              ? (EpiLayout<4>::kBytes > EpiLayout<2>::kBytes ? EpiLayout<4>::kBytes : EpiLayout<2>::kBytes)
-                              : 2 * kStageBytes;
 
 enum { kEpiI32 = 0, kEpiDequant = 1, kEpiGelu = 2 };
 
@@ -61,11 +48,20 @@ struct GemmArgs {
   float* row_absmax;
   int64_t M, N, K, ldd;
   int ws_per_channel;
-  int vec_store;  // 16-byte row stores allowed (d and ldd 16-byte aligned)
+  int vec_store;  // run stores allowed (d aligned to 4 elements and ldd % 4 == 0)
   int tiles_m, tiles_n;
 };
 
-MXQ_DEVICE int swz(int r, int c) { return r * kBK + ((c ^ (r & 7) ^ ((r >> 3) & 1)) << 4); }
+// LDS operand layout: a tile row is 64 bytes = four 16-byte chunks; chunk c of row r sits at
+// slot c ^ f(r), f(r) = (r >> 2) & 3. gfx950 serves a ds_read_b128 sixteen lanes per clock;
+// with this map the sixteen rows one MFMA operand read touches per clock fall in distinct
+// banks (measured: 4 LDS cycles per ds_read_b128, no SQ_LDS_BANK_CONFLICT cycles, whereas
+// f(r) = ((r >> 1) ^ (r >> 3)) & 3 costs 8).
+MXQ_DEVICE int swz_f(int r) { return (r >> 2) & 3; }
+MXQ_DEVICE int swz(int r, int c) { return r * kBK + ((c ^ swz_f(r)) << 4); }
+
+// Zero source for the K tail of A (B's tail may hold anything: it meets zeros).
+static __device__ __attribute__((aligned(16))) uint8_t kZeroChunk[16];
 
 // Tile order: first spread contiguous tile ranges over the 8 XCDs (workgroup ids are dealt to
 // XCDs round-robin), then walk each range in groups of kGroupM tile-rows so that the ~32 tiles
@@ -84,88 +80,161 @@ MXQ_DEVICE void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn)
   tn = in / gm;
 }
 
-// Global -> register staging: thread t moves chunk (t % 8) of rows t / 8 + 32 i, i = 0..7.
-struct Stage {
-  v4u a[8];
-  v4u b[8];
+// Direct-to-LDS stage loads (global_load_lds_dwordx4). One instruction fills 1 KB of LDS:
+// lane i writes slot i % 4 of tile row 16 b + i / 4, so the lane fetches logical chunk
+// (i % 4) ^ f(row) of that row. Wave w loads A and B blocks b = 4 w .. 4 w + 3 of each stage.
+struct Loader {
+  const int8_t* a[4];
+  const int8_t* b[4];
+  int64_t koff[4];   // logical chunk offset (bytes) of this lane's 16-byte piece
+  int blk[4];
 };
 
-MXQ_DEVICE void load_stage(Stage& s, const int8_t* __restrict__ A, const int8_t* __restrict__ B,
-                           int64_t M, int64_t N, int64_t K, int64_t m0, int64_t n0, int64_t k0) {
-  const int t = threadIdx.x;
-  const int c = t & 7;
-  const int64_t kk = k0 + c * 16;
-  const bool kin = kk < K;
+MXQ_DEVICE void make_loader(Loader& L, const GemmArgs& p, int64_t m0, int64_t n0) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = (t >> 3) + 32 * i;
-    const int64_t am = min(m0 + r, M - 1);
-    const int64_t bn = min(n0 + r, N - 1);
-    if (kin) {
-      s.a[i] = *reinterpret_cast<const v4u*>(A + am * K + kk);
-      s.b[i] = *reinterpret_cast<const v4u*>(B + bn * K + kk);
-    } else {
-      s.a[i] = v4u{0, 0, 0, 0};
-      s.b[i] = v4u{0, 0, 0, 0};
-    }
+  for (int t = 0; t < 4; ++t) {
+    const int b = w * 4 + t;
+    const int r = b * 16 + (lane >> 2);
+    const int c = (lane & 3) ^ swz_f(r);
+    L.blk[t] = b;
+    L.koff[t] = c * 16;
+    L.a[t] = p.a + min(m0 + r, p.M - 1) * p.K + c * 16;
+    L.b[t] = p.b + min(n0 + r, p.N - 1) * p.K;
   }
 }
 
-MXQ_DEVICE void store_stage(const Stage& s, char* lds) {
-  const int t = threadIdx.x;
-  const int c = t & 7;
+typedef const void __attribute__((address_space(1)))* gptr_t;
+typedef void __attribute__((address_space(3)))* lptr_t;
+
+MXQ_DEVICE void issue_stage(const Loader& L, char* stage, int64_t k0, int64_t K) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = (t >> 3) + 32 * i;
-    *reinterpret_cast<v4u*>(lds + swz(r, c)) = s.a[i];
-    *reinterpret_cast<v4u*>(lds + kStageA + swz(r, c)) = s.b[i];
+  for (int t = 0; t < 4; ++t) {
+    const bool kin = k0 + L.koff[t] < K;
+    const void* sa = kin ? (const void*)(L.a[t] + k0) : (const void*)kZeroChunk;
+    const void* sb = kin ? (const void*)(L.b[t] + k0 + L.koff[t]) : (const void*)L.b[t];
+    __builtin_amdgcn_global_load_lds((gptr_t)sa, (lptr_t)(stage + L.blk[t] * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((gptr_t)sb, (lptr_t)(stage + kStageA + L.blk[t] * 1024), 16, 0, 0);
   }
 }
 
-MXQ_DEVICE void load_frags(const char* lds, int wm, int wn, int ks, v4i fa[4], v4i fb[4]) {
+// s_waitcnt with vmcnt <= n (lgkmcnt and expcnt left alone); n is a compile-time constant.
+template <int n> MXQ_DEVICE void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier without the implicit drain of __syncthreads(): loads in flight stay in
+// flight. The empty asm statements keep the compiler from moving memory accesses across it
+// (the barrier intrinsic itself is not a memory operation to the optimiser); the hardware
+// ordering comes from the s_waitcnt that precedes each call.
+MXQ_DEVICE void barrier_no_drain() {
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
+MXQ_DEVICE void load_frags(const char* stage, int wm, int wn, int ks, v4i fa[4], v4i fb[4]) {
   const int lane = threadIdx.x & 63;
   const int c = ks * 2 + (lane >> 5);
   const int lr = lane & 31;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    fa[i] = *reinterpret_cast<const v4i*>(lds + swz(wm * kWaveM + i * 32 + lr, c));
+    fa[i] = *reinterpret_cast<const v4i*>(stage + swz(wm * kWaveM + i * 32 + lr, c));
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    fb[j] = *reinterpret_cast<const v4i*>(lds + kStageA + swz(wn * kWaveN + j * 32 + lr, c));
+    fb[j] = *reinterpret_cast<const v4i*>(stage + kStageA + swz(wn * kWaveN + j * 32 + lr, c));
 }
 
-MXQ_DEVICE void mma_stage(const char* lds, int wm, int wn, v16i acc[4][4]) {
-  v4i fa[2][4], fb[2][4];
-  load_frags(lds, wm, wn, 0, fa[0], fb[0]);
+// The MFMAs compute C^T blocks (weights as the first operand): lane l of a 32 x 32 block then
+// holds output row l % 32 and, in registers r = 0..15, output columns
+// (r / 4) * 8 + (l / 32) * 4 + r % 4 -- four runs of four consecutive columns of one row.
+MXQ_DEVICE void mma16(const v4i fa[4], const v4i fb[4], v16i acc[4][4]) {
 #pragma unroll
-  for (int ks = 0; ks < kBK / 32; ++ks) {
-    if (ks + 1 < kBK / 32) load_frags(lds, wm, wn, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 4; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j], fa[i], acc[i][j], 0, 0, 0);
+}
+
+// One run of four consecutive outputs as store words: fp32/int32 outputs give four words,
+// 16-bit outputs two words of two values each (the lower column in the low half).
+// Dequant: y = out(fp32(acc) * (xs * ws)); y = out(y + bias). A missing bias is passed as
+// -0.0, for which y + (-0.0) == y for every y (signed zeros, infinities and NaN included).
+template <int kEpi, int kOut>
+MXQ_DEVICE void epi_run(const v16i& acc, int q, float xs, const float* w, const float* bias,
+                        uint32_t* out) {
+  if constexpr (kEpi == kEpiI32) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks & 1][i], fb[ks & 1][j], acc[i][j],
-                                                          0, 0, 0);
+    for (int e = 0; e < 4; ++e) out[e] = (uint32_t)acc[q * 4 + e];
+  } else if constexpr (kOut == 0) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float y = (float)acc[q * 4 + e] * (xs * w[e]);
+      out[e] = __float_as_uint(y + bias[e]);
+    }
+  } else if constexpr (kOut == 1) {
+    uint32_t h[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float y = round_f16((float)acc[q * 4 + e] * (xs * w[e]));
+      h[e] = f32_to_f16_bits(y + bias[e]);
+    }
+    out[0] = h[0] | (h[1] << 16);
+    out[1] = h[2] | (h[3] << 16);
+  } else {
+    float y[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = (float)acc[q * 4 + e] * (xs * w[e]);
+    const uint32_t p0 = pack_bf16x2(y[0], y[1]), p1 = pack_bf16x2(y[2], y[3]);
+    out[0] = pack_bf16x2(__uint_as_float(p0 << 16) + bias[0], __uint_as_float(p0 & 0xFFFF0000u) + bias[1]);
+    out[1] = pack_bf16x2(__uint_as_float(p1 << 16) + bias[2], __uint_as_float(p1 & 0xFFFF0000u) + bias[3]);
   }
 }
 
-// Element (i, j, r) of a lane's accumulators: tile row wm*128 + i*32 + (r/4)*8 + (lane/32)*4
-// + r%4, tile column wn*128 + j*32 + lane%32 (the v_mfma_i32_32x32x32_i8 layout).
-MXQ_DEVICE int acc_row(int wm, int i, int r, int lh) { return wm * kWaveM + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3); }
+// Store one run (words as produced by epi_run) of row `row` from column `col`. `fast`: the
+// caller has established that the four columns are inside the output and the run aligned.
+template <int kElem>
+MXQ_DEVICE void store_run(void* d, int64_t ldd, int64_t row, int64_t col, int64_t N, bool fast,
+                          const uint32_t* w) {
+  char* base = reinterpret_cast<char*>(d) + (row * ldd + col) * kElem;
+  if (fast) {
+    if constexpr (kElem == 4)
+      *reinterpret_cast<v4u*>(base) = v4u{w[0], w[1], w[2], w[3]};
+    else
+      *reinterpret_cast<v2u*>(base) = v2u{w[0], w[1]};
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (col + e < N) {
+        if constexpr (kElem == 4)
+          reinterpret_cast<uint32_t*>(base)[e] = w[e];
+        else
+          reinterpret_cast<uint16_t*>(base)[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+      }
+    }
+  }
+}
 
-template <int kEpi, int kOut>
-MXQ_DEVICE uint32_t epi_value(int32_t acc, float xs, float ws, float bias, bool has_bias) {
-  if (kEpi == kEpiI32) return (uint32_t)acc;
-  float y = OutT<kOut>::round((float)acc * (xs * ws));
-  if (has_bias) y = OutT<kOut>::round(y + bias);
-  if (kOut == 0) return __float_as_uint(y);
-  if (kOut == 1) return f32_to_f16_bits(y);
-  return f32_to_bf16_bits(y);
+// Stores the four runs of one 32 x 32 block row. Interior tiles (`full`) store unguarded.
+template <int kElem>
+MXQ_DEVICE void store_block_row(const GemmArgs& p, bool full, int64_t row, int64_t col0,
+                                const uint32_t* w) {
+  constexpr int kWords = kElem == 4 ? 4 : 2;
+  if (full) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) store_run<kElem>(p.d, p.ldd, row, col0 + q * 8, p.N, true, w + q * kWords);
+  } else if (row < p.M) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t col = col0 + q * 8;
+      store_run<kElem>(p.d, p.ldd, row, col, p.N, p.vec_store && col + 4 <= p.N, w + q * kWords);
+    }
+  }
 }
 
 template <int kEpi, int kOut>
 __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
-  __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+  __shared__ __attribute__((aligned(16))) char lds[kNS * kStageBytes + 2 * kBN * 4];
 
   int tm, tn;
   tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
@@ -179,107 +248,154 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v16i{};
 
+  // Pipeline: stage s lives in LDS buffer s % 4. Entering iteration kt, stages kt and kt+1 are
+  // complete and visible, the loads of stage kt+2 are in flight and F0 holds the fragments of
+  // (stage kt, K-step 0). Iteration kt issues stage kt+3 into the buffer stage kt-1 used,
+  // prefetches (kt, 1) and (kt+1, 0) fragments behind the MFMAs, then waits for stage kt+2.
   const int ktiles = (int)((p.K + kBK - 1) / kBK);
-  Stage st;
-  load_stage(st, p.a, p.b, p.M, p.N, p.K, m0, n0, 0);
-  store_stage(st, lds);
-  __syncthreads();
+  Loader ld;
+  make_loader(ld, p, m0, n0);
+  issue_stage(ld, lds, 0, p.K);
+  if (ktiles > 1) issue_stage(ld, lds + kStageBytes, kBK, p.K);
+  if (ktiles > 2) {
+    issue_stage(ld, lds + 2 * kStageBytes, 2 * kBK, p.K);
+    wait_vmcnt<kLoadsPerStage>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  barrier_no_drain();
+
+  v4i f0a[4], f0b[4], f1a[4], f1b[4];
+  load_frags(lds, wm, wn, 0, f0a, f0b);
   for (int kt = 0; kt < ktiles; ++kt) {
-    char* cur = lds + (kt & 1) * kStageBytes;
-    const bool more = kt + 1 < ktiles;
-    if (more) load_stage(st, p.a, p.b, p.M, p.N, p.K, m0, n0, (int64_t)(kt + 1) * kBK);
-    mma_stage(cur, wm, wn, acc);
-    if (more) store_stage(st, lds + ((kt + 1) & 1) * kStageBytes);
-    __syncthreads();
+    const char* cur = lds + (kt & 3) * kStageBytes;
+    const bool issue = kt + 3 < ktiles;
+    if (issue) issue_stage(ld, lds + ((kt + 3) & 3) * kStageBytes, (int64_t)(kt + 3) * kBK, p.K);
+    load_frags(cur, wm, wn, 1, f1a, f1b);
+    mma16(f0a, f0b, acc);
+    // Unconditional (after the last stage it reads a stale buffer, never used): a branch here
+    // would make the compiler drain every LDS read before the next MFMAs.
+    load_frags(lds + ((kt + 1) & 3) * kStageBytes, wm, wn, 0, f0a, f0b);
+    mma16(f1a, f1b, acc);
+    if (issue)
+      wait_vmcnt<kLoadsPerStage>();
+    else
+      wait_vmcnt<0>();
+    barrier_no_drain();
   }
 
   // ---- epilogue ----
-  constexpr int kElem = (kOut == 0 || kEpi == kEpiI32) ? 4 : 2;
-  typedef EpiLayout<kElem> L;
+  // Lane l holds, for m-block i and n-block j, row wm*128 + i*32 + l%32 and the four column
+  // runs j*32 + q*8 + (l/32)*4 + {0..3}, q = 0..3 (see mma16). The main loop's last barrier
+  // left the LDS free: per-column factors go behind the four stage buffers and, for GELU, the
+  // 128 KB bf16 -> bf16 table is fetched into the buffers themselves while the dequant runs.
+  constexpr int kElem = (kEpi == kEpiI32 || kOut == 0) ? 4 : 2;
   const int lr = lane & 31, lh = lane >> 5;
   const int t = threadIdx.x;
-  float* s_xs = reinterpret_cast<float*>(lds + L::kFactors);
-  float* s_ws = s_xs + kBM;
+  float* s_ws = reinterpret_cast<float*>(lds + kNS * kStageBytes);
   float* s_bias = s_ws + kBN;
-  const bool has_bias = p.bias != nullptr;
+  const uint16_t* s_gelu = reinterpret_cast<const uint16_t*>(lds);
+  const bool has_b = p.bias != nullptr;
+  float xsv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (kEpi != kEpiI32) {
-    const int64_t row = min(m0 + t, p.M - 1);
+    // Global reads of the factors are issued before the table fetch, so waiting for them
+    // leaves the fetch in flight.
     const int64_t col = min(n0 + t, p.N - 1);
-    s_xs[t] = p.xs[row];
-    s_ws[t] = p.ws_per_channel ? p.ws[col] : p.ws[0];
-    s_bias[t] = has_bias ? OutT<kOut>::load(reinterpret_cast<const typename OutT<kOut>::T*>(p.bias) + col) : 0.0f;
-    __syncthreads();
-  }
-
-  constexpr int kPasses = kBM / L::kRows;
-  constexpr int kCpr = kBN * kElem / 16;  // 16-byte chunks per tile row
-  constexpr int kPerRow = 16 / kElem;     // elements per chunk
+    const float wsl = p.ws_per_channel ? p.ws[col] : p.ws[0];
+    const float bl = has_b ? OutT<kOut>::load(reinterpret_cast<const typename OutT<kOut>::T*>(p.bias) + col) : -0.0f;
 #pragma unroll
-  for (int pass = 0; pass < kPasses; ++pass) {
-    if (kPasses == 1 || wm == pass) {
-      const int rbase = (kPasses == 1) ? 0 : pass * L::kRows;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int cl = wn * kWaveN + j * 32 + lr;
-          const float wsv = s_ws[cl], bv = s_bias[cl];
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int rl = acc_row(wm, i, r, lh);
-            const uint32_t v = epi_value<kEpi, kOut>(acc[i][j][r], s_xs[rl], wsv, bv, has_bias);
-            char* dst = lds + (rl - rbase) * L::kPitch + cl * kElem;
-            if (kElem == 4)
-              *reinterpret_cast<uint32_t*>(dst) = v;
-            else
-              *reinterpret_cast<uint16_t*>(dst) = (uint16_t)v;
-          }
-        }
-    }
-    __syncthreads();
-
-    // Stream the LDS tile out: each 16-byte chunk of a row to HBM; a half-wave covers one row.
-    constexpr int kIters = L::kRows * kCpr / kGemmThreads;
+    for (int i = 0; i < 4; ++i) xsv[i] = p.xs[min(m0 + wm * kWaveM + i * 32 + lr, p.M - 1)];
+    if (kEpi == kEpiGelu) {
+      const char* src = reinterpret_cast<const char*>(&kGeluFull) + lane * 16;
 #pragma unroll 4
-    for (int it = 0; it < kIters; ++it) {
-      const int idx = it * kGemmThreads + t;
-      const int rl = idx / kCpr, c = idx % kCpr;
-      v4u v = *reinterpret_cast<const v4u*>(lds + rl * L::kPitch + c * 16);
-      const int64_t row = m0 + pass * L::kRows + rl;
-      const int64_t col = n0 + c * kPerRow;
-      float m = 0.0f;
-      if (kEpi == kEpiGelu) {
+      for (int q = wave; q < 128; q += 4)
+        __builtin_amdgcn_global_load_lds((gptr_t)(src + q * 1024), (lptr_t)(lds + q * 1024), 16, 0, 0);
+    }
+    s_ws[t] = wsl;
+    s_bias[t] = bl;
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt left open (max)
+    barrier_no_drain();
+  }
+  const bool full = p.vec_store && m0 + kBM <= p.M && n0 + kBN <= p.N;
+
+  // GELU: pre-activation bf16 pairs, kept until the table has landed.
+  uint32_t yp[kEpi == kEpiGelu ? 4 : 1][4][8];
+  static_for<4>([&](auto J) {
+    constexpr int j = decltype(J)::value;
+    const int cl0 = wn * kWaveN + j * 32 + lh * 4;  // tile column of run q = 0
+    float wsv[16], bsv[16];
+    if constexpr (kEpi != kEpiI32) {
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const uint32_t lo = gelu_bf16(v[w] & 0xFFFFu), hi = gelu_bf16(v[w] >> 16);
-          v[w] = lo | (hi << 16);
-          if (col + 2 * w < p.N) m = fmaxf(m, fabsf(bf16_to_f32(lo)));
-          if (col + 2 * w + 1 < p.N) m = fmaxf(m, fabsf(bf16_to_f32(hi)));
-        }
-      }
-      if (row < p.M) {
-        char* out = reinterpret_cast<char*>(p.d) + (row * p.ldd + col) * kElem;
-        if (p.vec_store && col + kPerRow <= p.N) {
-          *reinterpret_cast<v4u*>(out) = v;
-        } else {
+      for (int q = 0; q < 4; ++q) {
+        const v4f w4 = *reinterpret_cast<const v4f*>(s_ws + cl0 + q * 8);
+        const v4f b4 = *reinterpret_cast<const v4f*>(s_bias + cl0 + q * 8);
 #pragma unroll
-          for (int e = 0; e < kPerRow; ++e) {
-            if (col + e < p.N) {
-              if (kElem == 4)
-                reinterpret_cast<uint32_t*>(out)[e] = v[e];
-              else
-                reinterpret_cast<uint16_t*>(out)[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
-            }
-          }
+        for (int e = 0; e < 4; ++e) {
+          wsv[q * 4 + e] = w4[e];
+          bsv[q * 4 + e] = b4[e];
         }
-      }
-      if (kEpi == kEpiGelu) {
-        // kCpr == 32: lanes 0-31 and 32-63 of a wave each hold one full tile row.
-        m = halfwave_max(m);
-        if ((lane & 31) == 0 && row < p.M) atomic_max_nonneg(p.row_absmax + row, m);
       }
     }
-    if (kPasses > 1) __syncthreads();
+    static_for<4>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      constexpr int kWords = kElem == 4 ? 4 : 2;
+      uint32_t w[4 * kWords];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) epi_run<kEpi, kOut>(acc[i][j], q, xsv[i], wsv + q * 4, bsv + q * 4, w + q * kWords);
+      if constexpr (kEpi == kEpiGelu) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) yp[i][j][r] = w[r];
+      } else {
+        store_block_row<kElem>(p, full, m0 + wm * kWaveM + i * 32 + lr, n0 + cl0, w);
+      }
+    });
+  });
+  if constexpr (kEpi == kEpiGelu) {
+    typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+    wait_vmcnt<0>();
+    barrier_no_drain();  // every wave's part of the table has landed
+    // |h| as bf16 bits: non-negative values order like their bit patterns (NaN above +inf), so
+    // the row maximum is an integer maximum, kept for both halves of a word at once.
+    us2 rmax[4] = {};
+    // Interior tiles run a copy of the pass without column masks or store guards.
+    auto gelu_pass = [&](auto FullC) {
+      constexpr bool kFull = decltype(FullC)::value;
+      static_for<4>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        const int cl0 = wn * kWaveN + j * 32 + lh * 4;
+        static_for<4>([&](auto I) {
+          constexpr int i = decltype(I)::value;
+          uint32_t g[8];
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            const uint32_t h = yp[i][j][r];
+            g[r] = (uint32_t)s_gelu[h & 0xFFFFu] | ((uint32_t)s_gelu[h >> 16] << 16);
+          }
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            uint32_t m = g[r] & 0x7FFF7FFFu;
+            if constexpr (!kFull) {
+              const int64_t col = n0 + cl0 + (r >> 1) * 8 + (r & 1) * 2;
+              m &= (col < p.N ? 0xFFFFu : 0u) | (col + 1 < p.N ? 0xFFFF0000u : 0u);
+            }
+            rmax[i] = __builtin_elementwise_max(rmax[i], __builtin_bit_cast(us2, m));
+          }
+          store_block_row<2>(p, kFull, m0 + wm * kWaveM + i * 32 + lr, n0 + cl0, g);
+        });
+      });
+    };
+    if (full)
+      gelu_pass(std::true_type{});
+    else
+      gelu_pass(std::false_type{});
+    // Lanes l and l + 32 hold the two halves of each row's 128 columns of this wave.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t m = max((uint32_t)rmax[i][0], (uint32_t)rmax[i][1]);
+      m = max(m, (uint32_t)__shfl_xor((int)m, 32, kWave));
+      const int64_t row = m0 + wm * kWaveM + i * 32 + lr;
+      if (lh == 0 && row < p.M) atomicMax(reinterpret_cast<unsigned int*>(p.row_absmax + row), m << 16);
+    }
   }
 }
 
@@ -289,7 +405,7 @@ static int launch_gemm(const GemmArgs& args0, hipStream_t stream) {
   args.tiles_m = (int)((args.M + kBM - 1) / kBM);
   args.tiles_n = (int)((args.N + kBN - 1) / kBN);
   const int elem = (kOut == 0 || kEpi == kEpiI32) ? 4 : 2;
-  args.vec_store = ((uintptr_t)args.d % 16 == 0) && ((args.ldd * elem) % 16 == 0);
+  args.vec_store = ((uintptr_t)args.d % (4 * elem) == 0) && (args.ldd % 4 == 0);
   const int64_t tiles = (int64_t)args.tiles_m * args.tiles_n;
   if (tiles > INT32_MAX) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "too many tiles");
   gemm_i8_kernel<kEpi, kOut><<<(unsigned)tiles, kGemmThreads, 0, stream>>>(args);

@@ -11,6 +11,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 #include "../../include/mx_qlinear.h"
 
 #define MXQ_DEVICE __device__ __forceinline__
@@ -24,6 +27,17 @@ typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 namespace mxq {
 
 constexpr int kWave = 64;
+
+// static_for<N>(f) calls f(std::integral_constant<int, 0>{}) ... f(integral_constant<N-1>): a
+// loop whose index is a compile-time constant in every body.
+template <typename F, int... Is>
+MXQ_DEVICE void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+MXQ_DEVICE void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 // ---- bfloat16 / float16 -------------------------------------------------------
 
@@ -109,34 +123,40 @@ MXQ_DEVICE int quant_round_clamp(float qf) {
 // Bit-exact torch CPU gelu(approximate="tanh") on a bfloat16 input (the routine the reference
 // applies, backends/turbo/vendor/comfy_kitchen/backends/_activations.py:47-48). The function
 // depends on the 16 input bits only: inputs with biased exponent below MXQ_GELU_E_LO map to
-// bf16(x / 2), finite inputs at or above MXQ_GELU_E_HI to x (x > 0) or -0.0 (x < 0); the
-// 3072 inputs in between are looked up in a table generated from torch by gen_gelu_table.py,
-// which verifies each rule against all 65,536 torch outputs.
-#define MXQ_GELU_TABLE_DECL static __constant__ uint16_t kGeluTable[3072]
+// bf16(x / 2), finite inputs at or above MXQ_GELU_E_HI to x (x > 0) or -0.0 (x < 0), +inf to
+// +inf and -inf / NaN to MXQ_GELU_NAN; the 3072 inputs in between come from a table generated
+// from torch by gen_gelu_table.py, which verifies each rule against all 65,536 torch outputs.
+#define MXQ_GELU_TABLE_DECL constexpr uint16_t kGeluTableC[3072]
 #include "gelu_tanh_bf16_table.inc"
 #undef MXQ_GELU_TABLE_DECL
 
-MXQ_DEVICE uint32_t gelu_table_index(uint32_t b) {
-  const int e = (int)((b >> 7) & 0xFFu);
-  const int ei = min(max(e - MXQ_GELU_E_LO, 0), MXQ_GELU_E_HI - MXQ_GELU_E_LO - 1);
-  return ((b >> 15) * (MXQ_GELU_E_HI - MXQ_GELU_E_LO) + ei) * 128u + (b & 0x7Fu);
-}
-
-// Result for inputs outside the table range; `looked_up` is table[gelu_table_index(b)].
-MXQ_DEVICE uint32_t gelu_bf16_finish(uint32_t b, uint32_t looked_up) {
+constexpr uint32_t gelu_rule_c(uint32_t b) {
   const uint32_t e = (b >> 7) & 0xFFu, sign = b & 0x8000u, mag = b & 0x7FFFu;
-  const uint32_t v = mag & 0xFFu;
-  const uint32_t half_sub = (v >> 1) + ((v & 1u) & ((v >> 1) & 1u));
-  const uint32_t half = sign | (e >= 2 ? mag - 0x80u : half_sub);
-  const uint32_t big = sign ? 0x8000u : b;
-  const uint32_t special = (b == 0x7F80u) ? 0x7F80u : MXQ_GELU_NAN;
-  return e < MXQ_GELU_E_LO ? half : e < MXQ_GELU_E_HI ? looked_up : e < 255u ? big : special;
+  if (e < MXQ_GELU_E_LO) {
+    // x / 2: one exponent step down, or for e < 2 a right shift of the significand with
+    // round-half-to-even.
+    const uint32_t v = mag & 0xFFu;
+    return sign | (e >= 2 ? mag - 0x80u : (v >> 1) + ((v & 1u) & ((v >> 1) & 1u)));
+  }
+  if (e < MXQ_GELU_E_HI)
+    return kGeluTableC[((b >> 15) * (MXQ_GELU_E_HI - MXQ_GELU_E_LO) + (e - MXQ_GELU_E_LO)) * 128u + (b & 0x7Fu)];
+  if (e < 255u) return sign ? 0x8000u : b;
+  return b == 0x7F80u ? 0x7F80u : MXQ_GELU_NAN;
 }
 
-// GELU of one bf16 (bits) using the table in constant memory.
-MXQ_DEVICE uint32_t gelu_bf16(uint32_t b) {
-  return gelu_bf16_finish(b, kGeluTable[gelu_table_index(b)]);
+// The function over all 65,536 inputs (v[b] = gelu(b)), evaluated at compile time: 128 KB in
+// global memory that kernels gather from, or that a GEMM epilogue copies into LDS whole.
+struct GeluFullTable {
+  uint16_t v[65536];
+};
+constexpr GeluFullTable make_gelu_full() {
+  GeluFullTable t{};
+  for (uint32_t b = 0; b < 65536u; ++b) t.v[b] = (uint16_t)gelu_rule_c(b);
+  return t;
 }
+static __device__ __attribute__((aligned(16))) const GeluFullTable kGeluFull = make_gelu_full();
+
+MXQ_DEVICE uint32_t gelu_bf16(uint32_t b) { return kGeluFull.v[b & 0xFFFFu]; }
 
 // ---- wave reductions --------------------------------------------------------------
 
@@ -156,6 +176,27 @@ MXQ_DEVICE float wave_sum(float v) {
 MXQ_DEVICE float halfwave_max(float v) {
 #pragma unroll
   for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// One DPP step of a max reduction: v = max(v, v of the lane selected by kCtrl). Lanes of rows
+// outside kRowMask keep their own value.
+template <int kCtrl, int kRowMask = 0xF>
+MXQ_DEVICE float dpp_max(float v) {
+  const int s = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), kCtrl, kRowMask,
+                                            0xF, false);
+  return fmaxf(v, __int_as_float(s));
+}
+
+// Max over each half-wave (lanes 0-31, 32-63) with DPP only: swap neighbours, swap pairs,
+// half-row mirror, row mirror (each 16-lane row now holds its max), then broadcast lane 15 of
+// rows 0 and 2 into rows 1 and 3. The result is valid in lanes 16-31 and 48-63.
+MXQ_DEVICE float halfwave_max_dpp(float v) {
+  v = dpp_max<0xB1>(v);        // quad_perm [1, 0, 3, 2]
+  v = dpp_max<0x4E>(v);        // quad_perm [2, 3, 0, 1]
+  v = dpp_max<0x141>(v);       // row_half_mirror
+  v = dpp_max<0x140>(v);       // row_mirror
+  v = dpp_max<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
   return v;
 }
 

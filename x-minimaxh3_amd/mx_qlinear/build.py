@@ -32,6 +32,8 @@ COMMON_FLAGS = [
     # Packed fp32 VALU instructions are kept out of all device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
+    # The 65,536-entry GELU table is evaluated at compile time.
+    "-fconstexpr-steps=100000000",
 ]
 
 
