@@ -129,10 +129,14 @@ class FfnWorkload:
         return self.m
 
     def dominant(self, timer):
-        """(kernel label, ops per launch, mean launch ms) of the slower GEMM launch."""
-        cands = [("fc1_gemm", timer.mean_ms("fc1_gemm")), ("fc2_gemm", timer.mean_ms("fc2_gemm"))]
-        name, ms = max(cands, key=lambda c: c[1])
-        return ("gemm_i8_kernel (" + name + ")", 2 * self.m * self.k * self.hidden, ms)
+        """The slower GEMM launch: label, kernel symbol, ops and algorithmic bytes per launch, mean ms."""
+        m, k, h = self.m, self.k, self.hidden
+        fc1 = {"span": "fc1_gemm", "symbol": "gemm_i8_kernel<2, 2>", "ops": 2 * m * k * h,
+               # A, W1, out H (bf16), xs, ws, bias, row absmax
+               "bytes": m * k + h * k + 2 * m * h + 4 * m + 4 * h + 2 * h + 4 * m}
+        fc2 = {"span": "fc2_gemm", "symbol": "gemm_i8_kernel<1, 2>", "ops": 2 * m * k * h,
+               "bytes": m * h + k * h + 2 * m * k + 4 * m + 4 * k + 2 * k}
+        return max((fc1, fc2), key=lambda d: timer.mean_ms(d["span"]))
 
     def config(self):
         return {"workload": self.name, "tokens": self.m, "d_model": self.k, "d_ff": self.hidden,
@@ -194,7 +198,9 @@ class QkvWorkload:
         return self.m
 
     def dominant(self, timer):
-        return ("gemm_i8_kernel (qkv)", self.ops_per_step(), timer.mean_ms("qkv_gemm"))
+        m, k, n = self.m, self.k, self.n
+        return {"span": "qkv_gemm", "symbol": "gemm_i8_kernel<1, 2>", "ops": 2 * m * n * k,
+                "bytes": m * k + n * k + 2 * m * n + 4 * m + 4 * n + 2 * n}
 
     def config(self):
         return {"workload": self.name, "tokens": self.m, "d_model": self.k, "qkv_out": self.n,
@@ -244,7 +250,8 @@ class W4A8Workload:
         return self.m * self.k + self.n * self.k // 2 + (self.k // self.g) * self.n * 2 + self.m * 4 + self.m * self.n * 2
 
     def dominant(self, timer):
-        return ("w4a8_grouped_kernel", self.ops_per_step(), timer.mean_ms("w4a8_gemm"))
+        return {"span": "w4a8_gemm", "symbol": "w4a8_grouped_kernel", "ops": self.ops_per_step(),
+                "bytes": self.alg_bytes()}
 
     def config(self):
         return {"workload": self.name, "m": self.m, "n": self.n, "k": self.k, "group": self.g,
@@ -274,12 +281,20 @@ class LinearC1Workload:
         self.x = make_activations(self.m, self.k, dev, 30)
         self.w, self.s = make_int8_weight(self.n, self.k, dev, 31)
         self.b = make_bias(self.n, dev, 32)
+        self.xq = torch.empty(self.m, self.k, dtype=torch.int8, device=dev)
+        self.xs = torch.empty(self.m, dtype=torch.float32, device=dev)
+        self.out = torch.empty(self.m, self.n, dtype=torch.bfloat16, device=dev)
         self.dev = dev
 
     def step(self, timer=None):
+        st = _stream(self.dev)
         t = timer.span if timer else (lambda name: _Null())
-        with t("linear"):
-            mx_qlinear.int8_linear(self.x, self.w, self.s, self.b)
+        with t("quant_x"):
+            _lib.call("mxq_quantize_int8_rowwise", _p(self.x), _lib.DTYPE_BF16, _p(self.xq), _p(self.xs), self.m,
+                      self.k, _lib.ACT_NONE, st)
+        with t("gemm"):
+            _lib.call("mxq_int8_gemm_dequant", _p(self.xq), _p(self.w), _p(self.xs), _p(self.s), self.n,
+                      _p(self.b), _p(self.out), self.m, self.n, self.k, self.n, _lib.DTYPE_BF16, st)
 
     def ops_per_step(self):
         return 2 * self.m * self.n * self.k
@@ -288,7 +303,9 @@ class LinearC1Workload:
         return self.m
 
     def dominant(self, timer):
-        return ("int8_linear (quant + gemm)", self.ops_per_step(), timer.mean_ms("linear"))
+        m, k, n = self.m, self.k, self.n
+        return {"span": "gemm", "symbol": "gemm_i8_kernel<1, 2>", "ops": 2 * m * n * k,
+                "bytes": m * k + n * k + 2 * m * n + 4 * m + 4 * n + 2 * n}
 
     def config(self):
         return {"workload": self.name, "m": self.m, "n": self.n, "k": self.k}
@@ -308,18 +325,105 @@ class LinearC1Workload:
 
 
 def _cpu_sample(run, budget_s, max_rows, unit, what):
+    """Times `run(rows)` on a growing leading slice of the workload until one pass takes about
+    budget_s / 2, then repeats passes until budget_s seconds of CPU work have been timed."""
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     rows = 16
     elapsed = run(rows)
-    while elapsed < budget_s / 4 and rows < max_rows:
+    while elapsed < budget_s / 8 and rows < max_rows:
         rows = min(max_rows, rows * 4)
         elapsed = run(rows)
     if elapsed < budget_s / 2 and rows < max_rows:
-        rows = min(max_rows, int(rows * budget_s / 2 / max(elapsed, 1e-3)))
+        rows = min(max_rows, max(rows, int(rows * budget_s / 2 / max(elapsed, 1e-3))))
         elapsed = run(rows)
-    return {"value": rows / elapsed, "unit": unit, "cores": threads, "kind": "port",
-            "sample": what.format(rows=rows) + f" ({elapsed:.1f} s, torch {torch.__version__} CPU)"}
+    total, passes = elapsed, 1
+    while total < budget_s:
+        total += run(rows)
+        passes += 1
+    return {"value": rows * passes / total, "unit": unit, "cores": threads, "kind": "port",
+            "sample": what.format(rows=rows) + f", {passes} pass(es), {total:.1f} s, torch {torch.__version__} CPU"}
+
+
+# ----------------------------------------------------------------------------------------
+# HBM traffic of the dominant kernel from rocprofv3 counters
+# ----------------------------------------------------------------------------------------
+
+CALIB_BYTES = 1 << 30  # the calibration pass reads and writes 1 GiB
+
+
+def _pmc_child(wl):
+    """Body profiled by one counter pass: a plain elementwise pass that reads 1 GiB and writes
+    1 GiB (torch.neg, the calibration), then one step."""
+    src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=wl.dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    wl.step()
+    torch.cuda.synchronize()
+
+
+def _counter_pass(workload, counter, symbol, out_root):
+    """Runs `rocprofv3 --pmc <counter>` over a child bench process; returns (KiB per launch of
+    `symbol`, KiB of the calibration copy) or raises."""
+    import csv
+    import glob
+    import shutil
+    import signal
+    import statistics
+    import subprocess
+
+    exe = shutil.which("rocprofv3")
+    if not exe:
+        raise RuntimeError("rocprofv3 not found")
+    out = os.path.join(out_root, f"pmc_{workload}_{counter}")
+    shutil.rmtree(out, ignore_errors=True)
+    env = dict(os.environ, TMPDIR="/tmp")
+    cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "pmc", "--",
+           sys.executable, os.path.abspath(__file__), "--pmc-child", "--workload", workload]
+    proc = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                            start_new_session=True)
+    try:
+        log, _ = proc.communicate(timeout=180)
+    except subprocess.TimeoutExpired:
+        os.killpg(proc.pid, signal.SIGKILL)
+        proc.communicate()
+        raise RuntimeError(f"{counter} pass timed out")
+    files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        tail = log.decode(errors="replace")[-400:]
+        raise RuntimeError(f"{counter} pass wrote no counters (exit {proc.returncode}): {tail}")
+    kern, copy = [], []
+    with open(files[0], newline="") as f:
+        for row in csv.DictReader(f):
+            if row["Counter_Name"] != counter:
+                continue
+            name, val = row["Kernel_Name"], float(row["Counter_Value"])
+            if symbol in name:
+                kern.append(val)
+            elif "neg_kernel" in name:
+                copy.append(val)
+    if not kern or not copy:
+        raise RuntimeError(f"{counter} pass: kernel or calibration copy not found")
+    return statistics.median(kern), max(copy)
+
+
+def pmc_traffic(workload, symbol):
+    """HBM bytes per launch of `symbol`: FETCH_SIZE and WRITE_SIZE (KiB per dispatch, one
+    rocprofv3 pass each), each scaled by the ratio of the true size of a 1 GiB copy to what the
+    same counter reads for it."""
+    out_root = os.path.join(ROOT, "gpurun_out")
+    os.makedirs(out_root, exist_ok=True)
+    fetch, cf = _counter_pass(workload, "FETCH_SIZE", symbol, out_root)
+    write, cw = _counter_pass(workload, "WRITE_SIZE", symbol, out_root)
+    kib = CALIB_BYTES / 1024
+    f_scale, w_scale = kib / cf, kib / cw
+    total = fetch * 1024 * f_scale + write * 1024 * w_scale
+    detail = {"fetch_kib": round(fetch, 1), "write_kib": round(write, 1), "copy_fetch_kib": round(cf, 1),
+              "copy_write_kib": round(cw, 1), "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4)}
+    return total, detail
 
 
 WORKLOADS = {
@@ -346,6 +450,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="ffn", choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work (0: skip)")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
+    ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (the path shards over "
@@ -354,6 +460,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     wl = WORKLOADS[args.workload](dev)
+    if args.pmc_child:
+        _pmc_child(wl)
+        return
     torch.cuda.synchronize()
     for _ in range(args.warmup):
         wl.step()
@@ -373,8 +482,19 @@ def main():
         value = wl.alg_bytes() * args.steps / wall / 1e9
     else:
         value = units
-    kname, kops, kms = wl.dominant(timer)
-    achieved = kops / (kms * 1e-3) / 1e12
+    dom = wl.dominant(timer)
+    kms = timer.mean_ms(dom["span"])
+    achieved = dom["ops"] / (kms * 1e-3) / 1e12
+    roof = {"bound": "mfma", "kernel": f"{dom['symbol']} ({dom['span']})", "achieved": round(achieved, 2),
+            "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4),
+            "traffic": None, "alg_bytes": dom["bytes"], "launch_ms": round(kms, 4)}
+    if not args.no_traffic:
+        try:
+            traffic, detail = pmc_traffic(args.workload, dom["symbol"])
+            roof["traffic"] = int(traffic)
+            roof["traffic_detail"] = detail
+        except Exception as e:  # counters unavailable: traffic stays null, with the reason
+            roof["traffic_error"] = str(e)[:300]
     line = {
         "metric": metric, "value": round(value, 3), "unit": unit, "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
@@ -384,8 +504,7 @@ def main():
         "tops_per_step": round(wl.ops_per_step() / (ms * 1e-3) / 1e12, 2),
         "int8_peak_frac_per_step": round(wl.ops_per_step() / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
         "kernel_ms": {k: round(timer.mean_ms(k), 4) for k in timer.spans},
-        "roofline": {"bound": "mfma", "kernel": kname, "achieved": round(achieved, 2), "peak": INT8_PEAK_TOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": None},
+        "roofline": roof,
     }
     if args.cpu_budget > 0:
         line["cpu_baseline"] = wl.cpu_baseline(args.cpu_budget)

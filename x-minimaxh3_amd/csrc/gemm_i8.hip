@@ -27,13 +27,13 @@
 
 namespace mxq {
 
-constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kBM = 256, kBN = 256, kBK = 128;
 constexpr int kGemmThreads = 256;
 constexpr int kWaveM = 128, kWaveN = 128;
-constexpr int kNS = 4;                                  // LDS pipeline stages
-constexpr int kStageA = kBM * kBK, kStageB = kBN * kBK; // 16 KB each
+constexpr int kNS = 2;                                  // LDS pipeline stages
+constexpr int kStageA = kBM * kBK, kStageB = kBN * kBK; // 32 KB each
 constexpr int kStageBytes = kStageA + kStageB;
-constexpr int kLoadsPerStage = 8;                       // direct-to-LDS loads per wave per stage
+constexpr int kLoadsPerStage = 16;                      // direct-to-LDS loads per wave per stage
 constexpr int kGroupM = 8;
 
 enum { kEpiI32 = 0, kEpiDequant = 1, kEpiGelu = 2 };
@@ -52,12 +52,11 @@ struct GemmArgs {
   int tiles_m, tiles_n;
 };
 
-// LDS operand layout: a tile row is 64 bytes = four 16-byte chunks; chunk c of row r sits at
-// slot c ^ f(r), f(r) = (r >> 2) & 3. gfx950 serves a ds_read_b128 sixteen lanes per clock;
-// with this map the sixteen rows one MFMA operand read touches per clock fall in distinct
-// banks (measured: 4 LDS cycles per ds_read_b128, no SQ_LDS_BANK_CONFLICT cycles, whereas
-// f(r) = ((r >> 1) ^ (r >> 3)) & 3 costs 8).
-MXQ_DEVICE int swz_f(int r) { return (r >> 2) & 3; }
+// LDS operand layout: a tile row is 128 bytes = eight 16-byte chunks; chunk c of row r sits at
+// slot c ^ f(r), f(r) = (r >> 1) & 7. gfx950 serves a ds_read_b128 sixteen lanes per clock:
+// an MFMA operand read has those lanes on sixteen consecutive rows at one chunk, and the map
+// gives them sixteen distinct (r & 1, slot) pairs, i.e. all 64 banks once.
+MXQ_DEVICE int swz_f(int r) { return (r >> 1) & 7; }
 MXQ_DEVICE int swz(int r, int c) { return r * kBK + ((c ^ swz_f(r)) << 4); }
 
 // Zero source for the K tail of A (B's tail may hold anything: it meets zeros).
@@ -81,24 +80,23 @@ MXQ_DEVICE void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn)
 }
 
 // Direct-to-LDS stage loads (global_load_lds_dwordx4). One instruction fills 1 KB of LDS:
-// lane i writes slot i % 4 of tile row 16 b + i / 4, so the lane fetches logical chunk
-// (i % 4) ^ f(row) of that row. Wave w loads A and B blocks b = 4 w .. 4 w + 3 of each stage.
+// lane i writes slot i % 8 of tile row 8 b + i / 8, so the lane fetches logical chunk
+// (i % 8) ^ f(row) of that row, and eight lanes read one whole 128-byte line of the row-major
+// operand (half lines, as 64-byte steps would read, halve the L2 -> CU throughput). Wave w
+// loads A and B blocks b = 8 w .. 8 w + 7 of each stage.
 struct Loader {
-  const int8_t* a[4];
-  const int8_t* b[4];
-  int64_t koff[4];   // logical chunk offset (bytes) of this lane's 16-byte piece
-  int blk[4];
+  const int8_t* a[8];
+  const int8_t* b[8];
+  int koff[2];   // logical chunk offset (bytes) of this lane's piece, for even and odd t
 };
 
 MXQ_DEVICE void make_loader(Loader& L, const GemmArgs& p, int64_t m0, int64_t n0) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int b = w * 4 + t;
-    const int r = b * 16 + (lane >> 2);
-    const int c = (lane & 3) ^ swz_f(r);
-    L.blk[t] = b;
-    L.koff[t] = c * 16;
+  for (int t = 0; t < 8; ++t) {
+    const int r = (w * 8 + t) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ swz_f(r);  // depends on t only through t & 1
+    if (t < 2) L.koff[t] = c * 16;
     L.a[t] = p.a + min(m0 + r, p.M - 1) * p.K + c * 16;
     L.b[t] = p.b + min(n0 + r, p.N - 1) * p.K;
   }
@@ -108,13 +106,15 @@ typedef const void __attribute__((address_space(1)))* gptr_t;
 typedef void __attribute__((address_space(3)))* lptr_t;
 
 MXQ_DEVICE void issue_stage(const Loader& L, char* stage, int64_t k0, int64_t K) {
+  const int w = threadIdx.x >> 6;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const bool kin = k0 + L.koff[t] < K;
+  for (int t = 0; t < 8; ++t) {
+    const int koff = L.koff[t & 1];
+    const bool kin = k0 + koff < K;
     const void* sa = kin ? (const void*)(L.a[t] + k0) : (const void*)kZeroChunk;
-    const void* sb = kin ? (const void*)(L.b[t] + k0 + L.koff[t]) : (const void*)L.b[t];
-    __builtin_amdgcn_global_load_lds((gptr_t)sa, (lptr_t)(stage + L.blk[t] * 1024), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((gptr_t)sb, (lptr_t)(stage + kStageA + L.blk[t] * 1024), 16, 0, 0);
+    const void* sb = kin ? (const void*)(L.b[t] + k0 + koff) : (const void*)L.b[t];
+    __builtin_amdgcn_global_load_lds((gptr_t)sa, (lptr_t)(stage + (w * 8 + t) * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((gptr_t)sb, (lptr_t)(stage + kStageA + (w * 8 + t) * 1024), 16, 0, 0);
   }
 }
 
@@ -122,6 +122,12 @@ MXQ_DEVICE void issue_stage(const Loader& L, char* stage, int64_t k0, int64_t K)
 template <int n> MXQ_DEVICE void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
+
+// s_waitcnt vmcnt(0) lgkmcnt(0).
+MXQ_DEVICE void wait_all() { __builtin_amdgcn_s_waitcnt(0x0070); }
+
+// s_waitcnt lgkmcnt(8): all but the eight most recent LDS reads have completed.
+MXQ_DEVICE void wait_lgkm8() { __builtin_amdgcn_s_waitcnt(0xC87F); }
 
 // Workgroup barrier without the implicit drain of __syncthreads(): loads in flight stay in
 // flight. The empty asm statements keep the compiler from moving memory accesses across it
@@ -133,16 +139,35 @@ MXQ_DEVICE void barrier_no_drain() {
   __asm__ volatile("" ::: "memory");
 }
 
-MXQ_DEVICE void load_frags(const char* stage, int wm, int wn, int ks, v4i fa[4], v4i fb[4]) {
+// ds_read_b128 issued as inline assembly, so that the compiler's wait-count pass does not see it:
+// with direct-to-LDS loads in flight that pass only ever waits for LDS reads with lgkmcnt(0),
+// which would serialise every fragment read with the MFMAs it should overlap. The main loop
+// therefore places its LDS waits itself (wait_lgkm8 / wait_all); a fragment is never used
+// before one of them has covered it.
+template <int kOff>
+MXQ_DEVICE v4i lds_read_b128(uint32_t addr) {
+  v4i r;
+  __asm__ volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(kOff));
+  return r;
+}
+
+// Fragments of K-step ks (32 K-bytes) of a stage: A rows wm*128 + i*32 + l%32 and B rows
+// wn*128 + j*32 + l%32, chunk ks*2 + l/32. Every row a lane touches has the same swizzle
+// f = ((l % 32) >> 1) & 7, so one base address per operand serves all four blocks.
+MXQ_DEVICE void load_frags(uint32_t stage, int wm, int wn, int ks, v4i fa[4], v4i fb[4]) {
   const int lane = threadIdx.x & 63;
-  const int c = ks * 2 + (lane >> 5);
   const int lr = lane & 31;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    fa[i] = *reinterpret_cast<const v4i*>(stage + swz(wm * kWaveM + i * 32 + lr, c));
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    fb[j] = *reinterpret_cast<const v4i*>(stage + kStageA + swz(wn * kWaveN + j * 32 + lr, c));
+  const uint32_t x = (uint32_t)(((ks * 2 + (lane >> 5)) ^ swz_f(lr)) << 4);
+  const uint32_t ba = stage + (uint32_t)(wm * kWaveM + lr) * kBK + x;
+  const uint32_t bb = stage + (uint32_t)(wn * kWaveN + lr) * kBK + x;
+  fa[0] = lds_read_b128<0>(ba);
+  fa[1] = lds_read_b128<32 * kBK>(ba);
+  fa[2] = lds_read_b128<64 * kBK>(ba);
+  fa[3] = lds_read_b128<96 * kBK>(ba);
+  fb[0] = lds_read_b128<kStageA>(bb);
+  fb[1] = lds_read_b128<kStageA + 32 * kBK>(bb);
+  fb[2] = lds_read_b128<kStageA + 64 * kBK>(bb);
+  fb[3] = lds_read_b128<kStageA + 96 * kBK>(bb);
 }
 
 // The MFMAs compute C^T blocks (weights as the first operand): lane l of a 32 x 32 block then
@@ -248,41 +273,66 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v16i{};
 
-  // Pipeline: stage s lives in LDS buffer s % 4. Entering iteration kt, stages kt and kt+1 are
-  // complete and visible, the loads of stage kt+2 are in flight and F0 holds the fragments of
-  // (stage kt, K-step 0). Iteration kt issues stage kt+3 into the buffer stage kt-1 used,
-  // prefetches (kt, 1) and (kt+1, 0) fragments behind the MFMAs, then waits for stage kt+2.
+  // Pipeline: stage s (128 K-bytes of A and B) lives in LDS buffer s % 2. Entering iteration kt,
+  // stage kt is complete and visible, the loads of stage kt+1 are in flight and F0 holds the
+  // fragments of (stage kt, K-step 0). The iteration runs K-steps 0..3 with each step's
+  // fragments read behind the previous step's MFMAs; before the last step's MFMAs it waits for
+  // stage kt+1, passes the barrier that frees buffer kt % 2, issues stage kt+2 into it and
+  // reads (kt+1, 0) -- so that read, too, overlaps matrix work.
   const int ktiles = (int)((p.K + kBK - 1) / kBK);
   Loader ld;
   make_loader(ld, p, m0, n0);
   issue_stage(ld, lds, 0, p.K);
-  if (ktiles > 1) issue_stage(ld, lds + kStageBytes, kBK, p.K);
-  if (ktiles > 2) {
-    issue_stage(ld, lds + 2 * kStageBytes, 2 * kBK, p.K);
+  if (ktiles > 1) {
+    issue_stage(ld, lds + kStageBytes, kBK, p.K);
     wait_vmcnt<kLoadsPerStage>();
   } else {
     wait_vmcnt<0>();
   }
   barrier_no_drain();
 
+  // LDS byte address of the stage buffers (the low 32 bits of the shared-memory pointer).
+  const uint32_t lds_addr = (uint32_t)(uintptr_t)(lptr_t)lds;
   v4i f0a[4], f0b[4], f1a[4], f1b[4];
-  load_frags(lds, wm, wn, 0, f0a, f0b);
+  load_frags(lds_addr, wm, wn, 0, f0a, f0b);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   for (int kt = 0; kt < ktiles; ++kt) {
-    const char* cur = lds + (kt & 3) * kStageBytes;
-    const bool issue = kt + 3 < ktiles;
-    if (issue) issue_stage(ld, lds + ((kt + 3) & 3) * kStageBytes, (int64_t)(kt + 3) * kBK, p.K);
-    load_frags(cur, wm, wn, 1, f1a, f1b);
+    char* cur = lds + (kt & 1) * kStageBytes;
+    const uint32_t cur_a = lds_addr + (uint32_t)((kt & 1) * kStageBytes);
+    const uint32_t nxt_a = lds_addr + (uint32_t)(((kt + 1) & 1) * kStageBytes);
+    // Each group: issue the next K-step's eight fragment reads, wait until only those are
+    // outstanding, run the current K-step's sixteen MFMAs. sched_barrier(0) keeps the groups
+    // in this order.
+    load_frags(cur_a, wm, wn, 1, f1a, f1b);
+    wait_lgkm8();
+    __builtin_amdgcn_sched_barrier(0);
     mma16(f0a, f0b, acc);
-    // Unconditional (after the last stage it reads a stale buffer, never used): a branch here
-    // would make the compiler drain every LDS read before the next MFMAs.
-    load_frags(lds + ((kt + 1) & 3) * kStageBytes, wm, wn, 0, f0a, f0b);
+    __builtin_amdgcn_sched_barrier(0);
+    load_frags(cur_a, wm, wn, 2, f0a, f0b);
+    wait_lgkm8();
+    __builtin_amdgcn_sched_barrier(0);
     mma16(f1a, f1b, acc);
-    if (issue)
-      wait_vmcnt<kLoadsPerStage>();
-    else
-      wait_vmcnt<0>();
-    barrier_no_drain();
+    __builtin_amdgcn_sched_barrier(0);
+    load_frags(cur_a, wm, wn, 3, f1a, f1b);
+    wait_lgkm8();
+    __builtin_amdgcn_sched_barrier(0);
+    mma16(f0a, f0b, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    // Stage kt+1 landed and this wave's reads of buffer kt % 2 (K-step 3 included) are done.
+    wait_all();
+    if (kt + 1 < ktiles) {
+      barrier_no_drain();
+      if (kt + 2 < ktiles) issue_stage(ld, cur, (int64_t)(kt + 2) * kBK, p.K);
+    }
+    // Unconditional (after the last stage it reads a buffer nobody writes, never used).
+    load_frags(nxt_a, wm, wn, 0, f0a, f0b);
+    __builtin_amdgcn_sched_barrier(0);
+    mma16(f1a, f1b, acc);
+    __builtin_amdgcn_sched_barrier(0);
   }
+  // Every wave is done reading the stage buffers before the epilogue reuses them.
+  wait_all();
+  barrier_no_drain();
 
   // ---- epilogue ----
   // Lane l holds, for m-block i and n-block j, row wm*128 + i*32 + l%32 and the four column
