@@ -1,0 +1,115 @@
+"""The C ABI without a GPU: the library loads, exports every function the header declares
+with the argument list the ctypes table uses, and rejects bad requests on the host before
+any launch (the error paths of the reference's launchers and bindings, e.g.
+CK/backends/cuda/ops/cutlass_gemm_int8.cu:613-665, w4a8_gemm.cu:93-164)."""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "mx_qlinear.h"
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    decls = {}
+    for m in re.finditer(r"^(?:const char\*|int)\s+(mxq_\w+)\s*\(([^;]*)\)\s*;", text, re.M):
+        args = [a.strip() for a in m.group(2).replace("\n", " ").split(",")]
+        decls[m.group(1)] = [] if args == ["void"] else args
+    return decls
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from mx_qlinear import _lib
+
+    if not _lib.LIB_PATH.exists():
+        from mx_qlinear import build
+
+        build.build()
+    return _lib.load()
+
+
+def test_header_declares_the_ctypes_table():
+    from mx_qlinear import _lib
+
+    decls = _declared()
+    assert set(_lib.SIGNATURES) | {"mxq_last_error", "mxq_abi_version"} == set(decls)
+    for name, argtypes in _lib.SIGNATURES.items():
+        assert len(argtypes) == len(decls[name]), name
+        for ctype, decl in zip(argtypes, decls[name]):
+            if ctype is ctypes.c_int64:
+                assert decl.startswith("int64_t"), (name, decl)
+            elif ctype is ctypes.c_int:
+                assert decl.startswith("int "), (name, decl)
+            elif ctype is ctypes.c_float:
+                assert decl.startswith("float "), (name, decl)
+            else:
+                assert "*" in decl, (name, decl)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_error_string(lib):
+    from mx_qlinear import _lib
+
+    assert lib.mxq_abi_version() == 1
+    lib.mxq_last_error.restype = ctypes.c_char_p
+    assert isinstance(lib.mxq_last_error(), bytes)
+    # a rejected call leaves a message naming the problem
+    rc = _lib.load().mxq_int8_gemm_i32(None, None, None, -1, 4, 16, 4, None)
+    assert rc == _lib.MXQ_ERR_INVALID
+    assert b"negative" in lib.mxq_last_error()
+
+
+@pytest.mark.parametrize(
+    "args, code",
+    [
+        ((-1, 16, 16, 16), "INVALID"),   # negative M
+        ((16, 16, 24, 16), "UNSUPPORTED"),  # K not a multiple of 16
+        ((16, 16, 131072, 16), "UNSUPPORTED"),  # K beyond the int32 accumulator bound
+        ((16, 32, 16, 16), "INVALID"),   # ldc < N
+        ((16, 16, 0, 16), "UNSUPPORTED"),  # K == 0 with a non-empty output
+    ],
+)
+def test_gemm_shape_checks(lib, args, code):
+    from mx_qlinear import _lib
+
+    m, n, k, ldc = args
+    dummy = ctypes.c_void_p(16)  # never dereferenced: every case is rejected on the host
+    rc = lib.mxq_int8_gemm_i32(dummy, dummy, dummy, m, n, k, ldc, None)
+    assert rc == getattr(_lib, "MXQ_ERR_" + code)
+
+
+def test_empty_gemm_is_a_no_op(lib):
+    from mx_qlinear import _lib
+
+    assert lib.mxq_int8_gemm_i32(None, None, None, 0, 0, 16, 0, None) == _lib.MXQ_OK
+
+
+def test_dequant_rejects_bad_scale_count_and_dtype(lib):
+    from mx_qlinear import _lib
+
+    d = ctypes.c_void_p(256)
+    rc = lib.mxq_int8_gemm_dequant(d, d, d, d, 3, None, d, 16, 16, 16, 16, _lib.DTYPE_BF16, None)
+    assert rc == _lib.MXQ_ERR_INVALID
+    rc = lib.mxq_int8_gemm_dequant(d, d, d, d, 16, None, d, 16, 16, 16, 16, 7, None)
+    assert rc == _lib.MXQ_ERR_UNSUPPORTED
+
+
+def test_python_maps_codes_to_the_reference_exceptions(lib):
+    from mx_qlinear import _lib
+
+    with pytest.raises(ValueError):
+        _lib.call("mxq_int8_gemm_i32", None, None, None, -1, 4, 16, 4, None)
+    with pytest.raises(RuntimeError):
+        d = ctypes.c_void_p(16)
+        _lib.call("mxq_int8_gemm_i32", d, d, d, 16, 16, 24, 16, None)
