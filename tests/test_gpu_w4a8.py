@@ -94,8 +94,10 @@ def test_grouped_power_of_two_scales_are_exact(dev):
     assert np.array_equal(y.cpu().numpy().astype(np.float64), exact)
 
 
-@pytest.mark.parametrize("m,n,k,g", [(512, 1024, 5120, 128), (2048, 640, 1024, 128), (100, 200, 1024, 256),
-                                     (33, 70, 512, 128)])
+# group 128 with N % 8 == 0 runs the pipelined kernel (edge tiles in M and N included); group 256
+# and N = 70 run the general kernel.
+@pytest.mark.parametrize("m,n,k,g", [(512, 1024, 5120, 128), (2048, 640, 1024, 128), (100, 200, 1024, 128),
+                                     (257, 136, 640, 128), (100, 200, 1024, 256), (33, 70, 512, 128)])
 def test_grouped_matches_oracle(dev, m, n, k, g):
     print(f"w4a8 grouped m={m} n={n} k={k} g={g}", flush=True)
     x = activations(m, k, 1000 + m, outlier_frac=0.0)
@@ -112,10 +114,11 @@ def test_grouped_matches_oracle(dev, m, n, k, g):
     assert np.all(np.abs(yv - exact) <= bound)
 
 
-def test_grouped_with_bias(dev):
-    m, n, k, g = 64, 256, 512, 128
+@pytest.mark.parametrize("m,n", [(64, 256), (130, 200)])
+def test_grouped_with_bias(dev, m, n):
+    k, g = 512, 128
     x = activations(m, k, 70)
-    qd = packed_int4(n, k, 71)
+    qd = packed_int4(n, k, 71 + m)
     gs = group_scales(k, n, g, 72)
     bias = bf16_vec(n, 73, 0.01)
     y = _mx().w4a8_grouped_linear(x.to(dev), qd.to(dev), gs.to(dev), g, bias=bias.to(dev))

@@ -102,9 +102,6 @@ MXQ_DEVICE void make_loader(Loader& L, const GemmArgs& p, int64_t m0, int64_t n0
   }
 }
 
-typedef const void __attribute__((address_space(1)))* gptr_t;
-typedef void __attribute__((address_space(3)))* lptr_t;
-
 MXQ_DEVICE void issue_stage(const Loader& L, char* stage, int64_t k0, int64_t K) {
   const int w = threadIdx.x >> 6;
 #pragma unroll
@@ -116,39 +113,6 @@ MXQ_DEVICE void issue_stage(const Loader& L, char* stage, int64_t k0, int64_t K)
     __builtin_amdgcn_global_load_lds((gptr_t)sa, (lptr_t)(stage + (w * 8 + t) * 1024), 16, 0, 0);
     __builtin_amdgcn_global_load_lds((gptr_t)sb, (lptr_t)(stage + kStageA + (w * 8 + t) * 1024), 16, 0, 0);
   }
-}
-
-// s_waitcnt with vmcnt <= n (lgkmcnt and expcnt left alone); n is a compile-time constant.
-template <int n> MXQ_DEVICE void wait_vmcnt() {
-  __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-// s_waitcnt vmcnt(0) lgkmcnt(0).
-MXQ_DEVICE void wait_all() { __builtin_amdgcn_s_waitcnt(0x0070); }
-
-// s_waitcnt lgkmcnt(8): all but the eight most recent LDS reads have completed.
-MXQ_DEVICE void wait_lgkm8() { __builtin_amdgcn_s_waitcnt(0xC87F); }
-
-// Workgroup barrier without the implicit drain of __syncthreads(): loads in flight stay in
-// flight. The empty asm statements keep the compiler from moving memory accesses across it
-// (the barrier intrinsic itself is not a memory operation to the optimiser); the hardware
-// ordering comes from the s_waitcnt that precedes each call.
-MXQ_DEVICE void barrier_no_drain() {
-  __asm__ volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  __asm__ volatile("" ::: "memory");
-}
-
-// ds_read_b128 issued as inline assembly, so that the compiler's wait-count pass does not see it:
-// with direct-to-LDS loads in flight that pass only ever waits for LDS reads with lgkmcnt(0),
-// which would serialise every fragment read with the MFMAs it should overlap. The main loop
-// therefore places its LDS waits itself (wait_lgkm8 / wait_all); a fragment is never used
-// before one of them has covered it.
-template <int kOff>
-MXQ_DEVICE v4i lds_read_b128(uint32_t addr) {
-  v4i r;
-  __asm__ volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(kOff));
-  return r;
 }
 
 // Fragments of K-step ks (32 K-bytes) of a stage: A rows wm*128 + i*32 + l%32 and B rows
@@ -296,6 +260,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
   v4i f0a[4], f0b[4], f1a[4], f1b[4];
   load_frags(lds_addr, wm, wn, 0, f0a, f0b);
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_sched_barrier(0);
   for (int kt = 0; kt < ktiles; ++kt) {
     char* cur = lds + (kt & 1) * kStageBytes;
     const uint32_t cur_a = lds_addr + (uint32_t)((kt & 1) * kStageBytes);
@@ -320,18 +285,22 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
     __builtin_amdgcn_sched_barrier(0);
     // Stage kt+1 landed and this wave's reads of buffer kt % 2 (K-step 3 included) are done.
     wait_all();
+    __builtin_amdgcn_sched_barrier(0);
     if (kt + 1 < ktiles) {
       barrier_no_drain();
       if (kt + 2 < ktiles) issue_stage(ld, cur, (int64_t)(kt + 2) * kBK, p.K);
     }
-    // Unconditional (after the last stage it reads a buffer nobody writes, never used).
-    load_frags(nxt_a, wm, wn, 0, f0a, f0b);
+    // The last stage reads nothing more: a read left in flight past the loop could land in
+    // registers the compiler has already given to the epilogue.
+    if (kt + 1 < ktiles) load_frags(nxt_a, wm, wn, 0, f0a, f0b);
     __builtin_amdgcn_sched_barrier(0);
     mma16(f1a, f1b, acc);
     __builtin_amdgcn_sched_barrier(0);
   }
-  // Every wave is done reading the stage buffers before the epilogue reuses them.
+  // Every wave is done reading the stage buffers before the epilogue reuses them, and the
+  // last (unused) fragment reads have landed before their registers are reused.
   wait_all();
+  __builtin_amdgcn_sched_barrier(0);
   barrier_no_drain();
 
   // ---- epilogue ----

@@ -205,6 +205,46 @@ MXQ_DEVICE void atomic_max_nonneg(float* addr, float v) {
   atomicMax(reinterpret_cast<unsigned int*>(addr), __float_as_uint(v));
 }
 
+// ---- direct-to-LDS pipelines -------------------------------------------------------
+
+typedef const void __attribute__((address_space(1)))* gptr_t;
+typedef void __attribute__((address_space(3)))* lptr_t;
+
+// s_waitcnt with vmcnt <= n (lgkmcnt and expcnt left alone); n is a compile-time constant.
+template <int n> MXQ_DEVICE void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// s_waitcnt vmcnt(0) lgkmcnt(0).
+MXQ_DEVICE void wait_all() { __builtin_amdgcn_s_waitcnt(0x0070); }
+
+// s_waitcnt lgkmcnt(n): all but the n most recent LDS reads have completed (n <= 15).
+template <int n> MXQ_DEVICE void wait_lgkm() { __builtin_amdgcn_s_waitcnt(0xC07F | (n << 8)); }
+MXQ_DEVICE void wait_lgkm8() { wait_lgkm<8>(); }
+
+// Workgroup barrier without the implicit drain of __syncthreads(): loads in flight stay in
+// flight. The empty asm statements keep the compiler from moving memory accesses across it
+// (the barrier intrinsic itself is not a memory operation to the optimiser); the hardware
+// ordering comes from the s_waitcnt that precedes each call.
+MXQ_DEVICE void barrier_no_drain() {
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
+// ds_read_b128 / ds_read_b64 issued as inline assembly, so that the compiler's wait-count pass
+// does not see them: with direct-to-LDS loads in flight that pass only ever waits for LDS reads
+// with lgkmcnt(0), which would serialise every fragment read with the MFMAs it should overlap.
+// A kernel using them places its LDS waits itself (wait_lgkm / wait_all) and follows each such
+// wait with __builtin_amdgcn_sched_barrier(0): the compiler sees no dependence between the wait
+// and the registers it covers, so without the barrier it may schedule their first use above it.
+template <int kOff>
+MXQ_DEVICE v4i lds_read_b128(uint32_t addr) {
+  v4i r;
+  __asm__ volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(kOff));
+  return r;
+}
+
 }  // namespace mxq
 
 // ---- host-side error plumbing (defined in capi.hip) -------------------------------

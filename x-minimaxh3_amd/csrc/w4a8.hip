@@ -24,7 +24,7 @@
 //    exactly, and the final multiply uses xs / 16, so the result is bit-identical to the
 //    unscaled recipe while the unpack costs 6 ALU ops per 8 weights.
 
-#include "mxq_common.h"
+#include "w4a8_common.h"
 
 namespace mxq {
 
@@ -113,29 +113,7 @@ static int check_decode_args(const int8_t* qdata, const void* s_rel, int s_rel_d
 // (2) group-scaled int4 GEMM
 // ---------------------------------------------------------------------------------------
 
-constexpr int kW4BK = 128;
-
-struct W4Args {
-  const int8_t* a;
-  const float* xs;
-  const uint8_t* w;       // [N, K/2]
-  const uint16_t* gs;     // [K/G, N] fp16
-  const void* bias;
-  void* d;
-  int64_t M, N, K, ldd;
-  int group_tiles;        // K-stages per group (G / 128)
-  int tiles_m, tiles_n;
-};
-
 MXQ_DEVICE int w4_swz(int r, int c) { return r * kW4BK + ((c ^ (r & 7) ^ ((r >> 3) & 1)) << 4); }
-
-// 4 packed bytes (8 codes, even k low nibble) -> 8 int8 holding 16 (c - 8), natural k order.
-MXQ_DEVICE void unpack8(uint32_t w, uint32_t& o0, uint32_t& o1) {
-  const uint32_t x = w ^ 0x88888888u;
-  const uint32_t xs = x << 4;
-  o0 = __builtin_amdgcn_perm(x, xs, 0x05010400u) & 0xF0F0F0F0u;
-  o1 = __builtin_amdgcn_perm(x, xs, 0x07030602u) & 0xF0F0F0F0u;
-}
 
 template <int BM, int BN, int WM, int WN, int kOut>
 __global__ __launch_bounds__(256, 1) void w4a8_grouped_kernel(W4Args p) {
@@ -373,7 +351,14 @@ extern "C" int mxq_w4a8_gemm_grouped(const int8_t* a, const float* xs, const int
   p.a = a; p.xs = xs; p.w = (const uint8_t*)qdata; p.gs = group_scale; p.bias = bias; p.d = d;
   p.M = M; p.N = N; p.K = K; p.ldd = ldd; p.group_tiles = (int)(group_size / kW4BK);
   hipStream_t st = (hipStream_t)stream;
-  // Large M: 256 x 128 tiles (waves 128 x 64). Skinny M: 128 x 64 tiles for more workgroups.
+  // Group 128 (one group per K stage) with 16-byte aligned scale rows: the pipelined kernel on
+  // 128 x 128 tiles. (128 x 256 tiles need more than the 512 registers a lane has: the two
+  // accumulator sets alone fill the 256 AGPRs and the fp32 accumulators half the VGPRs.)
+  if (group_size == 128 && N % 8 == 0 && (uintptr_t)group_scale % 16 == 0) {
+    const int rc = launch_w4_g128(p, out_dtype, st);
+    if (rc != MXQ_ERR_UNSUPPORTED) return rc;  // else: operands too large for 32-bit offsets
+  }
+  // Other group sizes: 256 x 128 tiles (waves 128 x 64) for large M, 128 x 64 otherwise.
   if (M >= 2048) return launch_w4<256, 128, 128, 64>(p, out_dtype, st);
   return launch_w4<128, 64, 64, 32>(p, out_dtype, st);
 }

@@ -1,0 +1,282 @@
+// Group-128 W4A8 GEMM with a direct-to-LDS pipeline (gfx950).
+//
+// y[m, n] = out(facc[m, n] * xs[m]), facc = fma(fp32(P_g), s[g, n], facc) over the 128-wide
+// K-groups g in order, P_g = sum over the group of a[m, k] * (c[n, k] - 8) exactly in int32
+// (the contract of the general kernel in w4a8.hip; this file is its fast path for group 128).
+//
+// This translation unit is compiled with the MFMA accumulators in VGPRs
+// (-mllvm --amdgpu-mfma-vgpr-form, set by the build): the per-group fold reads every
+// accumulator with VALU instructions, which cannot address AGPRs, so AGPR accumulators would
+// cost one extra copy per element and group.
+//
+// Workgroup: 4 wave64s side by side along N; a 128 x 128 tile, wave w owning channels
+// w*32 + [0, 32) of all 128 rows as four v_mfma_i32_32x32x32_i8 blocks (activations first:
+// lane l holds channel l % 32, so a lane needs one group scale per group).
+//  * One K stage = one group. Each stage's A (128 rows x 128 B), packed B (128 rows x 64 B) and
+//    the group's 128 fp16 scales are fetched with direct-to-LDS loads into a ring of kNS stages
+//    (scales into a ring of 8 slots), kNS - 1 stages ahead.
+//  * Lane half h = l / 32 consumes k in [64 h, 64 h + 64) of the stage; K-step s the 16 k from
+//    64 h + 16 s on both operands (the int32 sum over a group is order-free).
+//  * At the start of group g each block's int32 accumulators still hold group g-1's sum; the
+//    block is folded into its fp32 accumulators just before its first MFMA of group g, so the
+//    fold of one block issues while the previous block's MFMA executes (a wave issues in order:
+//    MFMAs issued back to back would leave the VALU work serialised behind them). The next
+//    K-step's A fragment reads and nibble unpack are interleaved with the MFMAs the same way.
+// LDS rows: A 128 B with chunk c at slot c ^ ((r >> 1) & 7); B 64 B with chunk c at slot
+// c ^ ((r >> 2) & 3) -- conflict-free for sixteen consecutive rows read at one chunk.
+
+#include "w4a8_common.h"
+
+namespace mxq {
+
+namespace {
+
+constexpr int kBM = 128, kBN = 128, kNS = 4;
+constexpr int kStageA = kBM * 128;  // 16 KB
+constexpr int kStageB = kBN * 64;   // 8 KB packed
+constexpr int kStage = kStageA + kStageB;
+constexpr int kScaleRing = 8;       // > kNS + 1: a slot is refilled only after its fold
+constexpr int kScaleBytes = kBN * 2;
+constexpr int kLds = kNS * kStage + kScaleRing * kScaleBytes;
+constexpr int kALoads = kStageA / 1024 / 4;   // 4 direct-to-LDS loads per wave per stage
+constexpr int kBLoads = kStageB / 1024 / 4;   // 2
+constexpr int kLoads = kALoads + kBLoads + 1;  // + the wave's share of the scales
+constexpr int kScaleLanes = kScaleBytes / 4 / 16;  // lanes per wave fetching scales
+static_assert(kScaleRing >= kNS + 2, "scale slot refilled before it is folded");
+
+struct Tile {
+  int64_t m0, n0;
+};
+
+MXQ_DEVICE Tile tile_of(const W4Args& p) {
+  const int num = p.tiles_m * p.tiles_n, per = num / 8, bid = blockIdx.x;
+  const int t = bid < per * 8 ? (bid % 8) * per + bid / 8 : bid;  // XCD-contiguous ranges
+  const int group = 8 * p.tiles_n, g = t / group, first = g * 8;
+  const int gm = min(p.tiles_m - first, 8), in = t % group;
+  return Tile{(int64_t)(first + in % gm) * kBM, (int64_t)(in / gm) * kBN};
+}
+
+template <int kOut>
+__global__ __launch_bounds__(256, 1) void w4a8_g128_kernel(W4Args p) {
+  __shared__ __attribute__((aligned(16))) char lds[kLds];
+  char* const scale_ring = lds + kNS * kStage;
+
+  const Tile tile = tile_of(p);
+  const int64_t m0 = tile.m0, n0 = tile.n0;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int lr = lane & 31, lh = lane >> 5;
+  const int64_t khalf = p.K / 2;
+  const int ktiles = (int)(p.K / 128);
+
+  // ---- direct-to-LDS sources: 32-bit byte offsets of this lane from a wave-uniform base that
+  // advances with K (the launcher guarantees M*K and N*K/2 fit in 31 bits).
+  uint32_t a_off[kALoads], b_off[kBLoads];
+#pragma unroll
+  for (int t = 0; t < kALoads; ++t) {
+    const int r = (wave * kALoads + t) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    a_off[t] = (uint32_t)(min(m0 + r, p.M - 1) * p.K + c * 16);
+  }
+#pragma unroll
+  for (int t = 0; t < kBLoads; ++t) {
+    const int r = (wave * kBLoads + t) * 16 + (lane >> 2);
+    const int c = (lane & 3) ^ ((r >> 2) & 3);
+    b_off[t] = (uint32_t)(min(n0 + r, p.N - 1) * khalf + c * 16);
+  }
+  // wave w fetches scale bytes [64 w, 64 w + 64) of the group's row of 128 (8 per lane).
+  const int64_t s_col = n0 + wave * (kBN / 4) + lane * 8;
+  const uint32_t s_off = (uint32_t)((s_col < p.N ? s_col : 0) * 2);
+
+  auto issue_stage = [&](int kt) {
+    char* st = lds + (kt % kNS) * kStage;
+    const int64_t k0 = (int64_t)kt * 128;
+    const char* abase = reinterpret_cast<const char*>(p.a) + k0;
+    const char* bbase = reinterpret_cast<const char*>(p.w) + k0 / 2;
+    const char* sbase = reinterpret_cast<const char*>(p.gs + (int64_t)kt * p.N);
+#pragma unroll
+    for (int t = 0; t < kALoads; ++t)
+      __builtin_amdgcn_global_load_lds((gptr_t)(abase + a_off[t]), (lptr_t)(st + (wave * kALoads + t) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int t = 0; t < kBLoads; ++t)
+      __builtin_amdgcn_global_load_lds((gptr_t)(bbase + b_off[t]),
+                                       (lptr_t)(st + kStageA + (wave * kBLoads + t) * 1024), 16, 0, 0);
+    char* sd = scale_ring + (kt & (kScaleRing - 1)) * kScaleBytes + wave * (kScaleBytes / 4);
+    if (lane < kScaleLanes) __builtin_amdgcn_global_load_lds((gptr_t)(sbase + s_off), (lptr_t)sd, 16, 0, 0);
+  };
+
+  v16i acc[4];
+  float facc[4][16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc[i] = v16i{};
+#pragma unroll
+    for (int r = 0; r < 16; ++r) facc[i][r] = 0.0f;
+  }
+
+  const uint32_t lds_addr = (uint32_t)(uintptr_t)(lptr_t)lds;
+  const uint32_t a_row = (uint32_t)lr * 128;  // block i adds i * 32 rows
+  const int a_f = (lr >> 1) & 7;
+  const uint32_t b_row = (uint32_t)kStageA + (uint32_t)(wave * 32 + lr) * 64;
+  const int b_f = (lr >> 2) & 3;
+  const uint32_t b_lo = (uint32_t)(((2 * lh) ^ b_f) << 4), b_hi = (uint32_t)(((2 * lh + 1) ^ b_f) << 4);
+  const int s_idx = wave * 32 + lr;  // this lane's channel within the tile
+
+#pragma unroll
+  for (int s = 0; s < kNS - 1; ++s)
+    if (s < ktiles) issue_stage(s);
+  if (ktiles >= kNS - 1)
+    wait_vmcnt<(kNS - 2) * kLoads>();
+  else
+    wait_vmcnt<0>();
+  barrier_no_drain();
+
+  auto unpack_step = [&](const v4i (&bq)[2], int s) {
+    uint32_t o0, o1, o2, o3;
+    unpack8((uint32_t)bq[s >> 1][(s & 1) * 2], o0, o1);
+    unpack8((uint32_t)bq[s >> 1][(s & 1) * 2 + 1], o2, o3);
+    return v4i{(int)o0, (int)o1, (int)o2, (int)o3};
+  };
+
+  // One stage = group kt. At K-step 0, block i's accumulators still hold group kt-1's sum: they
+  // are folded (16 x cvt + fma) right before block i's first MFMA of group kt, so each fold
+  // issues while the previous block's MFMA executes. The A fragment of block i for K-step s+1
+  // is read right after block i's MFMA of step s; the next step's nibble unpack follows the
+  // second MFMA of each step.
+  auto stage = [&](int kt) {
+    const uint32_t st = lds_addr + (uint32_t)((kt % kNS) * kStage);
+    v4i bq[2];
+    bq[0] = lds_read_b128<0>(st + b_row + b_lo);
+    bq[1] = lds_read_b128<0>(st + b_row + b_hi);
+    v4i fa[4];
+    {
+      const uint32_t x = (uint32_t)(((lh * 4) ^ a_f) << 4);
+      fa[0] = lds_read_b128<0>(st + a_row + x);
+      fa[1] = lds_read_b128<32 * 128>(st + a_row + x);
+      fa[2] = lds_read_b128<64 * 128>(st + a_row + x);
+      fa[3] = lds_read_b128<96 * 128>(st + a_row + x);
+    }
+    // Scale of group kt-1; zero before the first group (an exact no-op fold of zeros).
+    const uint16_t* srow =
+        reinterpret_cast<const uint16_t*>(scale_ring + ((kt - 1) & (kScaleRing - 1)) * kScaleBytes);
+    const float sc = kt > 0 ? f16_to_f32(srow[s_idx]) : 0.0f;
+    if (kt + kNS - 1 < ktiles) issue_stage(kt + kNS - 1);
+    wait_lgkm<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    v4i fb = unpack_step(bq, 0);
+    static_for<4>([&](auto S) {
+      constexpr int s = decltype(S)::value;
+      const uint32_t xn = (uint32_t)(((lh * 4 + s + 1) ^ a_f) << 4);  // chunk of K-step s+1
+      v4i fb_next;
+      static_for<4>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        if constexpr (s == 0) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) facc[i][r] = fmaf((float)acc[i][r], sc, facc[i][r]);
+        } else {
+          // block i's fragment of this step was read after its previous MFMA; the reads of the
+          // later blocks may still be in flight
+          wait_lgkm<3 - i>();
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb, s == 0 ? v16i{} : acc[i], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (s < 3) fa[i] = lds_read_b128<i * 32 * 128>(st + a_row + xn);
+        if constexpr (i == 1 && s < 3) fb_next = unpack_step(bq, s + 1);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      if constexpr (s < 3) fb = fb_next;
+    });
+    // Stage kt+1 has landed (later stages may stay in flight); buffer kt % kNS is free.
+    if (kt + kNS - 1 < ktiles)
+      wait_vmcnt<(kNS - 2) * kLoads>();
+    else if (kt + kNS - 2 < ktiles)
+      wait_vmcnt<(kNS - 3) * kLoads>();
+    else
+      wait_vmcnt<0>();
+    wait_lgkm<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    barrier_no_drain();
+  };
+
+  for (int kt = 0; kt < ktiles; ++kt) stage(kt);
+  {
+    const int g = ktiles - 1;
+    const uint16_t* srow = reinterpret_cast<const uint16_t*>(scale_ring + (g & (kScaleRing - 1)) * kScaleBytes);
+    const float sc = f16_to_f32(srow[s_idx]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) facc[i][r] = fmaf((float)acc[i][r], sc, facc[i][r]);
+  }
+
+  // ---- epilogue: y = out(facc * (xs / 16)); y = out(y + bias). The main loop's last barrier
+  // left the LDS free: the tile's 128 row scales go there first (every global read of the
+  // epilogue is done before its first store, so no store can delay a later load), then the
+  // output tile, which is written back as 16-byte row chunks.
+  typedef typename OutT<kOut>::T OT;
+  constexpr int kE = sizeof(OT);
+  constexpr int kPitch = kBN * kE + 16;  // padded row: the two half-waves' rows hit different banks
+  static_assert(128 * 4 + kBM * kPitch <= kLds, "epilogue staging exceeds the LDS allocation");
+  float* s_xs = reinterpret_cast<float*>(lds);
+  char* s_out = lds + 128 * 4;
+  const OT* bias = reinterpret_cast<const OT*>(p.bias);
+  const int64_t col = n0 + s_idx;
+  const float bv = bias ? OutT<kOut>::load(bias + min(col, p.N - 1)) : -0.0f;
+  if (threadIdx.x < kBM) s_xs[threadIdx.x] = p.xs[min(m0 + threadIdx.x, p.M - 1)] * 0.0625f;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
+      const float y = OutT<kOut>::round(facc[i][r] * s_xs[row]);
+      const float yb = y + bv;
+      if constexpr (kE == 4) {
+        *reinterpret_cast<float*>(s_out + row * kPitch + s_idx * 4) = yb;
+      } else {
+        const uint16_t h = kOut == 1 ? (uint16_t)f32_to_f16_bits(yb) : (uint16_t)f32_to_bf16_bits(yb);
+        *reinterpret_cast<uint16_t*>(s_out + row * kPitch + s_idx * 2) = h;
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int kChunksRow = kBN * kE / 16;
+  constexpr int kPerElem = 16 / kE;
+  char* D = reinterpret_cast<char*>(p.d);
+  const bool vec = ((uintptr_t)p.d % 16 == 0) && ((p.ldd * kE) % 16 == 0);
+#pragma unroll
+  for (int q = 0; q < kBM * kChunksRow / 256; ++q) {
+    const int id = q * 256 + threadIdx.x;
+    const int row = id / kChunksRow, ch = id % kChunksRow;
+    const int64_t grow = m0 + row, gcol = n0 + ch * kPerElem;
+    if (grow >= p.M) continue;
+    const v4u v = *reinterpret_cast<const v4u*>(s_out + row * kPitch + ch * 16);
+    char* dst = D + (grow * p.ldd + gcol) * kE;
+    if (vec && gcol + kPerElem <= p.N) {
+      *reinterpret_cast<v4u*>(dst) = v;
+    } else {
+      const char* src = reinterpret_cast<const char*>(&v);
+      for (int e = 0; e < kPerElem && gcol + e < p.N; ++e)
+        for (int b = 0; b < kE; ++b) dst[e * kE + b] = src[e * kE + b];
+    }
+  }
+}
+
+}  // namespace
+
+int launch_w4_g128(W4Args p, int out_dtype, hipStream_t st) {
+  if (p.M * p.K >= (int64_t)1 << 31 || p.N * (p.K / 2) >= (int64_t)1 << 31 || p.N * (p.K / 128) * 2 >= (int64_t)1 << 31)
+    return MXQ_ERR_UNSUPPORTED;  // the caller falls back to the general kernel
+  p.tiles_m = (int)((p.M + kBM - 1) / kBM);
+  p.tiles_n = (int)((p.N + kBN - 1) / kBN);
+  const unsigned grid = (unsigned)(p.tiles_m * p.tiles_n);
+  switch (out_dtype) {
+    case MXQ_DTYPE_F32: w4a8_g128_kernel<0><<<grid, 256, 0, st>>>(p); break;
+    case MXQ_DTYPE_F16: w4a8_g128_kernel<1><<<grid, 256, 0, st>>>(p); break;
+    case MXQ_DTYPE_BF16: w4a8_g128_kernel<2><<<grid, 256, 0, st>>>(p); break;
+    default: return mxq_set_error(MXQ_ERR_UNSUPPORTED, "output dtype code %d", out_dtype);
+  }
+  return mxq_check_launch("w4a8_g128_kernel");
+}
+
+}  // namespace mxq

@@ -48,9 +48,16 @@ def _hipcc() -> str:
     return found
 
 
+# Per-source flags. w4a8_g128.hip keeps MFMA accumulators in VGPRs: its per-group fold reads
+# every accumulator with VALU instructions, which cannot address AGPRs.
+FILE_FLAGS = {
+    # "w4a8_g128.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: pathlib.Path, extra: list[str]) -> pathlib.Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [_hipcc(), *COMMON_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *COMMON_FLAGS, *FILE_FLAGS.get(src.name, []), *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")
