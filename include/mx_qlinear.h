@@ -39,6 +39,7 @@ extern "C" {
 /* Pre-quantization activation codes: CK/backends/_activations.py:19-24. */
 #define MXQ_ACT_NONE 0
 #define MXQ_ACT_GELU_TANH 1
+#define MXQ_ACT_SWIGLU 2
 
 /* Thread-local description of the last failure in this thread ("" if none). */
 const char* mxq_last_error(void);
@@ -130,6 +131,30 @@ int mxq_int8_gemm_dequant_gelu_absmax(const int8_t* a, const int8_t* b, const fl
  * Replaces: apply_input_act(x, "gelu_tanh"), CK/backends/_activations.py:40-53.
  */
 int mxq_gelu_tanh_bf16(const void* x, void* y, int64_t n, void* stream);
+
+/*
+ * ConvRot rotation + per-row INT8 quantization, optionally after an activation:
+ *   a = act(x)  (MXQ_ACT_NONE; MXQ_ACT_GELU_TANH; MXQ_ACT_SWIGLU: x is [rows, 2*cols] = [gate | up]
+ *               and a = bf16(bf16(silu(gate)) * up), CK/backends/_activations.py:40-53)
+ *   r = a @ H_G per group of group_size columns, H_G = kron(h4, ..., h4) / sqrt(G), rounded once
+ *       to x's dtype (the exact product; CK/tensor/int8_utils.py:11-74), skipped if group_size == 0
+ *   q, scales = the row quantizer of r (CK/backends/eager/quantization.py:857-875).
+ *   x_dtype: bf16 (any activation) or fp32 (no activation); cols % 16 == 0; group_size a power
+ *   of 4 up to 1024 dividing cols (or 0).
+ * Replaces: launch_quantize_int8_rowwise_convrot{,64} (CK/backends/cuda/ops/int8_linear.cu:
+ * 1086-1157, 1295-1409) and the eager rotation before quantize_int8_rowwise
+ * (CK/backends/eager/quantization.py:1012-1025).
+ */
+int mxq_quantize_int8_rowwise_convrot(const void* x, int x_dtype, int8_t* q, float* scales,
+                                      int64_t rows, int64_t cols, int64_t group_size,
+                                      int input_act, void* stream);
+
+/*
+ * y[r, c] = bf16(bf16(silu(x[r, c])) * x[r, cols + c]) for a [rows, 2*cols] bf16 x (SwiGLU:
+ * gate | up halves), bit-identical to torch's CPU silu(gate).mul_(up) on bfloat16.
+ * Replaces: apply_input_act(x, "swiglu"), CK/backends/_activations.py:50-52.
+ */
+int mxq_swiglu_bf16(const void* x, void* y, int64_t rows, int64_t cols, void* stream);
 
 /* p[0..n) = value on the stream (a kernel, so it is safe inside captured graphs). */
 int mxq_fill_f32(float* p, float value, int64_t n, void* stream);

@@ -1,0 +1,198 @@
+"""CPU tests that pin the ConvRot and SwiGLU parts of the oracle (no GPU).
+
+The rotation is pinned by exact arithmetic (Hadamard orthogonality, the radix-4 transform
+against the explicit matrix product on inputs where float64 is exact, exact rational rounding
+at constructed midpoints) and against the routine the reference calls (torch's CPU bf16 matmul,
+which agrees except where its own float32 accumulation crosses a bfloat16 rounding boundary).
+SiLU / SwiGLU are pinned by the golden table of torch's CPU silu and the mathematical function.
+"""
+
+import math
+import pathlib
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from _util import activations, bits, from_bits, gen
+from oracle import convrot as cr
+from oracle import eager_np
+from oracle.bf16 import bf16_bits, bf16_to_f32, bf16_ulp
+
+GOLDEN = pathlib.Path(__file__).parent / "golden"
+CSRC = pathlib.Path(__file__).parents[1] / "x-minimaxh3_amd" / "csrc"
+
+
+# ---- Hadamard ------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("g", [4, 16, 64, 256, 1024])
+def test_hadamard_is_the_regular_kron_construction_and_orthogonal(g):
+    h4 = torch.tensor([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=torch.float64)
+    h = h4
+    while h.shape[0] < g:
+        h = torch.kron(h, h4)
+    assert np.array_equal(cr.hadamard(g), (h / math.sqrt(g)).numpy())
+    hh = cr.hadamard(g)
+    assert np.array_equal(hh @ hh.T, np.eye(g))
+    assert np.array_equal(hh, hh.T)
+
+
+@pytest.mark.parametrize("g", [2, 8, 32, 128, 0, 6])
+def test_hadamard_rejects_sizes_that_are_not_powers_of_four(g):
+    with pytest.raises(ValueError):
+        cr.hadamard(g)
+
+
+@pytest.mark.parametrize("g", [4, 16, 64, 256, 1024])
+def test_fht_equals_the_matrix_product_where_float64_is_exact(g):
+    rng = np.random.default_rng(g)
+    x = rng.integers(-5000, 5000, size=(6, 3 * g)).astype(np.float64) * 2.0 ** -7
+    ref = (x.reshape(6, 3, g) @ cr.hadamard(g)).reshape(6, 3 * g)
+    assert np.array_equal(cr.fht_f64(x, g), ref)
+
+
+def test_fht_planted_sign_mistake_is_caught():
+    """A transform with column k of h4 negated in row k (not 3-k) must fail the product check."""
+    g = 16
+    x = np.arange(2 * g, dtype=np.float64).reshape(2, g) - 7.0
+
+    def wrong(x):
+        y = x.reshape(-1, 1, g)
+        for t in range(2):
+            v = y.reshape(y.shape[0], 1, g // 4 ** (t + 1), 4, 4 ** t)
+            s = (v[:, :, :, 0] + v[:, :, :, 1]) + (v[:, :, :, 2] + v[:, :, :, 3])
+            out = np.stack([s - 2 * v[:, :, :, k] for k in range(4)], axis=3)
+            y = out.reshape(y.shape)
+        return y.reshape(x.shape) / 4
+
+    ref = x @ cr.hadamard(g)
+    assert np.array_equal(cr.fht_f64(x, g), ref)
+    assert not np.array_equal(wrong(x), ref)
+
+
+def test_rotation_is_an_involution():
+    """H symmetric and orthogonal: rotating twice gives the input back (exact in float64)."""
+    x = np.random.default_rng(1).integers(-999, 999, size=(4, 512)).astype(np.float64)
+    assert np.array_equal(cr.fht_f64(cr.fht_f64(x, 256), 256), x)
+
+
+# ---- rounding ------------------------------------------------------------------------------
+
+def _exact_bf16_bits(v: float) -> int:
+    """Round-to-nearest-even of a float64 to bfloat16 in rational arithmetic (normal range)."""
+    sign = 0x8000 if v < 0 else 0
+    a = Fraction(abs(v))
+    e = math.floor(math.log2(abs(v)))
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    q = a / Fraction(2) ** (e - 7)
+    n = math.floor(q)
+    r = q - n
+    if r > Fraction(1, 2) or (r == Fraction(1, 2) and n % 2):
+        n += 1
+    val = float(n * Fraction(2) ** (e - 7))
+    return sign | int(np.array([val], np.float32).view(np.uint32)[0] >> 16)
+
+
+def test_f64_to_bf16_rounding_is_exact_at_midpoints():
+    rng = np.random.default_rng(3)
+    vals = []
+    for b in rng.integers(0x3000, 0x5000, size=1500):
+        base = float(bf16_to_f32(np.array([b], np.uint16))[0])
+        ulp = 2.0 ** (math.floor(math.log2(base)) - 7)
+        for off in (0.5, 0.5 + 2 ** -30, 0.5 - 2 ** -30, 0.5 + 2 ** -45, 0.25, 0.75, 0.0):
+            vals += [base + off * ulp, -(base + off * ulp)]
+    vals = np.array(vals)
+    got = cr.round_f64_to_bf16(vals)
+    exp = np.array([_exact_bf16_bits(v) for v in vals], dtype=np.uint16)
+    assert np.array_equal(got, exp)
+    # the plain float32 detour double-rounds some of them
+    assert not np.array_equal(bf16_bits(vals.astype(np.float32)), exp)
+
+
+# ---- against the reference's routine ---------------------------------------------------------
+
+def test_rotation_agrees_with_torch_cpu_bf16_matmul():
+    """The reference rotates with torch.matmul in bfloat16 (CK/tensor/int8_utils.py:58-74).
+    Its float32 accumulation rounds; the exact product differs from it only where that error
+    crosses a bfloat16 rounding boundary, which is rare and never more than one ulp."""
+    x = activations(256, 5120, 11)
+    h = torch.from_numpy(cr.hadamard(256)).to(torch.bfloat16)
+    yt = bits(torch.matmul(x.reshape(256, 20, 256), h).reshape(256, 5120))
+    yo = cr.round_f64_to_bf16(cr.fht_f64(bf16_to_f32(bits(x)).astype(np.float64), 256))
+    assert (yo == yt).mean() > 0.9999
+    a, b = bf16_to_f32(yo).astype(np.float64), bf16_to_f32(yt).astype(np.float64)
+    assert np.all(np.abs(a - b) <= bf16_ulp(np.abs(a).astype(np.float32)))
+
+
+def test_rotation_equals_torch_where_accumulation_is_exact():
+    """Inputs with a narrow exponent range make torch's float32 sums exact: then equality."""
+    g = gen(5)
+    x = (torch.randint(-127, 128, (64, 1024), generator=g).float() / 64).to(torch.bfloat16)
+    h = torch.from_numpy(cr.hadamard(256)).to(torch.bfloat16)
+    yt = bits(torch.matmul(x.reshape(64, 4, 256), h).reshape(64, 1024))
+    yo = cr.round_f64_to_bf16(cr.fht_f64(bf16_to_f32(bits(x)).astype(np.float64), 256))
+    assert np.array_equal(yo, yt)
+
+
+# ---- SiLU / SwiGLU ---------------------------------------------------------------------------
+
+def test_silu_golden_is_torch_and_close_to_the_mathematical_function():
+    """torch evaluates x / (1 + exp(-x)) in float32: within 1 bf16 ulp of the float64 value,
+    except that exp(-x) overflows float32 for x < -88.72 and the result is then -0."""
+    golden = np.load(GOLDEN / "silu_bf16.npy")
+    assert golden.shape == (65536,) and golden.dtype == np.uint16
+    with np.errstate(all="ignore"):
+        x = bf16_to_f32(np.arange(65536, dtype=np.uint32).astype(np.uint16)).astype(np.float64)
+        s = x / (1.0 + np.exp(-x))
+    fin = np.isfinite(x)
+    y = bf16_to_f32(golden).astype(np.float64)
+    ulp = bf16_ulp(np.abs(s).astype(np.float32)).astype(np.float64)
+    overflow = fin & (-x > np.log(np.float64(np.finfo(np.float32).max)))
+    ok = fin & ~overflow & (np.abs(s) > 1e-37)
+    assert np.all(np.abs(y[ok] - s[ok]) <= ulp[ok])
+    assert np.all(golden[overflow] == 0x8000)
+
+
+def test_device_silu_table_matches_golden():
+    """The table compiled into the kernels, plus its closed-form rules, reproduce the fixture."""
+    inc = (CSRC / "silu_bf16_table.inc").read_text()
+    defs = dict(line.split()[1:3] for line in inc.splitlines() if line.startswith("#define"))
+    e_lo, e_pos, e_neg = int(defs["MXQ_SILU_E_LO"]), int(defs["MXQ_SILU_E_POS"]), int(defs["MXQ_SILU_E_NEG"])
+    nan = int(defs["MXQ_SILU_NAN"].rstrip("u"), 16)
+    body = inc[inc.index("{") + 1:inc.rindex("}")]
+    table = np.array([int(v, 16) for v in body.replace("\n", "").split(",") if v.strip()], np.uint32)
+    golden = np.load(GOLDEN / "silu_bf16.npy").astype(np.uint32)
+    b = np.arange(65536, dtype=np.uint32)
+    e = (b >> 7) & 0xFF
+    sign, mag = b & 0x8000, b & 0x7FFF
+    v = mag & 0xFF
+    half = sign | np.where(e >= 2, mag - 0x80, (v >> 1) + ((v & 1) & ((v >> 1) & 1)))
+    ei = np.clip(e.astype(np.int64) - e_lo, 0, e_neg - e_lo - 1)
+    looked = table[((b >> 15) * (e_neg - e_lo) + ei) * 128 + (b & 0x7F)]
+    special = np.where(b == 0x7F80, 0x7F80, nan)
+    dev = np.where(e < e_lo, half,
+                   np.where(e == 255, special,
+                            np.where((sign == 0) & (e >= e_pos), b,
+                                     np.where((sign != 0) & (e >= e_neg), 0x8000, looked))))
+    assert np.array_equal(dev, golden)
+
+
+def test_swiglu_oracle_matches_torch():
+    x = activations(32, 2 * 768, 21, outlier_frac=0.0) * 3
+    gate, up = x.chunk(2, dim=-1)
+    ref = torch.nn.functional.silu(gate).mul_(up)
+    assert np.array_equal(cr.swiglu_bf16(bits(x)), bits(ref))
+
+
+def test_convrot_quantize_composes_rotation_and_quantizer():
+    x = activations(8, 512, 31)
+    q, s, rot = cr.convrot_quantize_bf16(bits(x), 256)
+    q2, s2 = eager_np.quantize_int8_rowwise(rot)
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
+    # group size 0: no rotation
+    q3, s3, rot3 = cr.convrot_quantize_bf16(bits(x), 0)
+    assert np.array_equal(rot3, bits(x))

@@ -1,0 +1,291 @@
+// ConvRot: regular-Hadamard rotation of each group of G columns, fused with the pre-quantization
+// activation and the per-token INT8 quantizer (gfx950).
+//
+// Reference: activations x_rot = x_grouped @ H_G, H_G = kron(h4, ..., h4) / sqrt(G) with
+// h4 = [[1,1,1,-1],[1,1,-1,1],[1,-1,1,1],[-1,1,1,1]] (backends/turbo/vendor/comfy_kitchen/
+// tensor/int8_utils.py:11-74), applied in int8_linear before the row quantizer
+// (CK/backends/eager/quantization.py:1012-1025, 857-875); the activation first
+// (CK/backends/_activations.py:40-53). The reference multiplies with torch's CPU matmul, whose
+// accumulation order is internal to the library; here the rotated value is the exact product
+// rounded once to the input dtype.
+//
+// Transform: with y = x H, y_j = sum_i x_i prod_t h4[i_t][j_t] over the base-4 digits t of the
+// in-group index, so the rotation is one 4-point transform per digit; column k of h4 is all ones
+// but -1 in row 3-k, so a quad (x0..x3) becomes y_k = S - 2 x_{3-k}, S = (x0 + x1) + (x2 + x3).
+// It runs in float64: every operation is exact while a group's exponent spread is at most 37
+// bits, which makes the result the exact product; the fixed operation order (digit 0 first,
+// pairwise S, the same association in every lane) makes it reproducible in all other cases.
+//
+// Layout: one wave per row. Pass p covers columns [1024 p, 1024 p + 1024): lane l holds 16
+// consecutive columns, so digits 0 and 1 of the in-group index are inside the lane and digit
+// d >= 2 is lane bit pair d-2: those quads are combined with xor shuffles (masks m, 2m, 3m,
+// m = 4^(d-2)). Groups never straddle lanes (G % 16 == 0, or G = 4 with four groups per lane).
+// The rotated row is kept in LDS (each lane reads back only what it wrote, so no barrier), its
+// absmax reduced across the wave, then quantized and stored with 16-byte stores.
+
+#include "mxq_common.h"
+
+namespace mxq {
+
+// ---- SiLU on bfloat16 ---------------------------------------------------------------------
+// Bit-exact torch CPU silu on a bfloat16 input (the gate activation of the reference's SwiGLU,
+// CK/backends/_activations.py:50-52); rules and table from gen_silu_table.py, which checks them
+// against all 65,536 torch outputs.
+#define MXQ_SILU_TABLE_DECL constexpr uint16_t kSiluTableC[3840]
+#include "silu_bf16_table.inc"
+#undef MXQ_SILU_TABLE_DECL
+
+constexpr uint32_t silu_rule_c(uint32_t b) {
+  const uint32_t e = (b >> 7) & 0xFFu, sign = b & 0x8000u, mag = b & 0x7FFFu;
+  if (e < MXQ_SILU_E_LO) {
+    const uint32_t v = mag & 0xFFu;
+    return sign | (e >= 2 ? mag - 0x80u : (v >> 1) + ((v & 1u) & ((v >> 1) & 1u)));
+  }
+  if (e == 255u) return b == 0x7F80u ? 0x7F80u : MXQ_SILU_NAN;
+  if (!sign && e >= MXQ_SILU_E_POS) return b;
+  if (sign && e >= MXQ_SILU_E_NEG) return 0x8000u;
+  return kSiluTableC[((b >> 15) * (MXQ_SILU_E_NEG - MXQ_SILU_E_LO) + (e - MXQ_SILU_E_LO)) * 128u + (b & 0x7Fu)];
+}
+struct SiluFullTable {
+  uint16_t v[65536];
+};
+constexpr SiluFullTable make_silu_full() {
+  SiluFullTable t{};
+  for (uint32_t b = 0; b < 65536u; ++b) t.v[b] = (uint16_t)silu_rule_c(b);
+  return t;
+}
+static __device__ __attribute__((aligned(16))) const SiluFullTable kSiluFull = make_silu_full();
+
+MXQ_DEVICE uint32_t silu_bf16(uint32_t b) { return kSiluFull.v[b & 0xFFFFu]; }
+
+// SwiGLU of one bf16 pair: bf16(bf16(silu(gate)) * up) -- the product of two bf16 is exact in
+// fp32, so this is torch's bf16 mul_ (one rounding); a NaN product becomes 0x7FC0, the pattern
+// torch's float -> bfloat16 conversion gives every NaN.
+MXQ_DEVICE uint32_t swiglu_bf16(uint32_t gate, uint32_t up) {
+  const float p = bf16_to_f32(silu_bf16(gate)) * bf16_to_f32(up);
+  return p != p ? 0x7FC0u : f32_to_bf16_bits(p);
+}
+
+// float64 -> bfloat16 bits with one round-to-nearest-even rounding: through float32 (RNE),
+// exact except where that float32 is itself a bfloat16 midpoint and x is not; then x lies
+// strictly on one side of the midpoint and the result is the neighbour on that side.
+MXQ_DEVICE uint32_t f64_to_bf16_bits(double x) {
+  const float f = (float)x;
+  const uint32_t u = __float_as_uint(f);
+  uint32_t b = f32_to_bf16_bits(f);
+  if ((u & 0xFFFFu) == 0x8000u && (double)f != x) b = (u >> 16) + (fabs(x) > fabs((double)f) ? 1u : 0u);
+  return b;
+}
+
+namespace {
+
+constexpr int kRows = 4;  // rows (waves) per 256-thread block
+
+struct CrArgs {
+  const void* x;
+  int8_t* q;
+  float* scales;
+  int64_t rows;
+  int K;       // columns of the quantized row (the raw row has 2K for SwiGLU)
+  int digits;  // log4(G); 0: no rotation
+};
+
+// One radix-4 step on four values (the quad of one digit).
+MXQ_DEVICE void h4_quad(double& x0, double& x1, double& x2, double& x3) {
+  const double s = (x0 + x1) + (x2 + x3);
+  const double y0 = s - (x3 + x3), y1 = s - (x2 + x2), y2 = s - (x1 + x1), y3 = s - (x0 + x0);
+  x0 = y0;
+  x1 = y1;
+  x2 = y2;
+  x3 = y3;
+}
+
+template <int kAct, int kDtype>
+__global__ __launch_bounds__(256) void convrot_quant_kernel(CrArgs p) {
+  constexpr int kE = kDtype == MXQ_DTYPE_F32 ? 4 : 2;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  char* rowbuf = smem + (int64_t)wave * p.K * kE;
+  const int passes = (p.K + 1023) / 1024;
+  const double inv = 1.0 / (double)(1 << p.digits);  // 1/sqrt(G), exact
+
+  for (int64_t row = (int64_t)blockIdx.x * kRows + wave; row < p.rows; row += (int64_t)gridDim.x * kRows) {
+    float amax = 0.0f;
+    for (int ps = 0; ps < passes; ++ps) {
+      const int e0 = ps * 1024 + lane * 16;
+      const bool on = e0 < p.K;
+      double v[16];
+      // ---- load (+ activation)
+      if (kDtype == MXQ_DTYPE_F32) {
+        const v4f* src = reinterpret_cast<const v4f*>(reinterpret_cast<const float*>(p.x) + row * p.K + e0);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const v4f f = on ? src[c] : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[c * 4 + e] = (double)f[e];
+        }
+      } else {
+        const uint16_t* xr = reinterpret_cast<const uint16_t*>(p.x) + row * (kAct == MXQ_ACT_SWIGLU ? 2 * (int64_t)p.K : p.K);
+        v4u w[2], up[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          w[c] = on ? reinterpret_cast<const v4u*>(xr + e0)[c] : v4u{0, 0, 0, 0};
+          if (kAct == MXQ_ACT_SWIGLU) up[c] = on ? reinterpret_cast<const v4u*>(xr + p.K + e0)[c] : v4u{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const uint32_t word = w[i >> 3][(i >> 1) & 3];
+          uint32_t b = (i & 1) ? (word >> 16) : (word & 0xFFFFu);
+          if (kAct == MXQ_ACT_GELU_TANH) b = gelu_bf16(b);
+          if (kAct == MXQ_ACT_SWIGLU) {
+            const uint32_t uw = up[i >> 3][(i >> 1) & 3];
+            b = swiglu_bf16(b, (i & 1) ? (uw >> 16) : (uw & 0xFFFFu));
+          }
+          v[i] = (double)bf16_to_f32(b);
+        }
+      }
+      // ---- transform
+      if (p.digits >= 1) {
+#pragma unroll
+        for (int j = 0; j < 16; j += 4) h4_quad(v[j], v[j + 1], v[j + 2], v[j + 3]);
+      }
+      if (p.digits >= 2) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) h4_quad(v[j], v[j + 4], v[j + 8], v[j + 12]);
+      }
+      for (int d = 2; d < p.digits; ++d) {
+        const int m = 1 << (2 * (d - 2));
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const double t = v[j] + __shfl_xor(v[j], m, kWave);
+          const double s = t + __shfl_xor(t, 2 * m, kWave);
+          const double q3 = __shfl_xor(v[j], 3 * m, kWave);
+          v[j] = s - (q3 + q3);
+        }
+      }
+      // ---- scale, round to the row dtype, keep, absmax
+      if (on) {
+        if (kDtype == MXQ_DTYPE_F32) {
+          float r[16];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            r[i] = (float)(v[i] * inv);
+            amax = fmaxf(amax, fabsf(r[i]));
+          }
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            reinterpret_cast<v4f*>(rowbuf + (int64_t)e0 * 4)[c] = v4f{r[c * 4], r[c * 4 + 1], r[c * 4 + 2], r[c * 4 + 3]};
+        } else {
+          uint32_t h[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const uint32_t lo = f64_to_bf16_bits(v[2 * i] * inv), hi = f64_to_bf16_bits(v[2 * i + 1] * inv);
+            h[i] = lo | (hi << 16);
+            amax = fmaxf(amax, fmaxf(fabsf(bf16_to_f32(lo)), fabsf(bf16_to_f32(hi))));
+          }
+#pragma unroll
+          for (int c = 0; c < 2; ++c)
+            reinterpret_cast<v4u*>(rowbuf + (int64_t)e0 * 2)[c] = v4u{h[c * 4], h[c * 4 + 1], h[c * 4 + 2], h[c * 4 + 3]};
+        }
+      }
+    }
+    amax = wave_max(amax);
+    const float s = row_scale_from_absmax(amax);
+    const float r = 1.0f / round_bf16(s);
+    for (int ps = 0; ps < passes; ++ps) {
+      const int e0 = ps * 1024 + lane * 16;
+      if (e0 >= p.K) continue;
+      int qv[16];
+      if (kDtype == MXQ_DTYPE_F32) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const v4f f = reinterpret_cast<const v4f*>(rowbuf + (int64_t)e0 * 4)[c];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) qv[c * 4 + e] = quant_round_clamp(f[e] / s);
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const v4u w = reinterpret_cast<const v4u*>(rowbuf + (int64_t)e0 * 2)[c];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            qv[c * 8 + 2 * i] = quant_round_clamp(round_bf16(bf16_to_f32(w[i] & 0xFFFFu) * r));
+            qv[c * 8 + 2 * i + 1] = quant_round_clamp(round_bf16(bf16_to_f32(w[i] >> 16) * r));
+          }
+        }
+      }
+      uint32_t o[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        o[c] = (uint32_t)(qv[4 * c] & 0xFF) | ((uint32_t)(qv[4 * c + 1] & 0xFF) << 8) |
+               ((uint32_t)(qv[4 * c + 2] & 0xFF) << 16) | ((uint32_t)(qv[4 * c + 3] & 0xFF) << 24);
+      *reinterpret_cast<v4u*>(p.q + row * p.K + e0) = v4u{o[0], o[1], o[2], o[3]};
+    }
+    if (lane == 0) p.scales[row] = s;
+  }
+}
+
+__global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+                                                      int64_t rows, int64_t cols) {
+  const int64_t n = rows * cols;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / cols, c = i - r * cols;
+    y[i] = (uint16_t)swiglu_bf16(x[r * 2 * cols + c], x[r * 2 * cols + cols + c]);
+  }
+}
+
+}  // namespace
+}  // namespace mxq
+
+using namespace mxq;
+
+extern "C" int mxq_quantize_int8_rowwise_convrot(const void* x, int x_dtype, int8_t* q, float* scales,
+                                                 int64_t rows, int64_t cols, int64_t group_size,
+                                                 int input_act, void* stream) {
+  if (rows < 0 || cols < 0) return mxq_set_error(MXQ_ERR_INVALID, "negative shape");
+  int digits = 0;
+  if (group_size != 0) {
+    if (group_size < 4 || (group_size & (group_size - 1)) || __builtin_ctzll((uint64_t)group_size) % 2)
+      return mxq_set_error(MXQ_ERR_INVALID, "Regular Hadamard size must be a power of 4, got %lld", (long long)group_size);
+    digits = __builtin_ctzll((uint64_t)group_size) / 2;
+    if (cols % group_size)
+      return mxq_set_error(MXQ_ERR_INVALID, "ConvRot group size %lld does not divide input features %lld",
+                           (long long)group_size, (long long)cols);
+    if (group_size > 1024) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "ConvRot group size above 1024");
+  }
+  if (input_act < MXQ_ACT_NONE || input_act > MXQ_ACT_SWIGLU)
+    return mxq_set_error(MXQ_ERR_INVALID, "unsupported input_act code %d", input_act);
+  if (x_dtype != MXQ_DTYPE_BF16 && !(x_dtype == MXQ_DTYPE_F32 && input_act == MXQ_ACT_NONE))
+    return mxq_set_error(MXQ_ERR_UNSUPPORTED, "rotation quantizer takes bfloat16 (or float32 without an activation)");
+  if (rows == 0 || cols == 0) return MXQ_OK;
+  if (!x || !q || !scales) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  if (cols % 16) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "columns must be a multiple of 16");
+  if ((uintptr_t)x % 16 || (uintptr_t)q % 16) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "x and q must be 16-byte aligned");
+  const int e = x_dtype == MXQ_DTYPE_F32 ? 4 : 2;
+  const int64_t lds = (int64_t)kRows * cols * e;
+  if (lds > 160 * 1024) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "row of %lld columns too wide", (long long)cols);
+  CrArgs a{x, q, scales, rows, (int)cols, digits};
+  const int64_t blocks = std::min<int64_t>((rows + kRows - 1) / kRows, 65536);
+  hipStream_t st = (hipStream_t)stream;
+  const unsigned grid = (unsigned)blocks;
+  if (x_dtype == MXQ_DTYPE_F32) {
+    convrot_quant_kernel<MXQ_ACT_NONE, MXQ_DTYPE_F32><<<grid, 256, (size_t)lds, st>>>(a);
+  } else {
+    switch (input_act) {
+      case MXQ_ACT_NONE: convrot_quant_kernel<MXQ_ACT_NONE, MXQ_DTYPE_BF16><<<grid, 256, (size_t)lds, st>>>(a); break;
+      case MXQ_ACT_GELU_TANH: convrot_quant_kernel<MXQ_ACT_GELU_TANH, MXQ_DTYPE_BF16><<<grid, 256, (size_t)lds, st>>>(a); break;
+      default: convrot_quant_kernel<MXQ_ACT_SWIGLU, MXQ_DTYPE_BF16><<<grid, 256, (size_t)lds, st>>>(a); break;
+    }
+  }
+  return mxq_check_launch("convrot_quant_kernel");
+}
+
+extern "C" int mxq_swiglu_bf16(const void* x, void* y, int64_t rows, int64_t cols, void* stream) {
+  if (rows < 0 || cols < 0) return mxq_set_error(MXQ_ERR_INVALID, "negative shape");
+  if (rows == 0 || cols == 0) return MXQ_OK;
+  if (!x || !y) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  const int64_t n = rows * cols;
+  const int64_t blocks = std::min<int64_t>((n + 255) / 256, 65536);
+  swiglu_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>((const uint16_t*)x, (uint16_t*)y, rows, cols);
+  return mxq_check_launch("swiglu_kernel");
+}

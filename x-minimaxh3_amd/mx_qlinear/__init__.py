@@ -2,7 +2,8 @@
 
 Per-token INT8 activation quantization (optionally fused with adaLN), INT8 x INT8 -> INT32
 GEMMs on CDNA4 matrix cores with fused dequant / bias / tanh-GELU / re-quant epilogues, and
-W4A8 GEMMs, behind the reference's Comfy-Kitchen function names and its quantized-linear
+W4A8 GEMMs, with the ConvRot (regular Hadamard) rotation and the GELU / SwiGLU input
+activations folded into the quantizer, behind the reference's Comfy-Kitchen function names and its quantized-linear
 module contract. All compute runs in hand-written HIP kernels (libmx_qlinear.so, C ABI in
 include/mx_qlinear.h); there is no CPU path.
 """
@@ -18,6 +19,7 @@ from .ops import (  # noqa: F401
     int8_linear_prequantized,
     mm_int8,
     quantize_int8_rowwise,
+    quantize_int8_rowwise_convrot,
     w4a8_grouped_linear,
     w4a8_int8_linear,
 )

@@ -19,7 +19,7 @@ MXQ_ERR_UNSUPPORTED = -2
 MXQ_ERR_HIP = -3
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_E4M3 = 0, 1, 2, 5
-ACT_NONE, ACT_GELU_TANH = 0, 1
+ACT_NONE, ACT_GELU_TANH, ACT_SWIGLU = 0, 1, 2
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -36,6 +36,8 @@ SIGNATURES: dict[str, list] = {
     "mxq_int8_gemm_dequant": [_P, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I, _P],
     "mxq_int8_gemm_dequant_gelu_absmax": [_P, _P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "mxq_fill_f32": [_P, _F, _I64, _P],
+    "mxq_quantize_int8_rowwise_convrot": [_P, _I, _P, _P, _I64, _I64, _I64, _I, _P],
+    "mxq_swiglu_bf16": [_P, _P, _I64, _I64, _P],
     "mxq_gelu_tanh_bf16": [_P, _P, _I64, _P],
     "mxq_dequant_int4_grouped_to_int8": [_P, _P, _I, _P, _P, _I64, _I64, _I64, _P],
     "mxq_w4a8_codebook_gemm": [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P],

@@ -203,9 +203,11 @@ class ConvRotInt8Linear(nn.Module):
         _gpu_only(value)
         if value.shape[1] != self.in_features:
             raise ValueError("input width does not match quantized weight")
+        contiguous = value if value.is_contiguous() else value.contiguous()
         if self.spec.convrot:
-            raise NotImplementedError("ConvRot rotation is not provided by this build of mx_qlinear")
-        qdata, scale = ops.quantize_int8_rowwise(value.contiguous())
+            qdata, scale = ops.quantize_int8_rowwise_convrot(contiguous, self.spec.convrot_groupsize)
+        else:
+            qdata, scale = ops.quantize_int8_rowwise(contiguous)
         return PreparedConvRotInt8Input(qdata=qdata, scale=scale, rows=int(value.shape[0]),
                                         width=int(value.shape[1]), dtype=value.dtype)
 

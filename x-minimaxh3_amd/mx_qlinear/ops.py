@@ -17,7 +17,8 @@ from . import _lib
 from ._lib import call
 
 _OUT_CODES = {torch.float32: _lib.DTYPE_F32, torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16}
-_ACT_CODES = {None: _lib.ACT_NONE, "none": _lib.ACT_NONE, "gelu_tanh": _lib.ACT_GELU_TANH}
+_ACT_CODES = {None: _lib.ACT_NONE, "none": _lib.ACT_NONE, "gelu_tanh": _lib.ACT_GELU_TANH,
+              "swiglu": _lib.ACT_SWIGLU}
 
 
 def _p(t: torch.Tensor | None):
@@ -47,8 +48,18 @@ def _act_code(input_act: str | None) -> int:
         return _ACT_CODES[input_act]
     except KeyError:
         raise ValueError(
-            f"unsupported input_act: {input_act!r} (expected one of ['gelu_tanh', 'none'])"
+            f"unsupported input_act: {input_act!r} (expected one of ['gelu_tanh', 'none', 'swiglu'])"
         ) from None
+
+
+def _act_width(input_act: str | None) -> int:
+    """Raw input columns per activated column (CK/backends/_activations.py:34-36)."""
+    return 2 if input_act == "swiglu" else 1
+
+
+def _check_power_of_four(g: int) -> None:
+    if g < 4 or g & (g - 1) or (g.bit_length() - 1) % 2:
+        raise ValueError(f"Regular Hadamard size must be a power of 4, got {g}")
 
 
 def _out_code(dtype: torch.dtype) -> int:
@@ -67,14 +78,20 @@ def quantize_int8_rowwise(x: torch.Tensor, stochastic_rounding: int | None = 0,
     """Per-row INT8 quantization: ``(q int8 [..., K], scale fp32 [..., 1])``.
 
     CK/__init__.py:702-709 / CK/backends/eager/quantization.py:857-875. Stochastic rounding
-    is not provided (the reference default, 0, is). ``input_act='gelu_tanh'`` applies the
-    activation to a bf16 input first (CK/backends/_activations.py:40-53).
+    is not provided (the reference default, 0, is). ``input_act`` ('gelu_tanh' or 'swiglu',
+    bf16 inputs; CK/backends/_activations.py:40-53) is applied first; with 'swiglu' the
+    input is ``[..., 2K]`` and the result ``[..., K]``.
     """
     if stochastic_rounding:
         raise NotImplementedError("stochastic rounding is not provided by mx_qlinear")
+    act = _act_code(input_act)
+    if act == _lib.ACT_SWIGLU:
+        return quantize_int8_rowwise_convrot(x, 0, input_act)
     dev = _require_gpu(x)
     if x.dtype not in (torch.bfloat16, torch.float16, torch.float32):
         raise ValueError(f"unsupported input dtype {x.dtype}")
+    if act and x.dtype != torch.bfloat16:
+        raise NotImplementedError(f"input_act={input_act!r} is provided for bfloat16 inputs")
     k = x.shape[-1]
     if k == 0:
         raise ValueError("quantize_int8_rowwise needs a non-empty last dimension")
@@ -83,23 +100,71 @@ def quantize_int8_rowwise(x: torch.Tensor, stochastic_rounding: int | None = 0,
     q = torch.empty((m, k), dtype=torch.int8, device=dev)
     s = torch.empty((m, 1), dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
-        call("mxq_quantize_int8_rowwise", _p(x2), _OUT_CODES[x.dtype], _p(q), _p(s), m, k,
-             _act_code(input_act), _stream(dev))
+        call("mxq_quantize_int8_rowwise", _p(x2), _OUT_CODES[x.dtype], _p(q), _p(s), m, k, act, _stream(dev))
     return q.reshape(x.shape), s.reshape(*x.shape[:-1], 1)
+
+
+def quantize_int8_rowwise_convrot(x: torch.Tensor, group_size: int = 256,
+                                  input_act: str | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """ConvRot rotation + per-row INT8 quantization in one pass: ``(q, scale [..., 1])``.
+
+    The reference's fused rotate-and-quantize (quantize_int8_rowwise_convrot64 of its CUDA
+    backend, CK/backends/cuda/ops/int8_linear.cu:942-1030; eager
+    CK/backends/eager/quantization.py:876-895 and 1012-1025): optional activation
+    (CK/backends/_activations.py:40-53), then x @ H_G per group of ``group_size`` columns
+    (CK/tensor/int8_utils.py:11-74, the exact product rounded once to x's dtype), then the row
+    quantizer. ``group_size=0`` skips the rotation. bf16 inputs (any activation) or fp32
+    inputs (no activation).
+    """
+    act = _act_code(input_act)
+    dev = _require_gpu(x)
+    if group_size:
+        _check_power_of_four(group_size)
+    if x.dtype not in (torch.bfloat16, torch.float32) or (act and x.dtype != torch.bfloat16):
+        raise NotImplementedError("the rotation quantizer takes bfloat16 inputs (or float32 without an activation)")
+    width = x.shape[-1]
+    if width % _act_width(input_act):
+        raise ValueError(f"{input_act} needs an even last dimension, got {width}")
+    k = width // _act_width(input_act)
+    if k == 0:
+        raise ValueError("quantize_int8_rowwise needs a non-empty last dimension")
+    if group_size and k % group_size:
+        raise ValueError(f"ConvRot group size {group_size} does not divide input features {k}")
+    if k % 16:
+        raise NotImplementedError(f"the rotation quantizer needs a multiple of 16 columns, got {k}")
+    x2 = x.reshape(-1, width).contiguous()
+    m = x2.shape[0]
+    q = torch.empty((m, k), dtype=torch.int8, device=dev)
+    s = torch.empty((m, 1), dtype=torch.float32, device=dev)
+    if m:
+        with torch.cuda.device(dev):
+            call("mxq_quantize_int8_rowwise_convrot", _p(x2), _OUT_CODES[x.dtype], _p(q), _p(s), m, k,
+                 group_size, act, _stream(dev))
+    return q.reshape(*x.shape[:-1], k), s.reshape(*x.shape[:-1], 1)
 
 
 def apply_input_act(x: torch.Tensor, input_act: str | None) -> torch.Tensor:
     """The pre-quantization activation (CK/backends/_activations.py:40-53) for bf16 inputs.
 
-    ``gelu_tanh`` is bit-identical to torch's CPU ``gelu(approximate='tanh')`` on bfloat16.
+    ``gelu_tanh`` is bit-identical to torch's CPU ``gelu(approximate='tanh')`` on bfloat16;
+    ``swiglu`` maps ``[..., 2K]`` to ``[..., K]`` as torch's ``silu(gate).mul_(up)``.
     """
     code = _act_code(input_act)
     if code == _lib.ACT_NONE:
         return x
     dev = _require_gpu(x)
     if x.dtype != torch.bfloat16:
-        raise NotImplementedError("gelu_tanh is provided for bfloat16 tensors")
+        raise NotImplementedError(f"{input_act} is provided for bfloat16 tensors")
     xc = x.contiguous()
+    if code == _lib.ACT_SWIGLU:
+        if x.shape[-1] % 2:
+            raise ValueError(f"swiglu needs an even last dimension, got {x.shape[-1]}")
+        k = x.shape[-1] // 2
+        rows = xc.numel() // max(x.shape[-1], 1)
+        y = torch.empty((*x.shape[:-1], k), dtype=x.dtype, device=dev)
+        with torch.cuda.device(dev):
+            call("mxq_swiglu_bf16", _p(xc), _p(y), rows, k, _stream(dev))
+        return y
     y = torch.empty_like(xc)
     with torch.cuda.device(dev):
         call("mxq_gelu_tanh_bf16", _p(xc), _p(y), xc.numel(), _stream(dev))
@@ -260,28 +325,36 @@ def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tenso
                 input_act: str | None = None) -> torch.Tensor:
     """Dynamically quantized INT8 linear (CK/__init__.py:722-764, eager quantization.py:971-1056).
 
-    x [..., K] (bf16 / fp16 / fp32); weight int8 [N, K]; weight_scale scalar or [N] (any
-    shape with that many elements); bias [N] or None. Returns [..., N] of ``out_dtype``
-    (default bf16). ``input_act='gelu_tanh'`` is folded into the quantizer.
+    x [..., K] (bf16 / fp16 / fp32; [..., 2K] with ``input_act='swiglu'``); weight int8 [N, K];
+    weight_scale scalar or [N] (any shape with that many elements); bias [N] or None. Returns
+    [..., N] of ``out_dtype`` (default bf16). The activation and the ConvRot rotation are folded
+    into the quantizer.
     """
     if out_dtype is None:
         out_dtype = torch.bfloat16
     act = _act_code(input_act)
-    if x.shape[-1] != weight.shape[-1]:
+    width = x.shape[-1] // _act_width(input_act)
+    if width != weight.shape[-1] or x.shape[-1] % _act_width(input_act):
         raise ValueError(
-            f"Input and weight inner dimensions must match, got {x.shape[-1]} and {weight.shape[-1]}"
+            f"Input and weight inner dimensions must match, got {width} and {weight.shape[-1]}"
         )
     if convrot:
-        raise NotImplementedError("ConvRot rotation is not provided by this build of mx_qlinear")
+        _check_power_of_four(convrot_groupsize)
+        if width % convrot_groupsize:
+            raise ValueError(f"ConvRot group size {convrot_groupsize} does not divide input features {width}")
     dev = _require_gpu(x, weight)
     n = weight.shape[0]
     _weight_scale(weight_scale, n, dev)  # validate before launching anything
     if act and x.dtype != torch.bfloat16:
-        raise NotImplementedError("input_act='gelu_tanh' needs a bfloat16 input")
+        raise NotImplementedError(f"input_act={input_act!r} needs a bfloat16 input")
     lead = x.shape[:-1]
     if x.numel() == 0:
         return torch.empty((*lead, n), dtype=out_dtype, device=dev)
-    q, s = quantize_int8_rowwise(x.reshape(-1, x.shape[-1]), input_act=input_act)
+    x2 = x.reshape(-1, x.shape[-1])
+    if convrot:
+        q, s = quantize_int8_rowwise_convrot(x2, convrot_groupsize, input_act)
+    else:
+        q, s = quantize_int8_rowwise(x2, input_act=input_act)
     out = int8_linear_prequantized(q, s, weight, weight_scale, bias, out_dtype)
     return out.reshape(*lead, n)
 
@@ -386,16 +459,17 @@ def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, 
                      codebook: torch.Tensor | None = None, correction: torch.Tensor | None = None,
                      bias: torch.Tensor | None = None, group_size: int = 16,
                      convrot_groupsize: int = 256, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
-    """Reference-format W4A8 linear (CK/tensor/w4a8_int8.py:89-115, eager w4a8_int8.py:457-508).
-
-    The reference always rotates activations with ConvRot before quantizing; that rotation is
-    not part of this build, so only ``convrot_groupsize=0`` (no rotation) is accepted.
+    """Reference-format W4A8 linear (CK/tensor/w4a8_int8.py:89-115, eager w4a8_int8.py:457-508):
+    the int4 codes are decoded to the int8 grid chunk by chunk and multiplied with the ConvRot-
+    rotated, per-token quantized activations (int8_linear with convrot=True).
+    ``convrot_groupsize=0`` skips the rotation (for unrotated weights). The ``correction`` form,
+    which the reference evaluates as a dense floating-point linear on the dequantized weight,
+    is not provided.
     """
-    if convrot_groupsize:
-        raise NotImplementedError("ConvRot rotation is not provided by this build of mx_qlinear; "
-                                  "pass convrot_groupsize=0 for unrotated weights")
     if correction is not None:
         raise NotImplementedError("the W4A8 correction term is not provided by this build")
+    if convrot_groupsize:
+        _check_power_of_four(convrot_groupsize)
     if qdata.dim() != 2 or qdata.dtype != torch.int8:
         raise ValueError("packed weight must be a 2D int8 tensor")
     n, kh = qdata.shape
@@ -417,7 +491,12 @@ def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, 
     dev = _require_gpu(x, qdata)
     code = _out_code(out_dtype)
     lead = x.shape[:-1]
-    xq, xs = quantize_int8_rowwise(x.reshape(-1, k))
+    if convrot_groupsize:
+        if k % convrot_groupsize:
+            raise ValueError(f"ConvRot group size {convrot_groupsize} does not divide input features {k}")
+        xq, xs = quantize_int8_rowwise_convrot(x.reshape(-1, k), convrot_groupsize)
+    else:
+        xq, xs = quantize_int8_rowwise(x.reshape(-1, k))
     m = xq.shape[0]
     out = torch.empty((m, n), dtype=out_dtype, device=dev)
     if m == 0:
