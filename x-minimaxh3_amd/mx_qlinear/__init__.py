@@ -18,10 +18,18 @@ from .ops import (  # noqa: F401
     int8_linear,
     int8_linear_prequantized,
     mm_int8,
+    quantize_int8_convrot_weight,
     quantize_int8_rowwise,
     quantize_int8_rowwise_convrot,
     w4a8_grouped_linear,
     w4a8_int8_linear,
+)
+from .checkpoint import (  # noqa: F401
+    MappingTensorSource,
+    SafeTensorSource,
+    audit_quantized_layer,
+    quant_linear,
+    save_checkpoint,
 )
 from .modules import (  # noqa: F401
     ComfyQuantSpec,

@@ -143,6 +143,16 @@ def quantize_int8_rowwise_convrot(x: torch.Tensor, group_size: int = 256,
     return q.reshape(*x.shape[:-1], k), s.reshape(*x.shape[:-1], 1)
 
 
+def quantize_int8_convrot_weight(weight: torch.Tensor, group_size: int = 256) -> tuple[torch.Tensor, torch.Tensor]:
+    """Offline ConvRot weight preparation (CK/backends/eager/quantization.py:898-906): each row's
+    groups are rotated (W_grouped @ H_G^T; H_G is symmetric, so the activation transform) and the
+    rows quantized: ``(q int8 [N, K], scale fp32 [N, 1])``, the checkpoint's weight and
+    weight_scale."""
+    if weight.dim() != 2:
+        raise ValueError("weight must be 2D [out_features, in_features]")
+    return quantize_int8_rowwise_convrot(weight, group_size)
+
+
 def apply_input_act(x: torch.Tensor, input_act: str | None) -> torch.Tensor:
     """The pre-quantization activation (CK/backends/_activations.py:40-53) for bf16 inputs.
 
