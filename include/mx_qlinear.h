@@ -126,6 +126,24 @@ int mxq_int8_gemm_dequant_gelu_absmax(const int8_t* a, const int8_t* b, const fl
                                       int64_t K, int64_t ldh, void* stream);
 
 /*
+ * INT8 GEMM + dequant epilogue + gated residual update, in place:
+ *   y = the bf16 output of mxq_int8_gemm_dequant (same arguments and roundings)
+ *   residual[m, n] = bf16(residual[m, n] + y[m, n] * gate[gate_rows[m], n])
+ *   residual  bf16 [M, ldr] (read and written); gate bf16 [gate_count, ldg]; gate_rows int32 [M]
+ *   (each row's modulation row; indices outside [0, gate_count) are clamped into it, so a bad
+ *   map gives wrong values, never an out-of-bounds read; callers validate it).
+ * Semantics: int8_linear followed by residual[a:b].addcmul_(y[a:b], gate[row].to(bf16)) per
+ * modulation segment (h3serve/native_engine/model/layers.py:944-960, fused_mlp.py:386-420).
+ * Replaces: _fused_down_gated_residual's GEMM + epilogue kernel
+ * (h3serve/native_engine/model/fused_mlp.py:63-143, 159-219).
+ */
+int mxq_int8_gemm_gated_residual(const int8_t* a, const int8_t* b, const float* xs,
+                                 const float* ws, int64_t ws_numel, const void* bias_bf16,
+                                 void* residual_bf16, int64_t ldr, const void* gate_bf16,
+                                 int64_t ldg, int64_t gate_count, const int32_t* gate_rows,
+                                 int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
  * y[i] = gelu_tanh(x[i]) for n bf16 values, bit-identical to torch's CPU
  * gelu(approximate="tanh") on bfloat16 (x and y may alias).
  * Replaces: apply_input_act(x, "gelu_tanh"), CK/backends/_activations.py:40-53.

@@ -181,6 +181,39 @@ def gelu_tanh_bf16(x_bits: np.ndarray) -> np.ndarray:
 
 
 # ---------------------------------------------------------------------------
+# gated residual after fc2
+# ---------------------------------------------------------------------------
+
+def segment_row_map(length: int, segments) -> np.ndarray:
+    """Modulation row of every token from ordered (start, stop, row) segments
+    (h3serve/native_engine/model/fused_mlp.py:34-55; same partition checks)."""
+    out = np.empty(length, dtype=np.int32)
+    previous = 0
+    for start, stop, row in segments:
+        if start != previous or stop <= start:
+            raise ValueError("modulation segments must be an ordered partition")
+        out[start:stop] = row
+        previous = stop
+    if previous != length:
+        raise ValueError("modulation segments do not cover the packed sequence")
+    return out
+
+
+def gated_residual_bf16(residual_bits: np.ndarray, update_bits: np.ndarray, gate_bits: np.ndarray,
+                        gate_rows: np.ndarray) -> np.ndarray:
+    """``residual[m] = bf16(residual[m] + update[m] * gate[gate_rows[m]])`` on bfloat16 bits.
+
+    h3serve/native_engine/model/layers.py:944-960: ``residual[a:b].addcmul_(update[a:b],
+    gate[row].to(update.dtype))`` per segment. addcmul_ evaluates in float32; the product of
+    two bfloat16 values is exact in float32, so the value is one float32 addition rounded to
+    bfloat16 (the gate is already bfloat16 bits here)."""
+    r = bf16_to_f32(residual_bits)
+    u = bf16_to_f32(update_bits)
+    g = bf16_to_f32(np.asarray(gate_bits, dtype=np.uint16)[np.asarray(gate_rows)])
+    return bf16_bits((r + u * g).astype(F32))
+
+
+# ---------------------------------------------------------------------------
 # a6: adaLN (LayerNorm without affine, then modulation)
 # ---------------------------------------------------------------------------
 

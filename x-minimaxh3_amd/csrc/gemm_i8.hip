@@ -22,6 +22,10 @@
 //   kEpiGelu    bf16 dequant as above, then h = gelu_tanh(y) in bf16 (table in LDS), and the
 //               per-row absmax of h folded into row_absmax[m] with atomics (it feeds the next
 //               layer's quantizer, backends/_activations.py:40-53 + quantization.py:857-875).
+//   kEpiGatedRes bf16 dequant as above, then the gated residual update in place:
+//               res[m, n] = bf16(res[m, n] + y * gate[gate_rows[m], n])  (the reference's
+//               addcmul_ after fc2, h3serve/native_engine/model/layers.py:944-960 and
+//               fused_mlp.py:157-219; y * gate is exact in fp32, so one fp32 add, then RNE).
 
 #include "mxq_common.h"
 
@@ -36,7 +40,7 @@ constexpr int kStageBytes = kStageA + kStageB;
 constexpr int kLoadsPerStage = 16;                      // direct-to-LDS loads per wave per stage
 constexpr int kGroupM = 8;
 
-enum { kEpiI32 = 0, kEpiDequant = 1, kEpiGelu = 2 };
+enum { kEpiI32 = 0, kEpiDequant = 1, kEpiGelu = 2, kEpiGatedRes = 3 };
 
 struct GemmArgs {
   const int8_t* a;
@@ -50,6 +54,11 @@ struct GemmArgs {
   int ws_per_channel;
   int vec_store;  // run stores allowed (d aligned to 4 elements and ldd % 4 == 0)
   int tiles_m, tiles_n;
+  // kEpiGatedRes: bf16 residual [M, ldr] (read and written), bf16 gate [*, ldg], gate_rows [M]
+  uint16_t* res;
+  const uint16_t* gate;
+  const int32_t* gate_rows;
+  int64_t ldr, ldg, gate_count;
 };
 
 // LDS operand layout: a tile row is 128 bytes = eight 16-byte chunks; chunk c of row r sits at
@@ -221,6 +230,46 @@ MXQ_DEVICE void store_block_row(const GemmArgs& p, bool full, int64_t row, int64
   }
 }
 
+// Gated residual update of one 32 x 32 block row (four runs of four columns, bf16 words as
+// produced by epi_run): res = bf16(res + y * gate[grow]). Interior tiles (`full`, with the
+// residual and gate rows 8-byte aligned) use 8-byte accesses.
+MXQ_DEVICE uint32_t gated_pair(uint32_t r, uint32_t y, uint32_t g) {
+  const float lo = bf16_to_f32(r & 0xFFFFu) + bf16_to_f32(y & 0xFFFFu) * bf16_to_f32(g & 0xFFFFu);
+  const float hi = bf16_to_f32(r >> 16) + bf16_to_f32(y >> 16) * bf16_to_f32(g >> 16);
+  return pack_bf16x2(lo, hi);
+}
+
+MXQ_DEVICE void gated_block_row(const GemmArgs& p, bool full, int64_t row, int64_t grow, int64_t col0,
+                                const uint32_t* w) {
+  uint16_t* __restrict__ res = p.res;
+  const uint16_t* __restrict__ gate = p.gate;
+  if (full) {
+    v2u r[4], g[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      r[q] = *reinterpret_cast<const v2u*>(res + row * p.ldr + col0 + q * 8);
+      g[q] = *reinterpret_cast<const v2u*>(gate + grow * p.ldg + col0 + q * 8);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<v2u*>(res + row * p.ldr + col0 + q * 8) =
+          v2u{gated_pair(r[q][0], w[2 * q], g[q][0]), gated_pair(r[q][1], w[2 * q + 1], g[q][1])};
+  } else if (row < p.M) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t col = col0 + q * 8 + e;
+        if (col < p.N) {
+          const uint32_t y = (w[2 * q + (e >> 1)] >> (16 * (e & 1))) & 0xFFFFu;
+          const float v = bf16_to_f32(res[row * p.ldr + col]) + bf16_to_f32(y) * bf16_to_f32(gate[grow * p.ldg + col]);
+          res[row * p.ldr + col] = (uint16_t)f32_to_bf16_bits(v);
+        }
+      }
+    }
+  }
+}
+
 template <int kEpi, int kOut>
 __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(16))) char lds[kNS * kStageBytes + 2 * kBN * 4];
@@ -336,6 +385,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
     barrier_no_drain();
   }
   const bool full = p.vec_store && m0 + kBM <= p.M && n0 + kBN <= p.N;
+  int64_t grow[4] = {0, 0, 0, 0};  // kEpiGatedRes: the gate row of each of this lane's rows
+  if constexpr (kEpi == kEpiGatedRes) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // clamped into the gate so a bad row index cannot fault
+      const int64_t gr = p.gate_rows[min(m0 + wm * kWaveM + i * 32 + lr, p.M - 1)];
+      grow[i] = gr < 0 ? 0 : (gr >= p.gate_count ? p.gate_count - 1 : gr);
+    }
+  }
 
   // GELU: pre-activation bf16 pairs, kept until the table has landed.
   uint32_t yp[kEpi == kEpiGelu ? 4 : 1][4][8];
@@ -364,6 +421,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
       if constexpr (kEpi == kEpiGelu) {
 #pragma unroll
         for (int r = 0; r < 8; ++r) yp[i][j][r] = w[r];
+      } else if constexpr (kEpi == kEpiGatedRes) {
+        gated_block_row(p, full, m0 + wm * kWaveM + i * 32 + lr, grow[i], n0 + cl0, w);
       } else {
         store_block_row<kElem>(p, full, m0 + wm * kWaveM + i * 32 + lr, n0 + cl0, w);
       }
@@ -425,6 +484,8 @@ static int launch_gemm(const GemmArgs& args0, hipStream_t stream) {
   args.tiles_n = (int)((args.N + kBN - 1) / kBN);
   const int elem = (kOut == 0 || kEpi == kEpiI32) ? 4 : 2;
   args.vec_store = ((uintptr_t)args.d % (4 * elem) == 0) && (args.ldd % 4 == 0);
+  if (kEpi == kEpiGatedRes)
+    args.vec_store = args.vec_store && ((uintptr_t)args.gate % 8 == 0) && (args.ldg % 4 == 0);
   const int64_t tiles = (int64_t)args.tiles_m * args.tiles_n;
   if (tiles > INT32_MAX) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "too many tiles");
   gemm_i8_kernel<kEpi, kOut><<<(unsigned)tiles, kGemmThreads, 0, stream>>>(args);
@@ -493,4 +554,24 @@ extern "C" int mxq_int8_gemm_dequant_gelu_absmax(const int8_t* a, const int8_t* 
   g.a = a; g.b = b; g.xs = xs; g.ws = ws; g.bias = bias_bf16; g.d = h_bf16; g.row_absmax = row_absmax;
   g.M = M; g.N = N; g.K = K; g.ldd = ldh; g.ws_per_channel = ws_numel == N && N != 1;
   return launch_gemm<kEpiGelu, 2>(g, (hipStream_t)stream);
+}
+
+extern "C" int mxq_int8_gemm_gated_residual(const int8_t* a, const int8_t* b, const float* xs,
+                                            const float* ws, int64_t ws_numel, const void* bias_bf16,
+                                            void* residual_bf16, int64_t ldr, const void* gate_bf16,
+                                            int64_t ldg, int64_t gate_count, const int32_t* gate_rows,
+                                            int64_t M, int64_t N, int64_t K, void* stream) {
+  int rc = check_gemm_shape(a, b, residual_bf16, M, N, K, ldr);
+  if (rc) return rc;
+  if (M == 0 || N == 0) return MXQ_OK;
+  if (!xs || !ws || !gate_bf16 || !gate_rows) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  if (ws_numel != 1 && ws_numel != N) return mxq_set_error(MXQ_ERR_INVALID, "bad weight scale length");
+  if (ldg < N) return mxq_set_error(MXQ_ERR_INVALID, "gate stride %lld < N %lld", (long long)ldg, (long long)N);
+  if (gate_count < 1) return mxq_set_error(MXQ_ERR_INVALID, "gate has no rows");
+  GemmArgs g{};
+  g.a = a; g.b = b; g.xs = xs; g.ws = ws; g.bias = bias_bf16; g.d = residual_bf16;
+  g.res = (uint16_t*)residual_bf16; g.ldr = ldr; g.gate = (const uint16_t*)gate_bf16; g.ldg = ldg;
+  g.gate_rows = gate_rows; g.gate_count = gate_count;
+  g.M = M; g.N = N; g.K = K; g.ldd = ldr; g.ws_per_channel = ws_numel == N && N != 1;
+  return launch_gemm<kEpiGatedRes, 2>(g, (hipStream_t)stream);
 }

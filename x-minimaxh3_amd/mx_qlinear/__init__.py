@@ -14,13 +14,16 @@ from .ops import (  # noqa: F401
     adaln_quantize_int8,
     apply_input_act,
     dequantize_int4_grouped_to_int8,
+    fused_down_gated_residual,
     int8_ffn_gelu,
     int8_linear,
+    int8_linear_gated_residual_,
     int8_linear_prequantized,
     mm_int8,
     quantize_int8_convrot_weight,
     quantize_int8_rowwise,
     quantize_int8_rowwise_convrot,
+    segment_row_map,
     w4a8_grouped_linear,
     w4a8_int8_linear,
 )

@@ -35,6 +35,8 @@ SIGNATURES: dict[str, list] = {
     "mxq_int8_gemm_i32": [_P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "mxq_int8_gemm_dequant": [_P, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I, _P],
     "mxq_int8_gemm_dequant_gelu_absmax": [_P, _P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "mxq_int8_gemm_gated_residual": [_P, _P, _P, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64,
+                                     _P],
     "mxq_fill_f32": [_P, _F, _I64, _P],
     "mxq_quantize_int8_rowwise_convrot": [_P, _I, _P, _P, _I64, _I64, _I64, _I, _P],
     "mxq_swiglu_bf16": [_P, _P, _I64, _I64, _P],

@@ -435,6 +435,115 @@ def int8_ffn_gelu(x: torch.Tensor, fc1_weight: torch.Tensor, fc1_scale: torch.Te
 
 
 # ---------------------------------------------------------------------------------------
+# fc2 with the gated residual update
+# ---------------------------------------------------------------------------------------
+
+_ROW_MAP_CACHE: dict[tuple, torch.Tensor] = {}
+
+
+def segment_row_map(length: int, segments, device) -> torch.Tensor:
+    """int32 [length] modulation row of every token, from ordered ``(start, stop, row)``
+    segments that partition ``[0, length)``; cached per device and segmentation
+    (h3serve/native_engine/model/fused_mlp.py:34-55, same errors)."""
+    normalized = tuple((int(a), int(b), int(r)) for a, b, r in segments)
+    device = torch.device(device)
+    key = (device.type, device.index, int(length), normalized)
+    cached = _ROW_MAP_CACHE.get(key)
+    if cached is not None:
+        return cached
+    host = torch.empty(length, dtype=torch.int32)
+    previous = 0
+    for start, stop, row in normalized:
+        if start != previous or stop <= start:
+            raise ValueError("modulation segments must be an ordered partition")
+        host[start:stop] = row
+        previous = stop
+    if previous != length:
+        raise ValueError("modulation segments do not cover the packed sequence")
+    cached = host.to(device=device)
+    _ROW_MAP_CACHE[key] = cached
+    return cached
+
+
+def int8_linear_gated_residual_(residual: torch.Tensor, x: torch.Tensor, weight: torch.Tensor,
+                                weight_scale: torch.Tensor, bias: torch.Tensor | None,
+                                gate: torch.Tensor, gate_rows, *, convrot: bool = False,
+                                convrot_groupsize: int = 256, input_act: str | None = None) -> torch.Tensor:
+    """``residual += int8_linear(x, ...) * gate[gate_rows]`` in place; returns ``residual``.
+
+    The composition the reference runs after fc2 (fused_mlp.py:386-420 and
+    layers.py:944-960): ``y = int8_linear(x, weight, weight_scale, bias, convrot=...,
+    input_act=...)`` then ``residual[a:b].addcmul_(y[a:b], gate[row].to(bf16))`` per segment.
+    Here the quantizer is one launch and the GEMM's epilogue applies the update, so ``y`` is
+    never written. ``gate_rows`` is an int32 tensor [rows] or a sequence of segments.
+    Bit-identical to the composition; bfloat16 residual.
+    """
+    if residual.dtype != torch.bfloat16:
+        raise NotImplementedError("the gated residual update takes a bfloat16 residual")
+    dev = _require_gpu(residual, x, weight)
+    n = weight.shape[0]
+    rows = x.numel() // x.shape[-1] if x.shape[-1] else 0
+    res2 = residual.view(-1, n) if residual.numel() else residual.reshape(0, n)
+    if res2.shape[0] != rows or res2.shape[1] != n:
+        raise ValueError(f"residual {tuple(residual.shape)} does not match the update [{rows}, {n}]")
+    if res2.stride(1) != 1:
+        raise ValueError("residual rows must be contiguous")
+    if gate.dim() == 1:
+        gate = gate.reshape(1, -1)
+    if gate.dim() != 2 or gate.shape[1] != n:
+        raise ValueError(f"gate must be [rows, {n}], got {tuple(gate.shape)}")
+    g = gate.to(device=dev, dtype=torch.bfloat16).contiguous()
+    if isinstance(gate_rows, torch.Tensor):
+        gr = gate_rows.to(device=dev, dtype=torch.int32).reshape(-1).contiguous()
+        if gr.numel() != rows:
+            raise ValueError(f"gate_rows has {gr.numel()} entries, expected {rows}")
+        if rows:
+            lo, hi = torch.aminmax(gr)
+            if int(lo) < 0 or int(hi) >= g.shape[0]:
+                raise ValueError("gate_rows index outside the gate")
+    else:
+        gr = segment_row_map(rows, gate_rows, dev)
+        if rows and max(int(r) for _, _, r in gate_rows) >= g.shape[0]:
+            raise ValueError("modulation segment row outside the gate")
+    if rows == 0 or n == 0:
+        return residual
+    ws = _weight_scale(weight_scale, n, dev)
+    b = _bias(bias, n, torch.bfloat16, dev)
+    act = _act_code(input_act)
+    width = x.shape[-1] // _act_width(input_act)
+    if width != weight.shape[-1] or x.shape[-1] % _act_width(input_act):
+        raise ValueError(f"Input and weight inner dimensions must match, got {width} and {weight.shape[-1]}")
+    if act and x.dtype != torch.bfloat16:
+        raise NotImplementedError(f"input_act={input_act!r} needs a bfloat16 input")
+    x2 = x.reshape(-1, x.shape[-1])
+    if convrot:
+        _check_power_of_four(convrot_groupsize)
+        if width % convrot_groupsize:
+            raise ValueError(f"ConvRot group size {convrot_groupsize} does not divide input features {width}")
+        q, xs = quantize_int8_rowwise_convrot(x2, convrot_groupsize, input_act)
+    else:
+        q, xs = quantize_int8_rowwise(x2, input_act=input_act)
+    q2, w2, k = _pad_k(q, weight.contiguous())
+    with torch.cuda.device(dev):
+        call("mxq_int8_gemm_gated_residual", _p(q2), _p(w2), _p(xs), _p(ws), ws.numel(), _p(b), _p(res2),
+             res2.stride(0), _p(g), g.stride(0), g.shape[0], _p(gr), rows, n, k, _stream(dev))
+    return residual
+
+
+def fused_down_gated_residual(hidden: torch.Tensor, residual: torch.Tensor, gate: torch.Tensor,
+                              gate_rows: torch.Tensor, qweight: torch.Tensor, weight_scale: torch.Tensor,
+                              bias: torch.Tensor | None) -> None:
+    """fc2 of the SwiGLU MLP with the gated residual update, in place
+    (h3serve/native_engine/model/fused_mlp.py:159-219): ``hidden`` is fc1's raw output
+    [rows, 2 * inner] = [gate | up]; SwiGLU, the 256-column ConvRot rotation and the row
+    quantizer run in one launch, the GEMM epilogue updates ``residual`` [rows, N]."""
+    if weight_scale.numel() not in (1, qweight.shape[0]):
+        raise ValueError("fc2 scale must be scalar or per output channel")
+    int8_linear_gated_residual_(residual, hidden.reshape(-1, hidden.shape[-1]), qweight, weight_scale, bias,
+                                gate, gate_rows, convrot=True, convrot_groupsize=256, input_act="swiglu")
+
+
+# ---------------------------------------------------------------------------------------
 # W4A8
 # ---------------------------------------------------------------------------------------
 
