@@ -151,6 +151,28 @@ int mxq_int8_gemm_gated_residual(const int8_t* a, const int8_t* b, const float* 
 int mxq_gelu_tanh_bf16(const void* x, void* y, int64_t n, void* stream);
 
 /*
+ * RMS adaLN (RMSNorm with weight, then segmented modulation), optionally fused with the ConvRot
+ * rotation and the per-row INT8 quantizer:
+ *   n = bf16((x * r) * w),  r = 1 / sqrt(fp32(sum x^2) / cols + eps)
+ *   y = bf16(bf16(n * bf16(1 + scale[mod_rows[m]])) + shift[mod_rows[m]])
+ *   q, scales = the row quantizer of y rotated per group of group_size columns (as
+ *   mxq_quantize_int8_rowwise_convrot; group_size 0: no rotation).
+ *   x bf16 [rows, cols]; norm_weight bf16 [cols]; scale, shift bf16 [mod_count, ld_mod];
+ *   mod_rows int32 [rows] (clamped into [0, mod_count)). y_out (bf16 [rows, cols]) and q/scales
+ *   are each optional (NULL), not both. cols % 16 == 0, ld_mod % 8 == 0, 16-byte aligned tensors.
+ * Semantics: rms_adaln, h3serve/native_engine/model/kernels.py:7594-7640 (eager branch) with
+ * RMSNorm = F.rms_norm(x, weight.to(x.dtype), eps) (h3serve/native_engine/model/layers.py:33-48).
+ * Replaces: segmented_rms_adaln / native_rms_one_pass_adaln
+ * (backends/original/kernels/fused_norm_rope.py:319-428) and, with q, the quantizer launch of the
+ * QKV / fc1 ConvRotInt8Linear that consumes the result.
+ */
+int mxq_rms_adaln_quantize_int8(const void* x, const void* norm_weight, const void* scale,
+                                const void* shift, int64_t ld_mod, int64_t mod_count,
+                                const int32_t* mod_rows, float eps, void* y_out, int8_t* q,
+                                float* scales, int64_t rows, int64_t cols, int64_t group_size,
+                                void* stream);
+
+/*
  * ConvRot rotation + per-row INT8 quantization, optionally after an activation:
  *   a = act(x)  (MXQ_ACT_NONE; MXQ_ACT_GELU_TANH; MXQ_ACT_SWIGLU: x is [rows, 2*cols] = [gate | up]
  *               and a = bf16(bf16(silu(gate)) * up), CK/backends/_activations.py:40-53)

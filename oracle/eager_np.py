@@ -246,6 +246,44 @@ def layer_norm_f64(x_bits: np.ndarray, eps: float = 1e-6) -> np.ndarray:
 
 
 # ---------------------------------------------------------------------------
+# RMS adaLN (the H3 block's norm + segmented modulation)
+# ---------------------------------------------------------------------------
+
+def rms_norm_bf16(x_bits: np.ndarray, w_bits: np.ndarray, eps: float) -> np.ndarray:
+    """``F.rms_norm(x, (D,), weight=w, eps)`` on bfloat16 with torch's CPU routine, the
+    function the reference's RMSNorm calls (h3serve/native_engine/model/layers.py:39-48)."""
+    import torch
+
+    xt = torch.from_numpy(np.asarray(x_bits, dtype=np.uint16).view(np.int16)).view(torch.bfloat16)
+    wt = torch.from_numpy(np.asarray(w_bits, dtype=np.uint16).view(np.int16)).view(torch.bfloat16)
+    n = torch.nn.functional.rms_norm(xt, xt.shape[-1:], weight=wt, eps=eps)
+    return n.view(torch.int16).numpy().view(np.uint16).copy()
+
+
+def rms_norm_f64(x_bits: np.ndarray, w_bits: np.ndarray, eps: float) -> np.ndarray:
+    """float64 x / sqrt(mean(x^2) + eps) * w, used to bound torch's result."""
+    x = bf16_to_f32(x_bits).astype(np.float64)
+    r = 1.0 / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps)
+    return x * r * bf16_to_f32(w_bits).astype(np.float64)
+
+
+def modulate_bf16(n_bits: np.ndarray, scale_bits: np.ndarray, shift_bits: np.ndarray,
+                  rows: np.ndarray) -> np.ndarray:
+    """``h[a:b].mul_(1.0 + scale[row].to(bf16)).add_(shift[row].to(bf16))`` per segment
+    (h3serve/native_engine/model/kernels.py:7629-7639): three bfloat16 roundings."""
+    rows = np.asarray(rows)
+    t = round_bf16(F32(1.0) + bf16_to_f32(np.asarray(scale_bits, dtype=np.uint16)[rows]))
+    y = round_bf16(bf16_to_f32(n_bits) * t)
+    return bf16_bits(round_bf16(y + bf16_to_f32(np.asarray(shift_bits, dtype=np.uint16)[rows])))
+
+
+def rms_adaln(x_bits: np.ndarray, w_bits: np.ndarray, eps: float, scale_bits: np.ndarray,
+              shift_bits: np.ndarray, rows: np.ndarray) -> np.ndarray:
+    """rms_adaln (kernels.py:7594-7640, eager branch): RMSNorm then the segmented modulation."""
+    return modulate_bf16(rms_norm_bf16(x_bits, w_bits, eps), scale_bits, shift_bits, rows)
+
+
+# ---------------------------------------------------------------------------
 # a7 / a9: int4 packing and grouped decode to the int8 grid
 # ---------------------------------------------------------------------------
 

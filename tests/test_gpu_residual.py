@@ -118,3 +118,76 @@ def test_gated_residual_rejects_bad_maps(dev):
         _mx().int8_linear_gated_residual_(res, x, w.to(dev), ws.to(dev), None, gate, ((0, 8, 0), (9, 16, 1)))
     with pytest.raises(ValueError):
         _mx().int8_linear_gated_residual_(res[:8], x, w.to(dev), ws.to(dev), None, gate, ((0, 16, 0),))
+
+
+# ---- RMS adaLN (+ ConvRot quantizer) -----------------------------------------------------------
+
+def _rms_inputs(m, d, seed):
+    x = activations(m, d, seed) * 2
+    w = (1 + 0.2 * torch.randn(d, generator=gen(seed + 1))).to(torch.bfloat16)
+    scale = (0.1 * torch.randn(3, d, generator=gen(seed + 2))).to(torch.bfloat16)
+    shift = (0.1 * torch.randn(3, d, generator=gen(seed + 3))).to(torch.bfloat16)
+    return x, w, scale, shift
+
+
+def _check_rms_adaln_bound(y, x, w, scale, shift, rows, eps):
+    """Modulated bf16 within max(1 ulp of y, 1 ulp of the product term) of the oracle: the
+    mean of squares is a reduction whose order differs from torch's CPU kernel, so the
+    normalised value may differ by one bf16 ulp, which the product with bf16(1 + scale) and
+    the shift add can carry into y."""
+    from oracle.bf16 import bf16_bits, bf16_to_f32, bf16_ulp
+
+    ref = eager_np.rms_adaln(bits(x), bits(w), eps, bits(scale), bits(shift), rows)
+    yv, rv = bf16_to_f32(bits(y)), bf16_to_f32(ref)
+    n64 = eager_np.rms_norm_f64(bits(x), bits(w), eps)
+    t = bf16_to_f32(bf16_bits(np.float32(1.0) + bf16_to_f32(bits(scale))[rows]))
+    tol = np.maximum(bf16_ulp(np.maximum(np.abs(rv), np.abs(yv))), bf16_ulp(np.abs(n64 * t).astype(np.float32)))
+    assert np.all(np.abs(yv - rv) <= tol)
+    mismatch = np.mean(bits(y) != ref)
+    print(f"rms_adaln bf16 mismatch rate vs torch CPU: {mismatch:.2e}")
+    assert mismatch < 1e-2
+
+
+@pytest.mark.parametrize("m,d,eps", [(64, 5120, 1e-6), (33, 1024, 1e-5), (7, 3072, 1e-6), (300, 5120, 1e-6)])
+def test_rms_adaln_matches_oracle(dev, m, d, eps):
+    print(f"rms_adaln m={m} d={d}", flush=True)
+    x, w, scale, shift = _rms_inputs(m, d, m + d)
+    segs = _segments(m, 3)
+    rows = eager_np.segment_row_map(m, segs)
+    y = _mx().rms_adaln(x.to(dev), (w.to(dev), eps), shift.to(dev), scale.to(dev), segs)
+    _check_rms_adaln_bound(y, x, w, scale, shift, rows, eps)
+
+
+@pytest.mark.parametrize("g", [256, 0])
+def test_rms_adaln_quantize_matches_oracle(dev, g):
+    m, d, eps = 150, 5120, 1e-6
+    x, w, scale, shift = _rms_inputs(m, d, 9 + g)
+    segs = ((0, 20, 2), (20, 64, 1), (64, 150, 0))
+    rows = eager_np.segment_row_map(m, segs)
+
+    class Norm:  # the reference's RMSNorm attributes
+        weight = w.to(dev)
+        eps = 1e-6
+
+    q, s, y = _mx().rms_adaln_quantize_int8(x.to(dev), Norm, shift.to(dev), scale.to(dev), segs,
+                                            convrot_groupsize=g, return_modulated=True)
+    _check_rms_adaln_bound(y, x, w, scale, shift, rows, eps)
+    # the quantizer of the kernel's own modulated rows is bit-exact
+    qr, sr, _ = cr.convrot_quantize_bf16(bits(y), g)
+    assert np.array_equal(q.cpu().numpy(), qr) and np.array_equal(s.cpu().numpy(), sr)
+    # the standalone norm and the fused path agree exactly; a row map tensor is the same as segments
+    y2 = _mx().rms_adaln(x.to(dev), Norm, shift.to(dev), scale.to(dev), torch.from_numpy(rows))
+    assert torch.equal(y, y2)
+    q3, s3 = _mx().rms_adaln_quantize_int8(x.to(dev), Norm, shift.to(dev), scale.to(dev), segs, convrot_groupsize=g)
+    assert torch.equal(q3, q) and torch.equal(s3, s)
+
+
+def test_rms_adaln_rejects_bad_segments(dev):
+    x, w, scale, shift = _rms_inputs(16, 256, 3)
+    args = (x.to(dev), (w.to(dev), 1e-6), shift.to(dev), scale.to(dev))
+    with pytest.raises(ValueError):
+        _mx().rms_adaln(*args, ((0, 8, 0), (9, 16, 1)))
+    with pytest.raises(ValueError):
+        _mx().rms_adaln(*args, ((0, 16, 3),))
+    with pytest.raises(ValueError):
+        _mx().rms_adaln_quantize_int8(*args, ((0, 16, 0),), convrot_groupsize=1024)

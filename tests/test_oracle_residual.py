@@ -66,3 +66,40 @@ def test_host_segment_row_map_matches_oracle():
     assert mx_qlinear.segment_row_map(64, SEGMENTS, "cpu") is got  # cached
     with pytest.raises(ValueError):
         mx_qlinear.segment_row_map(64, ((0, 7, 0), (8, 64, 1)), "cpu")
+
+
+# ---- RMS adaLN -------------------------------------------------------------------------------
+
+def _rms_inputs(m=48, d=1024, seed=30):
+    x = activations(m, d, seed) * 2
+    w = (1 + 0.2 * torch.randn(d, generator=gen(seed + 1))).to(torch.bfloat16)
+    scale = (0.1 * torch.randn(3, d, generator=gen(seed + 2))).to(torch.bfloat16)
+    shift = (0.1 * torch.randn(3, d, generator=gen(seed + 3))).to(torch.bfloat16)
+    return x, w, scale, shift
+
+
+def test_rms_adaln_matches_the_reference_eager_composition():
+    """kernels.py:7629-7639 run with torch on the CPU: norm(x), then in-place mul_/add_ per
+    segment, against the oracle."""
+    x, w, scale, shift = _rms_inputs()
+    segs = ((0, 5, 2), (5, 30, 0), (30, 48, 1))
+    h = torch.nn.functional.rms_norm(x, (x.shape[-1],), weight=w, eps=1e-6)
+    for a, b, row in segs:
+        h[a:b].mul_(1.0 + scale[row].to(h.dtype)).add_(shift[row].to(h.dtype))
+    got = eager_np.rms_adaln(bits(x), bits(w), 1e-6, bits(scale), bits(shift), eager_np.segment_row_map(48, segs))
+    assert np.array_equal(got, bits(h))
+
+
+def test_rms_norm_routine_is_one_rounding_of_the_float64_value():
+    """torch's bfloat16 rms_norm is within one bfloat16 ulp of the float64 value (its float32
+    statistics and single final rounding), which bounds the device kernel's freedom."""
+    from oracle.bf16 import bf16_ulp
+
+    x, w, _, _ = _rms_inputs(64, 5120, 40)
+    n = bf16_to_f32(eager_np.rms_norm_bf16(bits(x), bits(w), 1e-6)).astype(np.float64)
+    e = eager_np.rms_norm_f64(bits(x), bits(w), 1e-6)
+    assert np.all(np.abs(n - e) <= bf16_ulp(np.abs(e).astype(np.float32)))
+    # a planted mistake (weight applied after an intermediate bfloat16 rounding) breaks equality
+    r = 1.0 / np.sqrt((bf16_to_f32(bits(x)).astype(np.float64) ** 2).mean(-1, keepdims=True) + 1e-6)
+    two = bf16_bits(bf16_to_f32(bf16_bits((bf16_to_f32(bits(x)) * r.astype(np.float32)))) * bf16_to_f32(bits(w)))
+    assert not np.array_equal(two, eager_np.rms_norm_bf16(bits(x), bits(w), 1e-6))

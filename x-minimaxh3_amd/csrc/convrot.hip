@@ -22,6 +22,13 @@
 // m = 4^(d-2)). Groups never straddle lanes (G % 16 == 0, or G = 4 with four groups per lane).
 // The rotated row is kept in LDS (each lane reads back only what it wrote, so no barrier), its
 // absmax reduced across the wave, then quantized and stored with 16-byte stores.
+//
+// RMS adaLN front end (the H3 block's norm before the QKV and fc1 projections,
+// h3serve/native_engine/model/kernels.py:7594-7640 with RMSNorm at layers.py:33-48): a first
+// pass over the row sums x^2 (float64, then rounded once: mean = fp32(sum) / K), r =
+// 1 / sqrt(mean + eps); every element becomes n = bf16((x * r) * w), then the segment's
+// modulation in the eager order: y = bf16(bf16(n * bf16(1 + scale[seg])) + shift[seg]).
+// y is optionally stored (the rms_adaln output) and then rotated and quantized as above.
 
 #include "mxq_common.h"
 
@@ -88,7 +95,23 @@ struct CrArgs {
   int64_t rows;
   int K;       // columns of the quantized row (the raw row has 2K for SwiGLU)
   int digits;  // log4(G); 0: no rotation
+  // RMS adaLN front end (kMod != kModNone)
+  const uint16_t* norm_w;   // [K] bf16
+  const uint16_t* mscale;   // [mod_count, ldm] bf16
+  const uint16_t* mshift;   // [mod_count, ldm] bf16
+  const int32_t* mrows;     // [rows] segment row of each token
+  int64_t ldm, mod_count;
+  float eps;
+  uint16_t* y_out;          // [rows, K] bf16 modulated rows, or null
 };
+
+enum { kModNone = 0, kModQuant = 1, kModOnly = 2 };  // kModOnly: store y, no rotation / quantizer
+
+MXQ_DEVICE double wave_sum_f64(double v) {
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
 
 // One radix-4 step on four values (the quad of one digit).
 MXQ_DEVICE void h4_quad(double& x0, double& x1, double& x2, double& x3) {
@@ -100,7 +123,7 @@ MXQ_DEVICE void h4_quad(double& x0, double& x1, double& x2, double& x3) {
   x3 = y3;
 }
 
-template <int kAct, int kDtype>
+template <int kAct, int kDtype, int kMod = kModNone>
 __global__ __launch_bounds__(256) void convrot_quant_kernel(CrArgs p) {
   constexpr int kE = kDtype == MXQ_DTYPE_F32 ? 4 : 2;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -111,6 +134,35 @@ __global__ __launch_bounds__(256) void convrot_quant_kernel(CrArgs p) {
 
   for (int64_t row = (int64_t)blockIdx.x * kRows + wave; row < p.rows; row += (int64_t)gridDim.x * kRows) {
     float amax = 0.0f;
+    float rinv = 0.0f;
+    const uint16_t* msc = nullptr;
+    const uint16_t* msh = nullptr;
+    if constexpr (kMod != kModNone) {
+      const uint16_t* xr = reinterpret_cast<const uint16_t*>(p.x) + row * p.K;
+      double ss = 0.0;
+      for (int ps = 0; ps < passes; ++ps) {
+        const int e0 = ps * 1024 + lane * 16;
+        if (e0 >= p.K) continue;
+        double acc = 0.0;  // squares of bf16 values are exact in float32; summed in float64
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const v4u w = reinterpret_cast<const v4u*>(xr + e0)[c];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float lo = bf16_to_f32(w[i] & 0xFFFFu), hi = bf16_to_f32(w[i] >> 16);
+            acc += (double)(lo * lo) + (double)(hi * hi);
+          }
+        }
+        ss += acc;
+      }
+      ss = wave_sum_f64(ss);
+      const float mean = (float)ss / (float)p.K;
+      rinv = 1.0f / sqrtf(mean + p.eps);
+      int64_t mr = p.mrows[row];
+      mr = mr < 0 ? 0 : (mr >= p.mod_count ? p.mod_count - 1 : mr);
+      msc = p.mscale + mr * p.ldm;
+      msh = p.mshift + mr * p.ldm;
+    }
     for (int ps = 0; ps < passes; ++ps) {
       const int e0 = ps * 1024 + lane * 16;
       const bool on = e0 < p.K;
@@ -132,16 +184,43 @@ __global__ __launch_bounds__(256) void convrot_quant_kernel(CrArgs p) {
           w[c] = on ? reinterpret_cast<const v4u*>(xr + e0)[c] : v4u{0, 0, 0, 0};
           if (kAct == MXQ_ACT_SWIGLU) up[c] = on ? reinterpret_cast<const v4u*>(xr + p.K + e0)[c] : v4u{0, 0, 0, 0};
         }
+        v4u nw[2], sc[2], sh[2];
+        if constexpr (kMod != kModNone) {
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            nw[c] = on ? reinterpret_cast<const v4u*>(p.norm_w + e0)[c] : v4u{0, 0, 0, 0};
+            sc[c] = on ? reinterpret_cast<const v4u*>(msc + e0)[c] : v4u{0, 0, 0, 0};
+            sh[c] = on ? reinterpret_cast<const v4u*>(msh + e0)[c] : v4u{0, 0, 0, 0};
+          }
+        }
+        uint32_t ybits[8];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const uint32_t word = w[i >> 3][(i >> 1) & 3];
           uint32_t b = (i & 1) ? (word >> 16) : (word & 0xFFFFu);
+          if constexpr (kMod != kModNone) {
+            const int sh16 = 16 * (i & 1);
+            const float wn = bf16_to_f32((nw[i >> 3][(i >> 1) & 3] >> sh16) & 0xFFFFu);
+            const float t = round_bf16(1.0f + bf16_to_f32((sc[i >> 3][(i >> 1) & 3] >> sh16) & 0xFFFFu));
+            const float f = bf16_to_f32((sh[i >> 3][(i >> 1) & 3] >> sh16) & 0xFFFFu);
+            const float n = round_bf16((bf16_to_f32(b) * rinv) * wn);
+            b = f32_to_bf16_bits(round_bf16(n * t) + f);
+            if (i & 1) ybits[i >> 1] |= b << 16; else ybits[i >> 1] = b;
+          }
           if (kAct == MXQ_ACT_GELU_TANH) b = gelu_bf16(b);
           if (kAct == MXQ_ACT_SWIGLU) {
             const uint32_t uw = up[i >> 3][(i >> 1) & 3];
             b = swiglu_bf16(b, (i & 1) ? (uw >> 16) : (uw & 0xFFFFu));
           }
           v[i] = (double)bf16_to_f32(b);
+        }
+        if constexpr (kMod != kModNone) {
+          if (p.y_out && on) {
+            v4u* dst = reinterpret_cast<v4u*>(p.y_out + row * p.K + e0);
+            dst[0] = v4u{ybits[0], ybits[1], ybits[2], ybits[3]};
+            dst[1] = v4u{ybits[4], ybits[5], ybits[6], ybits[7]};
+          }
+          if constexpr (kMod == kModOnly) continue;
         }
       }
       // ---- transform
@@ -189,6 +268,7 @@ __global__ __launch_bounds__(256) void convrot_quant_kernel(CrArgs p) {
         }
       }
     }
+    if constexpr (kMod == kModOnly) continue;
     amax = wave_max(amax);
     const float s = row_scale_from_absmax(amax);
     const float r = 1.0f / round_bf16(s);
@@ -288,4 +368,49 @@ extern "C" int mxq_swiglu_bf16(const void* x, void* y, int64_t rows, int64_t col
   const int64_t blocks = std::min<int64_t>((n + 255) / 256, 65536);
   swiglu_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>((const uint16_t*)x, (uint16_t*)y, rows, cols);
   return mxq_check_launch("swiglu_kernel");
+}
+
+extern "C" int mxq_rms_adaln_quantize_int8(const void* x, const void* norm_weight, const void* scale,
+                                           const void* shift, int64_t ld_mod, int64_t mod_count,
+                                           const int32_t* mod_rows, float eps, void* y_out, int8_t* q,
+                                           float* scales, int64_t rows, int64_t cols, int64_t group_size,
+                                           void* stream) {
+  if (rows < 0 || cols < 0) return mxq_set_error(MXQ_ERR_INVALID, "negative shape");
+  int digits = 0;
+  if (q && group_size != 0) {
+    if (group_size < 4 || (group_size & (group_size - 1)) || __builtin_ctzll((uint64_t)group_size) % 2)
+      return mxq_set_error(MXQ_ERR_INVALID, "Regular Hadamard size must be a power of 4, got %lld", (long long)group_size);
+    digits = __builtin_ctzll((uint64_t)group_size) / 2;
+    if (cols % group_size)
+      return mxq_set_error(MXQ_ERR_INVALID, "ConvRot group size %lld does not divide input features %lld",
+                           (long long)group_size, (long long)cols);
+    if (group_size > 1024) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "ConvRot group size above 1024");
+  }
+  if (rows == 0 || cols == 0) return MXQ_OK;
+  if (!x || !norm_weight || !scale || !shift || !mod_rows) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  if (!q && !y_out) return mxq_set_error(MXQ_ERR_INVALID, "neither a modulated output nor a quantized output");
+  if (q && !scales) return mxq_set_error(MXQ_ERR_INVALID, "null scales");
+  if (mod_count < 1 || ld_mod < cols) return mxq_set_error(MXQ_ERR_INVALID, "bad modulation table");
+  if (cols % 16 || ld_mod % 8) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "columns and modulation stride must be multiples of 16 and 8");
+  if ((uintptr_t)x % 16 || (uintptr_t)q % 16 || (uintptr_t)y_out % 16 || (uintptr_t)norm_weight % 16 ||
+      (uintptr_t)scale % 16 || (uintptr_t)shift % 16)
+    return mxq_set_error(MXQ_ERR_UNSUPPORTED, "tensors must be 16-byte aligned");
+  const int64_t lds = q ? (int64_t)kRows * cols * 2 : 0;
+  if (lds > 160 * 1024) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "row of %lld columns too wide", (long long)cols);
+  CrArgs a{x, q, scales, rows, (int)cols, digits};
+  a.norm_w = (const uint16_t*)norm_weight;
+  a.mscale = (const uint16_t*)scale;
+  a.mshift = (const uint16_t*)shift;
+  a.mrows = mod_rows;
+  a.ldm = ld_mod;
+  a.mod_count = mod_count;
+  a.eps = eps;
+  a.y_out = (uint16_t*)y_out;
+  const unsigned grid = (unsigned)std::min<int64_t>((rows + kRows - 1) / kRows, 65536);
+  hipStream_t st = (hipStream_t)stream;
+  if (q)
+    convrot_quant_kernel<MXQ_ACT_NONE, MXQ_DTYPE_BF16, kModQuant><<<grid, 256, (size_t)lds, st>>>(a);
+  else
+    convrot_quant_kernel<MXQ_ACT_NONE, MXQ_DTYPE_BF16, kModOnly><<<grid, 256, 0, st>>>(a);
+  return mxq_check_launch("convrot_quant_kernel");
 }

@@ -23,6 +23,8 @@ from .ops import (  # noqa: F401
     quantize_int8_convrot_weight,
     quantize_int8_rowwise,
     quantize_int8_rowwise_convrot,
+    rms_adaln,
+    rms_adaln_quantize_int8,
     segment_row_map,
     w4a8_grouped_linear,
     w4a8_int8_linear,

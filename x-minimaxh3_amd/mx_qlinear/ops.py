@@ -240,6 +240,85 @@ def adaln_quantize_int8(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tenso
     return out + (y.reshape(x.shape),) if return_modulated else out
 
 
+def _norm_parts(norm, d: int, dev) -> tuple[torch.Tensor, float]:
+    """An RMSNorm module (``.weight`` [d], ``.eps``) or a ``(weight, eps)`` pair ->
+    (bf16 weight on ``dev``, eps); the weight is cast like ``weight.to(x.dtype)``."""
+    weight, eps = (norm.weight, norm.eps) if hasattr(norm, "weight") else norm
+    w = weight.detach().to(device=dev, dtype=torch.bfloat16).reshape(-1).contiguous()
+    if w.numel() != d:
+        raise ValueError(f"RMSNorm weight has {w.numel()} entries, expected {d}")
+    return w, float(eps)
+
+
+def _segment_table(t: torch.Tensor, d: int, dev, name: str) -> torch.Tensor:
+    t = t.detach()
+    if t.dim() == 1:
+        t = t.reshape(1, -1)
+    if t.dim() != 2 or t.shape[1] != d:
+        raise ValueError(f"{name} must be [rows, {d}], got {tuple(t.shape)}")
+    return t.to(device=dev, dtype=torch.bfloat16).contiguous()
+
+
+def rms_adaln_quantize_int8(value: torch.Tensor, norm, shift: torch.Tensor, scale: torch.Tensor,
+                            segments, convrot_groupsize: int = 256, return_modulated: bool = False):
+    """``quantize(rotate(rms_adaln(value, norm, shift, scale, segments)))`` in one launch.
+
+    The H3 block's pre-projection chain (h3serve/native_engine/model/layers.py:1094 ->
+    kernels.py:7594 -> the ConvRotInt8Linear quantizer, CK/backends/eager/quantization.py:
+    1012-1025). ``segments`` is a sequence of ``(start, stop, row)`` or an int32 row map.
+    ``convrot_groupsize`` 0 skips the rotation. Returns ``(q, x_scale)`` or
+    ``(q, x_scale, modulated)`` with ``return_modulated``.
+    """
+    return _rms_adaln_call(value, norm, shift, scale, segments, True, convrot_groupsize, return_modulated)
+
+
+def rms_adaln(value: torch.Tensor, norm, shift: torch.Tensor, scale: torch.Tensor, segments) -> torch.Tensor:
+    """RMSNorm then the segmented modulation ``h[a:b].mul_(1 + scale[row]).add_(shift[row])``
+    (h3serve/native_engine/model/kernels.py:7594-7640, same roundings); bfloat16 [rows, D]."""
+    return _rms_adaln_call(value, norm, shift, scale, segments, False, 0, True)
+
+
+def _rms_adaln_call(value, norm, shift, scale, segments, quant: bool, group: int, want_y: bool):
+    if value.dim() != 2:
+        raise ValueError("rms_adaln expects a 2-D [tokens, hidden] tensor")
+    if value.dtype != torch.bfloat16:
+        raise NotImplementedError("rms_adaln supports bfloat16 inputs")
+    dev = _require_gpu(value)
+    rows, d = value.shape
+    if quant and group:
+        _check_power_of_four(group)
+        if d % group:
+            raise ValueError(f"ConvRot group size {group} does not divide input features {d}")
+    w, eps = _norm_parts(norm, d, dev)
+    sc = _segment_table(scale, d, dev, "scale")
+    sh = _segment_table(shift, d, dev, "shift")
+    if sc.shape[0] != sh.shape[0]:
+        raise ValueError("scale and shift must have the same number of rows")
+    if isinstance(segments, torch.Tensor):
+        mr = segments.to(device=dev, dtype=torch.int32).reshape(-1).contiguous()
+        if mr.numel() != rows:
+            raise ValueError(f"modulation row map has {mr.numel()} entries, expected {rows}")
+        if rows:
+            lo, hi = torch.aminmax(mr)
+            if int(lo) < 0 or int(hi) >= sc.shape[0]:
+                raise ValueError("modulation row outside the scale/shift tables")
+    else:
+        mr = segment_row_map(rows, segments, dev)
+        if rows and max(int(r) for _, _, r in segments) >= sc.shape[0]:
+            raise ValueError("modulation segment row outside the scale/shift tables")
+    x = value.contiguous()
+    y = torch.empty_like(x) if want_y else None
+    q = torch.empty((rows, d), dtype=torch.int8, device=dev) if quant else None
+    s = torch.empty((rows, 1), dtype=torch.float32, device=dev) if quant else None
+    if rows and d:
+        with torch.cuda.device(dev):
+            call("mxq_rms_adaln_quantize_int8", _p(x), _p(w), _p(sc), _p(sh), sc.stride(0), sc.shape[0], _p(mr),
+                 eps, _p(y), _p(q), _p(s), rows, d, group if quant else 0, _stream(dev))
+    if not quant:
+        return y
+    return (q, s, y) if want_y else (q, s)
+
+
 # ---------------------------------------------------------------------------------------
 # INT8 GEMMs
 # ---------------------------------------------------------------------------------------
