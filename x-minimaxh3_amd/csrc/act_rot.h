@@ -1,0 +1,119 @@
+// Shared pieces of the kernels that quantize activation rows: the SiLU / SwiGLU input
+// activation (bit-identical to torch's CPU routines on bfloat16), the float64 -> bfloat16
+// rounding of rotated values, and the radix-4 step of the ConvRot (regular Hadamard) rotation.
+#pragma once
+
+#include "mxq_common.h"
+
+namespace mxq {
+
+// ---- SiLU on bfloat16 ---------------------------------------------------------------------
+// Bit-exact torch CPU silu on a bfloat16 input (the gate activation of the reference's SwiGLU,
+// CK/backends/_activations.py:50-52); rules and table from gen_silu_table.py, which checks them
+// against all 65,536 torch outputs.
+#define MXQ_SILU_TABLE_DECL constexpr uint16_t kSiluTableC[3840]
+#include "silu_bf16_table.inc"
+#undef MXQ_SILU_TABLE_DECL
+
+constexpr uint32_t silu_rule_c(uint32_t b) {
+  const uint32_t e = (b >> 7) & 0xFFu, sign = b & 0x8000u, mag = b & 0x7FFFu;
+  if (e < MXQ_SILU_E_LO) {
+    const uint32_t v = mag & 0xFFu;
+    return sign | (e >= 2 ? mag - 0x80u : (v >> 1) + ((v & 1u) & ((v >> 1) & 1u)));
+  }
+  if (e == 255u) return b == 0x7F80u ? 0x7F80u : MXQ_SILU_NAN;
+  if (!sign && e >= MXQ_SILU_E_POS) return b;
+  if (sign && e >= MXQ_SILU_E_NEG) return 0x8000u;
+  return kSiluTableC[((b >> 15) * (MXQ_SILU_E_NEG - MXQ_SILU_E_LO) + (e - MXQ_SILU_E_LO)) * 128u + (b & 0x7Fu)];
+}
+struct SiluFullTable {
+  uint16_t v[65536];
+};
+constexpr SiluFullTable make_silu_full() {
+  SiluFullTable t{};
+  for (uint32_t b = 0; b < 65536u; ++b) t.v[b] = (uint16_t)silu_rule_c(b);
+  return t;
+}
+static __device__ __attribute__((aligned(16))) const SiluFullTable kSiluFull = make_silu_full();
+
+MXQ_DEVICE uint32_t silu_bf16(uint32_t b) { return kSiluFull.v[b & 0xFFFFu]; }
+
+// SwiGLU of one bf16 pair: bf16(bf16(silu(gate)) * up) -- the product of two bf16 is exact in
+// fp32, so this is torch's bf16 mul_ (one rounding); a NaN product becomes 0x7FC0, the pattern
+// torch's float -> bfloat16 conversion gives every NaN.
+MXQ_DEVICE uint32_t swiglu_bf16(uint32_t gate, uint32_t up) {
+  const float p = bf16_to_f32(silu_bf16(gate)) * bf16_to_f32(up);
+  return p != p ? 0x7FC0u : f32_to_bf16_bits(p);
+}
+
+// float64 -> bfloat16 bits with one round-to-nearest-even rounding: through float32 (RNE),
+// exact except where that float32 is itself a bfloat16 midpoint and x is not; then x lies
+// strictly on one side of the midpoint and the result is the neighbour on that side.
+MXQ_DEVICE uint32_t f64_to_bf16_bits(double x) {
+  const float f = (float)x;
+  const uint32_t u = __float_as_uint(f);
+  uint32_t b = f32_to_bf16_bits(f);
+  if ((u & 0xFFFFu) == 0x8000u && (double)f != x) b = (u >> 16) + (fabs(x) > fabs((double)f) ? 1u : 0u);
+  return b;
+}
+
+// One radix-4 step on four values (the quad of one digit).
+MXQ_DEVICE void h4_quad(double& x0, double& x1, double& x2, double& x3) {
+  const double s = (x0 + x1) + (x2 + x3);
+  const double y0 = s - (x3 + x3), y1 = s - (x2 + x2), y2 = s - (x1 + x1), y3 = s - (x0 + x0);
+  x0 = y0;
+  x1 = y1;
+  x2 = y2;
+  x3 = y3;
+}
+
+// Loads 16 consecutive bf16 activations of one lane (columns e0 .. e0 + 15 of a row; zeros when
+// !on), applies the input activation (kAct; SwiGLU reads gate at xr[e] and up at xr[K + e]) and
+// returns them as float64.
+template <int kAct>
+MXQ_DEVICE void load16_act(const uint16_t* xr, int64_t K, int e0, bool on, double* v) {
+  v4u w[2], up[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    w[c] = on ? reinterpret_cast<const v4u*>(xr + e0)[c] : v4u{0, 0, 0, 0};
+    if (kAct == MXQ_ACT_SWIGLU) up[c] = on ? reinterpret_cast<const v4u*>(xr + K + e0)[c] : v4u{0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t word = w[i >> 3][(i >> 1) & 3];
+    uint32_t b = (i & 1) ? (word >> 16) : (word & 0xFFFFu);
+    if (kAct == MXQ_ACT_GELU_TANH) b = gelu_bf16(b);
+    if (kAct == MXQ_ACT_SWIGLU) {
+      const uint32_t uw = up[i >> 3][(i >> 1) & 3];
+      b = swiglu_bf16(b, (i & 1) ? (uw >> 16) : (uw & 0xFFFFu));
+    }
+    v[i] = (double)bf16_to_f32(b);
+  }
+}
+
+// The unscaled rotation (x @ H_G * sqrt(G)) of the 16 values of each lane, where lane l of the
+// wave holds columns 16 l .. 16 l + 15 of a 1024-column window: digits 0 and 1 of the in-group
+// index are inside the lane, digit d >= 2 is lane bit pair d - 2 (xor shuffles with masks m, 2m,
+// 3m, m = 4^(d-2)). All lanes of the wave must call it (the shuffles are wave-wide).
+MXQ_DEVICE void rotate16(double* v, int digits) {
+  if (digits >= 1) {
+#pragma unroll
+    for (int j = 0; j < 16; j += 4) h4_quad(v[j], v[j + 1], v[j + 2], v[j + 3]);
+  }
+  if (digits >= 2) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) h4_quad(v[j], v[j + 4], v[j + 8], v[j + 12]);
+  }
+  for (int d = 2; d < digits; ++d) {
+    const int m = 1 << (2 * (d - 2));
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const double t = v[j] + __shfl_xor(v[j], m, kWave);
+      const double s = t + __shfl_xor(t, 2 * m, kWave);
+      const double q3 = __shfl_xor(v[j], 3 * m, kWave);
+      v[j] = s - (q3 + q3);
+    }
+  }
+}
+
+}  // namespace mxq

@@ -16,6 +16,7 @@ from .ops import (  # noqa: F401
     dequantize_int4_grouped_to_int8,
     fused_down_gated_residual,
     int8_ffn_gelu,
+    int8_gemv_dequant,
     int8_linear,
     int8_linear_gated_residual_,
     int8_linear_prequantized,

@@ -375,6 +375,30 @@ def _bias(bias: torch.Tensor | None, n: int, dtype: torch.dtype, dev):
     return b
 
 
+_M1_MAX_K = 16384
+
+
+def _aligned16(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous, with a 16-byte aligned start (vector loads)."""
+    t = t.contiguous()
+    return t.clone() if t.data_ptr() % 16 else t
+
+
+def _m1_ok(k: int) -> bool:
+    """Shapes the single-launch M = 1 kernels take (a K tail goes through the padded GEMM)."""
+    return 0 < k <= _M1_MAX_K and k % 16 == 0
+
+
+def int8_gemv_dequant(x_qdata: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor,
+                      weight_scale: torch.Tensor, bias: torch.Tensor | None,
+                      out_dtype: torch.dtype) -> torch.Tensor:
+    """Single-row INT8 GEMV with the dequant epilogue, [1, N] (CK/backends/cuda/__init__.py:
+    1587-1610); the values of :func:`int8_linear_prequantized` for that row."""
+    if x_qdata.numel() != weight.shape[1]:
+        raise ValueError("x_qdata must hold one row of K values")
+    return int8_linear_prequantized(x_qdata.reshape(1, -1), x_scale, weight, weight_scale, bias, out_dtype)
+
+
 def int8_linear_prequantized(x_qdata: torch.Tensor, x_scale: torch.Tensor, weight: torch.Tensor,
                              weight_scale: torch.Tensor, bias: torch.Tensor | None = None,
                              out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
@@ -400,6 +424,12 @@ def int8_linear_prequantized(x_qdata: torch.Tensor, x_scale: torch.Tensor, weigh
         raise ValueError(f"x_scale has {xs.numel()} entries, expected {m}")
     out = torch.empty((m, n), dtype=out_dtype, device=dev)
     if m == 0 or n == 0:
+        return out
+    k = x_qdata.shape[1]
+    if m == 1 and _m1_ok(k):
+        with torch.cuda.device(dev):
+            call("mxq_int8_gemv_dequant", _p(_aligned16(x_qdata)), _p(xs), _p(_aligned16(weight)), _p(ws),
+                 ws.numel(), _p(b), _p(out), n, k, code, _stream(dev))
         return out
     q2, w2, k = _pad_k(x_qdata.contiguous(), weight.contiguous())
     with torch.cuda.device(dev):
@@ -440,6 +470,16 @@ def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tenso
     if x.numel() == 0:
         return torch.empty((*lead, n), dtype=out_dtype, device=dev)
     x2 = x.reshape(-1, x.shape[-1])
+    if x2.shape[0] == 1 and x.dtype == torch.bfloat16 and _m1_ok(width) and n:
+        # one token: quantizer, GEMV and epilogue in one launch (int8_linear_m1's route)
+        ws = _weight_scale(weight_scale, n, dev)
+        b = _bias(bias, n, out_dtype, dev)
+        out = torch.empty((1, n), dtype=out_dtype, device=dev)
+        with torch.cuda.device(dev):
+            call("mxq_int8_linear_m1", _p(_aligned16(x2)), _p(_aligned16(weight)), _p(ws), ws.numel(), _p(b),
+                 _p(out), n, width, convrot_groupsize if convrot else 0, act, _out_code(out_dtype), None, None,
+                 _stream(dev))
+        return out.reshape(*lead, n)
     if convrot:
         q, s = quantize_int8_rowwise_convrot(x2, convrot_groupsize, input_act)
     else:
