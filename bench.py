@@ -14,7 +14,9 @@ restatement) timed on this host on a bounded row sample.
 
 Other workloads (--workload): qkv_adaln (fused adaLN + quant + QKV GEMM, M=75600, N=15360),
 w4a8_gemm (8192 x 5120 x 5120, group 128), w4a8_skinny (512 x 10240 x 5120), linear_c1
-(1024 x 3072 x 3072).
+(1024 x 3072 x 3072), and the H3 model's own shapes (hidden 5376, ConvRot 256 on every layer):
+h3_mlp (rms_adaln -> fc1 -> SwiGLU -> fc2 with the gated residual epilogue), h3_qkv (rms_adaln +
+quant -> QKV 5376 -> 21504), linear_m1 (one token through the QKV projection, weight streaming).
 """
 
 from __future__ import annotations
@@ -250,7 +252,8 @@ class W4A8Workload:
         return self.m * self.k + self.n * self.k // 2 + (self.k // self.g) * self.n * 2 + self.m * 4 + self.m * self.n * 2
 
     def dominant(self, timer):
-        return {"span": "w4a8_gemm", "symbol": "w4a8_grouped_kernel", "ops": self.ops_per_step(),
+        sym = "w4a8_g128_kernel" if self.g == 128 and self.n % 8 == 0 else "w4a8_grouped_kernel"
+        return {"span": "w4a8_gemm", "symbol": sym, "ops": self.ops_per_step(),
                 "bytes": self.alg_bytes()}
 
     def config(self):
@@ -322,6 +325,230 @@ class LinearC1Workload:
             return time.perf_counter() - t0
 
         return _cpu_sample(run, budget_s, self.m, "tokens/s", "first {rows} of 1024 rows through eager int8_linear")
+
+
+# H3 block dimensions (hidden 5376, attention width 7168, SwiGLU inner 14336) and the packed
+# text / audio / video layout of one 720p x 5 s sample: three modulation segments.
+H3_D, H3_ATTN, H3_FFN = 5376, 7168, 14336
+
+
+def h3_segments(m, text=256, audio=1024):
+    return ((0, text, 0), (text, audio, 1), (audio, m, 2))
+
+
+def _clip_segments(segments, rows):
+    return tuple((a, min(b, rows), r) for a, b, r in segments if a < rows)
+
+
+class _H3Modulation:
+    """RMSNorm weight, adaLN scale/shift/gate tables [3, D] and the segment row map."""
+
+    def __init__(self, dev, m, d, seed):
+        self.norm_w = (1 + 0.1 * torch.randn(d, generator=_gen(dev, seed), device=dev)).to(torch.bfloat16)
+        self.scale = (0.1 * torch.randn(3, d, generator=_gen(dev, seed + 1), device=dev)).to(torch.bfloat16)
+        self.shift = (0.1 * torch.randn(3, d, generator=_gen(dev, seed + 2), device=dev)).to(torch.bfloat16)
+        self.gate = (0.1 * torch.randn(3, d, generator=_gen(dev, seed + 3), device=dev)).to(torch.bfloat16)
+        self.segments = h3_segments(m)
+        self.rows = mx_qlinear.segment_row_map(m, self.segments, dev)
+        self.eps = 1e-6
+
+
+class H3MlpWorkload:
+    """The H3 block's MLP half at 720p x 5 s: rms_adaln + ConvRot-256 quant -> fc1 (5376 ->
+    2 x 14336, bias) -> SwiGLU + ConvRot-256 quant -> fc2 (14336 -> 5376, bias) with the gated
+    residual update of the hidden state in place."""
+
+    name = "h3_mlp_swiglu_convrot_720p"
+
+    def __init__(self, dev, m=75600, d=H3_D, inner=H3_FFN):
+        self.m, self.d, self.inner = m, d, inner
+        self.res = make_activations(m, d, dev, 40)
+        self.mod = _H3Modulation(dev, m, d, 41)
+        self.w1, self.s1 = make_int8_weight(2 * inner, d, dev, 45)
+        self.w2, self.s2 = make_int8_weight(d, inner, dev, 46)
+        self.b1, self.b2 = make_bias(2 * inner, dev, 47), make_bias(d, dev, 48)
+        self.q1 = torch.empty(m, d, dtype=torch.int8, device=dev)
+        self.xs1 = torch.empty(m, dtype=torch.float32, device=dev)
+        self.raw = torch.empty(m, 2 * inner, dtype=torch.bfloat16, device=dev)
+        self.q2 = torch.empty(m, inner, dtype=torch.int8, device=dev)
+        self.xs2 = torch.empty(m, dtype=torch.float32, device=dev)
+        self.dev = dev
+
+    def step(self, timer=None):
+        st = _stream(self.dev)
+        t = timer.span if timer else (lambda name: _Null())
+        m, d, f, mod = self.m, self.d, self.inner, self.mod
+        with t("rms_adaln_quant"):
+            _lib.call("mxq_rms_adaln_quantize_int8", _p(self.res), _p(mod.norm_w), _p(mod.scale), _p(mod.shift), d, 3,
+                      _p(mod.rows), mod.eps, None, _p(self.q1), _p(self.xs1), m, d, 256, st)
+        with t("fc1_gemm"):
+            _lib.call("mxq_int8_gemm_dequant", _p(self.q1), _p(self.w1), _p(self.xs1), _p(self.s1), 2 * f,
+                      _p(self.b1), _p(self.raw), m, 2 * f, d, 2 * f, _lib.DTYPE_BF16, st)
+        with t("swiglu_convrot_quant"):
+            _lib.call("mxq_quantize_int8_rowwise_convrot", _p(self.raw), _lib.DTYPE_BF16, _p(self.q2), _p(self.xs2),
+                      m, f, 256, _lib.ACT_SWIGLU, st)
+        with t("fc2_gated_residual"):
+            _lib.call("mxq_int8_gemm_gated_residual", _p(self.q2), _p(self.w2), _p(self.xs2), _p(self.s2), d,
+                      _p(self.b2), _p(self.res), d, _p(mod.gate), d, 3, _p(mod.rows), m, d, f, st)
+
+    def ops_per_step(self):
+        return 2 * self.m * self.d * 2 * self.inner + 2 * self.m * self.inner * self.d
+
+    def units_per_step(self):
+        return self.m
+
+    def dominant(self, timer):
+        m, d, f = self.m, self.d, self.inner
+        fc1 = {"span": "fc1_gemm", "symbol": "gemm_i8_kernel<1, 2>", "ops": 2 * m * d * 2 * f,
+               "bytes": m * d + 2 * f * d + 2 * m * 2 * f + 4 * m + 4 * 2 * f + 2 * 2 * f}
+        fc2 = {"span": "fc2_gated_residual", "symbol": "gemm_i8_kernel<3, 2>", "ops": 2 * m * f * d,
+               # A, W2, residual read + written, gate rows, xs, ws, bias
+               "bytes": m * f + d * f + 4 * m * d + 4 * m + 4 * m + 4 * d + 2 * d + 6 * d}
+        return max((fc1, fc2), key=lambda x: timer.mean_ms(x["span"]))
+
+    def config(self):
+        return {"workload": self.name, "tokens": self.m, "d_model": self.d, "swiglu_inner": self.inner,
+                "norm": "rms_adaln eps 1e-6, 3 segments", "convrot_group": 256,
+                "epilogue": "fc2 gated residual in place"}
+
+    def cpu_baseline(self, budget_s):
+        from oracle import eager_torch
+
+        mod = self.mod
+        cpu = [t.cpu() for t in (mod.norm_w, mod.shift, mod.scale, mod.gate)]
+        ws = [t.cpu() for t in (self.w1, self.s1, self.b1, self.w2, self.s2, self.b2)]
+
+        def run(rows):
+            res = self.res[:rows].cpu()
+            segs = _clip_segments(mod.segments, rows)
+            t0 = time.perf_counter()
+            eager_torch.h3_mlp_(res, cpu[0], mod.eps, cpu[1], cpu[2], cpu[3], segs, *ws)
+            return time.perf_counter() - t0
+
+        return _cpu_sample(run, budget_s, self.m, "tokens/s", "first {rows} tokens through the eager rms_adaln -> "
+                           "fc1 (convrot) -> swiglu fc2 (convrot) -> addcmul_ composition")
+
+
+class H3QkvWorkload:
+    """rms_adaln + ConvRot-256 quant -> the fused QKV projection (5376 -> 3 x 7168, bias) at 720p."""
+
+    name = "h3_qkv_rms_adaln_convrot_720p"
+
+    def __init__(self, dev, m=75600, d=H3_D, n=3 * H3_ATTN):
+        self.m, self.d, self.n = m, d, n
+        self.x = make_activations(m, d, dev, 50)
+        self.mod = _H3Modulation(dev, m, d, 51)
+        self.w, self.s = make_int8_weight(n, d, dev, 55)
+        self.b = make_bias(n, dev, 56)
+        self.q = torch.empty(m, d, dtype=torch.int8, device=dev)
+        self.xs = torch.empty(m, dtype=torch.float32, device=dev)
+        self.out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        self.dev = dev
+
+    def step(self, timer=None):
+        st = _stream(self.dev)
+        t = timer.span if timer else (lambda name: _Null())
+        m, d, n, mod = self.m, self.d, self.n, self.mod
+        with t("rms_adaln_quant"):
+            _lib.call("mxq_rms_adaln_quantize_int8", _p(self.x), _p(mod.norm_w), _p(mod.scale), _p(mod.shift), d, 3,
+                      _p(mod.rows), mod.eps, None, _p(self.q), _p(self.xs), m, d, 256, st)
+        with t("qkv_gemm"):
+            _lib.call("mxq_int8_gemm_dequant", _p(self.q), _p(self.w), _p(self.xs), _p(self.s), n, _p(self.b),
+                      _p(self.out), m, n, d, n, _lib.DTYPE_BF16, st)
+
+    def ops_per_step(self):
+        return 2 * self.m * self.n * self.d
+
+    def units_per_step(self):
+        return self.m
+
+    def dominant(self, timer):
+        m, d, n = self.m, self.d, self.n
+        return {"span": "qkv_gemm", "symbol": "gemm_i8_kernel<1, 2>", "ops": 2 * m * n * d,
+                "bytes": m * d + n * d + 2 * m * n + 4 * m + 4 * n + 2 * n}
+
+    def config(self):
+        return {"workload": self.name, "tokens": self.m, "d_model": self.d, "qkv_out": self.n,
+                "norm": "rms_adaln eps 1e-6, 3 segments", "convrot_group": 256}
+
+    def cpu_baseline(self, budget_s):
+        from oracle import eager_torch
+
+        mod = self.mod
+        nw, sh, sc = mod.norm_w.cpu(), mod.shift.cpu(), mod.scale.cpu()
+        w, s, b = self.w.cpu(), self.s.cpu(), self.b.cpu()
+
+        def run(rows):
+            x = self.x[:rows].cpu()
+            segs = _clip_segments(mod.segments, rows)
+            t0 = time.perf_counter()
+            eager_torch.int8_linear(eager_torch.rms_adaln(x, nw, mod.eps, sh, sc, segs), w, s, b, convrot=True)
+            return time.perf_counter() - t0
+
+        return _cpu_sample(run, budget_s, self.m, "tokens/s", "first {rows} tokens through eager rms_adaln -> "
+                           "int8_linear(convrot=True)")
+
+
+class LinearM1Workload:
+    """One token through the H3 QKV projection (5376 -> 21504, ConvRot 256): quantizer + GEMV +
+    dequant in one launch per layer, cycling over 4 layers' weights (462 MB, more than the 256 MB
+    last-level cache) so the weights stream from HBM as in a layer-by-layer decode."""
+
+    name = "int8_linear_m1_5376x21504_convrot"
+    layers = 4
+
+    def __init__(self, dev, d=H3_D, n=3 * H3_ATTN):
+        self.d, self.n = d, n
+        self.x = make_activations(1, d, dev, 60)
+        self.ws = [make_int8_weight(n, d, dev, 61 + i) for i in range(self.layers)]
+        self.b = make_bias(n, dev, 70)
+        self.out = torch.empty(1, n, dtype=torch.bfloat16, device=dev)
+        self.dev = dev
+        self.calls = 0
+
+    def step(self, timer=None):
+        st = _stream(self.dev)
+        t = timer.span if timer else (lambda name: _Null())
+        w, s = self.ws[self.calls % self.layers]
+        self.calls += 1
+        with t("linear_m1"):
+            _lib.call("mxq_int8_linear_m1", _p(self.x), _p(w), _p(s), self.n, _p(self.b), _p(self.out), self.n,
+                      self.d, 256, _lib.ACT_NONE, _lib.DTYPE_BF16, None, None, st)
+
+    def ops_per_step(self):
+        return 2 * self.n * self.d
+
+    def units_per_step(self):
+        return 1
+
+    def alg_bytes(self):
+        return self.n * self.d + 2 * self.d + 2 * self.n + 4 * self.n + 2 * self.n
+
+    def dominant(self, timer):
+        return {"span": "linear_m1", "symbol": "linear_m1_kernel", "ops": self.ops_per_step(),
+                "bytes": self.alg_bytes(), "bound": "hbm"}
+
+    def config(self):
+        return {"workload": self.name, "m": 1, "n": self.n, "k": self.d, "convrot_group": 256,
+                "layers_cycled": self.layers}
+
+    def cpu_baseline(self, budget_s):
+        from oracle import eager_torch
+
+        w, s = (t.cpu() for t in self.ws[0])
+        b, x = self.b.cpu(), self.x.cpu()
+        total, calls = 0.0, 0
+        threads = len(os.sched_getaffinity(0))
+        torch.set_num_threads(threads)
+        while total < budget_s:
+            t0 = time.perf_counter()
+            eager_torch.int8_linear(x, w, s, b, convrot=True)
+            total += time.perf_counter() - t0
+            calls += 1
+        value = self.alg_bytes() * calls / total / 1e9
+        return {"value": round(value, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": f"{calls} single-token eager int8_linear(convrot=True) calls on the host, "
+                          f"{total:.1f} s"}
 
 
 def _cpu_sample(run, budget_s, max_rows, unit, what):
@@ -432,6 +659,9 @@ WORKLOADS = {
     "w4a8_gemm": lambda dev: W4A8Workload(dev, 8192, 5120, 5120, name="w4a8_gemm_8192x5120x5120"),
     "w4a8_skinny": lambda dev: W4A8Workload(dev, 512, 10240, 5120, name="w4a8_skinny_512x10240x5120"),
     "linear_c1": lambda dev: LinearC1Workload(dev),
+    "h3_mlp": lambda dev: H3MlpWorkload(dev),
+    "h3_qkv": lambda dev: H3QkvWorkload(dev),
+    "linear_m1": lambda dev: LinearM1Workload(dev),
 }
 
 METRICS = {
@@ -440,6 +670,10 @@ METRICS = {
     "w4a8_gemm": ("W4A8 GEMM TOPS", "TOPS"),
     "w4a8_skinny": ("W4A8 skinny projection HBM GB/s", "GB/s"),
     "linear_c1": ("W8A8 linear TOPS", "TOPS"),
+    "h3_mlp": ("H3 block MLP tokens/s at 720p (rms_adaln -> fc1 -> SwiGLU -> fc2 + gated residual, "
+               "ConvRot INT8)", "tokens/s"),
+    "h3_qkv": ("H3 QKV projection with fused rms_adaln + ConvRot quant, tokens/s at 720p", "tokens/s"),
+    "linear_m1": ("single-token INT8 linear weight-streaming GB/s", "GB/s"),
 }
 
 
@@ -484,9 +718,12 @@ def main():
         value = units
     dom = wl.dominant(timer)
     kms = timer.mean_ms(dom["span"])
-    achieved = dom["ops"] / (kms * 1e-3) / 1e12
-    roof = {"bound": "mfma", "kernel": f"{dom['symbol']} ({dom['span']})", "achieved": round(achieved, 2),
-            "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4),
+    if dom.get("bound") == "hbm":
+        achieved, peak, runit = dom["bytes"] / (kms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved, peak, runit = dom["ops"] / (kms * 1e-3) / 1e12, INT8_PEAK_TOPS, "TFLOP/s"
+    roof = {"bound": dom.get("bound", "mfma"), "kernel": f"{dom['symbol']} ({dom['span']})",
+            "achieved": round(achieved, 2), "peak": peak, "unit": runit, "frac": round(achieved / peak, 4),
             "traffic": None, "alg_bytes": dom["bytes"], "launch_ms": round(kms, 4)}
     if not args.no_traffic:
         try:

@@ -56,19 +56,46 @@ def dequant(result: torch.Tensor, x_scale: torch.Tensor, weight_scale: torch.Ten
 
 
 def apply_input_act(x: torch.Tensor, input_act: str | None) -> torch.Tensor:
-    """CK/backends/_activations.py:40-53 (gelu_tanh only; swiglu is out of this path)."""
+    """CK/backends/_activations.py:40-53."""
     if input_act in (None, "none"):
         return x
     if input_act == "gelu_tanh":
         return torch.nn.functional.gelu(x, approximate="tanh")
+    if input_act == "swiglu":
+        gate, up = x.chunk(2, dim=-1)
+        return torch.nn.functional.silu(gate).mul_(up)
     raise ValueError(f"unsupported input_act: {input_act!r}")
+
+
+_HADAMARD: dict = {}
+
+
+def hadamard(g: int, dtype: torch.dtype) -> torch.Tensor:
+    """kron(h4, ..., h4) / sqrt(g) (CK/tensor/int8_utils.py:11-38)."""
+    key = (g, dtype)
+    if key not in _HADAMARD:
+        h4 = torch.tensor([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=torch.float64)
+        h = h4
+        while h.shape[0] < g:
+            h = torch.kron(h, h4)
+        _HADAMARD[key] = (h / float(g) ** 0.5).to(dtype)
+    return _HADAMARD[key]
+
+
+def rotate(x: torch.Tensor, g: int) -> torch.Tensor:
+    """x_grouped @ H_g in x's dtype (CK/tensor/int8_utils.py:58-74)."""
+    k = x.shape[-1]
+    return torch.matmul(x.reshape(*x.shape[:-1], k // g, g), hadamard(g, x.dtype)).reshape(x.shape)
 
 
 def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
                 bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
-                input_act: str | None = None) -> torch.Tensor:
-    """CK/backends/eager/quantization.py:971-1056 with convrot=False."""
+                input_act: str | None = None, convrot: bool = False,
+                convrot_groupsize: int = 256) -> torch.Tensor:
+    """CK/backends/eager/quantization.py:971-1056."""
     x = apply_input_act(x, input_act)
+    if convrot:
+        x = rotate(x, convrot_groupsize)
     weight_scale = weight_scale.to(torch.float32).reshape(-1)
     x2 = x.reshape(-1, x.shape[-1])
     q, s = quantize_int8_rowwise(x2)
@@ -124,3 +151,29 @@ def ffn_gelu_int8(x, w1, s1, b1, w2, s2, b2):
     """fc1 -> tanh-GELU (as fc2's input_act) -> fc2, two eager int8_linear calls."""
     h = int8_linear(x, w1, s1, b1)
     return int8_linear(h, w2, s2, b2, input_act="gelu_tanh")
+
+
+def rms_adaln(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, shift: torch.Tensor,
+              scale: torch.Tensor, segments) -> torch.Tensor:
+    """h3serve/native_engine/model/kernels.py:7629-7640 with RMSNorm at layers.py:39-48."""
+    hidden = torch.nn.functional.rms_norm(x, (x.shape[-1],), weight=norm_weight.to(x.dtype), eps=eps)
+    for start, stop, row in segments:
+        hidden[start:stop].mul_(1.0 + scale[row].to(hidden.dtype)).add_(shift[row].to(hidden.dtype))
+    return hidden
+
+
+def gated_residual_(residual: torch.Tensor, update: torch.Tensor, gate: torch.Tensor, segments) -> torch.Tensor:
+    """h3serve/native_engine/model/layers.py:944-960."""
+    for start, stop, row in segments:
+        residual[start:stop].addcmul_(update[start:stop], gate[row].to(update.dtype))
+    return residual
+
+
+def h3_mlp_(residual, norm_weight, eps, shift, scale, gate, segments, w1, s1, b1, w2, s2, b2):
+    """The H3 block's MLP half as the reference composes it (layers.py:1138-1150 ->
+    fused_mlp.py:386-420): rms_adaln, fc1 (ConvRot 256), SwiGLU folded into fc2's ConvRot
+    int8_linear, gated residual update of ``residual`` in place."""
+    hidden = rms_adaln(residual, norm_weight, eps, shift, scale, segments)
+    raw = int8_linear(hidden, w1, s1, b1, convrot=True)
+    projected = int8_linear(raw, w2, s2, b2, input_act="swiglu", convrot=True)
+    return gated_residual_(residual, projected, gate, segments)
