@@ -16,12 +16,12 @@
 // bits, which makes the result the exact product; the fixed operation order (digit 0 first,
 // pairwise S, the same association in every lane) makes it reproducible in all other cases.
 //
-// Layout: one wave per row. Pass p covers columns [1024 p, 1024 p + 1024): lane l holds 16
-// consecutive columns, so digits 0 and 1 of the in-group index are inside the lane and digit
-// d >= 2 is lane bit pair d-2: those quads are combined with xor shuffles (masks m, 2m, 3m,
-// m = 4^(d-2)). Groups never straddle lanes (G % 16 == 0, or G = 4 with four groups per lane).
-// The rotated row is kept in LDS (each lane reads back only what it wrote, so no barrier), its
-// absmax reduced across the wave, then quantized and stored with 16-byte stores.
+// Layout: a row is cut into 1024-column windows; in a window lane l holds 16 consecutive
+// columns, so digits 0 and 1 of the in-group index are inside the lane and digit d >= 2 is lane
+// bit pair d-2: those quads are combined with xor shuffles (masks m, 2m, 3m, m = 4^(d-2)).
+// Groups never straddle lanes (G % 16 == 0, or G = 4 with four groups per lane). Up to four
+// waves share a row's windows; the rotated row stays in registers while its absmax is reduced
+// (through LDS across the row's waves), then it is quantized and stored with 16-byte stores.
 //
 // RMS adaLN front end (the H3 block's norm before the QKV and fc1 projections,
 // h3serve/native_engine/model/kernels.py:7594-7640 with RMSNorm at layers.py:33-48): a first
@@ -36,7 +36,7 @@ namespace mxq {
 
 namespace {
 
-constexpr int kRows = 4;  // rows (waves) per 256-thread block
+constexpr int kMaxWindows = 20;  // 1024-column windows per row: K <= 20480
 
 struct CrArgs {
   const void* x;
@@ -45,6 +45,7 @@ struct CrArgs {
   int64_t rows;
   int K;       // columns of the quantized row (the raw row has 2K for SwiGLU)
   int digits;  // log4(G); 0: no rotation
+  int wpr;     // waves per row: 1, 2 or 4 (4 / wpr rows per block)
   // RMS adaLN front end (kMod != kModNone)
   const uint16_t* norm_w;   // [K] bf16
   const uint16_t* mscale;   // [mod_count, ldm] bf16
@@ -63,68 +64,103 @@ MXQ_DEVICE double wave_sum_f64(double v) {
   return v;
 }
 
+MXQ_DEVICE uint32_t half_of(const v4u* w, int i) {  // bf16 i of 16 packed in two v4u
+  const uint32_t word = w[i >> 3][(i >> 1) & 3];
+  return (i & 1) ? (word >> 16) : (word & 0xFFFFu);
+}
 
-template <int kAct, int kDtype, int kMod = kModNone>
+// Layout: a 256-thread block holds 4 / wpr rows, wpr waves per row. Window j of wave w (of its
+// row) is window w + j * wpr of the row: 1024 columns, lane l holding columns 16 l .. 16 l + 15.
+// All raw loads of a wave are issued first; the rotated (or, for fp32, float) values stay in
+// registers until the row's absmax is known, so each element is read once and written once.
+// Per-row partial sums and maxima go through LDS, double-buffered by iteration parity so a
+// wave that runs ahead never overwrites a slot another wave still reads.
+template <int kAct, int kDtype, int kMod, int kNW>
 __global__ __launch_bounds__(256) void convrot_quant_kernel(CrArgs p) {
-  constexpr int kE = kDtype == MXQ_DTYPE_F32 ? 4 : 2;
-  extern __shared__ __attribute__((aligned(16))) char smem[];
+  constexpr bool kF32 = kDtype == MXQ_DTYPE_F32;
+  constexpr int kRawWords = kF32 ? 16 : (kAct == MXQ_ACT_SWIGLU ? 16 : 8);  // dwords per window
+  constexpr int kKeepWords = kF32 ? 16 : 8;
+  __shared__ float red_max[2][4];
+  __shared__ double red_ss[2][4];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  char* rowbuf = smem + (int64_t)wave * p.K * kE;
-  const int passes = (p.K + 1023) / 1024;
+  const int wpr = p.wpr, rpb = 4 / wpr;
+  const int slot = wave / wpr, wr = wave - slot * wpr;
+  const int windows = (p.K + 1023) >> 10;
   const double inv = 1.0 / (double)(1 << p.digits);  // 1/sqrt(G), exact
+  const int64_t xstride = kAct == MXQ_ACT_SWIGLU ? 2 * (int64_t)p.K : p.K;
+  int it = 0;
 
-  for (int64_t row = (int64_t)blockIdx.x * kRows + wave; row < p.rows; row += (int64_t)gridDim.x * kRows) {
-    float amax = 0.0f;
-    float rinv = 0.0f;
-    const uint16_t* msc = nullptr;
-    const uint16_t* msh = nullptr;
-    if constexpr (kMod != kModNone) {
-      const uint16_t* xr = reinterpret_cast<const uint16_t*>(p.x) + row * p.K;
-      double ss = 0.0;
-      for (int ps = 0; ps < passes; ++ps) {
-        const int e0 = ps * 1024 + lane * 16;
-        if (e0 >= p.K) continue;
-        double acc = 0.0;  // squares of bf16 values are exact in float32; summed in float64
+  for (int64_t r0 = (int64_t)blockIdx.x * rpb; r0 < p.rows; r0 += (int64_t)gridDim.x * rpb, it ^= 1) {
+    const int64_t row = r0 + slot;
+    const bool row_on = row < p.rows;
+    // ---- raw loads of every window of this wave
+    uint32_t raw[kNW][kRawWords];
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const v4u w = reinterpret_cast<const v4u*>(xr + e0)[c];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float lo = bf16_to_f32(w[i] & 0xFFFFu), hi = bf16_to_f32(w[i] >> 16);
-            acc += (double)(lo * lo) + (double)(hi * hi);
-          }
-        }
-        ss += acc;
-      }
-      ss = wave_sum_f64(ss);
-      const float mean = (float)ss / (float)p.K;
-      rinv = 1.0f / sqrtf(mean + p.eps);
-      int64_t mr = p.mrows[row];
-      mr = mr < 0 ? 0 : (mr >= p.mod_count ? p.mod_count - 1 : mr);
-      msc = p.mscale + mr * p.ldm;
-      msh = p.mshift + mr * p.ldm;
-    }
-    for (int ps = 0; ps < passes; ++ps) {
-      const int e0 = ps * 1024 + lane * 16;
-      const bool on = e0 < p.K;
-      double v[16];
-      // ---- load (+ activation)
-      if (kDtype == MXQ_DTYPE_F32) {
+    for (int j = 0; j < kNW; ++j) {
+      const int e0 = (wr + j * wpr) * 1024 + lane * 16;
+      const bool on = row_on && e0 < p.K;
+      if constexpr (kF32) {
         const v4f* src = reinterpret_cast<const v4f*>(reinterpret_cast<const float*>(p.x) + row * p.K + e0);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const v4f f = on ? src[c] : v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[c * 4 + e] = (double)f[e];
+          for (int e = 0; e < 4; ++e) raw[j][4 * c + e] = __float_as_uint(f[e]);
         }
       } else {
-        const uint16_t* xr = reinterpret_cast<const uint16_t*>(p.x) + row * (kAct == MXQ_ACT_SWIGLU ? 2 * (int64_t)p.K : p.K);
-        v4u w[2], up[2];
+        const uint16_t* xr = reinterpret_cast<const uint16_t*>(p.x) + row * xstride;
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          w[c] = on ? reinterpret_cast<const v4u*>(xr + e0)[c] : v4u{0, 0, 0, 0};
-          if (kAct == MXQ_ACT_SWIGLU) up[c] = on ? reinterpret_cast<const v4u*>(xr + p.K + e0)[c] : v4u{0, 0, 0, 0};
+        for (int c = 0; c < kRawWords / 4; ++c) {
+          const int64_t off = (c < 2 ? 0 : p.K) + e0 + 8 * (c & 1);  // [gate | up] for SwiGLU
+          const v4u w = on ? *reinterpret_cast<const v4u*>(xr + off) : v4u{0, 0, 0, 0};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) raw[j][4 * c + e] = w[e];
         }
+      }
+    }
+    // ---- RMS statistics of the row (RMS adaLN front end)
+    float rinv = 0.0f;
+    const uint16_t* msc = nullptr;
+    const uint16_t* msh = nullptr;
+    if constexpr (kMod != kModNone) {
+      double ss = 0.0;
+#pragma unroll
+      for (int j = 0; j < kNW; ++j) {
+        double acc = 0.0;  // squares of bf16 values are exact in float32; summed in float64
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float lo = bf16_to_f32(raw[j][e] & 0xFFFFu), hi = bf16_to_f32(raw[j][e] >> 16);
+          acc += (double)(lo * lo) + (double)(hi * hi);
+        }
+        ss += acc;
+      }
+      ss = wave_sum_f64(ss);
+      if (lane == 0) red_ss[it][wave] = ss;
+      __syncthreads();
+      double tot = 0.0;
+      for (int i = 0; i < wpr; ++i) tot += red_ss[it][slot * wpr + i];
+      const float mean = (float)tot / (float)p.K;
+      rinv = 1.0f / sqrtf(mean + p.eps);
+      int64_t mr = row_on ? p.mrows[row] : 0;
+      mr = mr < 0 ? 0 : (mr >= p.mod_count ? p.mod_count - 1 : mr);
+      msc = p.mscale + mr * p.ldm;
+      msh = p.mshift + mr * p.ldm;
+    }
+    // ---- activation / modulation, rotation, rounding to the row dtype; absmax
+    uint32_t keep[kNW][kKeepWords];
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kNW; ++j) {
+      const int win = wr + j * wpr;
+      if (win >= windows) break;  // uniform over the wave
+      const int e0 = win * 1024 + lane * 16;
+      const bool on = row_on && e0 < p.K;
+      double v[16];
+      if constexpr (kF32) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = (double)__uint_as_float(raw[j][i]);
+      } else {
+        const v4u* rw = reinterpret_cast<const v4u*>(raw[j]);
         v4u nw[2], sc[2], sh[2];
         if constexpr (kMod != kModNone) {
 #pragma unroll
@@ -137,21 +173,14 @@ __global__ __launch_bounds__(256) void convrot_quant_kernel(CrArgs p) {
         uint32_t ybits[8];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const uint32_t word = w[i >> 3][(i >> 1) & 3];
-          uint32_t b = (i & 1) ? (word >> 16) : (word & 0xFFFFu);
+          uint32_t b = half_of(rw, i);
+          if constexpr (kAct == MXQ_ACT_GELU_TANH) b = gelu_bf16(b);
+          if constexpr (kAct == MXQ_ACT_SWIGLU) b = swiglu_bf16(b, half_of(rw + 2, i));
           if constexpr (kMod != kModNone) {
-            const int sh16 = 16 * (i & 1);
-            const float wn = bf16_to_f32((nw[i >> 3][(i >> 1) & 3] >> sh16) & 0xFFFFu);
-            const float t = round_bf16(1.0f + bf16_to_f32((sc[i >> 3][(i >> 1) & 3] >> sh16) & 0xFFFFu));
-            const float f = bf16_to_f32((sh[i >> 3][(i >> 1) & 3] >> sh16) & 0xFFFFu);
-            const float n = round_bf16((bf16_to_f32(b) * rinv) * wn);
-            b = f32_to_bf16_bits(round_bf16(n * t) + f);
+            const float t = round_bf16(1.0f + bf16_to_f32(half_of(sc, i)));
+            const float n = round_bf16((bf16_to_f32(b) * rinv) * bf16_to_f32(half_of(nw, i)));
+            b = f32_to_bf16_bits(round_bf16(n * t) + bf16_to_f32(half_of(sh, i)));
             if (i & 1) ybits[i >> 1] |= b << 16; else ybits[i >> 1] = b;
-          }
-          if (kAct == MXQ_ACT_GELU_TANH) b = gelu_bf16(b);
-          if (kAct == MXQ_ACT_SWIGLU) {
-            const uint32_t uw = up[i >> 3][(i >> 1) & 3];
-            b = swiglu_bf16(b, (i & 1) ? (uw >> 16) : (uw & 0xFFFFu));
           }
           v[i] = (double)bf16_to_f32(b);
         }
@@ -164,58 +193,45 @@ __global__ __launch_bounds__(256) void convrot_quant_kernel(CrArgs p) {
           if constexpr (kMod == kModOnly) continue;
         }
       }
-      // ---- transform
       rotate16(v, p.digits);
-      // ---- scale, round to the row dtype, keep, absmax
-      if (on) {
-        if (kDtype == MXQ_DTYPE_F32) {
-          float r[16];
+      if constexpr (kF32) {
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            r[i] = (float)(v[i] * inv);
-            amax = fmaxf(amax, fabsf(r[i]));
-          }
+        for (int i = 0; i < 16; ++i) {
+          const float r = (float)(v[i] * inv);
+          keep[j][i] = __float_as_uint(r);
+          if (on) amax = fmaxf(amax, fabsf(r));
+        }
+      } else {
 #pragma unroll
-          for (int c = 0; c < 4; ++c)
-            reinterpret_cast<v4f*>(rowbuf + (int64_t)e0 * 4)[c] = v4f{r[c * 4], r[c * 4 + 1], r[c * 4 + 2], r[c * 4 + 3]};
-        } else {
-          uint32_t h[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const uint32_t lo = f64_to_bf16_bits(v[2 * i] * inv), hi = f64_to_bf16_bits(v[2 * i + 1] * inv);
-            h[i] = lo | (hi << 16);
-            amax = fmaxf(amax, fmaxf(fabsf(bf16_to_f32(lo)), fabsf(bf16_to_f32(hi))));
-          }
-#pragma unroll
-          for (int c = 0; c < 2; ++c)
-            reinterpret_cast<v4u*>(rowbuf + (int64_t)e0 * 2)[c] = v4u{h[c * 4], h[c * 4 + 1], h[c * 4 + 2], h[c * 4 + 3]};
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t lo = f64_to_bf16_bits(v[2 * i] * inv), hi = f64_to_bf16_bits(v[2 * i + 1] * inv);
+          keep[j][i] = lo | (hi << 16);
+          if (on) amax = fmaxf(amax, fmaxf(fabsf(bf16_to_f32(lo)), fabsf(bf16_to_f32(hi))));
         }
       }
     }
     if constexpr (kMod == kModOnly) continue;
+    // ---- row absmax across the row's waves, scale
     amax = wave_max(amax);
+    if (lane == 0) red_max[it][wave] = amax;
+    __syncthreads();
+    amax = red_max[it][slot * wpr];
+    for (int i = 1; i < wpr; ++i) amax = fmaxf(amax, red_max[it][slot * wpr + i]);
     const float s = row_scale_from_absmax(amax);
     const float r = 1.0f / round_bf16(s);
-    for (int ps = 0; ps < passes; ++ps) {
-      const int e0 = ps * 1024 + lane * 16;
-      if (e0 >= p.K) continue;
+    // ---- quantize from registers, 16-byte stores
+#pragma unroll
+    for (int j = 0; j < kNW; ++j) {
+      const int e0 = (wr + j * wpr) * 1024 + lane * 16;
+      if (!row_on || e0 >= p.K) continue;
       int qv[16];
-      if (kDtype == MXQ_DTYPE_F32) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const v4f f = reinterpret_cast<const v4f*>(rowbuf + (int64_t)e0 * 4)[c];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) qv[c * 4 + e] = quant_round_clamp(f[e] / s);
-        }
-      } else {
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const v4u w = reinterpret_cast<const v4u*>(rowbuf + (int64_t)e0 * 2)[c];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            qv[c * 8 + 2 * i] = quant_round_clamp(round_bf16(bf16_to_f32(w[i] & 0xFFFFu) * r));
-            qv[c * 8 + 2 * i + 1] = quant_round_clamp(round_bf16(bf16_to_f32(w[i] >> 16) * r));
-          }
+      for (int i = 0; i < 16; ++i) {
+        if constexpr (kF32) {
+          qv[i] = quant_round_clamp(__uint_as_float(keep[j][i]) / s);
+        } else {
+          const uint32_t h = (keep[j][i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+          qv[i] = quant_round_clamp(round_bf16(bf16_to_f32(h) * r));
         }
       }
       uint32_t o[4];
@@ -225,8 +241,30 @@ __global__ __launch_bounds__(256) void convrot_quant_kernel(CrArgs p) {
                ((uint32_t)(qv[4 * c + 2] & 0xFF) << 16) | ((uint32_t)(qv[4 * c + 3] & 0xFF) << 24);
       *reinterpret_cast<v4u*>(p.q + row * p.K + e0) = v4u{o[0], o[1], o[2], o[3]};
     }
-    if (lane == 0) p.scales[row] = s;
+    if (row_on && wr == 0 && lane == 0) p.scales[row] = s;
   }
+}
+
+// Waves per row and windows per wave for a row of K columns.
+void row_split(int64_t K, int& wpr, int& nw) {
+  const int windows = (int)((K + 1023) / 1024);
+  wpr = windows >= 4 ? 4 : (windows >= 2 ? 2 : 1);
+  nw = (windows + wpr - 1) / wpr;
+}
+
+template <int kAct, int kDtype, int kMod>
+int launch_convrot(const CrArgs& a, int nw, hipStream_t st) {
+  const int rpb = 4 / a.wpr;
+  const unsigned grid = (unsigned)std::min<int64_t>((a.rows + rpb - 1) / rpb, 1 << 20);
+  switch (nw) {
+    case 1: convrot_quant_kernel<kAct, kDtype, kMod, 1><<<grid, 256, 0, st>>>(a); break;
+    case 2: convrot_quant_kernel<kAct, kDtype, kMod, 2><<<grid, 256, 0, st>>>(a); break;
+    case 3: convrot_quant_kernel<kAct, kDtype, kMod, 3><<<grid, 256, 0, st>>>(a); break;
+    case 4: convrot_quant_kernel<kAct, kDtype, kMod, 4><<<grid, 256, 0, st>>>(a); break;
+    case 5: convrot_quant_kernel<kAct, kDtype, kMod, 5><<<grid, 256, 0, st>>>(a); break;
+    default: return mxq_set_error(MXQ_ERR_UNSUPPORTED, "row too wide");
+  }
+  return mxq_check_launch("convrot_quant_kernel");
 }
 
 __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
@@ -265,23 +303,18 @@ extern "C" int mxq_quantize_int8_rowwise_convrot(const void* x, int x_dtype, int
   if (!x || !q || !scales) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
   if (cols % 16) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "columns must be a multiple of 16");
   if ((uintptr_t)x % 16 || (uintptr_t)q % 16) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "x and q must be 16-byte aligned");
-  const int e = x_dtype == MXQ_DTYPE_F32 ? 4 : 2;
-  const int64_t lds = (int64_t)kRows * cols * e;
-  if (lds > 160 * 1024) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "row of %lld columns too wide", (long long)cols);
+  if (cols > (int64_t)kMaxWindows * 1024)
+    return mxq_set_error(MXQ_ERR_UNSUPPORTED, "row of %lld columns too wide (max %d)", (long long)cols, kMaxWindows * 1024);
   CrArgs a{x, q, scales, rows, (int)cols, digits};
-  const int64_t blocks = std::min<int64_t>((rows + kRows - 1) / kRows, 65536);
+  int nw = 1;
+  row_split(cols, a.wpr, nw);
   hipStream_t st = (hipStream_t)stream;
-  const unsigned grid = (unsigned)blocks;
-  if (x_dtype == MXQ_DTYPE_F32) {
-    convrot_quant_kernel<MXQ_ACT_NONE, MXQ_DTYPE_F32><<<grid, 256, (size_t)lds, st>>>(a);
-  } else {
-    switch (input_act) {
-      case MXQ_ACT_NONE: convrot_quant_kernel<MXQ_ACT_NONE, MXQ_DTYPE_BF16><<<grid, 256, (size_t)lds, st>>>(a); break;
-      case MXQ_ACT_GELU_TANH: convrot_quant_kernel<MXQ_ACT_GELU_TANH, MXQ_DTYPE_BF16><<<grid, 256, (size_t)lds, st>>>(a); break;
-      default: convrot_quant_kernel<MXQ_ACT_SWIGLU, MXQ_DTYPE_BF16><<<grid, 256, (size_t)lds, st>>>(a); break;
-    }
+  if (x_dtype == MXQ_DTYPE_F32) return launch_convrot<MXQ_ACT_NONE, MXQ_DTYPE_F32, kModNone>(a, nw, st);
+  switch (input_act) {
+    case MXQ_ACT_NONE: return launch_convrot<MXQ_ACT_NONE, MXQ_DTYPE_BF16, kModNone>(a, nw, st);
+    case MXQ_ACT_GELU_TANH: return launch_convrot<MXQ_ACT_GELU_TANH, MXQ_DTYPE_BF16, kModNone>(a, nw, st);
+    default: return launch_convrot<MXQ_ACT_SWIGLU, MXQ_DTYPE_BF16, kModNone>(a, nw, st);
   }
-  return mxq_check_launch("convrot_quant_kernel");
 }
 
 extern "C" int mxq_swiglu_bf16(const void* x, void* y, int64_t rows, int64_t cols, void* stream) {
@@ -319,9 +352,11 @@ extern "C" int mxq_rms_adaln_quantize_int8(const void* x, const void* norm_weigh
   if ((uintptr_t)x % 16 || (uintptr_t)q % 16 || (uintptr_t)y_out % 16 || (uintptr_t)norm_weight % 16 ||
       (uintptr_t)scale % 16 || (uintptr_t)shift % 16)
     return mxq_set_error(MXQ_ERR_UNSUPPORTED, "tensors must be 16-byte aligned");
-  const int64_t lds = q ? (int64_t)kRows * cols * 2 : 0;
-  if (lds > 160 * 1024) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "row of %lld columns too wide", (long long)cols);
+  if (cols > (int64_t)kMaxWindows * 1024)
+    return mxq_set_error(MXQ_ERR_UNSUPPORTED, "row of %lld columns too wide (max %d)", (long long)cols, kMaxWindows * 1024);
   CrArgs a{x, q, scales, rows, (int)cols, digits};
+  int nw = 1;
+  row_split(cols, a.wpr, nw);
   a.norm_w = (const uint16_t*)norm_weight;
   a.mscale = (const uint16_t*)scale;
   a.mshift = (const uint16_t*)shift;
@@ -330,11 +365,7 @@ extern "C" int mxq_rms_adaln_quantize_int8(const void* x, const void* norm_weigh
   a.mod_count = mod_count;
   a.eps = eps;
   a.y_out = (uint16_t*)y_out;
-  const unsigned grid = (unsigned)std::min<int64_t>((rows + kRows - 1) / kRows, 65536);
   hipStream_t st = (hipStream_t)stream;
-  if (q)
-    convrot_quant_kernel<MXQ_ACT_NONE, MXQ_DTYPE_BF16, kModQuant><<<grid, 256, (size_t)lds, st>>>(a);
-  else
-    convrot_quant_kernel<MXQ_ACT_NONE, MXQ_DTYPE_BF16, kModOnly><<<grid, 256, 0, st>>>(a);
-  return mxq_check_launch("convrot_quant_kernel");
+  if (q) return launch_convrot<MXQ_ACT_NONE, MXQ_DTYPE_BF16, kModQuant>(a, nw, st);
+  return launch_convrot<MXQ_ACT_NONE, MXQ_DTYPE_BF16, kModOnly>(a, nw, st);
 }
