@@ -34,10 +34,11 @@ namespace mxq {
 constexpr int kBM = 256, kBN = 256, kBK = 128;
 constexpr int kGemmThreads = 256;
 constexpr int kWaveM = 128, kWaveN = 128;
-constexpr int kNS = 2;                                  // LDS pipeline stages
 constexpr int kStageA = kBM * kBK, kStageB = kBN * kBK; // 32 KB each
-constexpr int kStageBytes = kStageA + kStageB;
-constexpr int kLoadsPerStage = 16;                      // direct-to-LDS loads per wave per stage
+constexpr int kSlots = 5;                               // LDS ring of 32 KB operand slots (160 KB)
+constexpr int kSlotBytes = 32768;
+constexpr int kLoadsPerOperand = 8;                     // direct-to-LDS loads per wave per operand slot
+constexpr int kEpiLds = 131072;                         // epilogue: per-column factors behind 128 KB
 constexpr int kGroupM = 8;
 
 enum { kEpiI32 = 0, kEpiDequant = 1, kEpiGelu = 2, kEpiGatedRes = 3 };
@@ -111,36 +112,44 @@ MXQ_DEVICE void make_loader(Loader& L, const GemmArgs& p, int64_t m0, int64_t n0
   }
 }
 
-MXQ_DEVICE void issue_stage(const Loader& L, char* stage, int64_t k0, int64_t K) {
+MXQ_DEVICE void issue_a(const Loader& L, char* slot, int64_t k0, int64_t K) {
+  const int w = threadIdx.x >> 6;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const bool kin = k0 + L.koff[t & 1] < K;
+    const void* sa = kin ? (const void*)(L.a[t] + k0) : (const void*)kZeroChunk;
+    __builtin_amdgcn_global_load_lds((gptr_t)sa, (lptr_t)(slot + (w * 8 + t) * 1024), 16, 0, 0);
+  }
+}
+
+MXQ_DEVICE void issue_b(const Loader& L, char* slot, int64_t k0, int64_t K) {
   const int w = threadIdx.x >> 6;
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     const int koff = L.koff[t & 1];
     const bool kin = k0 + koff < K;
-    const void* sa = kin ? (const void*)(L.a[t] + k0) : (const void*)kZeroChunk;
     const void* sb = kin ? (const void*)(L.b[t] + k0 + koff) : (const void*)L.b[t];
-    __builtin_amdgcn_global_load_lds((gptr_t)sa, (lptr_t)(stage + (w * 8 + t) * 1024), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((gptr_t)sb, (lptr_t)(stage + kStageA + (w * 8 + t) * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((gptr_t)sb, (lptr_t)(slot + (w * 8 + t) * 1024), 16, 0, 0);
   }
 }
 
 // Fragments of K-step ks (32 K-bytes) of a stage: A rows wm*128 + i*32 + l%32 and B rows
 // wn*128 + j*32 + l%32, chunk ks*2 + l/32. Every row a lane touches has the same swizzle
 // f = ((l % 32) >> 1) & 7, so one base address per operand serves all four blocks.
-MXQ_DEVICE void load_frags(uint32_t stage, int wm, int wn, int ks, v4i fa[4], v4i fb[4]) {
+MXQ_DEVICE void load_frags(uint32_t slot_a, uint32_t slot_b, int wm, int wn, int ks, v4i fa[4], v4i fb[4]) {
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31;
   const uint32_t x = (uint32_t)(((ks * 2 + (lane >> 5)) ^ swz_f(lr)) << 4);
-  const uint32_t ba = stage + (uint32_t)(wm * kWaveM + lr) * kBK + x;
-  const uint32_t bb = stage + (uint32_t)(wn * kWaveN + lr) * kBK + x;
+  const uint32_t ba = slot_a + (uint32_t)(wm * kWaveM + lr) * kBK + x;
+  const uint32_t bb = slot_b + (uint32_t)(wn * kWaveN + lr) * kBK + x;
   fa[0] = lds_read_b128<0>(ba);
   fa[1] = lds_read_b128<32 * kBK>(ba);
   fa[2] = lds_read_b128<64 * kBK>(ba);
   fa[3] = lds_read_b128<96 * kBK>(ba);
-  fb[0] = lds_read_b128<kStageA>(bb);
-  fb[1] = lds_read_b128<kStageA + 32 * kBK>(bb);
-  fb[2] = lds_read_b128<kStageA + 64 * kBK>(bb);
-  fb[3] = lds_read_b128<kStageA + 96 * kBK>(bb);
+  fb[0] = lds_read_b128<0>(bb);
+  fb[1] = lds_read_b128<32 * kBK>(bb);
+  fb[2] = lds_read_b128<64 * kBK>(bb);
+  fb[3] = lds_read_b128<96 * kBK>(bb);
 }
 
 // The MFMAs compute C^T blocks (weights as the first operand): lane l of a 32 x 32 block then
@@ -152,6 +161,28 @@ MXQ_DEVICE void mma16(const v4i fa[4], const v4i fb[4], v16i acc[4][4]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j], fa[i], acc[i][j], 0, 0, 0);
+}
+
+// The sixteen MFMAs of one K-step with kCount direct-to-LDS loads (loads kFirst .. of one
+// operand slot) interleaved, one after each of the first kCount MFMAs. Spread this way, a load
+// that waits for room in the memory pipeline holds up the wave while its MFMAs still run,
+// rather than after the last of them.
+template <bool kB, int kFirst, int kCount>
+MXQ_DEVICE void mma16_dma(const v4i fa[4], const v4i fb[4], v16i acc[4][4], const Loader& L, char* slot,
+                          int64_t k0, int64_t K, bool on) {
+  const int w = threadIdx.x >> 6;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    acc[q >> 2][q & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[q & 3], fa[q >> 2], acc[q >> 2][q & 3], 0, 0, 0);
+    if (q < kCount && on) {
+      const int t = kFirst + q;  // a constant once the loop is unrolled
+      const int koff = L.koff[t & 1];
+      const bool kin = k0 + koff < K;
+      const void* src = kB ? (kin ? (const void*)(L.b[t] + k0 + koff) : (const void*)L.b[t])
+                           : (kin ? (const void*)(L.a[t] + k0) : (const void*)kZeroChunk);
+      __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)(slot + (w * 8 + t) * 1024), 16, 0, 0);
+    }
+  }
 }
 
 // One run of four consecutive outputs as store words: fp32/int32 outputs give four words,
@@ -272,7 +303,7 @@ MXQ_DEVICE void gated_block_row(const GemmArgs& p, bool full, int64_t row, int64
 
 template <int kEpi, int kOut>
 __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
-  __shared__ __attribute__((aligned(16))) char lds[kNS * kStageBytes + 2 * kBN * 4];
+  __shared__ __attribute__((aligned(16))) char lds[kSlots * kSlotBytes];
 
   int tm, tn;
   tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
@@ -286,68 +317,76 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v16i{};
 
-  // Pipeline: stage s (128 K-bytes of A and B) lives in LDS buffer s % 2. Entering iteration kt,
-  // stage kt is complete and visible, the loads of stage kt+1 are in flight and F0 holds the
-  // fragments of (stage kt, K-step 0). The iteration runs K-steps 0..3 with each step's
-  // fragments read behind the previous step's MFMAs; before the last step's MFMAs it waits for
-  // stage kt+1, passes the barrier that frees buffer kt % 2, issues stage kt+2 into it and
-  // reads (kt+1, 0) -- so that read, too, overlaps matrix work.
+  // Pipeline: a ring of five 32 KB slots receives the operand chunks in the order A0 B0 A1 B1
+  // A2 ..., chunk i (A_j = 2j, B_j = 2j + 1) into slot i % 5; stage j (128 K-bytes) reads A_j
+  // and B_j. Entering iteration kt, A_kt and B_kt are complete and visible, B_kt+1 is in flight
+  // and F0 holds the fragments of (stage kt, K-step 0). The iteration runs K-steps 0..3, each
+  // step's fragments read behind the previous step's MFMAs. A_kt+2 goes into the slot of
+  // B_kt-1 (free since the previous barrier) with its loads spread over the MFMAs of K-steps 0
+  // and 1; before the MFMAs of K-step 3 the wave waits for B_kt+1, passes the barrier that
+  // frees the slots of A_kt and B_kt, reads (kt+1, 0), and spreads the loads of B_kt+2 over
+  // those MFMAs. A chunk is thus requested one to two stages before it is used, and no wave
+  // issues a burst of loads while its matrix pipe sits idle.
   const int ktiles = (int)((p.K + kBK - 1) / kBK);
   Loader ld;
   make_loader(ld, p, m0, n0);
-  issue_stage(ld, lds, 0, p.K);
+  issue_a(ld, lds, 0, p.K);
+  issue_b(ld, lds + kSlotBytes, 0, p.K);
   if (ktiles > 1) {
-    issue_stage(ld, lds + kStageBytes, kBK, p.K);
-    wait_vmcnt<kLoadsPerStage>();
+    issue_a(ld, lds + 2 * kSlotBytes, kBK, p.K);
+    issue_b(ld, lds + 3 * kSlotBytes, kBK, p.K);
+    wait_vmcnt<2 * kLoadsPerOperand>();
   } else {
     wait_vmcnt<0>();
   }
   barrier_no_drain();
 
-  // LDS byte address of the stage buffers (the low 32 bits of the shared-memory pointer).
   const uint32_t lds_addr = (uint32_t)(uintptr_t)(lptr_t)lds;
   v4i f0a[4], f0b[4], f1a[4], f1b[4];
-  load_frags(lds_addr, wm, wn, 0, f0a, f0b);
+  load_frags(lds_addr, lds_addr + kSlotBytes, wm, wn, 0, f0a, f0b);
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   __builtin_amdgcn_sched_barrier(0);
+  int sa = 0;  // slot of A_kt; B_kt is in (sa + 1) % 5
   for (int kt = 0; kt < ktiles; ++kt) {
-    char* cur = lds + (kt & 1) * kStageBytes;
-    const uint32_t cur_a = lds_addr + (uint32_t)((kt & 1) * kStageBytes);
-    const uint32_t nxt_a = lds_addr + (uint32_t)(((kt + 1) & 1) * kStageBytes);
-    // Each group: issue the next K-step's eight fragment reads, wait until only those are
-    // outstanding, run the current K-step's sixteen MFMAs. sched_barrier(0) keeps the groups
-    // in this order.
-    load_frags(cur_a, wm, wn, 1, f1a, f1b);
+    const int sb = sa == kSlots - 1 ? 0 : sa + 1;
+    const int na = sb == kSlots - 1 ? 0 : sb + 1;  // A_kt+1
+    const int nb = na == kSlots - 1 ? 0 : na + 1;  // B_kt+1
+    const int pa = nb == kSlots - 1 ? 0 : nb + 1;  // A_kt+2 (slot of B_kt-1)
+    const uint32_t cur_a = lds_addr + (uint32_t)(sa * kSlotBytes), cur_b = lds_addr + (uint32_t)(sb * kSlotBytes);
+    const bool more2 = kt + 2 < ktiles;
+    const int64_t k2 = (int64_t)(kt + 2) * kBK;
+    load_frags(cur_a, cur_b, wm, wn, 1, f1a, f1b);
+    wait_lgkm8();
+    __builtin_amdgcn_sched_barrier(0);
+    mma16_dma<false, 0, 4>(f0a, f0b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
+    __builtin_amdgcn_sched_barrier(0);
+    load_frags(cur_a, cur_b, wm, wn, 2, f0a, f0b);
+    wait_lgkm8();
+    __builtin_amdgcn_sched_barrier(0);
+    mma16_dma<false, 4, 4>(f1a, f1b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
+    __builtin_amdgcn_sched_barrier(0);
+    load_frags(cur_a, cur_b, wm, wn, 3, f1a, f1b);
     wait_lgkm8();
     __builtin_amdgcn_sched_barrier(0);
     mma16(f0a, f0b, acc);
     __builtin_amdgcn_sched_barrier(0);
-    load_frags(cur_a, wm, wn, 2, f0a, f0b);
-    wait_lgkm8();
-    __builtin_amdgcn_sched_barrier(0);
-    mma16(f1a, f1b, acc);
-    __builtin_amdgcn_sched_barrier(0);
-    load_frags(cur_a, wm, wn, 3, f1a, f1b);
-    wait_lgkm8();
-    __builtin_amdgcn_sched_barrier(0);
-    mma16(f0a, f0b, acc);
-    __builtin_amdgcn_sched_barrier(0);
-    // Stage kt+1 landed and this wave's reads of buffer kt % 2 (K-step 3 included) are done.
-    wait_all();
+    if (more2) {
+      __builtin_amdgcn_s_waitcnt((kLoadsPerOperand & 0xF) | (0x7 << 4));  // vmcnt(8) lgkmcnt(0)
+    } else {
+      wait_all();
+    }
     __builtin_amdgcn_sched_barrier(0);
     if (kt + 1 < ktiles) {
       barrier_no_drain();
-      if (kt + 2 < ktiles) issue_stage(ld, cur, (int64_t)(kt + 2) * kBK, p.K);
+      load_frags(lds_addr + (uint32_t)(na * kSlotBytes), lds_addr + (uint32_t)(nb * kSlotBytes), wm, wn, 0, f0a, f0b);
     }
-    // The last stage reads nothing more: a read left in flight past the loop could land in
-    // registers the compiler has already given to the epilogue.
-    if (kt + 1 < ktiles) load_frags(nxt_a, wm, wn, 0, f0a, f0b);
     __builtin_amdgcn_sched_barrier(0);
-    mma16(f1a, f1b, acc);
+    mma16_dma<true, 0, 8>(f1a, f1b, acc, ld, lds + sa * kSlotBytes, k2, p.K, more2 && kt + 1 < ktiles);
     __builtin_amdgcn_sched_barrier(0);
+    sa = na;
   }
-  // Every wave is done reading the stage buffers before the epilogue reuses them, and the
-  // last (unused) fragment reads have landed before their registers are reused.
+  // Every wave is done reading the ring before the epilogue reuses it, and the last (unused)
+  // fragment reads have landed before their registers are reused.
   wait_all();
   __builtin_amdgcn_sched_barrier(0);
   barrier_no_drain();
@@ -360,7 +399,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
   constexpr int kElem = (kEpi == kEpiI32 || kOut == 0) ? 4 : 2;
   const int lr = lane & 31, lh = lane >> 5;
   const int t = threadIdx.x;
-  float* s_ws = reinterpret_cast<float*>(lds + kNS * kStageBytes);
+  float* s_ws = reinterpret_cast<float*>(lds + kEpiLds);
   float* s_bias = s_ws + kBN;
   const uint16_t* s_gelu = reinterpret_cast<const uint16_t*>(lds);
   const bool has_b = p.bias != nullptr;
