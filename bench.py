@@ -503,6 +503,8 @@ class LinearM1Workload:
         self.ws = [make_int8_weight(n, d, dev, 61 + i) for i in range(self.layers)]
         self.b = make_bias(n, dev, 70)
         self.out = torch.empty(1, n, dtype=torch.bfloat16, device=dev)
+        self.xq = torch.empty(1, d, dtype=torch.int8, device=dev)
+        self.xs = torch.empty(1, dtype=torch.float32, device=dev)
         self.dev = dev
         self.calls = 0
 
@@ -513,7 +515,7 @@ class LinearM1Workload:
         self.calls += 1
         with t("linear_m1"):
             _lib.call("mxq_int8_linear_m1", _p(self.x), _p(w), _p(s), self.n, _p(self.b), _p(self.out), self.n,
-                      self.d, 256, _lib.ACT_NONE, _lib.DTYPE_BF16, None, None, st)
+                      self.d, 256, _lib.ACT_NONE, _lib.DTYPE_BF16, _p(self.xq), _p(self.xs), st)
 
     def ops_per_step(self):
         return 2 * self.n * self.d
@@ -525,7 +527,7 @@ class LinearM1Workload:
         return self.n * self.d + 2 * self.d + 2 * self.n + 4 * self.n + 2 * self.n
 
     def dominant(self, timer):
-        return {"span": "linear_m1", "symbol": "linear_m1_kernel", "ops": self.ops_per_step(),
+        return {"span": "linear_m1", "symbol": "gemv_i8_kernel", "ops": self.ops_per_step(),
                 "bytes": self.alg_bytes(), "bound": "hbm"}
 
     def config(self):

@@ -144,18 +144,18 @@ int mxq_int8_gemm_gated_residual(const int8_t* a, const int8_t* b, const float* 
                                  int64_t M, int64_t N, int64_t K, void* stream);
 
 /*
- * M = 1 INT8 linear in one launch: the row quantizer of x (after the optional input activation
- * and ConvRot rotation, exactly as mxq_quantize_int8_rowwise_convrot with rows = 1), the INT8
- * GEMV against w [N, K] and the dequant epilogue of mxq_int8_gemm_dequant (same roundings, so
- * the result equals the batched path's row). x bf16 [K] ([2K] for MXQ_ACT_SWIGLU); K % 16 == 0,
- * K <= 16384; group_size 0 or a power of 4 up to 1024 dividing K. xq_out (int8 [K]) and
- * xs_out (fp32 [1]) optionally receive the quantized row.
+ * M = 1 INT8 linear: the row quantizer of x (after the optional input activation and ConvRot
+ * rotation, exactly as mxq_quantize_int8_rowwise_convrot with rows = 1) into the caller's
+ * workspace xq (int8 [K], 16-byte aligned) / xs (fp32 [1]), then a weight-streaming INT8 GEMV
+ * against w [N, K] with the dequant epilogue of mxq_int8_gemm_dequant (same roundings, so the
+ * result equals the batched path's row). Two launches on `stream`. x bf16 [K] ([2K] for
+ * MXQ_ACT_SWIGLU); K % 16 == 0, K <= 16384; group_size 0 or a power of 4 up to 1024 dividing K.
  * Replaces: int8_linear_m1 (CK/backends/cuda/__init__.py:1999-2034; CK/backends/cuda/ops/
  * int8_linear.cu:1490-1590).
  */
 int mxq_int8_linear_m1(const void* x_bf16, const int8_t* w, const float* ws, int64_t ws_numel,
                        const void* bias, void* out, int64_t N, int64_t K, int64_t group_size,
-                       int input_act, int out_dtype, int8_t* xq_out, float* xs_out, void* stream);
+                       int input_act, int out_dtype, int8_t* xq, float* xs, void* stream);
 
 /*
  * M = 1 INT8 GEMV + dequant epilogue from an already quantized row (xq int8 [K], xs fp32 [1]);

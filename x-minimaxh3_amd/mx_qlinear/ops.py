@@ -471,13 +471,15 @@ def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tenso
         return torch.empty((*lead, n), dtype=out_dtype, device=dev)
     x2 = x.reshape(-1, x.shape[-1])
     if x2.shape[0] == 1 and x.dtype == torch.bfloat16 and _m1_ok(width) and n:
-        # one token: quantizer, GEMV and epilogue in one launch (int8_linear_m1's route)
+        # one token: the row quantizer, then the weight-streaming GEMV (int8_linear_m1's route)
         ws = _weight_scale(weight_scale, n, dev)
         b = _bias(bias, n, out_dtype, dev)
         out = torch.empty((1, n), dtype=out_dtype, device=dev)
+        xq = torch.empty((1, width), dtype=torch.int8, device=dev)
+        xs = torch.empty((1, 1), dtype=torch.float32, device=dev)
         with torch.cuda.device(dev):
             call("mxq_int8_linear_m1", _p(_aligned16(x2)), _p(_aligned16(weight)), _p(ws), ws.numel(), _p(b),
-                 _p(out), n, width, convrot_groupsize if convrot else 0, act, _out_code(out_dtype), None, None,
+                 _p(out), n, width, convrot_groupsize if convrot else 0, act, _out_code(out_dtype), _p(xq), _p(xs),
                  _stream(dev))
         return out.reshape(*lead, n)
     if convrot:
