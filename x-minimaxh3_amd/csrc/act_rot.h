@@ -58,9 +58,12 @@ MXQ_DEVICE uint32_t f64_to_bf16_bits(double x) {
 }
 
 // One radix-4 step on four values (the quad of one digit).
+// y_k = S - 2 x_{3-k} is one fma: -2 x is exact, so fma(-2, x, S) rounds S - (x + x) once, as
+// the separate doubling and subtraction do.
 MXQ_DEVICE void h4_quad(double& x0, double& x1, double& x2, double& x3) {
   const double s = (x0 + x1) + (x2 + x3);
-  const double y0 = s - (x3 + x3), y1 = s - (x2 + x2), y2 = s - (x1 + x1), y3 = s - (x0 + x0);
+  const double y0 = __builtin_fma(-2.0, x3, s), y1 = __builtin_fma(-2.0, x2, s);
+  const double y2 = __builtin_fma(-2.0, x1, s), y3 = __builtin_fma(-2.0, x0, s);
   x0 = y0;
   x1 = y1;
   x2 = y2;
@@ -111,7 +114,7 @@ MXQ_DEVICE void rotate16(double* v, int digits) {
       const double t = v[j] + __shfl_xor(v[j], m, kWave);
       const double s = t + __shfl_xor(t, 2 * m, kWave);
       const double q3 = __shfl_xor(v[j], 3 * m, kWave);
-      v[j] = s - (q3 + q3);
+      v[j] = __builtin_fma(-2.0, q3, s);
     }
   }
 }

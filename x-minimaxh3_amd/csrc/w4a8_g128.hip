@@ -4,10 +4,10 @@
 // K-groups g in order, P_g = sum over the group of a[m, k] * (c[n, k] - 8) exactly in int32
 // (the contract of the general kernel in w4a8.hip; this file is its fast path for group 128).
 //
-// This translation unit is compiled with the MFMA accumulators in VGPRs
-// (-mllvm --amdgpu-mfma-vgpr-form, set by the build): the per-group fold reads every
-// accumulator with VALU instructions, which cannot address AGPRs, so AGPR accumulators would
-// cost one extra copy per element and group.
+// The compiler places the int32 MFMA accumulators in AGPRs; the per-group fold reads them with
+// v_accvgpr_read (one copy per element and group). Keeping them in VGPRs instead
+// (-mllvm --amdgpu-mfma-vgpr-form) measured slower here: with the fp32 accumulators also live,
+// the VGPR form spilled.
 //
 // Workgroup: 4 wave64s side by side along N; a 128 x 128 tile, wave w owning channels
 // w*32 + [0, 32) of all 128 rows as four v_mfma_i32_32x32x32_i8 blocks (activations first:

@@ -48,11 +48,8 @@ def _hipcc() -> str:
     return found
 
 
-# Per-source flags. w4a8_g128.hip keeps MFMA accumulators in VGPRs: its per-group fold reads
-# every accumulator with VALU instructions, which cannot address AGPRs.
-FILE_FLAGS = {
-    # "w4a8_g128.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"],
-}
+# Per-source compiler flags (none needed at present; the hook stays for per-kernel tuning).
+FILE_FLAGS: dict[str, list[str]] = {}
 
 
 def _compile(src: pathlib.Path, extra: list[str]) -> pathlib.Path:
