@@ -147,3 +147,26 @@ def test_convrot_rejects_bad_group_sizes(dev):
     w, ws = int8_weight(64, 768, 2)
     with pytest.raises(ValueError):
         _mx().int8_linear(x, w.to(dev), ws.to(dev), convrot=True, convrot_groupsize=32)
+
+
+@pytest.mark.parametrize("g", [256, 0])
+def test_convrot_nan_and_inf_rows_follow_the_oracle(dev, g):
+    """NaN / inf inputs spread through the rotation group; the absmax propagates NaN (torch's
+    amax), so such rows quantize to 0 with a NaN or inf scale."""
+    x = activations(6, 1024, 41)
+    x[1, 17] = float("nan")
+    x[2, 5] = float("inf")
+    x[3, 9] = -float("inf")
+    x[3, 700] = float("inf")
+    q, s = _mx().quantize_int8_rowwise_convrot(x.to(dev), g)
+    with np.errstate(invalid="ignore"):
+        qr, sr, _ = cr.convrot_quantize_bf16(bits(x), g)
+    assert np.array_equal(q.cpu().numpy(), qr)
+    assert np.array_equal(s.cpu().numpy(), sr, equal_nan=True)
+    xf = x.float() * 1.5
+    xf[4, 3] = float("nan")
+    q2, s2 = _mx().quantize_int8_rowwise_convrot(xf.to(dev), g or 256)
+    with np.errstate(invalid="ignore"):
+        qr2, sr2, _ = cr.convrot_quantize_f32(xf.numpy(), g or 256)
+    assert np.array_equal(q2.cpu().numpy(), qr2)
+    assert np.array_equal(s2.cpu().numpy(), sr2, equal_nan=True)

@@ -163,3 +163,36 @@ def test_adaln_modulation_groups(dev):
     for g in range(4):
         yg = _mx().adaln(x[4 * g:4 * g + 4].to(dev), sc[g].to(dev), sh[g].to(dev))
         assert torch.equal(y[4 * g:4 * g + 4], yg)
+
+
+def _nan_inf_rows(m, k, dtype, seed):
+    """Rows with a NaN, with +-inf, with both, and plain rows (torch's amax propagates NaN)."""
+    x = activations(m, k, seed).to(dtype)
+    x[1, 17] = float("nan")
+    x[2, 5] = float("inf")
+    x[3, 9] = -float("inf")
+    x[4, 7] = float("nan")
+    x[4, 8] = float("inf")
+    return x
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("k", [1000, 5120])
+def test_quant_nan_and_inf_rows_follow_torch(dev, dtype, k):
+    """A NaN makes the row's scale NaN and every q 0; an inf makes the scale inf and q 0
+    (torch: amax propagates NaN, x / inf = 0, NaN -> int8 = 0)."""
+    x = _nan_inf_rows(7, k, dtype, 3)
+    q, s = _mx().quantize_int8_rowwise(x.to(dev))
+    q_ref, s_ref = eager_torch.quantize_int8_rowwise(x)
+    assert torch.equal(q.cpu(), q_ref)
+    assert torch.equal(s.cpu().isnan(), s_ref.isnan())
+    assert torch.equal(torch.nan_to_num(s.cpu()), torch.nan_to_num(s_ref))
+    assert bool(s[1].isnan()) and bool(s[2].isinf()) and int(q[1:5].abs().max()) == 0
+
+
+def test_adaln_quant_nan_row(dev):
+    x, sc, sh = _adaln_inputs(5, 1024, 9)
+    x[2, 100] = float("nan")
+    q, s = _mx().adaln_quantize_int8(x.to(dev), sc.to(dev), sh.to(dev), 1e-6)
+    assert bool(s[2].isnan()) and int(q[2].abs().max()) == 0
+    assert not bool(s[[0, 1, 3, 4]].isnan().any())

@@ -80,7 +80,7 @@ __global__ __launch_bounds__(256) void convrot_quant_kernel(CrArgs p) {
   constexpr bool kF32 = kDtype == MXQ_DTYPE_F32;
   constexpr int kRawWords = kF32 ? 16 : (kAct == MXQ_ACT_SWIGLU ? 16 : 8);  // dwords per window
   constexpr int kKeepWords = kF32 ? 16 : 8;
-  __shared__ float red_max[2][4];
+  __shared__ uint32_t red_max[2][4];
   __shared__ double red_ss[2][4];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int wpr = p.wpr, rpb = 4 / wpr;
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void convrot_quant_kernel(CrArgs p) {
     }
     // ---- activation / modulation, rotation, rounding to the row dtype; absmax
     uint32_t keep[kNW][kKeepWords];
-    float amax = 0.0f;
+    uint32_t amax = 0;  // |value| bits (f32 rows) or packed |bf16| pairs (bf16 rows)
 #pragma unroll
     for (int j = 0; j < kNW; ++j) {
       const int win = wr + j * wpr;
@@ -199,25 +199,25 @@ __global__ __launch_bounds__(256) void convrot_quant_kernel(CrArgs p) {
         for (int i = 0; i < 16; ++i) {
           const float r = (float)(v[i] * inv);
           keep[j][i] = __float_as_uint(r);
-          if (on) amax = fmaxf(amax, fabsf(r));
+          if (on) amax = amax > abs_bits(r) ? amax : abs_bits(r);
         }
       } else {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const uint32_t lo = f64_to_bf16_bits(v[2 * i] * inv), hi = f64_to_bf16_bits(v[2 * i + 1] * inv);
           keep[j][i] = lo | (hi << 16);
-          if (on) amax = fmaxf(amax, fmaxf(fabsf(bf16_to_f32(lo)), fabsf(bf16_to_f32(hi))));
+          if (on) amax = absmax_acc_bf16x2(amax, keep[j][i]);
         }
       }
     }
     if constexpr (kMod == kModOnly) continue;
     // ---- row absmax across the row's waves, scale
-    amax = wave_max(amax);
-    if (lane == 0) red_max[it][wave] = amax;
+    const float wmax = wave_absmax(kF32 ? amax : absmax_bits_of_bf16x2(amax));
+    if (lane == 0) red_max[it][wave] = __float_as_uint(wmax);
     __syncthreads();
-    amax = red_max[it][slot * wpr];
-    for (int i = 1; i < wpr; ++i) amax = fmaxf(amax, red_max[it][slot * wpr + i]);
-    const float s = row_scale_from_absmax(amax);
+    uint32_t rmax = red_max[it][slot * wpr];
+    for (int i = 1; i < wpr; ++i) rmax = rmax > red_max[it][slot * wpr + i] ? rmax : red_max[it][slot * wpr + i];
+    const float s = row_scale_from_absmax(__uint_as_float(rmax));
     const float r = 1.0f / round_bf16(s);
     // ---- quantize from registers, 16-byte stores
 #pragma unroll

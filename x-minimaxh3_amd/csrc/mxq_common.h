@@ -158,13 +158,7 @@ static __device__ __attribute__((aligned(16))) const GeluFullTable kGeluFull = m
 
 MXQ_DEVICE uint32_t gelu_bf16(uint32_t b) { return kGeluFull.v[b & 0xFFFFu]; }
 
-// ---- wave reductions --------------------------------------------------------------
-
-MXQ_DEVICE float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
-}
+// ---- wave reductions ----------------------------------------------------------------
 
 MXQ_DEVICE float wave_sum(float v) {
 #pragma unroll
@@ -172,32 +166,35 @@ MXQ_DEVICE float wave_sum(float v) {
   return v;
 }
 
-// max over the 32 lanes of each half-wave (lanes sharing l / 32).
-MXQ_DEVICE float halfwave_max(float v) {
+// ---- absolute maxima with torch's NaN propagation ----------------------------------------
+// |x| as bits: non-negative floats order like their bit patterns and a NaN (sign cleared) sorts
+// above +inf, so an integer maximum of these bits is |x|'s maximum with NaN propagated, as
+// torch's amax does (an IEEE fmax would drop the NaN).
+MXQ_DEVICE uint32_t abs_bits(float x) { return __float_as_uint(x) & 0x7FFFFFFFu; }
+
+typedef unsigned short mxq_us2 __attribute__((ext_vector_type(2)));
+
+// Running maximum of |bf16| over packed pairs: both halves at once (v_pk_max_u16).
+MXQ_DEVICE uint32_t absmax_acc_bf16x2(uint32_t acc, uint32_t w) {
+  const mxq_us2 m = __builtin_elementwise_max(__builtin_bit_cast(mxq_us2, acc),
+                                              __builtin_bit_cast(mxq_us2, w & 0x7FFF7FFFu));
+  return __builtin_bit_cast(uint32_t, m);
+}
+
+// The float bits of the larger half of such a packed accumulator.
+MXQ_DEVICE uint32_t absmax_bits_of_bf16x2(uint32_t acc) {
+  const uint32_t lo = acc & 0xFFFFu, hi = acc >> 16;
+  return (lo > hi ? lo : hi) << 16;
+}
+
+// Maximum of absolute-value bits across the wave, returned as the float.
+MXQ_DEVICE float wave_absmax(uint32_t bits) {
 #pragma unroll
-  for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
-}
-
-// One DPP step of a max reduction: v = max(v, v of the lane selected by kCtrl). Lanes of rows
-// outside kRowMask keep their own value.
-template <int kCtrl, int kRowMask = 0xF>
-MXQ_DEVICE float dpp_max(float v) {
-  const int s = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), kCtrl, kRowMask,
-                                            0xF, false);
-  return fmaxf(v, __int_as_float(s));
-}
-
-// Max over each half-wave (lanes 0-31, 32-63) with DPP only: swap neighbours, swap pairs,
-// half-row mirror, row mirror (each 16-lane row now holds its max), then broadcast lane 15 of
-// rows 0 and 2 into rows 1 and 3. The result is valid in lanes 16-31 and 48-63.
-MXQ_DEVICE float halfwave_max_dpp(float v) {
-  v = dpp_max<0xB1>(v);        // quad_perm [1, 0, 3, 2]
-  v = dpp_max<0x4E>(v);        // quad_perm [2, 3, 0, 1]
-  v = dpp_max<0x141>(v);       // row_half_mirror
-  v = dpp_max<0x140>(v);       // row_mirror
-  v = dpp_max<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
-  return v;
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t other = (uint32_t)__shfl_xor((int)bits, o, kWave);
+    bits = bits > other ? bits : other;
+  }
+  return __uint_as_float(bits);
 }
 
 // Non-negative floats order like their bit patterns; NaN (0x7FC00000) sorts above +inf.

@@ -45,9 +45,6 @@ MXQ_DEVICE uint32_t gelu_pair(uint32_t w) {
   return gelu_bf16(w & 0xFFFFu) | (gelu_bf16(w >> 16) << 16);
 }
 
-MXQ_DEVICE float absmax_pair(uint32_t w) {
-  return fmaxf(fabsf(bf16_lo(w)), fabsf(bf16_hi(w)));
-}
 
 // bf16 rows, cols % 8 == 0, cols <= 512 * NCH: row held in registers.
 template <int NCH, bool kGelu>
@@ -60,7 +57,7 @@ __global__ __launch_bounds__(kQuantBlock) void quant_rows_bf16_reg(
        row += (int64_t)gridDim.x * kRowsPerBlock) {
     const v4u* src = reinterpret_cast<const v4u*>(x + row * cols);
     v4u v[NCH];
-    float m = 0.0f;
+    uint32_t m = 0;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int c = lane + j * kWave;
@@ -71,10 +68,10 @@ __global__ __launch_bounds__(kQuantBlock) void quant_rows_bf16_reg(
           for (int i = 0; i < 4; ++i) v[j][i] = gelu_pair(v[j][i]);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) m = fmaxf(m, absmax_pair(v[j][i]));
+        for (int i = 0; i < 4; ++i) m = absmax_acc_bf16x2(m, v[j][i]);
       }
     }
-    const float amax = wave_max(m);
+    const float amax = wave_absmax(absmax_bits_of_bf16x2(m));
     const float s = row_scale_from_absmax(amax);
     const float r = 1.0f / round_bf16(s);
     v2u* dst = reinterpret_cast<v2u*>(q + row * cols);
@@ -106,9 +103,12 @@ __global__ __launch_bounds__(kQuantBlock) void quant_rows_generic(
       if (kGelu) f = bf16_to_f32(gelu_bf16(f32_to_bf16_bits(f)));
       return f;
     };
-    float m = 0.0f;
-    for (int64_t i = lane; i < cols; i += kWave) m = fmaxf(m, fabsf(load(i)));
-    const float amax = wave_max(m);
+    uint32_t m = 0;
+    for (int64_t i = lane; i < cols; i += kWave) {
+      const uint32_t b = abs_bits(load(i));
+      m = m > b ? m : b;
+    }
+    const float amax = wave_absmax(m);
     const float s = row_scale_from_absmax(amax);
     float s_math;
     if (kDtype == MXQ_DTYPE_BF16) {
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(kQuantBlock) void adaln_rows_reg(
     }
     const float var = wave_sum(ss) / (float)cols;
     const float rstd = 1.0f / sqrtf(var + eps);
-    float m = 0.0f;
+    uint32_t m = 0;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int c = lane + j * kWave;
@@ -209,13 +209,13 @@ __global__ __launch_bounds__(kQuantBlock) void adaln_rows_reg(
           const uint32_t lo = modulate(bf16_lo(v[j][i]), mean, rstd, sc[i] & 0xFFFF, sh[i] & 0xFFFF);
           const uint32_t hi = modulate(bf16_hi(v[j][i]), mean, rstd, sc[i] >> 16, sh[i] >> 16);
           v[j][i] = lo | (hi << 16);
-          m = fmaxf(m, absmax_pair(v[j][i]));
+          m = absmax_acc_bf16x2(m, v[j][i]);
         }
         if (y_out != nullptr) reinterpret_cast<v4u*>(y_out + row * cols)[c] = v[j];
       }
     }
     if (kQuant) {
-      const float amax = wave_max(m);
+      const float amax = wave_absmax(absmax_bits_of_bf16x2(m));
       const float s = row_scale_from_absmax(amax);
       const float r = 1.0f / round_bf16(s);
       v2u* dst = reinterpret_cast<v2u*>(q + row * cols);
