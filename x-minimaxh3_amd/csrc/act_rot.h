@@ -94,6 +94,16 @@ MXQ_DEVICE void load16_act(const uint16_t* xr, int64_t K, int e0, bool on, doubl
   }
 }
 
+// v of lane ^ x within each quad of lanes (x = 1, 2, 3 as quad_perm 0xB1, 0x4E, 0x1B), through
+// DPP moves on the two halves: no LDS traffic, unlike a general lane shuffle.
+template <int kQuadPerm>
+MXQ_DEVICE double quad_xor(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const int lo = __builtin_amdgcn_mov_dpp((int)(uint32_t)b, kQuadPerm, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_mov_dpp((int)(uint32_t)(b >> 32), kQuadPerm, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
 // The unscaled rotation (x @ H_G * sqrt(G)) of the 16 values of each lane, where lane l of the
 // wave holds columns 16 l .. 16 l + 15 of a 1024-column window: digits 0 and 1 of the in-group
 // index are inside the lane, digit d >= 2 is lane bit pair d - 2 (xor shuffles with masks m, 2m,
@@ -107,7 +117,15 @@ MXQ_DEVICE void rotate16(double* v, int digits) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) h4_quad(v[j], v[j + 4], v[j + 8], v[j + 12]);
   }
-  for (int d = 2; d < digits; ++d) {
+  if (digits >= 3) {  // digit 2: lane bits 0-1, the quads of one DPP quad_perm group
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const double t = v[j] + quad_xor<0xB1>(v[j]);  // lane ^ 1
+      const double s = t + quad_xor<0x4E>(t);        // lane ^ 2
+      v[j] = __builtin_fma(-2.0, quad_xor<0x1B>(v[j]), s);  // lane ^ 3
+    }
+  }
+  for (int d = 3; d < digits; ++d) {
     const int m = 1 << (2 * (d - 2));
 #pragma unroll
     for (int j = 0; j < 16; ++j) {

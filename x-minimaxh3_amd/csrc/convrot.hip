@@ -75,8 +75,12 @@ MXQ_DEVICE uint32_t half_of(const v4u* w, int i) {  // bf16 i of 16 packed in tw
 // registers until the row's absmax is known, so each element is read once and written once.
 // Per-row partial sums and maxima go through LDS, double-buffered by iteration parity so a
 // wave that runs ahead never overwrites a slot another wave still reads.
-template <int kAct, int kDtype, int kMod, int kNW>
-__global__ __launch_bounds__(256) void convrot_quant_kernel(CrArgs p) {
+// kOcc: waves per SIMD the register allocation must allow. Three keeps a bf16 row of up to four
+// windows per wave in registers (two leave the memory pipeline short of loads in flight); the
+// fp32, the five-window and the RMS-front-end four-window forms need more registers than that.
+template <int kAct, int kDtype, int kMod, int kNW,
+          int kOcc = (kDtype == MXQ_DTYPE_F32 || kNW > 4 || (kMod != kModNone && kNW > 3)) ? 2 : 3>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOcc))) void convrot_quant_kernel(CrArgs p) {
   constexpr bool kF32 = kDtype == MXQ_DTYPE_F32;
   constexpr int kRawWords = kF32 ? 16 : (kAct == MXQ_ACT_SWIGLU ? 16 : 8);  // dwords per window
   constexpr int kKeepWords = kF32 ? 16 : 8;
