@@ -104,10 +104,20 @@ MXQ_DEVICE double quad_xor(double v) {
   return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
 }
 
+// v of lane (i - kN) mod 16 within each 16-lane row (DPP row_ror), on the two halves.
+template <int kN>
+MXQ_DEVICE double row_ror(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const int lo = __builtin_amdgcn_mov_dpp((int)(uint32_t)b, 0x120 + kN, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_mov_dpp((int)(uint32_t)(b >> 32), 0x120 + kN, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
 // The unscaled rotation (x @ H_G * sqrt(G)) of the 16 values of each lane, where lane l of the
 // wave holds columns 16 l .. 16 l + 15 of a 1024-column window: digits 0 and 1 of the in-group
 // index are inside the lane, digit d >= 2 is lane bit pair d - 2 (xor shuffles with masks m, 2m,
-// 3m, m = 4^(d-2)). All lanes of the wave must call it (the shuffles are wave-wide).
+// 3m, m = 4^(d-2); DPP moves for d = 2, 3). All lanes of the wave must call it (the shuffles
+// are wave-wide).
 MXQ_DEVICE void rotate16(double* v, int digits) {
   if (digits >= 1) {
 #pragma unroll
@@ -125,7 +135,19 @@ MXQ_DEVICE void rotate16(double* v, int digits) {
       v[j] = __builtin_fma(-2.0, quad_xor<0x1B>(v[j]), s);  // lane ^ 3
     }
   }
-  for (int d = 3; d < digits; ++d) {
+  if (digits >= 4) {  // digit 3: lane bits 2-3, i.e. lanes i, i +- 4, i + 8 of a 16-lane row
+    // Partner digit k ^ 1 is the lane 4 above for even k and 4 below for odd k; k ^ 3 the other
+    // way round; k ^ 2 is 8 away either way. Row rotations by 12, 4 and 8 give all three.
+    const bool even = ((threadIdx.x >> 2) & 1) == 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const double up = row_ror<12>(v[j]), dn = row_ror<4>(v[j]);
+      const double t = v[j] + (even ? up : dn);
+      const double s = t + row_ror<8>(t);
+      v[j] = __builtin_fma(-2.0, even ? dn : up, s);
+    }
+  }
+  for (int d = 4; d < digits; ++d) {
     const int m = 1 << (2 * (d - 2));
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
