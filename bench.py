@@ -15,7 +15,7 @@ restatement) timed on this host on a bounded row sample.
 Other workloads (--workload): qkv_adaln (fused adaLN + quant + QKV GEMM, M=75600, N=15360),
 w4a8_gemm (8192 x 5120 x 5120, group 128), w4a8_skinny (512 x 10240 x 5120), linear_c1
 (1024 x 3072 x 3072), and the H3 model's own shapes (hidden 5376, ConvRot 256 on every layer):
-h3_mlp (rms_adaln -> fc1 -> SwiGLU -> fc2 with the gated residual epilogue), h3_qkv (rms_adaln +
+h3_mlp (rms_adaln -> fc1 with SwiGLU in the epilogue -> fc2 with the gated residual epilogue), h3_qkv (rms_adaln +
 quant -> QKV 5376 -> 21504), linear_m1 (one token through the QKV projection, weight streaming).
 """
 
@@ -355,8 +355,8 @@ class _H3Modulation:
 
 class H3MlpWorkload:
     """The H3 block's MLP half at 720p x 5 s: rms_adaln + ConvRot-256 quant -> fc1 (5376 ->
-    2 x 14336, bias) -> SwiGLU + ConvRot-256 quant -> fc2 (14336 -> 5376, bias) with the gated
-    residual update of the hidden state in place."""
+    2 x 14336, bias) with SwiGLU in its epilogue -> ConvRot-256 quant -> fc2 (14336 -> 5376,
+    bias) with the gated residual update of the hidden state in place."""
 
     name = "h3_mlp_swiglu_convrot_720p"
 
@@ -367,9 +367,10 @@ class H3MlpWorkload:
         self.w1, self.s1 = make_int8_weight(2 * inner, d, dev, 45)
         self.w2, self.s2 = make_int8_weight(d, inner, dev, 46)
         self.b1, self.b2 = make_bias(2 * inner, dev, 47), make_bias(d, dev, 48)
+        self.fc1 = mx_qlinear.prepare_swiglu_fc1(self.w1, self.s1, self.b1)  # once per layer
         self.q1 = torch.empty(m, d, dtype=torch.int8, device=dev)
         self.xs1 = torch.empty(m, dtype=torch.float32, device=dev)
-        self.raw = torch.empty(m, 2 * inner, dtype=torch.bfloat16, device=dev)
+        self.h = torch.empty(m, inner, dtype=torch.bfloat16, device=dev)
         self.q2 = torch.empty(m, inner, dtype=torch.int8, device=dev)
         self.xs2 = torch.empty(m, dtype=torch.float32, device=dev)
         self.dev = dev
@@ -381,12 +382,12 @@ class H3MlpWorkload:
         with t("rms_adaln_quant"):
             _lib.call("mxq_rms_adaln_quantize_int8", _p(self.res), _p(mod.norm_w), _p(mod.scale), _p(mod.shift), d, 3,
                       _p(mod.rows), mod.eps, None, _p(self.q1), _p(self.xs1), m, d, 256, st)
-        with t("fc1_gemm"):
-            _lib.call("mxq_int8_gemm_dequant", _p(self.q1), _p(self.w1), _p(self.xs1), _p(self.s1), 2 * f,
-                      _p(self.b1), _p(self.raw), m, 2 * f, d, 2 * f, _lib.DTYPE_BF16, st)
-        with t("swiglu_convrot_quant"):
-            _lib.call("mxq_quantize_int8_rowwise_convrot", _p(self.raw), _lib.DTYPE_BF16, _p(self.q2), _p(self.xs2),
-                      m, f, 256, _lib.ACT_SWIGLU, st)
+        with t("fc1_swiglu_gemm"):
+            _lib.call("mxq_int8_gemm_dequant_swiglu", _p(self.q1), _p(self.fc1.qweight), _p(self.xs1),
+                      _p(self.fc1.scale), 2 * f, _p(self.fc1.bias), _p(self.h), m, 2 * f, d, f, st)
+        with t("convrot_quant"):
+            _lib.call("mxq_quantize_int8_rowwise_convrot", _p(self.h), _lib.DTYPE_BF16, _p(self.q2), _p(self.xs2),
+                      m, f, 256, _lib.ACT_NONE, st)
         with t("fc2_gated_residual"):
             _lib.call("mxq_int8_gemm_gated_residual", _p(self.q2), _p(self.w2), _p(self.xs2), _p(self.s2), d,
                       _p(self.b2), _p(self.res), d, _p(mod.gate), d, 3, _p(mod.rows), m, d, f, st)
@@ -399,8 +400,8 @@ class H3MlpWorkload:
 
     def dominant(self, timer):
         m, d, f = self.m, self.d, self.inner
-        fc1 = {"span": "fc1_gemm", "symbol": "gemm_i8_kernel<1, 2>", "ops": 2 * m * d * 2 * f,
-               "bytes": m * d + 2 * f * d + 2 * m * 2 * f + 4 * m + 4 * 2 * f + 2 * 2 * f}
+        fc1 = {"span": "fc1_swiglu_gemm", "symbol": "gemm_i8_kernel<4, 2>", "ops": 2 * m * d * 2 * f,
+               "bytes": m * d + 2 * f * d + 2 * m * f + 4 * m + 4 * 2 * f + 2 * 2 * f}
         fc2 = {"span": "fc2_gated_residual", "symbol": "gemm_i8_kernel<3, 2>", "ops": 2 * m * f * d,
                # A, W2, residual read + written, gate rows, xs, ws, bias
                "bytes": m * f + d * f + 4 * m * d + 4 * m + 4 * m + 4 * d + 2 * d + 6 * d}
@@ -409,7 +410,7 @@ class H3MlpWorkload:
     def config(self):
         return {"workload": self.name, "tokens": self.m, "d_model": self.d, "swiglu_inner": self.inner,
                 "norm": "rms_adaln eps 1e-6, 3 segments", "convrot_group": 256,
-                "epilogue": "fc2 gated residual in place"}
+                "epilogue": "fc1 SwiGLU; fc2 gated residual in place"}
 
     def cpu_baseline(self, budget_s):
         from oracle import eager_torch

@@ -126,6 +126,22 @@ int mxq_int8_gemm_dequant_gelu_absmax(const int8_t* a, const int8_t* b, const fl
                                       int64_t K, int64_t ldh, void* stream);
 
 /*
+ * SwiGLU fc1: INT8 GEMM + the bf16 dequant epilogue of mxq_int8_gemm_dequant, then
+ *   h[m, c] = bf16(bf16(silu(y[m, gate c])) * y[m, up c])        (NaN products -> 0x7FC0)
+ * written as h bf16 [M, N / 2] (row stride ldh). b / ws / bias are fc1's [N] rows in the
+ * prepared order: for each block of 32 rows, the 16 gate rows 16 b .. 16 b + 15 of the original
+ * [gate | up] weight, then the 16 up rows N/2 + 16 b .. N/2 + 16 b + 15. N % 32 == 0.
+ * Equals mxq_int8_gemm_dequant (original row order) followed by the SwiGLU input activation of
+ * the next quantizer (CK/backends/_activations.py:50-52) bit for bit.
+ * Replaces: fc1 + the SwiGLU half of int8_linear(raw, ..., input_act="swiglu")
+ * (h3serve/native_engine/model/fused_mlp.py:386-420).
+ */
+int mxq_int8_gemm_dequant_swiglu(const int8_t* a, const int8_t* b, const float* xs,
+                                 const float* ws, int64_t ws_numel, const void* bias_bf16,
+                                 void* h_bf16, int64_t M, int64_t N, int64_t K, int64_t ldh,
+                                 void* stream);
+
+/*
  * INT8 GEMM + dequant epilogue + gated residual update, in place:
  *   y = the bf16 output of mxq_int8_gemm_dequant (same arguments and roundings)
  *   residual[m, n] = bf16(residual[m, n] + y[m, n] * gate[gate_rows[m], n])

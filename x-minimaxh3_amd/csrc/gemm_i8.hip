@@ -22,12 +22,17 @@
 //   kEpiGelu    bf16 dequant as above, then h = gelu_tanh(y) in bf16 (table in LDS), and the
 //               per-row absmax of h folded into row_absmax[m] with atomics (it feeds the next
 //               layer's quantizer, backends/_activations.py:40-53 + quantization.py:857-875).
+//   kEpiSwiGLU  bf16 dequant as above of a SwiGLU fc1 whose weight rows come in blocks of 16 gate
+//               rows then the 16 matching up rows (prepare_swiglu_fc1 on the host), then
+//               h = bf16(bf16(silu(gate)) * up) (table in LDS) written as [M, N/2]: the fused
+//               form of int8_linear followed by fc2's input_act="swiglu"
+//               (CK/backends/_activations.py:50-52, h3serve/native_engine/model/fused_mlp.py:386-420).
 //   kEpiGatedRes bf16 dequant as above, then the gated residual update in place:
 //               res[m, n] = bf16(res[m, n] + y * gate[gate_rows[m], n])  (the reference's
 //               addcmul_ after fc2, h3serve/native_engine/model/layers.py:944-960 and
 //               fused_mlp.py:157-219; y * gate is exact in fp32, so one fp32 add, then RNE).
 
-#include "mxq_common.h"
+#include "act_rot.h"
 
 namespace mxq {
 
@@ -41,7 +46,7 @@ constexpr int kLoadsPerOperand = 8;                     // direct-to-LDS loads p
 constexpr int kEpiLds = 131072;                         // epilogue: per-column factors behind 128 KB
 constexpr int kGroupM = 8;
 
-enum { kEpiI32 = 0, kEpiDequant = 1, kEpiGelu = 2, kEpiGatedRes = 3 };
+enum { kEpiI32 = 0, kEpiDequant = 1, kEpiGelu = 2, kEpiGatedRes = 3, kEpiSwiGLU = 4 };
 
 struct GemmArgs {
   const int8_t* a;
@@ -412,8 +417,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
     const float bl = has_b ? OutT<kOut>::load(reinterpret_cast<const typename OutT<kOut>::T*>(p.bias) + col) : -0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) xsv[i] = p.xs[min(m0 + wm * kWaveM + i * 32 + lr, p.M - 1)];
-    if (kEpi == kEpiGelu) {
-      const char* src = reinterpret_cast<const char*>(&kGeluFull) + lane * 16;
+    if (kEpi == kEpiGelu || kEpi == kEpiSwiGLU) {
+      const char* src = reinterpret_cast<const char*>(kEpi == kEpiGelu ? (const void*)&kGeluFull : (const void*)&kSiluFull) +
+                        lane * 16;
 #pragma unroll 4
       for (int q = wave; q < 128; q += 4)
         __builtin_amdgcn_global_load_lds((gptr_t)(src + q * 1024), (lptr_t)(lds + q * 1024), 16, 0, 0);
@@ -433,8 +439,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
     }
   }
 
-  // GELU: pre-activation bf16 pairs, kept until the table has landed.
-  uint32_t yp[kEpi == kEpiGelu ? 4 : 1][4][8];
+  // GELU / SwiGLU: pre-activation bf16 pairs, kept until the table has landed.
+  constexpr bool kTable = kEpi == kEpiGelu || kEpi == kEpiSwiGLU;
+  uint32_t yp[kTable ? 4 : 1][4][8];
   static_for<4>([&](auto J) {
     constexpr int j = decltype(J)::value;
     const int cl0 = wn * kWaveN + j * 32 + lh * 4;  // tile column of run q = 0
@@ -457,7 +464,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
       uint32_t w[4 * kWords];
 #pragma unroll
       for (int q = 0; q < 4; ++q) epi_run<kEpi, kOut>(acc[i][j], q, xsv[i], wsv + q * 4, bsv + q * 4, w + q * kWords);
-      if constexpr (kEpi == kEpiGelu) {
+      if constexpr (kTable) {
 #pragma unroll
         for (int r = 0; r < 8; ++r) yp[i][j][r] = w[r];
       } else if constexpr (kEpi == kEpiGatedRes) {
@@ -513,6 +520,35 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
       const int64_t row = m0 + wm * kWaveM + i * 32 + lr;
       if (lh == 0 && row < p.M) atomicMax(reinterpret_cast<unsigned int*>(p.row_absmax + row), m << 16);
     }
+  }
+  if constexpr (kEpi == kEpiSwiGLU) {
+    wait_vmcnt<0>();
+    barrier_no_drain();  // every wave's part of the SiLU table has landed
+    // Runs 0, 1 of a 32 x 32 block are gate columns, runs 2, 3 the matching up columns; output
+    // channel c of block b (tile column t0 = b * 32) is h column t0 / 2 + c.
+    const uint16_t* s_silu = reinterpret_cast<const uint16_t*>(lds);
+    const int64_t nh = p.N / 2;
+    const bool hfull = p.vec_store && m0 + kBM <= p.M && (n0 + kBN) / 2 <= nh;
+    static_for<4>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      const int64_t hc0 = (n0 + wn * kWaveN + j * 32) / 2 + lh * 4;
+      static_for<4>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        const int64_t row = m0 + wm * kWaveM + i * 32 + lr;
+        uint32_t hw[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t g = yp[i][j][r], u = yp[i][j][r + 4];
+          const float plo = bf16_to_f32(s_silu[g & 0xFFFFu]) * bf16_to_f32(u & 0xFFFFu);
+          const float phi = bf16_to_f32(s_silu[g >> 16]) * bf16_to_f32(u >> 16);
+          hw[r] = (plo != plo ? 0x7FC0u : f32_to_bf16_bits(plo)) | ((phi != phi ? 0x7FC0u : f32_to_bf16_bits(phi)) << 16);
+        }
+        if (hfull || row < p.M) {
+          store_run<2>(p.d, p.ldd, row, hc0, nh, hfull || (p.vec_store && hc0 + 4 <= nh), hw);
+          store_run<2>(p.d, p.ldd, row, hc0 + 8, nh, hfull || (p.vec_store && hc0 + 12 <= nh), hw + 2);
+        }
+      });
+    });
   }
 }
 
@@ -593,6 +629,22 @@ extern "C" int mxq_int8_gemm_dequant_gelu_absmax(const int8_t* a, const int8_t* 
   g.a = a; g.b = b; g.xs = xs; g.ws = ws; g.bias = bias_bf16; g.d = h_bf16; g.row_absmax = row_absmax;
   g.M = M; g.N = N; g.K = K; g.ldd = ldh; g.ws_per_channel = ws_numel == N && N != 1;
   return launch_gemm<kEpiGelu, 2>(g, (hipStream_t)stream);
+}
+
+extern "C" int mxq_int8_gemm_dequant_swiglu(const int8_t* a, const int8_t* b, const float* xs,
+                                            const float* ws, int64_t ws_numel, const void* bias_bf16,
+                                            void* h_bf16, int64_t M, int64_t N, int64_t K, int64_t ldh,
+                                            void* stream) {
+  if (N % 32) return mxq_set_error(MXQ_ERR_INVALID, "SwiGLU fc1 width %lld must be a multiple of 32", (long long)N);
+  int rc = check_gemm_shape(a, b, h_bf16, M, N / 2, K, ldh);
+  if (rc) return rc;
+  if (M == 0 || N == 0) return MXQ_OK;
+  if (!xs || !ws) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  if (ws_numel != 1 && ws_numel != N) return mxq_set_error(MXQ_ERR_INVALID, "bad weight scale length");
+  GemmArgs g{};
+  g.a = a; g.b = b; g.xs = xs; g.ws = ws; g.bias = bias_bf16; g.d = h_bf16;
+  g.M = M; g.N = N; g.K = K; g.ldd = ldh; g.ws_per_channel = ws_numel == N && N != 1;
+  return launch_gemm<kEpiSwiGLU, 2>(g, (hipStream_t)stream);
 }
 
 extern "C" int mxq_int8_gemm_gated_residual(const int8_t* a, const int8_t* b, const float* xs,

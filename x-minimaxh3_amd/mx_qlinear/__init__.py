@@ -10,23 +10,28 @@ include/mx_qlinear.h); there is no CPU path.
 
 from .ops import (  # noqa: F401
     FfnWorkspace,
+    PreparedSwiGLUFc1,
     adaln,
     adaln_quantize_int8,
     apply_input_act,
     dequantize_int4_grouped_to_int8,
     fused_down_gated_residual,
+    h3_mlp_,
     int8_ffn_gelu,
     int8_gemv_dequant,
+    int8_swiglu_fc1,
     int8_linear,
     int8_linear_gated_residual_,
     int8_linear_prequantized,
     mm_int8,
+    prepare_swiglu_fc1,
     quantize_int8_convrot_weight,
     quantize_int8_rowwise,
     quantize_int8_rowwise_convrot,
     rms_adaln,
     rms_adaln_quantize_int8,
     segment_row_map,
+    swiglu_mlp_gated_residual_,
     w4a8_grouped_linear,
     w4a8_int8_linear,
 )

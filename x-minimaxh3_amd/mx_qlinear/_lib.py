@@ -35,6 +35,7 @@ SIGNATURES: dict[str, list] = {
     "mxq_int8_gemm_i32": [_P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "mxq_int8_gemm_dequant": [_P, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I, _P],
     "mxq_int8_gemm_dequant_gelu_absmax": [_P, _P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "mxq_int8_gemm_dequant_swiglu": [_P, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P],
     "mxq_int8_gemm_gated_residual": [_P, _P, _P, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64,
                                      _P],
     "mxq_fill_f32": [_P, _F, _I64, _P],

@@ -665,6 +665,90 @@ def fused_down_gated_residual(hidden: torch.Tensor, residual: torch.Tensor, gate
 
 
 # ---------------------------------------------------------------------------------------
+# SwiGLU MLP: fc1 with the SwiGLU epilogue, ConvRot re-quant, fc2 with the gated residual
+# ---------------------------------------------------------------------------------------
+
+class PreparedSwiGLUFc1:
+    """An INT8 SwiGLU fc1 ([gate | up] rows, [2F, K]) with its rows reordered for the SwiGLU
+    epilogue: per block of 32 rows, 16 gate rows then the matching 16 up rows. The weight
+    scale and bias follow the same order. Built once per layer (``prepare_swiglu_fc1``)."""
+
+    def __init__(self, qweight: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None, inner: int):
+        self.qweight, self.scale, self.bias, self.inner = qweight, scale, bias, inner
+
+
+def _swiglu_order(n2: int, device) -> torch.Tensor:
+    f = n2 // 2
+    blk = torch.arange(f // 16, device=device).reshape(-1, 1) * 16
+    r = torch.arange(16, device=device).reshape(1, -1)
+    return torch.cat([blk + r, f + blk + r], dim=1).reshape(-1)
+
+
+def prepare_swiglu_fc1(qweight: torch.Tensor, weight_scale: torch.Tensor,
+                       bias: torch.Tensor | None = None) -> PreparedSwiGLUFc1:
+    """Reorder a SwiGLU fc1 (rows [gate | up], h3serve/native_engine/model/layers.py SwiGLUMLP)
+    for ``int8_swiglu_fc1``; the values are unchanged."""
+    if qweight.dim() != 2 or qweight.dtype != torch.int8:
+        raise ValueError("fc1 weight must be a 2-D int8 tensor")
+    n2 = qweight.shape[0]
+    if n2 % 32:
+        raise NotImplementedError("the SwiGLU epilogue needs 2 x inner to be a multiple of 32")
+    dev = qweight.device
+    order = _swiglu_order(n2, dev)
+    ws = _weight_scale(weight_scale, n2, dev)
+    ws = ws if ws.numel() == 1 else ws[order].contiguous()
+    b = None if bias is None else bias.to(device=dev, dtype=torch.bfloat16).reshape(-1)[order].contiguous()
+    return PreparedSwiGLUFc1(qweight[order].contiguous(), ws, b, n2 // 2)
+
+
+def int8_swiglu_fc1(x_qdata: torch.Tensor, x_scale: torch.Tensor, fc1: PreparedSwiGLUFc1,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """``swiglu(int8_linear_prequantized(x, fc1))`` as bf16 [M, inner] in one GEMM launch
+    (the SwiGLU half of fc2's ``input_act="swiglu"``, CK/backends/_activations.py:50-52)."""
+    if x_qdata.dim() != 2 or x_qdata.dtype != torch.int8:
+        raise ValueError("x_qdata must be a 2-D int8 tensor")
+    if x_qdata.shape[1] != fc1.qweight.shape[1]:
+        raise ValueError("Input and weight inner dimensions must match")
+    dev = _require_gpu(x_qdata, fc1.qweight)
+    m, n2 = x_qdata.shape[0], fc1.qweight.shape[0]
+    xs = x_scale.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+    if xs.numel() != m:
+        raise ValueError(f"x_scale has {xs.numel()} entries, expected {m}")
+    h = out if out is not None else torch.empty((m, n2 // 2), dtype=torch.bfloat16, device=dev)
+    if m == 0:
+        return h
+    q2, w2, k = _pad_k(x_qdata.contiguous(), fc1.qweight)
+    with torch.cuda.device(dev):
+        call("mxq_int8_gemm_dequant_swiglu", _p(q2), _p(w2), _p(xs), _p(fc1.scale), fc1.scale.numel(),
+             _p(fc1.bias), _p(h), m, n2, k, h.stride(0), _stream(dev))
+    return h
+
+
+def swiglu_mlp_gated_residual_(residual: torch.Tensor, x_qdata: torch.Tensor, x_scale: torch.Tensor,
+                               fc1: PreparedSwiGLUFc1, fc2_qweight: torch.Tensor, fc2_scale: torch.Tensor,
+                               fc2_bias: torch.Tensor | None, gate: torch.Tensor, segments,
+                               convrot_groupsize: int = 256) -> torch.Tensor:
+    """The H3 MLP after its quantized input, in place on ``residual``: fc1 (+ SwiGLU in the
+    epilogue) -> ConvRot re-quant -> fc2 + gated residual. Bit-identical to the reference's
+    default route (fused_mlp.py:386-420: ``raw = fc1(hidden)``, ``int8_linear(raw, fc2, convrot=True,
+    input_act="swiglu")``, then ``addcmul_`` per segment)."""
+    h = int8_swiglu_fc1(x_qdata, x_scale, fc1)
+    return int8_linear_gated_residual_(residual, h, fc2_qweight, fc2_scale, fc2_bias, gate, segments,
+                                       convrot=True, convrot_groupsize=convrot_groupsize)
+
+
+def h3_mlp_(residual: torch.Tensor, norm, shift: torch.Tensor, scale: torch.Tensor, gate: torch.Tensor,
+            segments, fc1: PreparedSwiGLUFc1, fc2_qweight: torch.Tensor, fc2_scale: torch.Tensor,
+            fc2_bias: torch.Tensor | None, convrot_groupsize: int = 256) -> torch.Tensor:
+    """The H3 block's MLP half in four launches, in place on ``residual`` (layers.py:1138-1160:
+    ``rms_adaln`` -> ``try_fused_gated_mlp``): RMS adaLN + ConvRot quant, fc1 + SwiGLU, ConvRot
+    re-quant, fc2 + gated residual."""
+    q, s = rms_adaln_quantize_int8(residual, norm, shift, scale, segments, convrot_groupsize=convrot_groupsize)
+    return swiglu_mlp_gated_residual_(residual, q, s, fc1, fc2_qweight, fc2_scale, fc2_bias, gate, segments,
+                                      convrot_groupsize)
+
+
+# ---------------------------------------------------------------------------------------
 # W4A8
 # ---------------------------------------------------------------------------------------
 
