@@ -36,14 +36,23 @@
 
 namespace mxq {
 
-constexpr int kBM = 256, kBN = 256, kBK = 128;
-constexpr int kGemmThreads = 256;
-constexpr int kWaveM = 128, kWaveN = 128;
-constexpr int kStageA = kBM * kBK, kStageB = kBN * kBK; // 32 KB each
-constexpr int kSlots = 5;                               // LDS ring of 32 KB operand slots (160 KB)
-constexpr int kSlotBytes = 32768;
-constexpr int kLoadsPerOperand = 8;                     // direct-to-LDS loads per wave per operand slot
-constexpr int kEpiLds = 131072;                         // epilogue: per-column factors behind 128 KB
+constexpr int kBK = 128;                                // K bytes per stage
+constexpr int kGemmThreads = 256;                       // 4 waves as 2 x 2
+constexpr int kSlots = 5;                               // LDS ring of operand slots
+
+// Tile shapes: kT x kT outputs per workgroup, each wave (kT/2)^2 as kBI x kBJ MFMA blocks of
+// 32 x 32. 256: one workgroup per CU, 160 KB ring, the GEMM of large problems. 128: two
+// workgroups per CU, 80 KB ring, for problems with fewer 256-tiles than CUs.
+template <int kT>
+struct TileCfg {
+  static constexpr int kBM = kT, kBN = kT;
+  static constexpr int kWaveM = kT / 2, kWaveN = kT / 2;
+  static constexpr int kBI = kWaveM / 32, kBJ = kWaveN / 32;
+  static constexpr int kSlotBytes = kT * kBK;                  // one operand chunk of a stage
+  static constexpr int kLoads = kSlotBytes / 1024 / 4;          // direct-to-LDS loads per wave per slot
+  static constexpr int kLds = kSlots * kSlotBytes;
+  static constexpr int kEpiLds = kT == 256 ? 131072 : 4 * kSlotBytes;  // per-column factors
+};
 constexpr int kGroupM = 8;
 
 enum { kEpiI32 = 0, kEpiDequant = 1, kEpiGelu = 2, kEpiGatedRes = 3, kEpiSwiGLU = 4 };
@@ -98,18 +107,20 @@ MXQ_DEVICE void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn)
 // lane i writes slot i % 8 of tile row 8 b + i / 8, so the lane fetches logical chunk
 // (i % 8) ^ f(row) of that row, and eight lanes read one whole 128-byte line of the row-major
 // operand (half lines, as 64-byte steps would read, halve the L2 -> CU throughput). Wave w
-// loads A and B blocks b = 8 w .. 8 w + 7 of each stage.
+// loads blocks b = kL w .. kL w + kL - 1 of each A and B slot.
+template <int kL>
 struct Loader {
-  const int8_t* a[8];
-  const int8_t* b[8];
+  const int8_t* a[kL];
+  const int8_t* b[kL];
   int koff[2];   // logical chunk offset (bytes) of this lane's piece, for even and odd t
 };
 
-MXQ_DEVICE void make_loader(Loader& L, const GemmArgs& p, int64_t m0, int64_t n0) {
+template <int kL>
+MXQ_DEVICE void make_loader(Loader<kL>& L, const GemmArgs& p, int64_t m0, int64_t n0) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const int r = (w * 8 + t) * 8 + (lane >> 3);
+  for (int t = 0; t < kL; ++t) {
+    const int r = (w * kL + t) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ swz_f(r);  // depends on t only through t & 1
     if (t < 2) L.koff[t] = c * 16;
     L.a[t] = p.a + min(m0 + r, p.M - 1) * p.K + c * 16;
@@ -117,76 +128,62 @@ MXQ_DEVICE void make_loader(Loader& L, const GemmArgs& p, int64_t m0, int64_t n0
   }
 }
 
-MXQ_DEVICE void issue_a(const Loader& L, char* slot, int64_t k0, int64_t K) {
+// Load t of this wave's share of an A (kB = false) or B slot.
+template <bool kB, int kL>
+MXQ_DEVICE void issue_one(const Loader<kL>& L, char* slot, int64_t k0, int64_t K, int t) {
   const int w = threadIdx.x >> 6;
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const bool kin = k0 + L.koff[t & 1] < K;
-    const void* sa = kin ? (const void*)(L.a[t] + k0) : (const void*)kZeroChunk;
-    __builtin_amdgcn_global_load_lds((gptr_t)sa, (lptr_t)(slot + (w * 8 + t) * 1024), 16, 0, 0);
-  }
+  const int koff = L.koff[t & 1];
+  const bool kin = k0 + koff < K;
+  const void* src = kB ? (kin ? (const void*)(L.b[t] + k0 + koff) : (const void*)L.b[t])
+                       : (kin ? (const void*)(L.a[t] + k0) : (const void*)kZeroChunk);
+  __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)(slot + (w * kL + t) * 1024), 16, 0, 0);
 }
 
-MXQ_DEVICE void issue_b(const Loader& L, char* slot, int64_t k0, int64_t K) {
-  const int w = threadIdx.x >> 6;
+template <bool kB, int kL>
+MXQ_DEVICE void issue_slot(const Loader<kL>& L, char* slot, int64_t k0, int64_t K) {
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const int koff = L.koff[t & 1];
-    const bool kin = k0 + koff < K;
-    const void* sb = kin ? (const void*)(L.b[t] + k0 + koff) : (const void*)L.b[t];
-    __builtin_amdgcn_global_load_lds((gptr_t)sb, (lptr_t)(slot + (w * 8 + t) * 1024), 16, 0, 0);
-  }
+  for (int t = 0; t < kL; ++t) issue_one<kB>(L, slot, k0, K, t);
 }
 
-// Fragments of K-step ks (32 K-bytes) of a stage: A rows wm*128 + i*32 + l%32 and B rows
-// wn*128 + j*32 + l%32, chunk ks*2 + l/32. Every row a lane touches has the same swizzle
-// f = ((l % 32) >> 1) & 7, so one base address per operand serves all four blocks.
-MXQ_DEVICE void load_frags(uint32_t slot_a, uint32_t slot_b, int wm, int wn, int ks, v4i fa[4], v4i fb[4]) {
+// Fragments of K-step ks (32 K-bytes) of a stage: A rows wm*kWaveM + i*32 + l%32 and B rows
+// wn*kWaveN + j*32 + l%32, chunk ks*2 + l/32. Every row a lane touches has the same swizzle
+// f = ((l % 32) >> 1) & 7, so one base address per operand serves all its blocks.
+template <class C>
+MXQ_DEVICE void load_frags(uint32_t slot_a, uint32_t slot_b, int wm, int wn, int ks, v4i fa[C::kBI], v4i fb[C::kBJ]) {
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31;
   const uint32_t x = (uint32_t)(((ks * 2 + (lane >> 5)) ^ swz_f(lr)) << 4);
-  const uint32_t ba = slot_a + (uint32_t)(wm * kWaveM + lr) * kBK + x;
-  const uint32_t bb = slot_b + (uint32_t)(wn * kWaveN + lr) * kBK + x;
-  fa[0] = lds_read_b128<0>(ba);
-  fa[1] = lds_read_b128<32 * kBK>(ba);
-  fa[2] = lds_read_b128<64 * kBK>(ba);
-  fa[3] = lds_read_b128<96 * kBK>(ba);
-  fb[0] = lds_read_b128<0>(bb);
-  fb[1] = lds_read_b128<32 * kBK>(bb);
-  fb[2] = lds_read_b128<64 * kBK>(bb);
-  fb[3] = lds_read_b128<96 * kBK>(bb);
+  const uint32_t ba = slot_a + (uint32_t)(wm * C::kWaveM + lr) * kBK + x;
+  const uint32_t bb = slot_b + (uint32_t)(wn * C::kWaveN + lr) * kBK + x;
+  static_for<C::kBI>([&](auto I) { fa[decltype(I)::value] = lds_read_b128<decltype(I)::value * 32 * kBK>(ba); });
+  static_for<C::kBJ>([&](auto J) { fb[decltype(J)::value] = lds_read_b128<decltype(J)::value * 32 * kBK>(bb); });
 }
 
 // The MFMAs compute C^T blocks (weights as the first operand): lane l of a 32 x 32 block then
 // holds output row l % 32 and, in registers r = 0..15, output columns
 // (r / 4) * 8 + (l / 32) * 4 + r % 4 -- four runs of four consecutive columns of one row.
-MXQ_DEVICE void mma16(const v4i fa[4], const v4i fb[4], v16i acc[4][4]) {
+template <class C>
+MXQ_DEVICE void mma_step(const v4i fa[C::kBI], const v4i fb[C::kBJ], v16i acc[C::kBI][C::kBJ]) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < C::kBI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < C::kBJ; ++j)
       acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j], fa[i], acc[i][j], 0, 0, 0);
 }
 
-// The sixteen MFMAs of one K-step with kCount direct-to-LDS loads (loads kFirst .. of one
-// operand slot) interleaved, one after each of the first kCount MFMAs. Spread this way, a load
-// that waits for room in the memory pipeline holds up the wave while its MFMAs still run,
-// rather than after the last of them.
-template <bool kB, int kFirst, int kCount>
-MXQ_DEVICE void mma16_dma(const v4i fa[4], const v4i fb[4], v16i acc[4][4], const Loader& L, char* slot,
-                          int64_t k0, int64_t K, bool on) {
-  const int w = threadIdx.x >> 6;
+// The MFMAs of one K-step with kCount direct-to-LDS loads (loads kFirst .. of one operand slot)
+// interleaved, one after each of the first kCount MFMAs (kCount <= kBI * kBJ). Spread this way,
+// a load that waits for room in the memory pipeline holds up the wave while its MFMAs still
+// run, rather than after the last of them.
+template <class C, bool kB, int kFirst, int kCount>
+MXQ_DEVICE void mma_step_dma(const v4i fa[C::kBI], const v4i fb[C::kBJ], v16i acc[C::kBI][C::kBJ],
+                             const Loader<C::kLoads>& L, char* slot, int64_t k0, int64_t K, bool on) {
+  static_assert(kCount <= C::kBI * C::kBJ, "more loads than MFMAs to spread them over");
 #pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    acc[q >> 2][q & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[q & 3], fa[q >> 2], acc[q >> 2][q & 3], 0, 0, 0);
-    if (q < kCount && on) {
-      const int t = kFirst + q;  // a constant once the loop is unrolled
-      const int koff = L.koff[t & 1];
-      const bool kin = k0 + koff < K;
-      const void* src = kB ? (kin ? (const void*)(L.b[t] + k0 + koff) : (const void*)L.b[t])
-                           : (kin ? (const void*)(L.a[t] + k0) : (const void*)kZeroChunk);
-      __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)(slot + (w * 8 + t) * 1024), 16, 0, 0);
-    }
+  for (int q = 0; q < C::kBI * C::kBJ; ++q) {
+    const int i = q / C::kBJ, j = q % C::kBJ;
+    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j], fa[i], acc[i][j], 0, 0, 0);
+    if (q < kCount && on) issue_one<kB>(L, slot, k0, K, kFirst + q);  // t is a constant once unrolled
   }
 }
 
@@ -306,9 +303,13 @@ MXQ_DEVICE void gated_block_row(const GemmArgs& p, bool full, int64_t row, int64
   }
 }
 
-template <int kEpi, int kOut>
-__global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
-  __shared__ __attribute__((aligned(16))) char lds[kSlots * kSlotBytes];
+template <int kEpi, int kOut, int kT>
+__global__ __launch_bounds__(kGemmThreads, kT == 256 ? 1 : 2) void gemm_i8_kernel(GemmArgs p) {
+  typedef TileCfg<kT> C;
+  constexpr int kBM = C::kBM, kBN = C::kBN, kWaveM = C::kWaveM, kWaveN = C::kWaveN;
+  constexpr int kBI = C::kBI, kBJ = C::kBJ, kSlotBytes = C::kSlotBytes, kLoads = C::kLoads;
+  static_assert(kT == 256 || (kEpi != kEpiGelu && kEpi != kEpiSwiGLU), "table epilogues need the 160 KB ring");
+  __shared__ __attribute__((aligned(16))) char lds[C::kLds];
 
   int tm, tn;
   tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
@@ -316,13 +317,13 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int wm = wave >> 1, wn = wave & 1;
 
-  v16i acc[4][4];
+  v16i acc[kBI][kBJ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kBI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v16i{};
+    for (int j = 0; j < kBJ; ++j) acc[i][j] = v16i{};
 
-  // Pipeline: a ring of five 32 KB slots receives the operand chunks in the order A0 B0 A1 B1
+  // Pipeline: a ring of five slots (one operand chunk each) receives the operand chunks in the order A0 B0 A1 B1
   // A2 ..., chunk i (A_j = 2j, B_j = 2j + 1) into slot i % 5; stage j (128 K-bytes) reads A_j
   // and B_j. Entering iteration kt, A_kt and B_kt are complete and visible, B_kt+1 is in flight
   // and F0 holds the fragments of (stage kt, K-step 0). The iteration runs K-steps 0..3, each
@@ -333,22 +334,22 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
   // those MFMAs. A chunk is thus requested one to two stages before it is used, and no wave
   // issues a burst of loads while its matrix pipe sits idle.
   const int ktiles = (int)((p.K + kBK - 1) / kBK);
-  Loader ld;
+  Loader<kLoads> ld;
   make_loader(ld, p, m0, n0);
-  issue_a(ld, lds, 0, p.K);
-  issue_b(ld, lds + kSlotBytes, 0, p.K);
+  issue_slot<false>(ld, lds, 0, p.K);
+  issue_slot<true>(ld, lds + kSlotBytes, 0, p.K);
   if (ktiles > 1) {
-    issue_a(ld, lds + 2 * kSlotBytes, kBK, p.K);
-    issue_b(ld, lds + 3 * kSlotBytes, kBK, p.K);
-    wait_vmcnt<2 * kLoadsPerOperand>();
+    issue_slot<false>(ld, lds + 2 * kSlotBytes, kBK, p.K);
+    issue_slot<true>(ld, lds + 3 * kSlotBytes, kBK, p.K);
+    wait_vmcnt<2 * kLoads>();
   } else {
     wait_vmcnt<0>();
   }
   barrier_no_drain();
 
   const uint32_t lds_addr = (uint32_t)(uintptr_t)(lptr_t)lds;
-  v4i f0a[4], f0b[4], f1a[4], f1b[4];
-  load_frags(lds_addr, lds_addr + kSlotBytes, wm, wn, 0, f0a, f0b);
+  v4i f0a[kBI], f0b[kBJ], f1a[kBI], f1b[kBJ];
+  load_frags<C>(lds_addr, lds_addr + kSlotBytes, wm, wn, 0, f0a, f0b);
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   __builtin_amdgcn_sched_barrier(0);
   int sa = 0;  // slot of A_kt; B_kt is in (sa + 1) % 5
@@ -360,33 +361,33 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
     const uint32_t cur_a = lds_addr + (uint32_t)(sa * kSlotBytes), cur_b = lds_addr + (uint32_t)(sb * kSlotBytes);
     const bool more2 = kt + 2 < ktiles;
     const int64_t k2 = (int64_t)(kt + 2) * kBK;
-    load_frags(cur_a, cur_b, wm, wn, 1, f1a, f1b);
-    wait_lgkm8();
+    load_frags<C>(cur_a, cur_b, wm, wn, 1, f1a, f1b);
+    wait_lgkm<kBI + kBJ>();
     __builtin_amdgcn_sched_barrier(0);
-    mma16_dma<false, 0, 4>(f0a, f0b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
+    mma_step_dma<C, false, 0, kLoads / 2>(f0a, f0b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
     __builtin_amdgcn_sched_barrier(0);
-    load_frags(cur_a, cur_b, wm, wn, 2, f0a, f0b);
-    wait_lgkm8();
+    load_frags<C>(cur_a, cur_b, wm, wn, 2, f0a, f0b);
+    wait_lgkm<kBI + kBJ>();
     __builtin_amdgcn_sched_barrier(0);
-    mma16_dma<false, 4, 4>(f1a, f1b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
+    mma_step_dma<C, false, kLoads / 2, kLoads / 2>(f1a, f1b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
     __builtin_amdgcn_sched_barrier(0);
-    load_frags(cur_a, cur_b, wm, wn, 3, f1a, f1b);
-    wait_lgkm8();
+    load_frags<C>(cur_a, cur_b, wm, wn, 3, f1a, f1b);
+    wait_lgkm<kBI + kBJ>();
     __builtin_amdgcn_sched_barrier(0);
-    mma16(f0a, f0b, acc);
+    mma_step<C>(f0a, f0b, acc);
     __builtin_amdgcn_sched_barrier(0);
     if (more2) {
-      __builtin_amdgcn_s_waitcnt((kLoadsPerOperand & 0xF) | (0x7 << 4));  // vmcnt(8) lgkmcnt(0)
+      __builtin_amdgcn_s_waitcnt((kLoads & 0xF) | (0x7 << 4));  // vmcnt(kLoads) lgkmcnt(0)
     } else {
       wait_all();
     }
     __builtin_amdgcn_sched_barrier(0);
     if (kt + 1 < ktiles) {
       barrier_no_drain();
-      load_frags(lds_addr + (uint32_t)(na * kSlotBytes), lds_addr + (uint32_t)(nb * kSlotBytes), wm, wn, 0, f0a, f0b);
+      load_frags<C>(lds_addr + (uint32_t)(na * kSlotBytes), lds_addr + (uint32_t)(nb * kSlotBytes), wm, wn, 0, f0a, f0b);
     }
     __builtin_amdgcn_sched_barrier(0);
-    mma16_dma<true, 0, 8>(f1a, f1b, acc, ld, lds + sa * kSlotBytes, k2, p.K, more2 && kt + 1 < ktiles);
+    mma_step_dma<C, true, 0, kLoads>(f1a, f1b, acc, ld, lds + sa * kSlotBytes, k2, p.K, more2 && kt + 1 < ktiles);
     __builtin_amdgcn_sched_barrier(0);
     sa = na;
   }
@@ -397,18 +398,18 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
   barrier_no_drain();
 
   // ---- epilogue ----
-  // Lane l holds, for m-block i and n-block j, row wm*128 + i*32 + l%32 and the four column
-  // runs j*32 + q*8 + (l/32)*4 + {0..3}, q = 0..3 (see mma16). The main loop's last barrier
+  // Lane l holds, for m-block i and n-block j, row wm*kWaveM + i*32 + l%32 and the four column
+  // runs j*32 + q*8 + (l/32)*4 + {0..3}, q = 0..3 (see mma_step). The main loop's last barrier
   // left the LDS free: per-column factors go behind the four stage buffers and, for GELU, the
   // 128 KB bf16 -> bf16 table is fetched into the buffers themselves while the dequant runs.
   constexpr int kElem = (kEpi == kEpiI32 || kOut == 0) ? 4 : 2;
   const int lr = lane & 31, lh = lane >> 5;
   const int t = threadIdx.x;
-  float* s_ws = reinterpret_cast<float*>(lds + kEpiLds);
+  float* s_ws = reinterpret_cast<float*>(lds + C::kEpiLds);
   float* s_bias = s_ws + kBN;
   const uint16_t* s_gelu = reinterpret_cast<const uint16_t*>(lds);
   const bool has_b = p.bias != nullptr;
-  float xsv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float xsv[kBI] = {};
   if (kEpi != kEpiI32) {
     // Global reads of the factors are issued before the table fetch, so waiting for them
     // leaves the fetch in flight.
@@ -416,7 +417,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
     const float wsl = p.ws_per_channel ? p.ws[col] : p.ws[0];
     const float bl = has_b ? OutT<kOut>::load(reinterpret_cast<const typename OutT<kOut>::T*>(p.bias) + col) : -0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xsv[i] = p.xs[min(m0 + wm * kWaveM + i * 32 + lr, p.M - 1)];
+    for (int i = 0; i < kBI; ++i) xsv[i] = p.xs[min(m0 + wm * kWaveM + i * 32 + lr, p.M - 1)];
     if (kEpi == kEpiGelu || kEpi == kEpiSwiGLU) {
       const char* src = reinterpret_cast<const char*>(kEpi == kEpiGelu ? (const void*)&kGeluFull : (const void*)&kSiluFull) +
                         lane * 16;
@@ -424,16 +425,18 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
       for (int q = wave; q < 128; q += 4)
         __builtin_amdgcn_global_load_lds((gptr_t)(src + q * 1024), (lptr_t)(lds + q * 1024), 16, 0, 0);
     }
-    s_ws[t] = wsl;
-    s_bias[t] = bl;
+    if (t < kBN) {
+      s_ws[t] = wsl;
+      s_bias[t] = bl;
+    }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt left open (max)
     barrier_no_drain();
   }
   const bool full = p.vec_store && m0 + kBM <= p.M && n0 + kBN <= p.N;
-  int64_t grow[4] = {0, 0, 0, 0};  // kEpiGatedRes: the gate row of each of this lane's rows
+  int64_t grow[kBI] = {};  // kEpiGatedRes: the gate row of each of this lane's rows
   if constexpr (kEpi == kEpiGatedRes) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {  // clamped into the gate so a bad row index cannot fault
+    for (int i = 0; i < kBI; ++i) {  // clamped into the gate so a bad row index cannot fault
       const int64_t gr = p.gate_rows[min(m0 + wm * kWaveM + i * 32 + lr, p.M - 1)];
       grow[i] = gr < 0 ? 0 : (gr >= p.gate_count ? p.gate_count - 1 : gr);
     }
@@ -441,8 +444,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
 
   // GELU / SwiGLU: pre-activation bf16 pairs, kept until the table has landed.
   constexpr bool kTable = kEpi == kEpiGelu || kEpi == kEpiSwiGLU;
-  uint32_t yp[kTable ? 4 : 1][4][8];
-  static_for<4>([&](auto J) {
+  uint32_t yp[kTable ? kBI : 1][kTable ? kBJ : 1][8];
+  static_for<kBJ>([&](auto J) {
     constexpr int j = decltype(J)::value;
     const int cl0 = wn * kWaveN + j * 32 + lh * 4;  // tile column of run q = 0
     float wsv[16], bsv[16];
@@ -458,7 +461,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
         }
       }
     }
-    static_for<4>([&](auto I) {
+    static_for<kBI>([&](auto I) {
       constexpr int i = decltype(I)::value;
       constexpr int kWords = kElem == 4 ? 4 : 2;
       uint32_t w[4 * kWords];
@@ -480,14 +483,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
     barrier_no_drain();  // every wave's part of the table has landed
     // |h| as bf16 bits: non-negative values order like their bit patterns (NaN above +inf), so
     // the row maximum is an integer maximum, kept for both halves of a word at once.
-    us2 rmax[4] = {};
+    us2 rmax[kBI] = {};
     // Interior tiles run a copy of the pass without column masks or store guards.
     auto gelu_pass = [&](auto FullC) {
       constexpr bool kFull = decltype(FullC)::value;
-      static_for<4>([&](auto J) {
+      static_for<kBJ>([&](auto J) {
         constexpr int j = decltype(J)::value;
         const int cl0 = wn * kWaveN + j * 32 + lh * 4;
-        static_for<4>([&](auto I) {
+        static_for<kBI>([&](auto I) {
           constexpr int i = decltype(I)::value;
           uint32_t g[8];
 #pragma unroll
@@ -512,9 +515,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
       gelu_pass(std::true_type{});
     else
       gelu_pass(std::false_type{});
-    // Lanes l and l + 32 hold the two halves of each row's 128 columns of this wave.
+    // Lanes l and l + 32 hold the two halves of each row's columns of this wave.
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kBI; ++i) {
       uint32_t m = max((uint32_t)rmax[i][0], (uint32_t)rmax[i][1]);
       m = max(m, (uint32_t)__shfl_xor((int)m, 32, kWave));
       const int64_t row = m0 + wm * kWaveM + i * 32 + lr;
@@ -529,10 +532,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
     const uint16_t* s_silu = reinterpret_cast<const uint16_t*>(lds);
     const int64_t nh = p.N / 2;
     const bool hfull = p.vec_store && m0 + kBM <= p.M && (n0 + kBN) / 2 <= nh;
-    static_for<4>([&](auto J) {
+    static_for<kBJ>([&](auto J) {
       constexpr int j = decltype(J)::value;
       const int64_t hc0 = (n0 + wn * kWaveN + j * 32) / 2 + lh * 4;
-      static_for<4>([&](auto I) {
+      static_for<kBI>([&](auto I) {
         constexpr int i = decltype(I)::value;
         const int64_t row = m0 + wm * kWaveM + i * 32 + lr;
         uint32_t hw[4];
@@ -555,15 +558,25 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_i8_kernel(GemmArgs p) {
 template <int kEpi, int kOut>
 static int launch_gemm(const GemmArgs& args0, hipStream_t stream) {
   GemmArgs args = args0;
-  args.tiles_m = (int)((args.M + kBM - 1) / kBM);
-  args.tiles_n = (int)((args.N + kBN - 1) / kBN);
+  // Problems with fewer 256-tiles than CUs run 128-tiles (four times as many workgroups).
+  const int64_t big_tiles = ((args.M + 255) / 256) * ((args.N + 255) / 256);
+  const bool small = kEpi != kEpiGelu && kEpi != kEpiSwiGLU && big_tiles < 256;
+  const int kt = small ? 128 : 256;
+  args.tiles_m = (int)((args.M + kt - 1) / kt);
+  args.tiles_n = (int)((args.N + kt - 1) / kt);
   const int elem = (kOut == 0 || kEpi == kEpiI32) ? 4 : 2;
   args.vec_store = ((uintptr_t)args.d % (4 * elem) == 0) && (args.ldd % 4 == 0);
   if (kEpi == kEpiGatedRes)
     args.vec_store = args.vec_store && ((uintptr_t)args.gate % 8 == 0) && (args.ldg % 4 == 0);
   const int64_t tiles = (int64_t)args.tiles_m * args.tiles_n;
   if (tiles > INT32_MAX) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "too many tiles");
-  gemm_i8_kernel<kEpi, kOut><<<(unsigned)tiles, kGemmThreads, 0, stream>>>(args);
+  if constexpr (kEpi != kEpiGelu && kEpi != kEpiSwiGLU) {
+    if (small) {
+      gemm_i8_kernel<kEpi, kOut, 128><<<(unsigned)tiles, kGemmThreads, 0, stream>>>(args);
+      return mxq_check_launch("gemm_i8_kernel");
+    }
+  }
+  gemm_i8_kernel<kEpi, kOut, 256><<<(unsigned)tiles, kGemmThreads, 0, stream>>>(args);
   return mxq_check_launch("gemm_i8_kernel");
 }
 
