@@ -685,11 +685,19 @@ METRICS = {
 }
 
 
+# Default (steps, warmup) per workload: sub-millisecond launches get enough warmup (~30 ms of GPU
+# work) for the shader clock to settle and enough timed steps for ~20-60 ms of timed work.
+DEFAULT_STEPS = {
+    "ffn": (10, 3), "qkv_adaln": (20, 5), "h3_mlp": (10, 3), "h3_qkv": (20, 5),
+    "w4a8_gemm": (100, 100), "w4a8_skinny": (400, 400), "linear_c1": (400, 400), "linear_m1": (1000, 1000),
+}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default: per workload)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed warmup steps (default: per workload)")
     ap.add_argument("--workload", default="ffn", choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work (0: skip)")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
@@ -699,6 +707,9 @@ def main():
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (the path shards over "
               "tokens with no communication; see the design notes)", file=sys.stderr)
         sys.exit(2)
+    steps, warmup = DEFAULT_STEPS.get(args.workload, (10, 3))
+    args.steps = steps if args.steps is None else args.steps
+    args.warmup = warmup if args.warmup is None else args.warmup
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     wl = WORKLOADS[args.workload](dev)

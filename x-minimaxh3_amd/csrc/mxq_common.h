@@ -235,6 +235,9 @@ MXQ_DEVICE void barrier_no_drain() {
 // A kernel using them places its LDS waits itself (wait_lgkm / wait_all) and follows each such
 // wait with __builtin_amdgcn_sched_barrier(0): the compiler sees no dependence between the wait
 // and the registers it covers, so without the barrier it may schedule their first use above it.
+// Every destination dword must also be used after that wait: the compiler takes the result as
+// written when the asm issues, so a dword with no later use may be handed to another value while
+// the read is in flight, and the read's late write then corrupts that value (an address, say).
 template <int kOff>
 MXQ_DEVICE v4i lds_read_b128(uint32_t addr) {
   v4i r;

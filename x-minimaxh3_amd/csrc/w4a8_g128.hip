@@ -4,10 +4,11 @@
 // K-groups g in order, P_g = sum over the group of a[m, k] * (c[n, k] - 8) exactly in int32
 // (the contract of the general kernel in w4a8.hip; this file is its fast path for group 128).
 //
-// The compiler places the int32 MFMA accumulators in AGPRs; the per-group fold reads them with
-// v_accvgpr_read (one copy per element and group). Keeping them in VGPRs instead
-// (-mllvm --amdgpu-mfma-vgpr-form) measured slower here: with the fp32 accumulators also live,
-// the VGPR form spilled.
+// Two workgroups per CU (a 3-stage ring of 24 KB stages; at most 128 VGPRs per lane of int32
+// and fp32 accumulators, all in VGPRs): each SIMD runs two waves, so one wave's per-group fold
+// (v_cvt_f32_i32 + v_fma_mix_f32 per accumulator, the fp16 scale converted inside the fma) and
+// nibble unpack issue while the other wave's MFMAs execute. With one workgroup per CU the
+// accumulators sat in AGPRs and every fold needed an extra v_accvgpr_read: 1.6x slower.
 //
 // Workgroup: 4 wave64s side by side along N; a 128 x 128 tile, wave w owning channels
 // w*32 + [0, 32) of all 128 rows as four v_mfma_i32_32x32x32_i8 blocks (activations first:
@@ -31,22 +32,40 @@ namespace mxq {
 
 namespace {
 
-constexpr int kBM = 128, kBN = 128, kNS = 4;
+// A CU holds two workgroups of four waves, i.e. two waves per SIMD: one wave's fold and
+// unpack VALU work issues while the other's MFMAs run. (A 128 x 256 tile with eight waves per
+// workgroup, a third less L2 -> LDS traffic per MAC, measured no faster.)
+constexpr int kBM = 128, kBN = 128, kNS = 3, kOcc = 2;
+constexpr int kWaves = kBN / 32;
+constexpr int kThreads = kWaves * 64;
 constexpr int kStageA = kBM * 128;  // 16 KB
 constexpr int kStageB = kBN * 64;   // 8 KB packed
 constexpr int kStage = kStageA + kStageB;
 constexpr int kScaleRing = 8;       // > kNS + 1: a slot is refilled only after its fold
 constexpr int kScaleBytes = kBN * 2;
 constexpr int kLds = kNS * kStage + kScaleRing * kScaleBytes;
-constexpr int kALoads = kStageA / 1024 / 4;   // 4 direct-to-LDS loads per wave per stage
-constexpr int kBLoads = kStageB / 1024 / 4;   // 2
-constexpr int kLoads = kALoads + kBLoads + 1;  // + the wave's share of the scales
-constexpr int kScaleLanes = kScaleBytes / 4 / 16;  // lanes per wave fetching scales
+constexpr int kALoads = kStageA / 1024 / kWaves;  // 4 direct-to-LDS loads per wave per stage
+constexpr int kBLoads = kStageB / 1024 / kWaves;  // 2
+constexpr int kLoads = kALoads + kBLoads + 1;     // + the wave's share of the scales
+constexpr int kScaleLanes = kScaleBytes / kWaves / 16;  // lanes per wave fetching scales
 static_assert(kScaleRing >= kNS + 2, "scale slot refilled before it is folded");
+static_assert(kALoads * kWaves * 8 == kBM && kBLoads * kWaves * 16 == kBN, "load split");
+static_assert(kOcc * kLds <= 160 * 1024, "LDS per CU");
 
 struct Tile {
   int64_t m0, n0;
 };
+
+// An empty asm that takes a block's 16 folded values and claims to rewrite its A fragment. The
+// block's first MFMA of a group (zero accumulator input) reads that fragment, so it cannot be
+// placed above the fold. Without this the fold, being plain arithmetic, was placed below all
+// sixteen MFMAs of the group, and every old accumulator had to be copied out first (32
+// v_mov_b64 per group and wave).
+MXQ_DEVICE void order_after_fold(v4i& frag, const float (&f)[16]) {
+  __asm__ volatile("" : "+v"(frag)
+                   : "v"(f[0]), "v"(f[1]), "v"(f[2]), "v"(f[3]), "v"(f[4]), "v"(f[5]), "v"(f[6]), "v"(f[7]),
+                     "v"(f[8]), "v"(f[9]), "v"(f[10]), "v"(f[11]), "v"(f[12]), "v"(f[13]), "v"(f[14]), "v"(f[15]));
+}
 
 MXQ_DEVICE Tile tile_of(const W4Args& p) {
   const int num = p.tiles_m * p.tiles_n, per = num / 8, bid = blockIdx.x;
@@ -57,7 +76,7 @@ MXQ_DEVICE Tile tile_of(const W4Args& p) {
 }
 
 template <int kOut>
-__global__ __launch_bounds__(256, 1) void w4a8_g128_kernel(W4Args p) {
+__global__ __launch_bounds__(kThreads, kOcc) void w4a8_g128_kernel(W4Args p) {
   __shared__ __attribute__((aligned(16))) char lds[kLds];
   char* const scale_ring = lds + kNS * kStage;
 
@@ -83,8 +102,8 @@ __global__ __launch_bounds__(256, 1) void w4a8_g128_kernel(W4Args p) {
     const int c = (lane & 3) ^ ((r >> 2) & 3);
     b_off[t] = (uint32_t)(min(n0 + r, p.N - 1) * khalf + c * 16);
   }
-  // wave w fetches scale bytes [64 w, 64 w + 64) of the group's row of 128 (8 per lane).
-  const int64_t s_col = n0 + wave * (kBN / 4) + lane * 8;
+  // wave w fetches scale bytes [64 w, 64 w + 64) of the group's row of kBN (8 per lane).
+  const int64_t s_col = n0 + wave * 32 + lane * 8;
   const uint32_t s_off = (uint32_t)((s_col < p.N ? s_col : 0) * 2);
 
   auto issue_stage = [&](int kt) {
@@ -100,7 +119,7 @@ __global__ __launch_bounds__(256, 1) void w4a8_g128_kernel(W4Args p) {
     for (int t = 0; t < kBLoads; ++t)
       __builtin_amdgcn_global_load_lds((gptr_t)(bbase + b_off[t]),
                                        (lptr_t)(st + kStageA + (wave * kBLoads + t) * 1024), 16, 0, 0);
-    char* sd = scale_ring + (kt & (kScaleRing - 1)) * kScaleBytes + wave * (kScaleBytes / 4);
+    char* sd = scale_ring + (kt & (kScaleRing - 1)) * kScaleBytes + wave * (kScaleBytes / kWaves);
     if (lane < kScaleLanes) __builtin_amdgcn_global_load_lds((gptr_t)(sbase + s_off), (lptr_t)sd, 16, 0, 0);
   };
 
@@ -172,6 +191,7 @@ __global__ __launch_bounds__(256, 1) void w4a8_g128_kernel(W4Args p) {
         if constexpr (s == 0) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) facc[i][r] = fmaf((float)acc[i][r], sc, facc[i][r]);
+          order_after_fold(fa[i], facc[i]);
         } else {
           // block i's fragment of this step was read after its previous MFMA; the reads of the
           // later blocks may still be in flight
@@ -245,8 +265,8 @@ __global__ __launch_bounds__(256, 1) void w4a8_g128_kernel(W4Args p) {
   char* D = reinterpret_cast<char*>(p.d);
   const bool vec = ((uintptr_t)p.d % 16 == 0) && ((p.ldd * kE) % 16 == 0);
 #pragma unroll
-  for (int q = 0; q < kBM * kChunksRow / 256; ++q) {
-    const int id = q * 256 + threadIdx.x;
+  for (int q = 0; q < kBM * kChunksRow / kThreads; ++q) {
+    const int id = q * kThreads + threadIdx.x;
     const int row = id / kChunksRow, ch = id % kChunksRow;
     const int64_t grow = m0 + row, gcol = n0 + ch * kPerElem;
     if (grow >= p.M) continue;
@@ -271,9 +291,9 @@ int launch_w4_g128(W4Args p, int out_dtype, hipStream_t st) {
   p.tiles_n = (int)((p.N + kBN - 1) / kBN);
   const unsigned grid = (unsigned)(p.tiles_m * p.tiles_n);
   switch (out_dtype) {
-    case MXQ_DTYPE_F32: w4a8_g128_kernel<0><<<grid, 256, 0, st>>>(p); break;
-    case MXQ_DTYPE_F16: w4a8_g128_kernel<1><<<grid, 256, 0, st>>>(p); break;
-    case MXQ_DTYPE_BF16: w4a8_g128_kernel<2><<<grid, 256, 0, st>>>(p); break;
+    case MXQ_DTYPE_F32: w4a8_g128_kernel<0><<<grid, kThreads, 0, st>>>(p); break;
+    case MXQ_DTYPE_F16: w4a8_g128_kernel<1><<<grid, kThreads, 0, st>>>(p); break;
+    case MXQ_DTYPE_BF16: w4a8_g128_kernel<2><<<grid, kThreads, 0, st>>>(p); break;
     default: return mxq_set_error(MXQ_ERR_UNSUPPORTED, "output dtype code %d", out_dtype);
   }
   return mxq_check_launch("w4a8_g128_kernel");
