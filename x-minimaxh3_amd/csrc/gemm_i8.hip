@@ -128,21 +128,28 @@ MXQ_DEVICE void make_loader(Loader<kL>& L, const GemmArgs& p, int64_t m0, int64_
   }
 }
 
-// Load t of this wave's share of an A (kB = false) or B slot.
-template <bool kB, int kL>
+// Load t of this wave's share of an A (kB = false) or B slot. With kCheck a chunk past K reads
+// zeros (A) or any valid bytes (B: their products with A's zeros vanish); without it the caller
+// guarantees the whole stage lies below K.
+template <bool kB, bool kCheck, int kL>
 MXQ_DEVICE void issue_one(const Loader<kL>& L, char* slot, int64_t k0, int64_t K, int t) {
   const int w = threadIdx.x >> 6;
   const int koff = L.koff[t & 1];
-  const bool kin = k0 + koff < K;
-  const void* src = kB ? (kin ? (const void*)(L.b[t] + k0 + koff) : (const void*)L.b[t])
-                       : (kin ? (const void*)(L.a[t] + k0) : (const void*)kZeroChunk);
+  const void* src;
+  if constexpr (kCheck) {
+    const bool kin = k0 + koff < K;
+    src = kB ? (kin ? (const void*)(L.b[t] + k0 + koff) : (const void*)L.b[t])
+             : (kin ? (const void*)(L.a[t] + k0) : (const void*)kZeroChunk);
+  } else {
+    src = kB ? (const void*)(L.b[t] + k0 + koff) : (const void*)(L.a[t] + k0);
+  }
   __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)(slot + (w * kL + t) * 1024), 16, 0, 0);
 }
 
 template <bool kB, int kL>
 MXQ_DEVICE void issue_slot(const Loader<kL>& L, char* slot, int64_t k0, int64_t K) {
 #pragma unroll
-  for (int t = 0; t < kL; ++t) issue_one<kB>(L, slot, k0, K, t);
+  for (int t = 0; t < kL; ++t) issue_one<kB, true>(L, slot, k0, K, t);
 }
 
 // Fragments of K-step ks (32 K-bytes) of a stage: A rows wm*kWaveM + i*32 + l%32 and B rows
@@ -175,7 +182,7 @@ MXQ_DEVICE void mma_step(const v4i fa[C::kBI], const v4i fb[C::kBJ], v16i acc[C:
 // interleaved, one after each of the first kCount MFMAs (kCount <= kBI * kBJ). Spread this way,
 // a load that waits for room in the memory pipeline holds up the wave while its MFMAs still
 // run, rather than after the last of them.
-template <class C, bool kB, int kFirst, int kCount>
+template <class C, bool kB, int kFirst, int kCount, bool kCheck>
 MXQ_DEVICE void mma_step_dma(const v4i fa[C::kBI], const v4i fb[C::kBJ], v16i acc[C::kBI][C::kBJ],
                              const Loader<C::kLoads>& L, char* slot, int64_t k0, int64_t K, bool on) {
   static_assert(kCount <= C::kBI * C::kBJ, "more loads than MFMAs to spread them over");
@@ -183,7 +190,7 @@ MXQ_DEVICE void mma_step_dma(const v4i fa[C::kBI], const v4i fb[C::kBJ], v16i ac
   for (int q = 0; q < C::kBI * C::kBJ; ++q) {
     const int i = q / C::kBJ, j = q % C::kBJ;
     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j], fa[i], acc[i][j], 0, 0, 0);
-    if (q < kCount && on) issue_one<kB>(L, slot, k0, K, kFirst + q);  // t is a constant once unrolled
+    if (q < kCount && on) issue_one<kB, kCheck>(L, slot, k0, K, kFirst + q);  // t is a constant once unrolled
   }
 }
 
@@ -353,23 +360,28 @@ __global__ __launch_bounds__(kGemmThreads, kT == 256 ? 1 : 2) void gemm_i8_kerne
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   __builtin_amdgcn_sched_barrier(0);
   int sa = 0;  // slot of A_kt; B_kt is in (sa + 1) % 5
-  for (int kt = 0; kt < ktiles; ++kt) {
+  // One iteration. kSteady: stage kt+2 exists and lies wholly below K, so every load of the
+  // iteration is issued and none needs the K-tail check (no per-load compare, select or branch);
+  // the last two or three iterations take the general form.
+  auto iteration = [&](int kt, auto steady) {
+    constexpr bool kSteady = decltype(steady)::value;
     const int sb = sa == kSlots - 1 ? 0 : sa + 1;
     const int na = sb == kSlots - 1 ? 0 : sb + 1;  // A_kt+1
     const int nb = na == kSlots - 1 ? 0 : na + 1;  // B_kt+1
     const int pa = nb == kSlots - 1 ? 0 : nb + 1;  // A_kt+2 (slot of B_kt-1)
     const uint32_t cur_a = lds_addr + (uint32_t)(sa * kSlotBytes), cur_b = lds_addr + (uint32_t)(sb * kSlotBytes);
-    const bool more2 = kt + 2 < ktiles;
+    const bool more2 = kSteady || kt + 2 < ktiles;
+    const bool more1 = kSteady || kt + 1 < ktiles;
     const int64_t k2 = (int64_t)(kt + 2) * kBK;
     load_frags<C>(cur_a, cur_b, wm, wn, 1, f1a, f1b);
     wait_lgkm<kBI + kBJ>();
     __builtin_amdgcn_sched_barrier(0);
-    mma_step_dma<C, false, 0, kLoads / 2>(f0a, f0b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
+    mma_step_dma<C, false, 0, kLoads / 2, !kSteady>(f0a, f0b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
     __builtin_amdgcn_sched_barrier(0);
     load_frags<C>(cur_a, cur_b, wm, wn, 2, f0a, f0b);
     wait_lgkm<kBI + kBJ>();
     __builtin_amdgcn_sched_barrier(0);
-    mma_step_dma<C, false, kLoads / 2, kLoads / 2>(f1a, f1b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
+    mma_step_dma<C, false, kLoads / 2, kLoads / 2, !kSteady>(f1a, f1b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
     __builtin_amdgcn_sched_barrier(0);
     load_frags<C>(cur_a, cur_b, wm, wn, 3, f1a, f1b);
     wait_lgkm<kBI + kBJ>();
@@ -382,15 +394,24 @@ __global__ __launch_bounds__(kGemmThreads, kT == 256 ? 1 : 2) void gemm_i8_kerne
       wait_all();
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (kt + 1 < ktiles) {
+    if (more1) {
       barrier_no_drain();
       load_frags<C>(lds_addr + (uint32_t)(na * kSlotBytes), lds_addr + (uint32_t)(nb * kSlotBytes), wm, wn, 0, f0a, f0b);
     }
     __builtin_amdgcn_sched_barrier(0);
-    mma_step_dma<C, true, 0, kLoads>(f1a, f1b, acc, ld, lds + sa * kSlotBytes, k2, p.K, more2 && kt + 1 < ktiles);
+    mma_step_dma<C, true, 0, kLoads, !kSteady>(f1a, f1b, acc, ld, lds + sa * kSlotBytes, k2, p.K, more2 && more1);
     __builtin_amdgcn_sched_barrier(0);
     sa = na;
-  }
+  };
+  // steady < ktiles always (ktiles >= 1): written as do-while, the tail is seen to run at least
+  // once, so no path leaves the steady loop with fragment reads in flight straight into the
+  // epilogue (whose register copies would otherwise race those reads).
+  const int steady = (int)max<int64_t>(p.K / kBK - 2, 0);  // iterations whose stage kt+2 is full
+  int kt = 0;
+  for (; kt < steady; ++kt) iteration(kt, std::true_type{});
+  do {
+    iteration(kt, std::false_type{});
+  } while (++kt < ktiles);
   // Every wave is done reading the ring before the epilogue reuses it, and the last (unused)
   // fragment reads have landed before their registers are reused.
   wait_all();
