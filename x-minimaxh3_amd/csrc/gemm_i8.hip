@@ -113,11 +113,13 @@ struct Loader {
   const int8_t* a[kL];
   const int8_t* b[kL];
   int koff[2];   // logical chunk offset (bytes) of this lane's piece, for even and odd t
+  int wave;      // the wave's index, as a scalar: LDS destinations (M0) are then scalar arithmetic
 };
 
 template <int kL>
 MXQ_DEVICE void make_loader(Loader<kL>& L, const GemmArgs& p, int64_t m0, int64_t n0) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  L.wave = __builtin_amdgcn_readfirstlane(w);
 #pragma unroll
   for (int t = 0; t < kL; ++t) {
     const int r = (w * kL + t) * 8 + (lane >> 3);
@@ -133,7 +135,7 @@ MXQ_DEVICE void make_loader(Loader<kL>& L, const GemmArgs& p, int64_t m0, int64_
 // guarantees the whole stage lies below K.
 template <bool kB, bool kCheck, int kL>
 MXQ_DEVICE void issue_one(const Loader<kL>& L, char* slot, int64_t k0, int64_t K, int t) {
-  const int w = threadIdx.x >> 6;
+  const int w = L.wave;
   const int koff = L.koff[t & 1];
   const void* src;
   if constexpr (kCheck) {
