@@ -1,0 +1,96 @@
+"""GPU parity of the 256 x 256-tile INT8 GEMM (the configuration every model-sized shape runs).
+
+The library runs a GEMM with 256 x 256 tiles once it has at least 256 of them (fewer: 128 x 128
+tiles, which the small-shape tests cover), so these shapes have M x N >= 4100 x 4104. K is chosen
+at the boundaries of the K loop: a single stage (128), stages that are all full with and without
+steady-state iterations (256, 384, 1024) and a partial last stage after zero, one or two steady
+iterations (144, 400, 528). Every epilogue is covered: int32, dequant (+ bias) to bf16, GELU +
+row absmax (in the FFN chain), SwiGLU and the gated residual.
+
+Bar: int32 and every bf16 output bit-exact against the oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from _util import activations, bf16_vec, bits, gen, int8_weight
+from oracle import convrot as cr
+from oracle import eager_np
+from oracle.bf16 import bf16_bits
+
+pytestmark = pytest.mark.gpu
+
+M, N = 4100, 4104  # 17 x 17 tiles of 256, both edges partial
+
+
+def _mx():
+    import mx_qlinear
+
+    return mx_qlinear
+
+
+def _i8(shape, seed):
+    return torch.randint(-128, 128, shape, generator=gen(seed), dtype=torch.int8)
+
+
+@pytest.mark.parametrize("k", [128, 144, 256, 384, 400, 528, 1024])
+def test_gemm_i32_256_tiles(dev, k):
+    print(f"gemm i32 256-tile m={M} n={N} k={k}", flush=True)
+    a, w = _i8((M, k), 40 + k), _i8((N, k), 41 + k)
+    c = _mx().mm_int8(a.to(dev), w.to(dev).t())
+    assert np.array_equal(c.cpu().numpy(), eager_np.int8_matmul(a.numpy(), w.numpy()))
+
+
+@pytest.mark.parametrize("k,bias", [(400, True), (1024, False)])
+def test_int8_linear_256_tiles(dev, k, bias):
+    print(f"int8_linear 256-tile m={M} n={N} k={k} bias={bias}", flush=True)
+    x = activations(M, k, 50 + k)
+    w, ws = int8_weight(N, k, 51 + k)
+    b = bf16_vec(N, 52, 0.01) if bias else None
+    y = _mx().int8_linear(x.to(dev), w.to(dev), ws.to(dev), None if b is None else b.to(dev))
+    ref = eager_np.int8_linear(bits(x), w.numpy(), ws.numpy(), None if b is None else bits(b), "bf16")
+    assert np.array_equal(bits(y), bf16_bits(ref))
+
+
+def test_ffn_chain_256_tiles(dev):
+    """fc1 (GELU + row absmax epilogue) and fc2 both run 256 x 256 tiles."""
+    m, k, hidden, n = M, 400, 4112, 4096  # hidden: a multiple of 16 with a partial edge tile
+    print(f"ffn 256-tile m={m} k={k} hidden={hidden} n={n}", flush=True)
+    x = activations(m, k, 60)
+    w1, s1 = int8_weight(hidden, k, 61)
+    w2, s2 = int8_weight(n, hidden, 62)
+    b1, b2 = bf16_vec(hidden, 63, 0.01), bf16_vec(n, 64, 0.01)
+    out = _mx().int8_ffn_gelu(x.to(dev), w1.to(dev), s1.to(dev), b1.to(dev), w2.to(dev), s2.to(dev), b2.to(dev))
+    ref, _ = eager_np.ffn_gelu_int8(bits(x), w1.numpy(), s1.numpy(), bits(b1), w2.numpy(), s2.numpy(), bits(b2))
+    assert np.array_equal(bits(out), bf16_bits(ref))
+
+
+def test_swiglu_fc1_256_tiles(dev):
+    m, f, k = M, 4096, 528
+    print(f"swiglu fc1 256-tile m={m} f={f} k={k}", flush=True)
+    x = activations(m, k, 70)
+    w, ws = int8_weight(2 * f, k, 71)
+    b = bf16_vec(2 * f, 72, 0.05)
+    q, s = eager_np.quantize_int8_rowwise(bits(x))
+    fc1 = _mx().prepare_swiglu_fc1(w.to(dev), ws.to(dev), b.to(dev))
+    h = _mx().int8_swiglu_fc1(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), fc1)
+    y = eager_np.dequant_epilogue(eager_np.int8_matmul(q, w.numpy()), s, ws.numpy(), bits(b), "bf16")
+    assert np.array_equal(bits(h), cr.swiglu_bf16(bf16_bits(y)))
+
+
+def test_gated_residual_256_tiles(dev):
+    k = 384
+    print(f"gated residual 256-tile m={M} n={N} k={k}", flush=True)
+    x = activations(M, k, 80)
+    w, ws = int8_weight(N, k, 81)
+    b = bf16_vec(N, 82, 0.02)
+    gate = torch.randn(3, N, generator=gen(83)).to(torch.bfloat16)
+    res = activations(M, N, 84) * 3
+    segs = ((0, 1000, 2), (1000, 2500, 0), (2500, M, 1))
+    out = res.to(dev)
+    _mx().int8_linear_gated_residual_(out, x.to(dev), w.to(dev), ws.to(dev), b.to(dev), gate.to(dev), segs)
+    q, s = eager_np.quantize_int8_rowwise(bits(x))
+    y = eager_np.dequant_epilogue(eager_np.int8_matmul(q, w.numpy()), s, ws.numpy(), bits(b), "bf16")
+    want = eager_np.gated_residual_bf16(bits(res), bf16_bits(y), bits(gate), eager_np.segment_row_map(M, segs))
+    assert np.array_equal(bits(out), want)

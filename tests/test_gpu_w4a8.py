@@ -94,10 +94,11 @@ def test_grouped_power_of_two_scales_are_exact(dev):
     assert np.array_equal(y.cpu().numpy().astype(np.float64), exact)
 
 
-# group 128 with N % 8 == 0 runs the pipelined kernel (edge tiles in M and N included); group 256
-# and N = 70 run the general kernel.
+# group 128 with N % 8 == 0 runs the pipelined kernel (edge tiles in M and N included; K of one
+# and two groups, shorter than its 3-stage ring); group 256 and N = 70 run the general kernel.
 @pytest.mark.parametrize("m,n,k,g", [(512, 1024, 5120, 128), (2048, 640, 1024, 128), (100, 200, 1024, 128),
-                                     (257, 136, 640, 128), (100, 200, 1024, 256), (33, 70, 512, 128)])
+                                     (257, 136, 640, 128), (64, 256, 128, 128), (130, 264, 256, 128),
+                                     (100, 200, 1024, 256), (33, 70, 512, 128)])
 def test_grouped_matches_oracle(dev, m, n, k, g):
     print(f"w4a8 grouped m={m} n={n} k={k} g={g}", flush=True)
     x = activations(m, k, 1000 + m, outlier_frac=0.0)
