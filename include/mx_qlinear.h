@@ -281,6 +281,26 @@ int mxq_w4a8_gemm_grouped(const int8_t* a, const float* xs, const int8_t* qdata,
                           int64_t N, int64_t K, int64_t group_size, int64_t ldd, int out_dtype,
                           void* stream);
 
+/*
+ * Weight preparation for mxq_w4a8_gemm_grouped_prepared (a load-time layout transform, no
+ * counterpart in the reference): qdata [N, K/2] as above -> out [N, K/2] (may alias qdata),
+ * K % 8 == 0. Each 32-bit word keeps the 8 codes of k = 8w .. 8w + 7; byte j of the result
+ * holds (c[8w + j] ^ 8) in its low nibble and (c[8w + 4 + j] ^ 8) in its high nibble (the code
+ * as the 4-bit two's complement value c - 8), so the GEMM unpacks a word with one shift and two
+ * masks instead of the six instructions the checkpoint layout needs.
+ */
+int mxq_w4a8_prepare_grouped(const int8_t* qdata, int8_t* out, int64_t N, int64_t K, void* stream);
+
+/*
+ * mxq_w4a8_gemm_grouped on weights prepared by mxq_w4a8_prepare_grouped: same arguments and
+ * results (bit for bit); group_size must be 128, N a multiple of 8 and group_scale 16-byte
+ * aligned (MXQ_ERR_UNSUPPORTED otherwise).
+ */
+int mxq_w4a8_gemm_grouped_prepared(const int8_t* a, const float* xs, const int8_t* qdata,
+                                   const uint16_t* group_scale, const void* bias, void* d, int64_t M,
+                                   int64_t N, int64_t K, int64_t group_size, int64_t ldd, int out_dtype,
+                                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

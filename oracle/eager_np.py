@@ -312,6 +312,29 @@ def unpack_int4(packed: np.ndarray) -> np.ndarray:
     return codes
 
 
+def prepare_w4a8_grouped(packed: np.ndarray) -> np.ndarray:
+    """The GEMM's load layout of packed offset-8 codes ``[N, K/2]`` (this build's own layout; the
+    reference has none): per 8 consecutive k (one 32-bit word), byte j holds ``c[j] ^ 8`` in its
+    low nibble and ``c[4 + j] ^ 8`` in its high nibble (``c ^ 8`` is ``c - 8`` as a 4-bit two's
+    complement value)."""
+    codes = unpack_int4(packed)
+    n, k = codes.shape
+    if k % 8:
+        raise ValueError("K must be a multiple of 8")
+    v = (codes ^ 8).reshape(n, k // 8, 8)
+    out = v[:, :, 0:4] | (v[:, :, 4:8] << 4)
+    return out.reshape(n, k // 2).astype(np.uint8).view(np.int8)
+
+
+def unprepare_w4a8_grouped(prepared: np.ndarray) -> np.ndarray:
+    """Offset-8 codes ``[N, K]`` (int32) of a :func:`prepare_w4a8_grouped` layout."""
+    p = np.asarray(prepared).view(np.uint8).astype(np.int32)
+    n, kh = p.shape
+    q = p.reshape(n, kh // 4, 4)
+    codes = np.concatenate([q & 0xF, (q >> 4) & 0xF], axis=2) ^ 8
+    return codes.reshape(n, kh * 2)
+
+
 def quantize_int4_symmetric(w: np.ndarray) -> np.ndarray:
     """Signed int4 values in [-8, 7] -> offset-8 codes (``u = v + 8``, w4a8_int8.py:171-173)."""
     v = np.asarray(w, dtype=np.int32)

@@ -126,3 +126,39 @@ def test_grouped_with_bias(dev, m, n):
     a, xs = eager_np.quantize_int8_rowwise(bits(x))
     ref = eager_np.w4a8_grouped_linear(a, xs, qd.numpy(), gs.numpy(), g, bits(bias))
     assert np.array_equal(bits(y), bf16_bits(ref))
+
+
+# ---- the prepared (load) layout of the group-128 kernel ------------------------------------
+
+@pytest.mark.parametrize("n,k", [(136, 640), (3, 8), (1024, 5120)])
+def test_prepare_matches_oracle(dev, n, k):
+    qd = packed_int4(n, k, 900 + n)
+    got = _mx().prepare_w4a8_grouped(qd.to(dev)).qdata.cpu().numpy()
+    assert np.array_equal(got, eager_np.prepare_w4a8_grouped(qd.numpy()))
+
+
+@pytest.mark.parametrize("m,n,k,bias,out_dtype", [(512, 1024, 5120, False, torch.bfloat16),
+                                                  (257, 136, 640, True, torch.bfloat16),
+                                                  (64, 256, 128, False, torch.float16),
+                                                  (130, 264, 256, True, torch.float32)])
+def test_prepared_equals_checkpoint_layout(dev, m, n, k, bias, out_dtype):
+    print(f"w4a8 prepared m={m} n={n} k={k} bias={bias} out={out_dtype}", flush=True)
+    x = activations(m, k, 910 + m).to(dev)
+    qd = packed_int4(n, k, 911 + n).to(dev)
+    gs = group_scales(k, n, 128, 912).to(dev)
+    b = bf16_vec(n, 913, 0.01).to(out_dtype).to(dev) if bias else None
+    ref = _mx().w4a8_grouped_linear(x, qd, gs, 128, bias=b, out_dtype=out_dtype)
+    got = _mx().w4a8_grouped_linear(x, _mx().prepare_w4a8_grouped(qd), gs, 128, bias=b, out_dtype=out_dtype)
+    assert torch.equal(got.view(torch.int16 if out_dtype != torch.float32 else torch.int32),
+                       ref.view(torch.int16 if out_dtype != torch.float32 else torch.int32))
+    if not bias and out_dtype == torch.bfloat16:
+        a, xs = eager_np.quantize_int8_rowwise(bits(x.cpu()))
+        want = eager_np.w4a8_grouped_linear(a, xs, qd.cpu().numpy(), gs.cpu().numpy(), 128)
+        assert np.array_equal(bits(got), bf16_bits(want))
+
+
+def test_prepared_needs_group_128(dev):
+    qd = packed_int4(64, 512, 920).to(dev)
+    x = activations(16, 512, 921).to(dev)
+    with pytest.raises(RuntimeError, match="group 128"):
+        _mx().w4a8_grouped_linear(x, _mx().prepare_w4a8_grouped(qd), group_scales(512, 64, 256, 922).to(dev), 256)

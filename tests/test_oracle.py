@@ -253,6 +253,31 @@ def test_pack_unpack_roundtrip_and_nibble_order():
     assert p1.view(np.uint8)[0, 0] == 0xC3
 
 
+def test_prepared_w4a8_layout():
+    """The load layout of the group-128 GEMM: a known word, the round trip, and the device's
+    unpack rule ((w << 4) & 0xF0F0F0F0, w & 0xF0F0F0F0 -> 16 (c - 8) in natural k order)."""
+    p = eager_np.pack_int4(np.arange(8).reshape(1, 8))
+    assert p.view(np.uint8).tolist() == [[0x10, 0x32, 0x54, 0x76]]
+    q = eager_np.prepare_w4a8_grouped(p)
+    assert q.view(np.uint8).tolist() == [[0xC8, 0xD9, 0xEA, 0xFB]]
+    codes = np.random.default_rng(5).integers(0, 16, size=(7, 64))
+    q = eager_np.prepare_w4a8_grouped(eager_np.pack_int4(codes))
+    assert np.array_equal(eager_np.unprepare_w4a8_grouped(q), codes)
+
+    def device_unpack(prepared):
+        w = np.ascontiguousarray(prepared).view(np.uint32)  # little-endian words
+        lo = ((w << 4) & 0xF0F0F0F0).astype(np.uint32)
+        hi = (w & 0xF0F0F0F0).astype(np.uint32)
+        b = np.stack([lo, hi], axis=-1).view(np.int8)      # per word: 4 bytes of lo, then 4 of hi
+        return b.reshape(prepared.shape[0], -1).astype(np.int32)
+
+    assert np.array_equal(device_unpack(q), 16 * (codes - 8))
+    # a planted mistake (nibble halves swapped) fails the unpack rule
+    bad = q.view(np.uint8)
+    bad = (((bad & 0xF) << 4) | (bad >> 4)).astype(np.uint8).view(np.int8)
+    assert not np.array_equal(device_unpack(bad), 16 * (codes - 8))
+
+
 def test_decode_closed_forms():
     n, k = 4, 64
     codes = (np.arange(n * k) % 16).reshape(n, k)

@@ -24,6 +24,8 @@
 //    exactly, and the final multiply uses xs / 16, so the result is bit-identical to the
 //    unscaled recipe while the unpack costs 6 ALU ops per 8 weights.
 
+#include <algorithm>
+
 #include "w4a8_common.h"
 
 namespace mxq {
@@ -332,10 +334,8 @@ extern "C" int mxq_w4a8_codebook_gemm(const int8_t* xq, const int8_t* qdata, con
   return MXQ_OK;
 }
 
-extern "C" int mxq_w4a8_gemm_grouped(const int8_t* a, const float* xs, const int8_t* qdata,
-                                     const uint16_t* group_scale, const void* bias, void* d,
-                                     int64_t M, int64_t N, int64_t K, int64_t group_size,
-                                     int64_t ldd, int out_dtype, void* stream) {
+static int check_grouped(const int8_t* a, const float* xs, const int8_t* qdata, const uint16_t* group_scale,
+                         void* d, int64_t M, int64_t N, int64_t K, int64_t group_size, int64_t ldd) {
   if (M < 0 || N < 0 || K < 0) return mxq_set_error(MXQ_ERR_INVALID, "negative shape");
   if (M == 0 || N == 0) return MXQ_OK;
   if (!a || !xs || !qdata || !group_scale || !d) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
@@ -347,18 +347,84 @@ extern "C" int mxq_w4a8_gemm_grouped(const int8_t* a, const float* xs, const int
   if (K > 131072) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "K too large");
   if ((uintptr_t)a % 16 || (uintptr_t)qdata % 16)
     return mxq_set_error(MXQ_ERR_UNSUPPORTED, "A and packed weights must be 16-byte aligned");
+  return MXQ_OK;
+}
+
+static W4Args grouped_args(const int8_t* a, const float* xs, const int8_t* qdata, const uint16_t* group_scale,
+                           const void* bias, void* d, int64_t M, int64_t N, int64_t K, int64_t group_size,
+                           int64_t ldd) {
   W4Args p{};
   p.a = a; p.xs = xs; p.w = (const uint8_t*)qdata; p.gs = group_scale; p.bias = bias; p.d = d;
   p.M = M; p.N = N; p.K = K; p.ldd = ldd; p.group_tiles = (int)(group_size / kW4BK);
+  return p;
+}
+
+extern "C" int mxq_w4a8_gemm_grouped(const int8_t* a, const float* xs, const int8_t* qdata,
+                                     const uint16_t* group_scale, const void* bias, void* d,
+                                     int64_t M, int64_t N, int64_t K, int64_t group_size,
+                                     int64_t ldd, int out_dtype, void* stream) {
+  const int rc0 = check_grouped(a, xs, qdata, group_scale, d, M, N, K, group_size, ldd);
+  if (rc0 != MXQ_OK || M == 0 || N == 0) return rc0;
+  const W4Args p = grouped_args(a, xs, qdata, group_scale, bias, d, M, N, K, group_size, ldd);
   hipStream_t st = (hipStream_t)stream;
   // Group 128 (one group per K stage) with 16-byte aligned scale rows: the pipelined kernel on
-  // 128 x 128 tiles. (128 x 256 tiles need more than the 512 registers a lane has: the two
-  // accumulator sets alone fill the 256 AGPRs and the fp32 accumulators half the VGPRs.)
+  // 128 x 128 tiles, two workgroups per CU.
   if (group_size == 128 && N % 8 == 0 && (uintptr_t)group_scale % 16 == 0) {
-    const int rc = launch_w4_g128(p, out_dtype, st);
+    const int rc = launch_w4_g128(p, out_dtype, false, st);
     if (rc != MXQ_ERR_UNSUPPORTED) return rc;  // else: operands too large for 32-bit offsets
   }
   // Other group sizes: 256 x 128 tiles (waves 128 x 64) for large M, 128 x 64 otherwise.
   if (M >= 2048) return launch_w4<256, 128, 128, 64>(p, out_dtype, st);
   return launch_w4<128, 64, 64, 32>(p, out_dtype, st);
+}
+
+extern "C" int mxq_w4a8_gemm_grouped_prepared(const int8_t* a, const float* xs, const int8_t* qdata,
+                                              const uint16_t* group_scale, const void* bias, void* d,
+                                              int64_t M, int64_t N, int64_t K, int64_t group_size,
+                                              int64_t ldd, int out_dtype, void* stream) {
+  const int rc0 = check_grouped(a, xs, qdata, group_scale, d, M, N, K, group_size, ldd);
+  if (rc0 != MXQ_OK || M == 0 || N == 0) return rc0;
+  if (group_size != 128 || N % 8 != 0 || (uintptr_t)group_scale % 16 != 0)
+    return mxq_set_error(MXQ_ERR_UNSUPPORTED,
+                         "prepared W4A8 weights need group 128, N %% 8 == 0 and 16-byte aligned scales "
+                         "(G=%lld, N=%lld)", (long long)group_size, (long long)N);
+  const W4Args p = grouped_args(a, xs, qdata, group_scale, bias, d, M, N, K, group_size, ldd);
+  const int rc = launch_w4_g128(p, out_dtype, true, (hipStream_t)stream);
+  if (rc == MXQ_ERR_UNSUPPORTED)
+    return mxq_set_error(MXQ_ERR_UNSUPPORTED, "prepared W4A8 operands exceed 2^31 bytes (M=%lld, N=%lld, K=%lld)",
+                         (long long)M, (long long)N, (long long)K);
+  return rc;
+}
+
+namespace mxq {
+namespace {
+
+// One 32-bit word (8 codes of k = 8w .. 8w + 7) per thread, grid-stride; in place allowed.
+__global__ __launch_bounds__(256) void w4_prepare_kernel(const uint32_t* in, uint32_t* out, int64_t words) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += stride) {
+    const uint32_t w = in[i] ^ 0x88888888u;  // every code c -> c ^ 8, the 4-bit value c - 8
+    uint32_t r = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      r |= (((w >> (4 * j)) & 0xFu) | (((w >> (4 * (4 + j))) & 0xFu) << 4)) << (8 * j);
+    out[i] = r;
+  }
+}
+
+}  // namespace
+}  // namespace mxq
+
+extern "C" int mxq_w4a8_prepare_grouped(const int8_t* qdata, int8_t* out, int64_t N, int64_t K, void* stream) {
+  if (N < 0 || K < 0) return mxq_set_error(MXQ_ERR_INVALID, "negative shape");
+  if (K % 8 != 0) return mxq_set_error(MXQ_ERR_INVALID, "K=%lld must be a multiple of 8", (long long)K);
+  const int64_t words = N * (K / 8);
+  if (words == 0) return MXQ_OK;
+  if (!qdata || !out) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  if ((uintptr_t)qdata % 4 || (uintptr_t)out % 4)
+    return mxq_set_error(MXQ_ERR_UNSUPPORTED, "packed weights must be 4-byte aligned");
+  const int64_t blocks = std::min<int64_t>((words + 255) / 256, 8192);
+  mxq::w4_prepare_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(
+      reinterpret_cast<const uint32_t*>(qdata), reinterpret_cast<uint32_t*>(out), words);
+  return mxq_check_launch("w4_prepare_kernel");
 }

@@ -75,7 +75,7 @@ MXQ_DEVICE Tile tile_of(const W4Args& p) {
   return Tile{(int64_t)(first + in % gm) * kBM, (int64_t)(in / gm) * kBN};
 }
 
-template <int kOut>
+template <int kOut, bool kPrepared>
 __global__ __launch_bounds__(kThreads, kOcc) void w4a8_g128_kernel(W4Args p) {
   __shared__ __attribute__((aligned(16))) char lds[kLds];
   char* const scale_ring = lds + kNS * kStage;
@@ -151,8 +151,13 @@ __global__ __launch_bounds__(kThreads, kOcc) void w4a8_g128_kernel(W4Args p) {
 
   auto unpack_step = [&](const v4i (&bq)[2], int s) {
     uint32_t o0, o1, o2, o3;
-    unpack8((uint32_t)bq[s >> 1][(s & 1) * 2], o0, o1);
-    unpack8((uint32_t)bq[s >> 1][(s & 1) * 2 + 1], o2, o3);
+    if constexpr (kPrepared) {
+      unpack8_prepared((uint32_t)bq[s >> 1][(s & 1) * 2], o0, o1);
+      unpack8_prepared((uint32_t)bq[s >> 1][(s & 1) * 2 + 1], o2, o3);
+    } else {
+      unpack8((uint32_t)bq[s >> 1][(s & 1) * 2], o0, o1);
+      unpack8((uint32_t)bq[s >> 1][(s & 1) * 2 + 1], o2, o3);
+    }
     return v4i{(int)o0, (int)o1, (int)o2, (int)o3};
   };
 
@@ -284,16 +289,19 @@ __global__ __launch_bounds__(kThreads, kOcc) void w4a8_g128_kernel(W4Args p) {
 
 }  // namespace
 
-int launch_w4_g128(W4Args p, int out_dtype, hipStream_t st) {
+int launch_w4_g128(W4Args p, int out_dtype, bool prepared, hipStream_t st) {
   if (p.M * p.K >= (int64_t)1 << 31 || p.N * (p.K / 2) >= (int64_t)1 << 31 || p.N * (p.K / 128) * 2 >= (int64_t)1 << 31)
     return MXQ_ERR_UNSUPPORTED;  // the caller falls back to the general kernel
   p.tiles_m = (int)((p.M + kBM - 1) / kBM);
   p.tiles_n = (int)((p.N + kBN - 1) / kBN);
   const unsigned grid = (unsigned)(p.tiles_m * p.tiles_n);
-  switch (out_dtype) {
-    case MXQ_DTYPE_F32: w4a8_g128_kernel<0><<<grid, kThreads, 0, st>>>(p); break;
-    case MXQ_DTYPE_F16: w4a8_g128_kernel<1><<<grid, kThreads, 0, st>>>(p); break;
-    case MXQ_DTYPE_BF16: w4a8_g128_kernel<2><<<grid, kThreads, 0, st>>>(p); break;
+  switch (out_dtype * 2 + (prepared ? 1 : 0)) {
+    case MXQ_DTYPE_F32 * 2: w4a8_g128_kernel<0, false><<<grid, kThreads, 0, st>>>(p); break;
+    case MXQ_DTYPE_F32 * 2 + 1: w4a8_g128_kernel<0, true><<<grid, kThreads, 0, st>>>(p); break;
+    case MXQ_DTYPE_F16 * 2: w4a8_g128_kernel<1, false><<<grid, kThreads, 0, st>>>(p); break;
+    case MXQ_DTYPE_F16 * 2 + 1: w4a8_g128_kernel<1, true><<<grid, kThreads, 0, st>>>(p); break;
+    case MXQ_DTYPE_BF16 * 2: w4a8_g128_kernel<2, false><<<grid, kThreads, 0, st>>>(p); break;
+    case MXQ_DTYPE_BF16 * 2 + 1: w4a8_g128_kernel<2, true><<<grid, kThreads, 0, st>>>(p); break;
     default: return mxq_set_error(MXQ_ERR_UNSUPPORTED, "output dtype code %d", out_dtype);
   }
   return mxq_check_launch("w4a8_g128_kernel");

@@ -33,6 +33,8 @@ from .ops import (  # noqa: F401
     segment_row_map,
     swiglu_mlp_gated_residual_,
     w4a8_grouped_linear,
+    PreparedW4A8Grouped,
+    prepare_w4a8_grouped,
     w4a8_int8_linear,
 )
 from .checkpoint import (  # noqa: F401

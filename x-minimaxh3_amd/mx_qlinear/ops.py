@@ -837,7 +837,33 @@ def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, 
     return out.reshape(*lead, n)
 
 
-def w4a8_grouped_linear(x: torch.Tensor, qdata: torch.Tensor, group_scale: torch.Tensor,
+class PreparedW4A8Grouped:
+    """Group-128 int4 weights in the GEMM's load layout (``prepare_w4a8_grouped``): the same
+    ``[N, K/2]`` bytes and codes, each 32-bit word's nibbles reordered so the kernel unpacks them
+    with one shift and two masks. Results are identical to the checkpoint layout's."""
+
+    def __init__(self, qdata: torch.Tensor):
+        self.qdata = qdata
+        self.shape = qdata.shape
+
+
+def prepare_w4a8_grouped(qdata: torch.Tensor) -> PreparedW4A8Grouped:
+    """Re-lay packed offset-8 int4 weights ``[N, K/2]`` (CK/backends/eager/w4a8_int8.py:200-202)
+    for ``w4a8_grouped_linear`` at group size 128; done once per layer when weights load."""
+    if qdata.dim() != 2 or qdata.dtype != torch.int8:
+        raise ValueError("packed weight must be a 2D int8 tensor")
+    n, kh = qdata.shape
+    if (2 * kh) % 8:
+        raise ValueError(f"K={2 * kh} must be a multiple of 8")
+    dev = _require_gpu(qdata)
+    src = qdata.contiguous()
+    out = torch.empty_like(src)
+    with torch.cuda.device(dev):
+        call("mxq_w4a8_prepare_grouped", _p(src), _p(out), n, 2 * kh, _stream(dev))
+    return PreparedW4A8Grouped(out)
+
+
+def w4a8_grouped_linear(x: torch.Tensor, qdata: torch.Tensor | PreparedW4A8Grouped, group_scale: torch.Tensor,
                         group_size: int = 128, bias: torch.Tensor | None = None,
                         out_dtype: torch.dtype = torch.bfloat16,
                         x_scale: torch.Tensor | None = None) -> torch.Tensor:
@@ -845,9 +871,13 @@ def w4a8_grouped_linear(x: torch.Tensor, qdata: torch.Tensor, group_scale: torch
 
     ``x`` is bf16/fp16/fp32 ``[..., K]`` (quantized per token here) or int8 ``[M, K]`` with its
     ``x_scale``; ``qdata`` int8 ``[N, K/2]`` packs offset-8 codes two per byte, even k in the
-    low nibble (CK/backends/eager/w4a8_int8.py:200-202); ``group_scale`` fp16 ``[K/G, N]``.
+    low nibble (CK/backends/eager/w4a8_int8.py:200-202), or is that tensor after
+    ``prepare_w4a8_grouped`` (group 128 only); ``group_scale`` fp16 ``[K/G, N]``.
     y = out(xs[m] * sum_g fp32(scale[g, n]) * P_g[m, n]), P_g the exact int32 partial of group g.
     """
+    prepared = isinstance(qdata, PreparedW4A8Grouped)
+    if prepared:
+        qdata = qdata.qdata
     if qdata.dim() != 2 or qdata.dtype != torch.int8:
         raise ValueError("packed weight must be a 2D int8 tensor")
     n, kh = qdata.shape
@@ -874,7 +904,8 @@ def w4a8_grouped_linear(x: torch.Tensor, qdata: torch.Tensor, group_scale: torch
         return out.reshape(*lead, n)
     gs = group_scale.to(device=dev, dtype=torch.float16).contiguous()
     b = _bias(bias, n, out_dtype, dev)
+    entry = "mxq_w4a8_gemm_grouped_prepared" if prepared else "mxq_w4a8_gemm_grouped"
     with torch.cuda.device(dev):
-        call("mxq_w4a8_gemm_grouped", _p(xq), _p(xs), _p(qdata.contiguous()), _p(gs), _p(b), _p(out),
+        call(entry, _p(xq), _p(xs), _p(qdata.contiguous()), _p(gs), _p(b), _p(out),
              m, n, k, group_size, n, code, _stream(dev))
     return out.reshape(*lead, n)
