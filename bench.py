@@ -497,6 +497,88 @@ class H3QkvWorkload:
                            "int8_linear(convrot=True)")
 
 
+class W4A8RefQkvWorkload:
+    """The reference's own W4A8 format on the H3 QKV projection at 720p (ConvRotW4A8Linear,
+    h3serve/native_engine/model/quantization.py:416-586): ConvRot-256 quant of x [75600, 5376],
+    then int4 codes [21504, 5376] with e4m3 relative scales per 16 weights and fp32 channel scales,
+    decoded to the int8 grid chunk by chunk (3584 columns, within the reference's 4096-column
+    workspace bound) and multiplied (mxq_w4a8_codebook_gemm). The timed steps call that entry;
+    the event pass issues the same launches through its two parts (decode, dequant GEMM into the
+    output's column slice), so that kernel_ms and the roofline are per GEMM launch (one chunk)."""
+
+    name = "w4a8_ref_h3_qkv_720p"
+    chunk = 3584
+
+    def __init__(self, dev, m=75600, d=H3_D, n=3 * H3_ATTN, g=16):
+        self.m, self.d, self.n, self.g = m, d, n, g
+        self.x = make_activations(m, d, dev, 60)
+        self.qdata = torch.randint(-128, 128, (n, d // 2), generator=_gen(dev, 61), device=dev, dtype=torch.int8)
+        srel = torch.rand(n, d // g, generator=_gen(dev, 62), device=dev) * 0.75 + 0.25
+        self.s_rel = srel.to(torch.float8_e4m3fn).view(torch.uint8)
+        self.s_ch = (torch.rand(n, generator=_gen(dev, 63), device=dev) * 0.5 + 0.5) * (0.06 / 127)
+        self.b = make_bias(n, dev, 64)
+        self.q = torch.empty(m, d, dtype=torch.int8, device=dev)
+        self.xs = torch.empty(m, dtype=torch.float32, device=dev)
+        self.work = torch.empty(self.chunk, d, dtype=torch.int8, device=dev)
+        self.out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        self.dev = dev
+
+    def step(self, timer=None):
+        st = _stream(self.dev)
+        m, d, n, g = self.m, self.d, self.n, self.g
+        if timer is None:
+            _lib.call("mxq_quantize_int8_rowwise_convrot", _p(self.x), _lib.DTYPE_BF16, _p(self.q), _p(self.xs), m, d,
+                      256, _lib.ACT_NONE, st)
+            _lib.call("mxq_w4a8_codebook_gemm", _p(self.q), _p(self.qdata), _p(self.s_rel), _lib.DTYPE_E4M3, None,
+                      _p(self.s_ch), _p(self.xs), _p(self.b), _p(self.work), _p(self.out), m, n, d, g, self.chunk,
+                      _lib.DTYPE_BF16, st)
+            return
+        with timer.span("convrot_quant"):
+            _lib.call("mxq_quantize_int8_rowwise_convrot", _p(self.x), _lib.DTYPE_BF16, _p(self.q), _p(self.xs), m, d,
+                      256, _lib.ACT_NONE, st)
+        for n0 in range(0, n, self.chunk):
+            cols = min(self.chunk, n - n0)
+            with timer.span("decode"):
+                _lib.call("mxq_dequant_int4_grouped_to_int8", _p(self.qdata[n0:]), _p(self.s_rel[n0:]), _lib.DTYPE_E4M3,
+                          None, _p(self.work), cols, d, g, st)
+            with timer.span("gemm"):
+                _lib.call("mxq_int8_gemm_dequant", _p(self.q), _p(self.work), _p(self.xs), _p(self.s_ch[n0:]), cols,
+                          _p(self.b[n0:]), _p(self.out[:, n0:]), m, cols, d, n, _lib.DTYPE_BF16, st)
+
+    def ops_per_step(self):
+        return 2 * self.m * self.n * self.d
+
+    def units_per_step(self):
+        return self.m
+
+    def dominant(self, timer):
+        m, d, c = self.m, self.d, self.chunk
+        return {"span": "gemm", "symbol": "gemm_i8_kernel<1, 2, 256>", "ops": 2 * m * c * d,
+                "bytes": m * d + c * d + 2 * m * c + 4 * m + 4 * c + 2 * c}
+
+    def config(self):
+        return {"workload": self.name, "tokens": self.m, "d_model": self.d, "qkv_out": self.n,
+                "weights": "int4 codes, e4m3 s_rel per 16, fp32 s_channel (the reference's W4A8 format)",
+                "convrot_group": 256, "decode_chunk_cols": self.chunk}
+
+    def cpu_baseline(self, budget_s):
+        from oracle import eager_torch
+
+        qd, b = self.qdata.cpu(), self.b.cpu()
+        sr = self.s_rel.cpu().view(torch.float8_e4m3fn).float()
+        sc = self.s_ch.cpu()
+
+        def run(rows):
+            x = self.x[:rows].cpu()
+            t0 = time.perf_counter()
+            w8 = eager_torch.dequant_int4_grouped_to_int8(qd, sr, None, self.g)
+            eager_torch.int8_linear(x, w8, sc, b, convrot=True)
+            return time.perf_counter() - t0
+
+        return _cpu_sample(run, budget_s, self.m, "tokens/s", "first {rows} tokens through the eager int4 decode -> "
+                           "int8_linear(convrot=True), the decode repeated per call")
+
+
 class LinearM1Workload:
     """One token through the H3 QKV projection (5376 -> 21504, ConvRot 256): the row quantizer,
     then the weight-streaming GEMV + dequant (the two launches of mxq_int8_linear_m1), cycling over
@@ -676,6 +758,7 @@ WORKLOADS = {
     "linear_c1": lambda dev: LinearC1Workload(dev),
     "h3_mlp": lambda dev: H3MlpWorkload(dev),
     "h3_qkv": lambda dev: H3QkvWorkload(dev),
+    "w4a8_ref": lambda dev: W4A8RefQkvWorkload(dev),
     "linear_m1": lambda dev: LinearM1Workload(dev),
 }
 
@@ -688,6 +771,8 @@ METRICS = {
     "h3_mlp": ("H3 block MLP tokens/s at 720p (rms_adaln -> fc1 -> SwiGLU -> fc2 + gated residual, "
                "ConvRot INT8)", "tokens/s"),
     "h3_qkv": ("H3 QKV projection with fused rms_adaln + ConvRot quant, tokens/s at 720p", "tokens/s"),
+    "w4a8_ref": ("H3 QKV projection with the reference's W4A8 weights (ConvRot quant + chunked int4 decode + GEMM), "
+                 "tokens/s at 720p", "tokens/s"),
     "linear_m1": ("single-token INT8 linear weight-streaming GB/s", "GB/s"),
 }
 
@@ -695,7 +780,7 @@ METRICS = {
 # Default (steps, warmup) per workload: sub-millisecond launches get enough warmup (~30 ms of GPU
 # work) for the shader clock to settle and enough timed steps for ~20-60 ms of timed work.
 DEFAULT_STEPS = {
-    "ffn": (10, 3), "qkv_adaln": (20, 5), "h3_mlp": (10, 3), "h3_qkv": (20, 5),
+    "ffn": (10, 3), "qkv_adaln": (20, 5), "h3_mlp": (10, 3), "h3_qkv": (20, 5), "w4a8_ref": (20, 5),
     "w4a8_gemm": (100, 100), "w4a8_skinny": (400, 400), "linear_c1": (400, 400), "linear_m1": (1000, 1000),
 }
 

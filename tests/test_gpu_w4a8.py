@@ -47,18 +47,21 @@ def test_decode_unit_scale_is_code_minus_8(dev):
     assert np.array_equal(w8.cpu().numpy(), codes - 8)
 
 
-def test_w4a8_reference_format_linear(dev):
-    m, n, k, g = 200, 300, 1024, 16
+# N = 4232 decodes in two chunks (4096 + 136 columns) into the GEMM's output column slices.
+@pytest.mark.parametrize("m,n,k,use_codebook", [(200, 300, 1024, True), (64, 4232, 256, False)])
+def test_w4a8_reference_format_linear(dev, m, n, k, use_codebook):
+    g = 16
     x = activations(m, k, 31)
     qd = packed_int4(n, k, 32)
     s_rel = (torch.rand(n, k // g, generator=gen(33)) * 15 + 1).to(torch.float8_e4m3fn)
     s_ch = torch.rand(n, generator=gen(34)) * 1e-3
-    cb = torch.linspace(-7.5, 7.5, 16)
+    cb = torch.linspace(-7.5, 7.5, 16) if use_codebook else None
     bias = bf16_vec(n, 35, 0.01)
-    y = _mx().w4a8_int8_linear(x.to(dev), qd.to(dev), s_rel.to(dev), s_ch.to(dev), codebook=cb.to(dev),
+    y = _mx().w4a8_int8_linear(x.to(dev), qd.to(dev), s_rel.to(dev), s_ch.to(dev),
+                               codebook=None if cb is None else cb.to(dev),
                                bias=bias.to(dev), group_size=g, convrot_groupsize=0)
     ref = eager_np.w4a8_reference_linear(bits(x), qd.numpy(), s_rel.view(torch.uint8).numpy(), s_ch.numpy(),
-                                         cb.numpy(), g, bits(bias), "bf16", s_rel_is_e4m3=True)
+                                         None if cb is None else cb.numpy(), g, bits(bias), "bf16", s_rel_is_e4m3=True)
     assert np.array_equal(bits(y), bf16_bits(ref))
 
 
