@@ -153,16 +153,20 @@ def test_adaln_matches_oracle(dev, m, d):
     assert torch.equal(y2, y)
 
 
-def test_adaln_modulation_groups(dev):
-    """scale/shift with one row per group of 4 consecutive x rows."""
-    m, d = 16, 512
+# The kernel takes 16-row runs: with groups of 4 every run spans several groups (modulation read
+# per row); with groups of 10 some runs lie in one group (modulation staged once in LDS).
+@pytest.mark.parametrize("m,rows_per_group", [(16, 4), (40, 10)])
+def test_adaln_modulation_groups(dev, m, rows_per_group):
+    """scale/shift with one row per group of consecutive x rows, against per-group calls."""
+    d, groups = 512, m // rows_per_group
     x = activations(m, d, 77)
-    sc = (torch.randn(4, d, generator=gen(1)) * 0.1).to(torch.bfloat16)
-    sh = (torch.randn(4, d, generator=gen(2)) * 0.1).to(torch.bfloat16)
+    sc = (torch.randn(groups, d, generator=gen(1)) * 0.1).to(torch.bfloat16)
+    sh = (torch.randn(groups, d, generator=gen(2)) * 0.1).to(torch.bfloat16)
     y = _mx().adaln(x.to(dev), sc.to(dev), sh.to(dev))
-    for g in range(4):
-        yg = _mx().adaln(x[4 * g:4 * g + 4].to(dev), sc[g].to(dev), sh[g].to(dev))
-        assert torch.equal(y[4 * g:4 * g + 4], yg)
+    for g in range(groups):
+        rows = slice(rows_per_group * g, rows_per_group * (g + 1))
+        yg = _mx().adaln(x[rows].to(dev), sc[g].to(dev), sh[g].to(dev))
+        assert torch.equal(y[rows], yg)
 
 
 def _nan_inf_rows(m, k, dtype, seed):

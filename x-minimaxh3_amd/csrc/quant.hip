@@ -169,73 +169,126 @@ MXQ_DEVICE uint32_t modulate(float xv, float mean, float rstd, uint32_t sc, uint
   return f32_to_bf16_bits(p + bf16_to_f32(sh));
 }
 
+// The same with t = bf16(1 + scale) given.
+MXQ_DEVICE uint32_t modulate_t(float xv, float mean, float rstd, float t, uint32_t sh) {
+  const float n = round_bf16((xv - mean) * rstd);
+  const float p = round_bf16(n * t);
+  return f32_to_bf16_bits(p + bf16_to_f32(sh));
+}
+
+// One row of adaLN (+ quant) with the row in registers. kLds: the modulation comes from LDS,
+// t = bf16(1 + scale) already formed; otherwise from global memory, t formed here.
+template <int NCH, bool kQuant, bool kLds>
+MXQ_DEVICE void adaln_row(const uint16_t* __restrict__ x, const v4u* scv, const v4u* shv, float eps,
+                          int8_t* __restrict__ q, float* __restrict__ scales, uint16_t* __restrict__ y_out,
+                          int64_t row, int cols, int lane) {
+  const int nchunk = cols / 8;
+  const v4u* src = reinterpret_cast<const v4u*>(x + row * cols);
+  v4u v[NCH];
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c = lane + j * kWave;
+    if (c < nchunk) {
+      v[j] = __builtin_nontemporal_load(src + c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sum += bf16_lo(v[j][i]) + bf16_hi(v[j][i]);
+    }
+  }
+  const float mean = wave_sum(sum) / (float)cols;
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c = lane + j * kWave;
+    if (c < nchunk) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a = bf16_lo(v[j][i]) - mean, b = bf16_hi(v[j][i]) - mean;
+        ss += a * a;
+        ss += b * b;
+      }
+    }
+  }
+  const float var = wave_sum(ss) / (float)cols;
+  const float rstd = 1.0f / sqrtf(var + eps);
+  uint32_t m = 0;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c = lane + j * kWave;
+    if (c < nchunk) {
+      const v4u sc = scv[c], sh = shv[c];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t lo, hi;
+        if constexpr (kLds) {
+          lo = modulate_t(bf16_lo(v[j][i]), mean, rstd, bf16_lo(sc[i]), sh[i] & 0xFFFF);
+          hi = modulate_t(bf16_hi(v[j][i]), mean, rstd, bf16_hi(sc[i]), sh[i] >> 16);
+        } else {
+          lo = modulate(bf16_lo(v[j][i]), mean, rstd, sc[i] & 0xFFFF, sh[i] & 0xFFFF);
+          hi = modulate(bf16_hi(v[j][i]), mean, rstd, sc[i] >> 16, sh[i] >> 16);
+        }
+        v[j][i] = lo | (hi << 16);
+        m = absmax_acc_bf16x2(m, v[j][i]);
+      }
+      if (y_out != nullptr) reinterpret_cast<v4u*>(y_out + row * cols)[c] = v[j];
+    }
+  }
+  if (kQuant) {
+    const float amax = wave_absmax(absmax_bits_of_bf16x2(m));
+    const float s = row_scale_from_absmax(amax);
+    const float r = 1.0f / round_bf16(s);
+    v2u* dst = reinterpret_cast<v2u*>(q + row * cols);
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = lane + j * kWave;
+      if (c < nchunk) __builtin_nontemporal_store(quant8_bf16(v[j], r), dst + c);
+    }
+    if (lane == 0) scales[row] = s;
+  }
+}
+
+// A workgroup takes kAdalnRows consecutive rows, kAdalnRows / 4 per wave. When they all share one
+// scale row and one shift row (the common case: one modulation per sample), the workgroup forms
+// t = bf16(1 + scale) once and keeps t and shift in LDS; otherwise each row reads its modulation
+// from global memory.
+constexpr int kAdalnRows = 16;
+constexpr int kAdalnMaxCols = 8192;
+
 template <int NCH, bool kQuant>
 __global__ __launch_bounds__(kQuantBlock) void adaln_rows_reg(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ scale,
     const uint16_t* __restrict__ shift, int64_t scale_group, int64_t shift_group, float eps,
     int8_t* __restrict__ q, float* __restrict__ scales, uint16_t* __restrict__ y_out,
     int64_t rows, int cols) {
-  const int lane = threadIdx.x % kWave;
+  __shared__ __attribute__((aligned(16))) uint16_t s_t[kAdalnMaxCols];
+  __shared__ __attribute__((aligned(16))) uint16_t s_sh[kAdalnMaxCols];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int nchunk = cols / 8;
-  for (int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave; row < rows;
-       row += (int64_t)gridDim.x * kRowsPerBlock) {
-    const v4u* src = reinterpret_cast<const v4u*>(x + row * cols);
-    const v4u* scv = reinterpret_cast<const v4u*>(scale + (row / scale_group) * cols);
-    const v4u* shv = reinterpret_cast<const v4u*>(shift + (row / shift_group) * cols);
-    v4u v[NCH];
-    float sum = 0.0f;
+  for (int64_t r0 = (int64_t)blockIdx.x * kAdalnRows; r0 < rows; r0 += (int64_t)gridDim.x * kAdalnRows) {
+    const int64_t r1 = min(r0 + kAdalnRows, rows) - 1;
+    const int64_t gs = r0 / scale_group, gh = r0 / shift_group;
+    if (gs == r1 / scale_group && gh == r1 / shift_group) {  // uniform over the workgroup
+      const v4u* scv = reinterpret_cast<const v4u*>(scale + gs * cols);
+      const v4u* shv = reinterpret_cast<const v4u*>(shift + gh * cols);
+      __syncthreads();  // the previous run's rows are done with the LDS copy
+      for (int c = threadIdx.x; c < nchunk; c += kQuantBlock) {
+        const v4u sc = scv[c];
+        v4u t;
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int c = lane + j * kWave;
-      if (c < nchunk) {
-        v[j] = __builtin_nontemporal_load(src + c);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sum += bf16_lo(v[j][i]) + bf16_hi(v[j][i]);
+        for (int i = 0; i < 4; ++i)
+          t[i] = f32_to_bf16_bits(1.0f + bf16_lo(sc[i])) | (f32_to_bf16_bits(1.0f + bf16_hi(sc[i])) << 16);
+        reinterpret_cast<v4u*>(s_t)[c] = t;
+        reinterpret_cast<v4u*>(s_sh)[c] = shv[c];
       }
-    }
-    const float mean = wave_sum(sum) / (float)cols;
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int c = lane + j * kWave;
-      if (c < nchunk) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float a = bf16_lo(v[j][i]) - mean, b = bf16_hi(v[j][i]) - mean;
-          ss += a * a;
-          ss += b * b;
-        }
-      }
-    }
-    const float var = wave_sum(ss) / (float)cols;
-    const float rstd = 1.0f / sqrtf(var + eps);
-    uint32_t m = 0;
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int c = lane + j * kWave;
-      if (c < nchunk) {
-        const v4u sc = scv[c], sh = shv[c];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t lo = modulate(bf16_lo(v[j][i]), mean, rstd, sc[i] & 0xFFFF, sh[i] & 0xFFFF);
-          const uint32_t hi = modulate(bf16_hi(v[j][i]), mean, rstd, sc[i] >> 16, sh[i] >> 16);
-          v[j][i] = lo | (hi << 16);
-          m = absmax_acc_bf16x2(m, v[j][i]);
-        }
-        if (y_out != nullptr) reinterpret_cast<v4u*>(y_out + row * cols)[c] = v[j];
-      }
-    }
-    if (kQuant) {
-      const float amax = wave_absmax(absmax_bits_of_bf16x2(m));
-      const float s = row_scale_from_absmax(amax);
-      const float r = 1.0f / round_bf16(s);
-      v2u* dst = reinterpret_cast<v2u*>(q + row * cols);
-#pragma unroll
-      for (int j = 0; j < NCH; ++j) {
-        const int c = lane + j * kWave;
-        if (c < nchunk) __builtin_nontemporal_store(quant8_bf16(v[j], r), dst + c);
-      }
-      if (lane == 0) scales[row] = s;
+      __syncthreads();
+      for (int64_t row = r0 + wave; row <= r1; row += kQuantBlock / kWave)
+        adaln_row<NCH, kQuant, true>(x, reinterpret_cast<const v4u*>(s_t), reinterpret_cast<const v4u*>(s_sh), eps,
+                                     q, scales, y_out, row, cols, lane);
+    } else {
+      for (int64_t row = r0 + wave; row <= r1; row += kQuantBlock / kWave)
+        adaln_row<NCH, kQuant, false>(x, reinterpret_cast<const v4u*>(scale + (row / scale_group) * cols),
+                                      reinterpret_cast<const v4u*>(shift + (row / shift_group) * cols), eps, q,
+                                      scales, y_out, row, cols, lane);
     }
   }
 }
@@ -366,6 +419,11 @@ extern "C" int mxq_quantize_int8_rowwise_absmax(const void* x_bf16, const float*
   return mxq_check_launch("quant_rows_bf16_absmax");
 }
 
+static unsigned adaln_grid(int64_t rows) {
+  const int64_t blocks = (rows + kAdalnRows - 1) / kAdalnRows;
+  return (unsigned)(blocks < 65536 * 4 ? blocks : 65536 * 4);
+}
+
 static int adaln_launch(const void* x, const void* scale, const void* shift, int64_t scale_group,
                         int64_t shift_group, float eps, int8_t* q, float* scales, void* y_out,
                         int64_t rows, int64_t cols, void* stream, bool quant) {
@@ -382,12 +440,12 @@ static int adaln_launch(const void* x, const void* scale, const void* shift, int
                          "adaLN needs cols %% 8 == 0, cols <= 8192 and 16-byte aligned rows");
   hipStream_t st = (hipStream_t)stream;
   if (quant) {
-    MXQ_NCH_SWITCH_16(nch, (adaln_rows_reg<N_, true><<<row_grid(rows), kQuantBlock, 0, st>>>(
+    MXQ_NCH_SWITCH_16(nch, (adaln_rows_reg<N_, true><<<adaln_grid(rows), kQuantBlock, 0, st>>>(
                              (const uint16_t*)x, (const uint16_t*)scale, (const uint16_t*)shift,
                              scale_group, shift_group, eps, q, scales, (uint16_t*)y_out, rows,
                              (int)cols)));
   } else {
-    MXQ_NCH_SWITCH_16(nch, (adaln_rows_reg<N_, false><<<row_grid(rows), kQuantBlock, 0, st>>>(
+    MXQ_NCH_SWITCH_16(nch, (adaln_rows_reg<N_, false><<<adaln_grid(rows), kQuantBlock, 0, st>>>(
                              (const uint16_t*)x, (const uint16_t*)scale, (const uint16_t*)shift,
                              scale_group, shift_group, eps, nullptr, nullptr, (uint16_t*)y_out,
                              rows, (int)cols)));
