@@ -105,7 +105,8 @@ def swiglu_bf16(x_bits: np.ndarray) -> np.ndarray:
         raise ValueError("swiglu needs an even last dimension")
     gate, up = x_bits[..., : k2 // 2], x_bits[..., k2 // 2:]
     a = bf16_to_f32(silu_table()[gate])
-    return bf16_bits(a * bf16_to_f32(up))
+    with np.errstate(over="ignore", invalid="ignore"):  # fp32 overflow to inf and inf * 0 = NaN, as in torch
+        return bf16_bits(a * bf16_to_f32(up))
 
 
 def apply_input_act_bf16(x_bits: np.ndarray, input_act: str | None) -> np.ndarray:
