@@ -60,6 +60,23 @@ def test_gemm_extremes_and_structure(dev):
     assert torch.equal(c, a[:, perm].to(torch.int32))
 
 
+def test_gemm_largest_k(dev):
+    """K = 131056, the largest K whose int32 sums cannot overflow (131056 * 128 * 128 < 2^31):
+    extreme operands sum exactly; one 16 beyond is rejected."""
+    k = 131056
+    a = torch.full((3, k), -128, dtype=torch.int8)
+    a[1] = 127
+    a[2, ::2] = 5
+    w = torch.full((2, k), -128, dtype=torch.int8)
+    w[1, 1::2] = 3
+    c = _mx().mm_int8(a.to(dev), w.to(dev).t()).cpu()
+    assert np.array_equal(c.numpy(), eager_np.int8_matmul(a.numpy(), w.numpy()))
+    assert c[0, 0] == k * 128 * 128 == 2147221504
+    with pytest.raises(RuntimeError, match="exceeds the int32 accumulator bound"):
+        _mx().mm_int8(torch.zeros(2, k + 16, dtype=torch.int8, device=dev),
+                      torch.zeros(k + 16, 2, dtype=torch.int8, device=dev))
+
+
 def test_gemm_i32_strided_output(dev):
     m, n, k, ldc = 100, 300, 256, 512
     a, w = _i8((m, k), 8), _i8((n, k), 9)
