@@ -282,6 +282,17 @@ int mxq_w4a8_gemm_grouped(const int8_t* a, const float* xs, const int8_t* qdata,
                           void* stream);
 
 /*
+ * Left operand of the reference-format W4A8 correction term:
+ *   out[m, g] = o(o(sum_{k in group g} xq[m, k]) * o(xs[m])), o = rounding to out_dtype
+ *   xq [M, K] int8 (the quantized, rotated activations); xs [M] fp32; out [M, K/G].
+ * The caller adds out @ correction ([K/G, N], out_dtype) to the linear's output with a library
+ * GEMM (out.addmm_ in the reference).
+ * Replaces: the correction branch of CK/backends/cuda/__init__.py:2294-2297 (its group sums).
+ */
+int mxq_int8_group_sums(const int8_t* xq, const float* xs, void* out, int64_t M, int64_t K,
+                        int64_t group_size, int out_dtype, void* stream);
+
+/*
  * Weight preparation for mxq_w4a8_gemm_grouped_prepared (a load-time layout transform, no
  * counterpart in the reference): qdata [N, K/2] as above -> out [N, K/2] (may alias qdata),
  * K % 8 == 0. Each 32-bit word keeps the 8 codes of k = 8w .. 8w + 7; byte j of the result

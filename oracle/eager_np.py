@@ -335,6 +335,17 @@ def unprepare_w4a8_grouped(prepared: np.ndarray) -> np.ndarray:
     return codes.reshape(n, kh * 2)
 
 
+def w4a8_correction_lhs(xq: np.ndarray, x_scale: np.ndarray, group_size: int, out_dtype: str = "bf16") -> np.ndarray:
+    """Left operand of the W4A8 correction term, as float32 values of ``out_dtype``:
+    ``o(o(sum of xq over each group) * o(xs))`` (CK/backends/cuda/__init__.py:2294-2296:
+    ``xq.view(m, groups, G).sum(-1, dtype=int32).to(out_dtype) * xs.to(out_dtype)``)."""
+    q = np.asarray(xq, dtype=np.int64)
+    m, k = q.shape
+    sums = q.reshape(m, k // group_size, group_size).sum(-1).astype(F32)  # |sum| < 2^24: exact
+    xs = np.asarray(x_scale, dtype=F32).reshape(-1, 1)
+    return round_to(round_to(sums, out_dtype) * round_to(xs, out_dtype), out_dtype)
+
+
 def quantize_int4_symmetric(w: np.ndarray) -> np.ndarray:
     """Signed int4 values in [-8, 7] -> offset-8 codes (``u = v + 8``, w4a8_int8.py:171-173)."""
     v = np.asarray(w, dtype=np.int32)

@@ -165,3 +165,63 @@ def test_prepared_needs_group_128(dev):
     x = activations(16, 512, 921).to(dev)
     with pytest.raises(RuntimeError, match="group 128"):
         _mx().w4a8_grouped_linear(x, _mx().prepare_w4a8_grouped(qd), group_scales(512, 64, 256, 922).to(dev), 256)
+
+
+# ---- the correction term of asymmetric int4 weights (reference CUDA backend) ---------------
+
+@pytest.mark.parametrize("g,out_dtype,code", [(16, torch.bfloat16, "bf16"), (4, torch.float16, "fp16"),
+                                              (32, torch.float32, "fp32")])
+def test_group_sums_match_oracle(dev, g, out_dtype, code):
+    from mx_qlinear import _lib as L
+    from mx_qlinear.ops import _p, _stream
+
+    m, k = 37, 640
+    xq = torch.randint(-128, 128, (m, k), generator=gen(950), dtype=torch.int8)
+    xs = torch.rand(m, generator=gen(951)) * 0.01
+    out = torch.empty(m, k // g, dtype=out_dtype, device=dev)
+    xqd, xsd = xq.to(dev), xs.to(dev)
+    L.call("mxq_int8_group_sums", _p(xqd), _p(xsd), _p(out), m, k, g,
+           {torch.bfloat16: L.DTYPE_BF16, torch.float16: L.DTYPE_F16, torch.float32: L.DTYPE_F32}[out_dtype], _stream(dev))
+    want = eager_np.w4a8_correction_lhs(xq.numpy(), xs.numpy(), g, code)
+    assert np.array_equal(out.float().cpu().numpy(), want)
+
+
+def _corr_case(dev, m, n, k, g):
+    x = activations(m, k, 960).to(dev)
+    qd = packed_int4(n, k, 961).to(dev)
+    s_rel = (torch.rand(n, k // g, generator=gen(962)) * 0.75 + 0.25).to(torch.float8_e4m3fn).to(dev)
+    s_ch = (torch.rand(n, generator=gen(963)) * 1e-3).to(dev)
+    corr = (torch.randn(k // g, n, generator=gen(964)) * 0.01).to(torch.bfloat16).to(dev)
+    bias = bf16_vec(n, 965, 0.01).to(dev)
+    return x, qd, s_rel, s_ch, corr, bias
+
+
+def test_correction_equals_the_reference_composition(dev):
+    """With a correction the output is the reference CUDA backend's composition run with torch on
+    the same device: the W8A8 result, then out.addmm_(bf16(group sums) * bf16(xs), correction)."""
+    m, n, k, g = 150, 264, 512, 16
+    x, qd, s_rel, s_ch, corr, bias = _corr_case(dev, m, n, k, g)
+    got = _mx().w4a8_int8_linear(x, qd, s_rel, s_ch, correction=corr, bias=bias, group_size=g, convrot_groupsize=256)
+    base = _mx().w4a8_int8_linear(x, qd, s_rel, s_ch, bias=bias, group_size=g, convrot_groupsize=256)
+    xq, xs = _mx().quantize_int8_rowwise_convrot(x, 256)
+    sx = xq.view(m, k // g, g).sum(-1, dtype=torch.int32).to(torch.bfloat16) * xs.reshape(-1, 1).to(torch.bfloat16)
+    ref = base.clone().addmm_(sx, corr)
+    assert torch.equal(got, ref)
+    # and within 1 ulp + the float32 accumulation bound of the exact value of that expression
+    lhs = eager_np.w4a8_correction_lhs(xq.cpu().numpy(), xs.cpu().numpy(), g, "bf16").astype(np.float64)
+    terms = lhs[:, :, None] * corr.float().cpu().numpy().astype(np.float64)[None, :, :]
+    exact = base.float().cpu().numpy().astype(np.float64) + terms.sum(1)
+    mag = np.abs(base.float().cpu().numpy()).astype(np.float64) + np.abs(terms).sum(1)
+    bound = bf16_ulp(np.abs(exact).astype(np.float32)).astype(np.float64) + (k // g + 2) * 2.0 ** -24 * mag
+    assert np.all(np.abs(got.float().cpu().numpy().astype(np.float64) - exact) <= bound)
+
+
+def test_correction_through_the_module(dev):
+    m, n, k, g = 64, 136, 256, 16
+    x, qd, s_rel, s_ch, corr, bias = _corr_case(dev, m, n, k, g)
+    from mx_qlinear.modules import ConvRotW4A8Linear, W4A8QuantSpec, w4a8_kernel
+
+    layer = ConvRotW4A8Linear(qd, s_rel, s_ch, correction=corr, bias=bias,
+                              spec=W4A8QuantSpec(group_size=g, convrot_groupsize=256), kernel=w4a8_kernel)
+    want = _mx().w4a8_int8_linear(x, qd, s_rel, s_ch, correction=corr, bias=bias, group_size=g, convrot_groupsize=256)
+    assert torch.equal(layer(x), want)

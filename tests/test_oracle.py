@@ -278,6 +278,23 @@ def test_prepared_w4a8_layout():
     assert not np.array_equal(device_unpack(bad), 16 * (codes - 8))
 
 
+def test_w4a8_correction_lhs_matches_torch_composition():
+    """The correction operand equals the reference's torch expression on the CPU
+    (CK/backends/cuda/__init__.py:2295-2296), and a known row."""
+    import torch
+
+    rng = np.random.default_rng(9)
+    xq = rng.integers(-128, 128, size=(5, 64)).astype(np.int8)
+    xs = (rng.random(5) * 0.01).astype(np.float32)
+    for g, dt, tdt in [(16, "bf16", torch.bfloat16), (4, "fp16", torch.float16), (32, "fp32", torch.float32)]:
+        t = torch.from_numpy(xq).view(5, 64 // g, g).sum(-1, dtype=torch.int32).to(tdt)
+        t = (t * torch.from_numpy(xs).reshape(-1, 1).to(tdt)).float().numpy()
+        assert np.array_equal(eager_np.w4a8_correction_lhs(xq, xs, g, dt), t)
+    row = np.array([[127] * 16 + [-128] * 16], dtype=np.int8)
+    got = eager_np.w4a8_correction_lhs(row, np.array([0.5], dtype=np.float32), 16, "bf16")
+    assert got.tolist() == [[1016.0, -1024.0]]  # 2032 -> bf16 2032 (exact), times 0.5
+
+
 def test_decode_closed_forms():
     n, k = 4, 64
     codes = (np.arange(n * k) % 16).reshape(n, k)

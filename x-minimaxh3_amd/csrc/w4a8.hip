@@ -415,6 +415,48 @@ __global__ __launch_bounds__(256) void w4_prepare_kernel(const uint32_t* in, uin
 }  // namespace
 }  // namespace mxq
 
+namespace mxq {
+namespace {
+
+// sx[m, g] = out(out(sum of xq[m, k] over group g) * out(xs[m])), one output per thread.
+template <int kOut>
+__global__ __launch_bounds__(256) void group_sums_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                                         void* __restrict__ out, int64_t M, int64_t K, int64_t G) {
+  typedef typename OutT<kOut>::T T;
+  const int64_t groups = K / G, total = M * groups;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t m = i / groups, g = i - m * groups;
+    const int8_t* src = xq + m * K + g * G;
+    int sum = 0;
+    for (int64_t e = 0; e < G; ++e) sum += src[e];
+    const float v = OutT<kOut>::round(OutT<kOut>::round((float)sum) * OutT<kOut>::round(xs[m]));
+    store_out<kOut>(reinterpret_cast<T*>(out) + i, v);
+  }
+}
+
+}  // namespace
+}  // namespace mxq
+
+extern "C" int mxq_int8_group_sums(const int8_t* xq, const float* xs, void* out, int64_t M, int64_t K,
+                                   int64_t group_size, int out_dtype, void* stream) {
+  if (M < 0 || K < 0) return mxq_set_error(MXQ_ERR_INVALID, "negative shape");
+  if (group_size <= 0 || K % group_size != 0)
+    return mxq_set_error(MXQ_ERR_INVALID, "group_size=%lld must divide K=%lld", (long long)group_size, (long long)K);
+  const int64_t total = M * (K / group_size);
+  if (total == 0) return MXQ_OK;
+  if (!xq || !xs || !out) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 65536);
+  hipStream_t st = (hipStream_t)stream;
+  switch (out_dtype) {
+    case MXQ_DTYPE_F32: mxq::group_sums_kernel<0><<<blocks, 256, 0, st>>>(xq, xs, out, M, K, group_size); break;
+    case MXQ_DTYPE_F16: mxq::group_sums_kernel<1><<<blocks, 256, 0, st>>>(xq, xs, out, M, K, group_size); break;
+    case MXQ_DTYPE_BF16: mxq::group_sums_kernel<2><<<blocks, 256, 0, st>>>(xq, xs, out, M, K, group_size); break;
+    default: return mxq_set_error(MXQ_ERR_UNSUPPORTED, "output dtype code %d", out_dtype);
+  }
+  return mxq_check_launch("group_sums_kernel");
+}
+
 extern "C" int mxq_w4a8_prepare_grouped(const int8_t* qdata, int8_t* out, int64_t N, int64_t K, void* stream) {
   if (N < 0 || K < 0) return mxq_set_error(MXQ_ERR_INVALID, "negative shape");
   if (K % 8 != 0) return mxq_set_error(MXQ_ERR_INVALID, "K=%lld must be a multiple of 8", (long long)K);

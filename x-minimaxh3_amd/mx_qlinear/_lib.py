@@ -50,6 +50,7 @@ SIGNATURES: dict[str, list] = {
     "mxq_w4a8_gemm_grouped": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "mxq_w4a8_gemm_grouped_prepared": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "mxq_w4a8_prepare_grouped": [_P, _P, _I64, _I64, _P],
+    "mxq_int8_group_sums": [_P, _P, _P, _I64, _I64, _I64, _I, _P],
 }
 
 _lib = None

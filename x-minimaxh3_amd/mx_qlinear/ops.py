@@ -786,12 +786,12 @@ def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, 
     """Reference-format W4A8 linear (CK/tensor/w4a8_int8.py:89-115, eager w4a8_int8.py:457-508):
     the int4 codes are decoded to the int8 grid chunk by chunk and multiplied with the ConvRot-
     rotated, per-token quantized activations (int8_linear with convrot=True).
-    ``convrot_groupsize=0`` skips the rotation (for unrotated weights). The ``correction`` form,
-    which the reference evaluates as a dense floating-point linear on the dequantized weight,
-    is not provided.
+    ``convrot_groupsize=0`` skips the rotation (for unrotated weights). A ``correction`` [K/G, N]
+    (asymmetric int4 weights) is added as the reference's CUDA backend does
+    (CK/backends/cuda/__init__.py:2294-2297): ``out += o(o(group sums of xq) * o(xs)) @ correction``
+    in the output dtype, the product by a library GEMM (``addmm_``). The reference's eager backend
+    instead runs a dense floating-point linear on the dequantized weight.
     """
-    if correction is not None:
-        raise NotImplementedError("the W4A8 correction term is not provided by this build")
     if convrot_groupsize:
         _check_power_of_four(convrot_groupsize)
     if qdata.dim() != 2 or qdata.dtype != torch.int8:
@@ -812,6 +812,8 @@ def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, 
         raise ValueError(f"s_channel must have shape {(n,)}, got {tuple(s_channel.shape)}")
     if codebook is not None and tuple(codebook.shape) != (16,):
         raise ValueError(f"codebook must have shape (16,), got {tuple(codebook.shape)}")
+    if correction is not None and tuple(correction.shape) != (k // group_size, n):
+        raise ValueError(f"correction must have shape {(k // group_size, n)}, got {tuple(correction.shape)}")
     dev = _require_gpu(x, qdata)
     code = _out_code(out_dtype)
     lead = x.shape[:-1]
@@ -834,6 +836,10 @@ def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, 
     with torch.cuda.device(dev):
         call("mxq_w4a8_codebook_gemm", _p(xq), _p(qdata.contiguous()), _p(sr), scode, _p(cb), _p(sch),
              _p(xs), _p(b), _p(work), _p(out), m, n, k, group_size, chunk, code, _stream(dev))
+        if correction is not None:
+            sx = torch.empty((m, k // group_size), dtype=out_dtype, device=dev)
+            call("mxq_int8_group_sums", _p(xq), _p(xs), _p(sx), m, k, group_size, code, _stream(dev))
+            out.addmm_(sx, correction.to(device=dev, dtype=out_dtype))
     return out.reshape(*lead, n)
 
 
