@@ -1,4 +1,5 @@
-"""GPU parity of the 256 x 256-tile INT8 GEMM (the configuration every model-sized shape runs).
+"""GPU parity of the 256 x 256-tile INT8 GEMM (the configuration every model-sized shape runs)
+and of the 128 x 128 one at a mid-sized shape with partial edge tiles.
 
 The library runs a GEMM with 256 x 256 tiles once it has at least 256 of them (fewer: 128 x 128
 tiles, which the small-shape tests cover), so these shapes have M x N >= 4100 x 4104. K is chosen
@@ -93,4 +94,35 @@ def test_gated_residual_256_tiles(dev):
     q, s = eager_np.quantize_int8_rowwise(bits(x))
     y = eager_np.dequant_epilogue(eager_np.int8_matmul(q, w.numpy()), s, ws.numpy(), bits(b), "bf16")
     want = eager_np.gated_residual_bf16(bits(res), bf16_bits(y), bits(gate), eager_np.segment_row_map(M, segs))
+    assert np.array_equal(bits(out), want)
+
+
+# ---- the 128 x 128-tile configuration: at least 256 tiles of 128, fewer than 256 of 256 ------
+
+M128, N128 = 2050, 2056  # 17 x 17 tiles of 128 (9 x 9 of 256), both edges partial
+
+
+@pytest.mark.parametrize("k", [128, 400, 1024])
+def test_gemm_i32_128_tiles(dev, k):
+    print(f"gemm i32 128-tile m={M128} n={N128} k={k}", flush=True)
+    a, w = _i8((M128, k), 140 + k), _i8((N128, k), 141 + k)
+    c = _mx().mm_int8(a.to(dev), w.to(dev).t())
+    assert np.array_equal(c.cpu().numpy(), eager_np.int8_matmul(a.numpy(), w.numpy()))
+
+
+def test_int8_linear_and_gated_residual_128_tiles(dev):
+    k = 528
+    x = activations(M128, k, 150)
+    w, ws = int8_weight(N128, k, 151)
+    b = bf16_vec(N128, 152, 0.01)
+    y = _mx().int8_linear(x.to(dev), w.to(dev), ws.to(dev), b.to(dev))
+    assert np.array_equal(bits(y), bf16_bits(eager_np.int8_linear(bits(x), w.numpy(), ws.numpy(), bits(b), "bf16")))
+    gate = torch.randn(2, N128, generator=gen(153)).to(torch.bfloat16)
+    res = activations(M128, N128, 154) * 3
+    segs = ((0, 700, 1), (700, M128, 0))
+    out = res.to(dev)
+    _mx().int8_linear_gated_residual_(out, x.to(dev), w.to(dev), ws.to(dev), b.to(dev), gate.to(dev), segs)
+    q, s = eager_np.quantize_int8_rowwise(bits(x))
+    yy = eager_np.dequant_epilogue(eager_np.int8_matmul(q, w.numpy()), s, ws.numpy(), bits(b), "bf16")
+    want = eager_np.gated_residual_bf16(bits(res), bf16_bits(yy), bits(gate), eager_np.segment_row_map(M128, segs))
     assert np.array_equal(bits(out), want)
