@@ -158,6 +158,45 @@ def test_int8_linear_rejects_bad_arguments(dev):
         _mx().int8_linear(x, w.to(dev), ws.to(dev), input_act="relu")
 
 
+def test_prequantized_accepts_unaligned_views(dev):
+    """Operands that start off a 16-byte boundary (views into a flat buffer) give the same int32
+    products and outputs as aligned copies."""
+    m, n, k = 48, 40, 64
+    a, w = torch.randint(-128, 128, (m, k), generator=gen(7), dtype=torch.int8), torch.randint(
+        -128, 128, (n, k), generator=gen(8), dtype=torch.int8)
+    buf = torch.zeros(m * k + 3, dtype=torch.int8, device=dev)
+    av = buf[3:].view(m, k)
+    av.copy_(a.to(dev))
+    assert av.data_ptr() % 16 and av.is_contiguous()
+    c = _mx().mm_int8(av, w.to(dev).t())
+    assert np.array_equal(c.cpu().numpy(), eager_np.int8_matmul(a.numpy(), w.numpy()))
+    xs = torch.rand(m, 1, generator=gen(9)) * 1e-2
+    ws = torch.rand(n, generator=gen(10)) * 1e-2
+    y = _mx().int8_linear_prequantized(av, xs.to(dev), w.to(dev), ws.to(dev))
+    ref = eager_np.dequant_epilogue(eager_np.int8_matmul(a.numpy(), w.numpy()), xs.numpy(), ws.numpy(), None, "bf16")
+    assert np.array_equal(bits(y), bf16_bits(ref))
+
+
+def test_output_and_scale_arguments_are_checked(dev):
+    """Buffers a kernel would write or read past are rejected before any launch."""
+    m, f, k = 32, 64, 128
+    q = torch.zeros(m, k, dtype=torch.int8, device=dev)
+    s = torch.ones(m, 1, device=dev)
+    w, ws = int8_weight(2 * f, k, 11)
+    fc1 = _mx().prepare_swiglu_fc1(w.to(dev), ws.to(dev))
+    for bad in (torch.empty(m, f - 8, dtype=torch.bfloat16, device=dev),
+                torch.empty(m, f, dtype=torch.float16, device=dev),
+                torch.empty(m, 2 * f, dtype=torch.bfloat16, device=dev)[:, ::2]):
+        with pytest.raises(ValueError):
+            _mx().int8_swiglu_fc1(q, s, fc1, out=bad)
+    qd = torch.zeros(f, k // 2, dtype=torch.int8, device=dev)
+    gs = torch.ones(k // 128, f, dtype=torch.float16, device=dev)
+    with pytest.raises(ValueError, match="x_scale"):
+        _mx().w4a8_grouped_linear(q, qd, gs, 128, x_scale=s[: m // 2])
+    with pytest.raises(ValueError, match="codebook"):
+        _mx().dequantize_int4_grouped_to_int8(qd, torch.ones(f, k // 16, device=dev), torch.zeros(8, device=dev), 16)
+
+
 @pytest.mark.parametrize("m,k,hidden,n", [(300, 256, 1024, 256), (64, 512, 2048, 384)])
 def test_ffn_chain_matches_oracle(dev, m, k, hidden, n):
     print(f"ffn m={m} k={k} hidden={hidden} n={n}", flush=True)

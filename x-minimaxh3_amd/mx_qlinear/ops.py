@@ -329,7 +329,7 @@ def _pad_k(q: torch.Tensor, w: torch.Tensor):
     k = q.shape[1]
     kp = (k + 15) // 16 * 16
     if kp == k:
-        return q, w, k
+        return _aligned16(q), _aligned16(w), k
     qp = torch.zeros((q.shape[0], kp), dtype=torch.int8, device=q.device)
     qp[:, :k] = q
     wp = torch.zeros((w.shape[0], kp), dtype=torch.int8, device=w.device)
@@ -537,7 +537,8 @@ def int8_ffn_gelu(x: torch.Tensor, fc1_weight: torch.Tensor, fc1_scale: torch.Te
     out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
     if m == 0:
         return out.reshape(*x.shape[:-1], n)
-    ws = workspace if workspace is not None and workspace.shape == (m, k, hidden) else FfnWorkspace(m, k, hidden, dev)
+    reuse = workspace is not None and workspace.shape == (m, k, hidden) and workspace.xq.device == dev
+    ws = workspace if reuse else FfnWorkspace(m, k, hidden, dev)
     w1 = fc1_weight.contiguous()
     w2 = fc2_weight.contiguous()
     st = _stream(dev)
@@ -714,7 +715,14 @@ def int8_swiglu_fc1(x_qdata: torch.Tensor, x_scale: torch.Tensor, fc1: PreparedS
     xs = x_scale.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
     if xs.numel() != m:
         raise ValueError(f"x_scale has {xs.numel()} entries, expected {m}")
-    h = out if out is not None else torch.empty((m, n2 // 2), dtype=torch.bfloat16, device=dev)
+    if out is None:
+        h = torch.empty((m, n2 // 2), dtype=torch.bfloat16, device=dev)
+    else:
+        h = out
+        if h.dtype != torch.bfloat16 or h.device != dev or h.dim() != 2 or tuple(h.shape) != (m, n2 // 2):
+            raise ValueError(f"out must be a bfloat16 [{m}, {n2 // 2}] tensor on {dev}")
+        if h.stride(1) != 1 or h.stride(0) < n2 // 2:
+            raise ValueError("out rows must be contiguous and must not overlap")
     if m == 0:
         return h
     q2, w2, k = _pad_k(x_qdata.contiguous(), fc1.qweight)
@@ -770,6 +778,8 @@ def dequantize_int4_grouped_to_int8(qdata: torch.Tensor, s_rel: torch.Tensor,
         raise ValueError(f"K={k} must be divisible by group_size={group_size}")
     if tuple(s_rel.shape) != (n, k // group_size):
         raise ValueError(f"s_rel must have shape {(n, k // group_size)}, got {tuple(s_rel.shape)}")
+    if codebook is not None and codebook.numel() != 16:
+        raise ValueError(f"codebook must have 16 entries, got {codebook.numel()}")
     sr, code = _srel_code(s_rel.to(dev))
     cb = None if codebook is None else codebook.to(device=dev, dtype=torch.float32).contiguous()
     out = torch.empty((n, k), dtype=torch.int8, device=dev)
@@ -901,6 +911,8 @@ def w4a8_grouped_linear(x: torch.Tensor, qdata: torch.Tensor | PreparedW4A8Group
             raise ValueError("an int8 input needs x_scale")
         xq = x.reshape(-1, k).contiguous()
         xs = x_scale.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+        if xs.numel() != xq.shape[0]:
+            raise ValueError(f"x_scale has {xs.numel()} entries, expected {xq.shape[0]}")
     else:
         xq, xs = quantize_int8_rowwise(x.reshape(-1, k))
     lead = x.shape[:-1]
