@@ -98,10 +98,12 @@ def test_grouped_power_of_two_scales_are_exact(dev):
 
 
 # group 128 with N % 8 == 0 runs the pipelined kernel (edge tiles in M and N included; K of one
-# and two groups, shorter than its 3-stage ring); group 256 and N = 70 run the general kernel.
+# and two groups, shorter than its 3-stage ring): with 64-row tiles below 512 tiles of 128 rows,
+# with 128-row tiles from there (2056 x 4104: 17 x 33 tiles, both edges partial); group 256 and
+# N = 70 run the general kernel.
 @pytest.mark.parametrize("m,n,k,g", [(512, 1024, 5120, 128), (2048, 640, 1024, 128), (100, 200, 1024, 128),
                                      (257, 136, 640, 128), (64, 256, 128, 128), (130, 264, 256, 128),
-                                     (100, 200, 1024, 256), (33, 70, 512, 128)])
+                                     (2056, 4104, 384, 128), (100, 200, 1024, 256), (33, 70, 512, 128)])
 def test_grouped_matches_oracle(dev, m, n, k, g):
     print(f"w4a8 grouped m={m} n={n} k={k} g={g}", flush=True)
     x = activations(m, k, 1000 + m, outlier_frac=0.0)
@@ -142,6 +144,8 @@ def test_prepare_matches_oracle(dev, n, k):
 
 @pytest.mark.parametrize("m,n,k,bias,out_dtype", [(512, 1024, 5120, False, torch.bfloat16),
                                                   (257, 136, 640, True, torch.bfloat16),
+                                                  (2056, 4104, 256, False, torch.bfloat16),
+                                                  (2056, 4104, 128, True, torch.float16),
                                                   (64, 256, 128, False, torch.float16),
                                                   (130, 264, 256, True, torch.float32)])
 def test_prepared_equals_checkpoint_layout(dev, m, n, k, bias, out_dtype):

@@ -32,25 +32,35 @@ namespace mxq {
 
 namespace {
 
-// A CU holds two workgroups of four waves, i.e. two waves per SIMD: one wave's fold and
-// unpack VALU work issues while the other's MFMAs run. (A 128 x 256 tile with eight waves per
-// workgroup, a third less L2 -> LDS traffic per MAC, measured no faster.)
-constexpr int kBM = 128, kBN = 128, kNS = 3, kOcc = 2;
+// A workgroup is four waves side by side along N. With 128-row tiles a CU holds two workgroups,
+// i.e. two waves per SIMD: one wave's fold and unpack VALU work issues while the other's MFMAs
+// run. (A 128 x 256 tile with eight waves per workgroup, a third less L2 -> LDS traffic per MAC,
+// measured no faster.) Problems with fewer 128-row tiles than two per CU (M = 512 at N = 10240:
+// 320 tiles) run 64-row tiles, three workgroups per CU, so that every CU holds two or three.
+constexpr int kBN = 128, kNS = 3;
 constexpr int kWaves = kBN / 32;
 constexpr int kThreads = kWaves * 64;
-constexpr int kStageA = kBM * 128;  // 16 KB
 constexpr int kStageB = kBN * 64;   // 8 KB packed
-constexpr int kStage = kStageA + kStageB;
 constexpr int kScaleRing = 8;       // > kNS + 1: a slot is refilled only after its fold
 constexpr int kScaleBytes = kBN * 2;
-constexpr int kLds = kNS * kStage + kScaleRing * kScaleBytes;
-constexpr int kALoads = kStageA / 1024 / kWaves;  // 4 direct-to-LDS loads per wave per stage
 constexpr int kBLoads = kStageB / 1024 / kWaves;  // 2
-constexpr int kLoads = kALoads + kBLoads + 1;     // + the wave's share of the scales
 constexpr int kScaleLanes = kScaleBytes / kWaves / 16;  // lanes per wave fetching scales
 static_assert(kScaleRing >= kNS + 2, "scale slot refilled before it is folded");
-static_assert(kALoads * kWaves * 8 == kBM && kBLoads * kWaves * 16 == kBN, "load split");
-static_assert(kOcc * kLds <= 160 * 1024, "LDS per CU");
+static_assert(kBLoads * kWaves * 16 == kBN, "load split");
+
+template <int kBM_>
+struct W4Cfg {
+  static constexpr int kBM = kBM_;
+  static constexpr int kBI = kBM / 32;                         // MFMA blocks per wave along M
+  static constexpr int kOcc = kBM == 128 ? 2 : 3;              // workgroups per CU
+  static constexpr int kStageA = kBM * 128;
+  static constexpr int kStage = kStageA + kStageB;
+  static constexpr int kLds = kNS * kStage + kScaleRing * kScaleBytes;
+  static constexpr int kALoads = kStageA / 1024 / kWaves;      // direct-to-LDS loads per wave per stage
+  static constexpr int kLoads = kALoads + kBLoads + 1;         // + the wave's share of the scales
+  static_assert(kALoads * kWaves * 8 == kBM, "load split");
+  static_assert(kOcc * kLds <= 160 * 1024, "LDS per CU");
+};
 
 struct Tile {
   int64_t m0, n0;
@@ -67,6 +77,7 @@ MXQ_DEVICE void order_after_fold(v4i& frag, const float (&f)[16]) {
                      "v"(f[8]), "v"(f[9]), "v"(f[10]), "v"(f[11]), "v"(f[12]), "v"(f[13]), "v"(f[14]), "v"(f[15]));
 }
 
+template <int kBM>
 MXQ_DEVICE Tile tile_of(const W4Args& p) {
   const int num = p.tiles_m * p.tiles_n, per = num / 8, bid = blockIdx.x;
   const int t = bid < per * 8 ? (bid % 8) * per + bid / 8 : bid;  // XCD-contiguous ranges
@@ -75,12 +86,15 @@ MXQ_DEVICE Tile tile_of(const W4Args& p) {
   return Tile{(int64_t)(first + in % gm) * kBM, (int64_t)(in / gm) * kBN};
 }
 
-template <int kOut, bool kPrepared>
-__global__ __launch_bounds__(kThreads, kOcc) void w4a8_g128_kernel(W4Args p) {
+template <int kOut, bool kPrepared, int kTileM>
+__global__ __launch_bounds__(kThreads, W4Cfg<kTileM>::kOcc) void w4a8_g128_kernel(W4Args p) {
+  typedef W4Cfg<kTileM> C;
+  constexpr int kBM = C::kBM, kBI = C::kBI, kStageA = C::kStageA, kStage = C::kStage, kLds = C::kLds;
+  constexpr int kALoads = C::kALoads, kLoads = C::kLoads;
   __shared__ __attribute__((aligned(16))) char lds[kLds];
   char* const scale_ring = lds + kNS * kStage;
 
-  const Tile tile = tile_of(p);
+  const Tile tile = tile_of<kBM>(p);
   const int64_t m0 = tile.m0, n0 = tile.n0;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
@@ -123,10 +137,10 @@ __global__ __launch_bounds__(kThreads, kOcc) void w4a8_g128_kernel(W4Args p) {
     if (lane < kScaleLanes) __builtin_amdgcn_global_load_lds((gptr_t)(sbase + s_off), (lptr_t)sd, 16, 0, 0);
   };
 
-  v16i acc[4];
-  float facc[4][16];
+  v16i acc[kBI];
+  float facc[kBI][16];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kBI; ++i) {
     acc[i] = v16i{};
 #pragma unroll
     for (int r = 0; r < 16; ++r) facc[i][r] = 0.0f;
@@ -171,13 +185,10 @@ __global__ __launch_bounds__(kThreads, kOcc) void w4a8_g128_kernel(W4Args p) {
     v4i bq[2];
     bq[0] = lds_read_b128<0>(st + b_row + b_lo);
     bq[1] = lds_read_b128<0>(st + b_row + b_hi);
-    v4i fa[4];
+    v4i fa[kBI];
     {
       const uint32_t x = (uint32_t)(((lh * 4) ^ a_f) << 4);
-      fa[0] = lds_read_b128<0>(st + a_row + x);
-      fa[1] = lds_read_b128<32 * 128>(st + a_row + x);
-      fa[2] = lds_read_b128<64 * 128>(st + a_row + x);
-      fa[3] = lds_read_b128<96 * 128>(st + a_row + x);
+      static_for<kBI>([&](auto I) { fa[decltype(I)::value] = lds_read_b128<decltype(I)::value * 32 * 128>(st + a_row + x); });
     }
     // Scale of group kt-1; zero before the first group (an exact no-op fold of zeros).
     const uint16_t* srow =
@@ -191,7 +202,7 @@ __global__ __launch_bounds__(kThreads, kOcc) void w4a8_g128_kernel(W4Args p) {
       constexpr int s = decltype(S)::value;
       const uint32_t xn = (uint32_t)(((lh * 4 + s + 1) ^ a_f) << 4);  // chunk of K-step s+1
       v4i fb_next;
-      static_for<4>([&](auto I) {
+      static_for<kBI>([&](auto I) {
         constexpr int i = decltype(I)::value;
         if constexpr (s == 0) {
 #pragma unroll
@@ -200,7 +211,7 @@ __global__ __launch_bounds__(kThreads, kOcc) void w4a8_g128_kernel(W4Args p) {
         } else {
           // block i's fragment of this step was read after its previous MFMA; the reads of the
           // later blocks may still be in flight
-          wait_lgkm<3 - i>();
+          wait_lgkm<kBI - 1 - i>();
         }
         __builtin_amdgcn_sched_barrier(0);
         acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb, s == 0 ? v16i{} : acc[i], 0, 0, 0);
@@ -229,13 +240,13 @@ __global__ __launch_bounds__(kThreads, kOcc) void w4a8_g128_kernel(W4Args p) {
     const uint16_t* srow = reinterpret_cast<const uint16_t*>(scale_ring + (g & (kScaleRing - 1)) * kScaleBytes);
     const float sc = f16_to_f32(srow[s_idx]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kBI; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) facc[i][r] = fmaf((float)acc[i][r], sc, facc[i][r]);
   }
 
   // ---- epilogue: y = out(facc * (xs / 16)); y = out(y + bias). The main loop's last barrier
-  // left the LDS free: the tile's 128 row scales go there first (every global read of the
+  // left the LDS free: the tile's row scales go there first (every global read of the
   // epilogue is done before its first store, so no store can delay a later load), then the
   // output tile, which is written back as 16-byte row chunks.
   typedef typename OutT<kOut>::T OT;
@@ -250,7 +261,7 @@ __global__ __launch_bounds__(kThreads, kOcc) void w4a8_g128_kernel(W4Args p) {
   if (threadIdx.x < kBM) s_xs[threadIdx.x] = p.xs[min(m0 + threadIdx.x, p.M - 1)] * 0.0625f;
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kBI; ++i) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
@@ -287,24 +298,32 @@ __global__ __launch_bounds__(kThreads, kOcc) void w4a8_g128_kernel(W4Args p) {
   }
 }
 
+template <int kBM>
+int launch_tiles(W4Args p, int out_dtype, bool prepared, hipStream_t st) {
+  p.tiles_m = (int)((p.M + kBM - 1) / kBM);
+  p.tiles_n = (int)((p.N + kBN - 1) / kBN);
+  const unsigned grid = (unsigned)(p.tiles_m * p.tiles_n);
+  switch (out_dtype * 2 + (prepared ? 1 : 0)) {
+    case MXQ_DTYPE_F32 * 2: w4a8_g128_kernel<0, false, kBM><<<grid, kThreads, 0, st>>>(p); break;
+    case MXQ_DTYPE_F32 * 2 + 1: w4a8_g128_kernel<0, true, kBM><<<grid, kThreads, 0, st>>>(p); break;
+    case MXQ_DTYPE_F16 * 2: w4a8_g128_kernel<1, false, kBM><<<grid, kThreads, 0, st>>>(p); break;
+    case MXQ_DTYPE_F16 * 2 + 1: w4a8_g128_kernel<1, true, kBM><<<grid, kThreads, 0, st>>>(p); break;
+    case MXQ_DTYPE_BF16 * 2: w4a8_g128_kernel<2, false, kBM><<<grid, kThreads, 0, st>>>(p); break;
+    case MXQ_DTYPE_BF16 * 2 + 1: w4a8_g128_kernel<2, true, kBM><<<grid, kThreads, 0, st>>>(p); break;
+    default: return mxq_set_error(MXQ_ERR_UNSUPPORTED, "output dtype code %d", out_dtype);
+  }
+  return mxq_check_launch("w4a8_g128_kernel");
+}
+
 }  // namespace
 
 int launch_w4_g128(W4Args p, int out_dtype, bool prepared, hipStream_t st) {
   if (p.M * p.K >= (int64_t)1 << 31 || p.N * (p.K / 2) >= (int64_t)1 << 31 || p.N * (p.K / 128) * 2 >= (int64_t)1 << 31)
     return MXQ_ERR_UNSUPPORTED;  // the caller falls back to the general kernel
-  p.tiles_m = (int)((p.M + kBM - 1) / kBM);
-  p.tiles_n = (int)((p.N + kBN - 1) / kBN);
-  const unsigned grid = (unsigned)(p.tiles_m * p.tiles_n);
-  switch (out_dtype * 2 + (prepared ? 1 : 0)) {
-    case MXQ_DTYPE_F32 * 2: w4a8_g128_kernel<0, false><<<grid, kThreads, 0, st>>>(p); break;
-    case MXQ_DTYPE_F32 * 2 + 1: w4a8_g128_kernel<0, true><<<grid, kThreads, 0, st>>>(p); break;
-    case MXQ_DTYPE_F16 * 2: w4a8_g128_kernel<1, false><<<grid, kThreads, 0, st>>>(p); break;
-    case MXQ_DTYPE_F16 * 2 + 1: w4a8_g128_kernel<1, true><<<grid, kThreads, 0, st>>>(p); break;
-    case MXQ_DTYPE_BF16 * 2: w4a8_g128_kernel<2, false><<<grid, kThreads, 0, st>>>(p); break;
-    case MXQ_DTYPE_BF16 * 2 + 1: w4a8_g128_kernel<2, true><<<grid, kThreads, 0, st>>>(p); break;
-    default: return mxq_set_error(MXQ_ERR_UNSUPPORTED, "output dtype code %d", out_dtype);
-  }
-  return mxq_check_launch("w4a8_g128_kernel");
+  // 128-row tiles unless they would leave CUs with fewer than two workgroups (256 CUs).
+  const int64_t tiles128 = ((p.M + 127) / 128) * ((p.N + kBN - 1) / kBN);
+  return tiles128 >= 2 * 256 ? launch_tiles<128>(p, out_dtype, prepared, st)
+                             : launch_tiles<64>(p, out_dtype, prepared, st);
 }
 
 }  // namespace mxq
