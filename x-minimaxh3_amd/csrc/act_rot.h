@@ -94,30 +94,28 @@ MXQ_DEVICE void load16_act(const uint16_t* xr, int64_t K, int e0, bool on, doubl
   }
 }
 
-// v of lane ^ x within each quad of lanes (x = 1, 2, 3 as quad_perm 0xB1, 0x4E, 0x1B), through
-// DPP moves on the two halves: no LDS traffic, unlike a general lane shuffle.
-template <int kQuadPerm>
-MXQ_DEVICE double quad_xor(double v) {
+// v of the lane that DPP control kCtrl selects, through moves of the two halves: no LDS
+// traffic, unlike a general lane shuffle. quad_perm 0xB1 / 0x4E / 0x1B give lane ^ 1 / ^ 2 / ^ 3
+// within each quad, row_ror:8 (0x128) lane ^ 8 within each 16-lane row, row_half_mirror (0x141)
+// lane ^ 7 within each 8-lane half.
+template <int kCtrl>
+MXQ_DEVICE double dpp_f64(double v) {
   const uint64_t b = __builtin_bit_cast(uint64_t, v);
-  const int lo = __builtin_amdgcn_mov_dpp((int)(uint32_t)b, kQuadPerm, 0xF, 0xF, false);
-  const int hi = __builtin_amdgcn_mov_dpp((int)(uint32_t)(b >> 32), kQuadPerm, 0xF, 0xF, false);
+  const int lo = __builtin_amdgcn_mov_dpp((int)(uint32_t)b, kCtrl, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_mov_dpp((int)(uint32_t)(b >> 32), kCtrl, 0xF, 0xF, false);
   return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
 }
 
-// v of lane (i - kN) mod 16 within each 16-lane row (DPP row_ror), on the two halves.
-template <int kN>
-MXQ_DEVICE double row_ror(double v) {
-  const uint64_t b = __builtin_bit_cast(uint64_t, v);
-  const int lo = __builtin_amdgcn_mov_dpp((int)(uint32_t)b, 0x120 + kN, 0xF, 0xF, false);
-  const int hi = __builtin_amdgcn_mov_dpp((int)(uint32_t)(b >> 32), 0x120 + kN, 0xF, 0xF, false);
-  return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
-}
+// One radix-4 step across the four lanes i, i ^ m, i ^ 2m, i ^ 3m holding x_k (k the lane's digit):
+// y_k = S - 2 x_{k^3} = (x_k + x_{k^1}) + (x_{k^2} - x_{k^3}), i.e. t + (u of lane ^ 2m) with
+// t = x + x', u = x - x', x' the value of lane ^ m: two exchanges instead of three.
+MXQ_DEVICE double h4_cross(double x, double partner, double u_of_2m) { return (x + partner) + u_of_2m; }
 
 // The unscaled rotation (x @ H_G * sqrt(G)) of the 16 values of each lane, where lane l of the
 // wave holds columns 16 l .. 16 l + 15 of a 1024-column window: digits 0 and 1 of the in-group
-// index are inside the lane, digit d >= 2 is lane bit pair d - 2 (xor shuffles with masks m, 2m,
-// 3m, m = 4^(d-2); DPP moves for d = 2, 3). All lanes of the wave must call it (the shuffles
-// are wave-wide).
+// index are inside the lane (h4_quad), digit d >= 2 is lane bit pair d - 2 (exchanges with lane
+// ^ m and ^ 2m, m = 4^(d-2); DPP moves for d = 2, 3). All lanes of the wave must call it (the
+// exchanges are wave-wide).
 MXQ_DEVICE void rotate16(double* v, int digits) {
   if (digits >= 1) {
 #pragma unroll
@@ -127,34 +125,26 @@ MXQ_DEVICE void rotate16(double* v, int digits) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) h4_quad(v[j], v[j + 4], v[j + 8], v[j + 12]);
   }
-  if (digits >= 3) {  // digit 2: lane bits 0-1, the quads of one DPP quad_perm group
+  if (digits >= 3) {  // digit 2: lane bits 0-1, within a DPP quad
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const double t = v[j] + quad_xor<0xB1>(v[j]);  // lane ^ 1
-      const double s = t + quad_xor<0x4E>(t);        // lane ^ 2
-      v[j] = __builtin_fma(-2.0, quad_xor<0x1B>(v[j]), s);  // lane ^ 3
+      const double p = dpp_f64<0xB1>(v[j]);  // lane ^ 1
+      v[j] = h4_cross(v[j], p, dpp_f64<0x4E>(v[j] - p));  // u of lane ^ 2
     }
   }
-  if (digits >= 4) {  // digit 3: lane bits 2-3, i.e. lanes i, i +- 4, i + 8 of a 16-lane row
-    // Partner digit k ^ 1 is the lane 4 above for even k and 4 below for odd k; k ^ 3 the other
-    // way round; k ^ 2 is 8 away either way. Row rotations by 12, 4 and 8 give all three.
-    const bool even = ((threadIdx.x >> 2) & 1) == 0;
+  if (digits >= 4) {  // digit 3: lane bits 2-3; lane ^ 4 = (lane ^ 7) ^ 3, lane ^ 8 a row rotation
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const double up = row_ror<12>(v[j]), dn = row_ror<4>(v[j]);
-      const double t = v[j] + (even ? up : dn);
-      const double s = t + row_ror<8>(t);
-      v[j] = __builtin_fma(-2.0, even ? dn : up, s);
+      const double p = dpp_f64<0x1B>(dpp_f64<0x141>(v[j]));
+      v[j] = h4_cross(v[j], p, dpp_f64<0x128>(v[j] - p));
     }
   }
   for (int d = 4; d < digits; ++d) {
     const int m = 1 << (2 * (d - 2));
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const double t = v[j] + __shfl_xor(v[j], m, kWave);
-      const double s = t + __shfl_xor(t, 2 * m, kWave);
-      const double q3 = __shfl_xor(v[j], 3 * m, kWave);
-      v[j] = __builtin_fma(-2.0, q3, s);
+      const double p = __shfl_xor(v[j], m, kWave);
+      v[j] = h4_cross(v[j], p, __shfl_xor(v[j] - p, 2 * m, kWave));
     }
   }
 }
