@@ -52,10 +52,10 @@ def fht_f64(x: np.ndarray, g: int) -> np.ndarray:
 
     For digit t = 0 .. log4(g) - 1 of the in-group index (stride 4**t), each quad
     (x0, x1, x2, x3) becomes y_k = S - 2 x_{3-k} (column k of h4 is all ones except -1 in row
-    3-k), evaluated as the kernel does: for t = 0, 1 (digits inside a lane) as
-    S - (x_{3-k} + x_{3-k}) with S = (x0 + x1) + (x2 + x3); for t >= 2 (digits across lanes) as
-    (x_k + x_{k^1}) + (x_{k^2} - x_{k^3}). The product with the 1/sqrt(g) factor (a power of two)
-    comes last.
+    3-k), evaluated as the kernel does: for t <= 3 (digits it applies inside a lane) as
+    S - (x_{3-k} + x_{3-k}) with S = (x0 + x1) + (x2 + x3); for t >= 4 (digits exchanged across
+    lanes) as (x_k + x_{k^1}) + (x_{k^2} - x_{k^3}). The product with the 1/sqrt(g) factor (a power
+    of two) comes last.
     """
     d = log4(g)
     x = np.asarray(x, dtype=np.float64)
@@ -66,7 +66,7 @@ def fht_f64(x: np.ndarray, g: int) -> np.ndarray:
     for t in range(d):
         v = y.reshape(y.shape[0], y.shape[1], g // 4 ** (t + 1), 4, 4 ** t)
         out = np.empty_like(v)
-        if t < 2:
+        if t < 4:
             s = (v[:, :, :, 0] + v[:, :, :, 1]) + (v[:, :, :, 2] + v[:, :, :, 3])
             for kk in range(4):
                 p = v[:, :, :, 3 - kk]

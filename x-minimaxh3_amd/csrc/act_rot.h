@@ -94,29 +94,35 @@ MXQ_DEVICE void load16_act(const uint16_t* xr, int64_t K, int e0, bool on, doubl
   }
 }
 
-// v of the lane that DPP control kCtrl selects, through moves of the two halves: no LDS
-// traffic, unlike a general lane shuffle. quad_perm 0xB1 / 0x4E / 0x1B give lane ^ 1 / ^ 2 / ^ 3
-// within each quad, row_ror:8 (0x128) lane ^ 8 within each 16-lane row, row_half_mirror (0x141)
-// lane ^ 7 within each 8-lane half.
-template <int kCtrl>
-MXQ_DEVICE double dpp_f64(double v) {
-  const uint64_t b = __builtin_bit_cast(uint64_t, v);
-  const int lo = __builtin_amdgcn_mov_dpp((int)(uint32_t)b, kCtrl, 0xF, 0xF, false);
-  const int hi = __builtin_amdgcn_mov_dpp((int)(uint32_t)(b >> 32), kCtrl, 0xF, 0xF, false);
-  return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
-}
-
 // One radix-4 step across the four lanes i, i ^ m, i ^ 2m, i ^ 3m holding x_k (k the lane's digit):
 // y_k = S - 2 x_{k^3} = (x_k + x_{k^1}) + (x_{k^2} - x_{k^3}), i.e. t + (u of lane ^ 2m) with
 // t = x + x', u = x - x', x' the value of lane ^ m: two exchanges instead of three.
 MXQ_DEVICE double h4_cross(double x, double partner, double u_of_2m) { return (x + partner) + u_of_2m; }
 
+// A wave's transpose buffer: per 16-lane group a 16 x 16 matrix of doubles with rows of 18
+// (144 bytes: sixteen rows written at one 16-byte slot start on sixteen distinct bank groups), and
+// 16 doubles between groups (the two groups of a half-wave read one row each on disjoint banks).
+// Every access is a per-lane base plus a constant offset.
+constexpr int kTRow = 18;
+constexpr int kTGroup = 16 * kTRow + 16;
+constexpr int kTWave = 4 * kTGroup;  // doubles per wave
+
+// Lanes of one wave exchange data through its own LDS region: the hardware performs a wave's LDS
+// operations in order, so only the compiler must keep each write above the reads of other lanes.
+MXQ_DEVICE void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // The unscaled rotation (x @ H_G * sqrt(G)) of the 16 values of each lane, where lane l of the
 // wave holds columns 16 l .. 16 l + 15 of a 1024-column window: digits 0 and 1 of the in-group
-// index are inside the lane (h4_quad), digit d >= 2 is lane bit pair d - 2 (exchanges with lane
-// ^ m and ^ 2m, m = 4^(d-2); DPP moves for d = 2, 3). All lanes of the wave must call it (the
-// exchanges are wave-wide).
-MXQ_DEVICE void rotate16(double* v, int digits) {
+// index are inside the lane, digits 2 and 3 are lane bits 0-1 and 2-3 within a 16-lane group, and
+// digit d >= 4 is lane bit pair d - 2. For digits 2 and 3 each 16-lane group transposes its
+// 16 x 16 values through the wave's LDS region `tb` (kTWave doubles): lane s then holds value s
+// of the group's sixteen lanes, applies both digits in registers with the same radix-4 step as
+// digits 0 and 1, and the transpose is undone. Digits >= 4 (G >= 1024) exchange with __shfl_xor.
+// All lanes of the wave must call it.
+MXQ_DEVICE void rotate16(double* v, int digits, double* tb) {
   if (digits >= 1) {
 #pragma unroll
     for (int j = 0; j < 16; j += 4) h4_quad(v[j], v[j + 1], v[j + 2], v[j + 3]);
@@ -125,19 +131,33 @@ MXQ_DEVICE void rotate16(double* v, int digits) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) h4_quad(v[j], v[j + 4], v[j + 8], v[j + 12]);
   }
-  if (digits >= 3) {  // digit 2: lane bits 0-1, within a DPP quad
+  if (digits >= 3) {
+    const int lane = threadIdx.x & 63, s = lane & 15;
+    double* gb = tb + (lane >> 4) * kTGroup;
+    typedef double d2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const double p = dpp_f64<0xB1>(v[j]);  // lane ^ 1
-      v[j] = h4_cross(v[j], p, dpp_f64<0x4E>(v[j] - p));  // u of lane ^ 2
-    }
-  }
-  if (digits >= 4) {  // digit 3: lane bits 2-3; lane ^ 4 = (lane ^ 7) ^ 3, lane ^ 8 a row rotation
+    for (int c = 0; c < 8; ++c) *reinterpret_cast<d2*>(gb + s * kTRow + 2 * c) = d2{v[2 * c], v[2 * c + 1]};
+    wave_lds_fence();
+    double w[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const double p = dpp_f64<0x1B>(dpp_f64<0x141>(v[j]));
-      v[j] = h4_cross(v[j], p, dpp_f64<0x128>(v[j] - p));
+    for (int r = 0; r < 16; ++r) w[r] = gb[r * kTRow + s];
+    wave_lds_fence();
+#pragma unroll
+    for (int j = 0; j < 16; j += 4) h4_quad(w[j], w[j + 1], w[j + 2], w[j + 3]);  // digit 2
+    if (digits >= 4) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) h4_quad(w[j], w[j + 4], w[j + 8], w[j + 12]);  // digit 3
     }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) gb[r * kTRow + s] = w[r];
+    wave_lds_fence();
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const d2 pr = *reinterpret_cast<const d2*>(gb + s * kTRow + 2 * c);
+      v[2 * c] = pr[0];
+      v[2 * c + 1] = pr[1];
+    }
+    wave_lds_fence();
   }
   for (int d = 4; d < digits; ++d) {
     const int m = 1 << (2 * (d - 2));

@@ -86,6 +86,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOcc))) voi
   constexpr int kKeepWords = kF32 ? 16 : 8;
   __shared__ uint32_t red_max[2][4];
   __shared__ double red_ss[2][4];
+  __shared__ __attribute__((aligned(16))) double tbuf[4 * kTWave];  // rotation transposes, per wave
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int wpr = p.wpr, rpb = 4 / wpr;
   const int slot = wave / wpr, wr = wave - slot * wpr;
@@ -197,7 +198,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOcc))) voi
           if constexpr (kMod == kModOnly) continue;
         }
       }
-      rotate16(v, p.digits);
+      rotate16(v, p.digits, tbuf + wave * kTWave);
       if constexpr (kF32) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
