@@ -6,11 +6,13 @@
 //
 // Main loop: a 256-thread workgroup (4 wave64s, 2 x 2) owns a 256 x 256 output tile; each wave
 // owns 128 x 128 as a 4 x 4 grid of v_mfma_i32_32x32x32_i8 blocks (256 int32 accumulators per
-// lane, held in AGPRs). K advances 64 bytes per stage; a stage (A 16 KB + B 16 KB) is fetched
-// with gfx950's direct-to-LDS 16-byte loads into one of four LDS buffers, three stages ahead of
-// the MFMAs, so global latency hides behind two stages of matrix work and no VGPRs stage data.
-// Waits and barriers are issued by hand (s_waitcnt vmcnt + s_barrier) so that the prefetches
-// stay in flight across the barrier that publishes the next stage.
+// lane, held in AGPRs). K advances 128 bytes per stage; a stage's A and B chunks (32 KB each) are
+// fetched with gfx950's direct-to-LDS 16-byte loads into a ring of five 32 KB slots, one to two
+// stages ahead of the MFMAs, the loads interleaved one per MFMA, so global latency hides behind
+// matrix work and no VGPRs stage data. Fragment reads are inline-asm ds_read_b128 with explicit
+// lgkmcnt waits; vmcnt waits and barriers are issued by hand too (s_waitcnt + s_barrier) so that
+// the prefetches stay in flight across the barrier that publishes the next stage. Problems with
+// fewer 256-tiles than CUs run the same code on 128 x 128 tiles, two workgroups per CU.
 //
 // Epilogue: the MFMAs run with the weights as first operand, so each lane's accumulators are
 // one output row in four runs of four consecutive columns. Every output type is converted in
