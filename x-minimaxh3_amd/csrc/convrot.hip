@@ -13,13 +13,15 @@
 // in-group index, so the rotation is one 4-point transform per digit; column k of h4 is all ones
 // but -1 in row 3-k, so a quad (x0..x3) becomes y_k = S - 2 x_{3-k}, S = (x0 + x1) + (x2 + x3).
 // It runs in float64: every operation is exact while a group's exponent spread is at most 37
-// bits, which makes the result the exact product; the fixed operation order (digit 0 first,
-// pairwise S, the same association in every lane) makes it reproducible in all other cases.
+// bits, which makes the result the exact product; the fixed operation order (digit 0 first, the
+// same association in every lane) makes it reproducible in all other cases.
 //
 // Layout: a row is cut into 1024-column windows; in a window lane l holds 16 consecutive
 // columns, so digits 0 and 1 of the in-group index are inside the lane and digit d >= 2 is lane
-// bit pair d-2: those quads are combined with xor shuffles (masks m, 2m, 3m, m = 4^(d-2)).
-// Groups never straddle lanes (G % 16 == 0, or G = 4 with four groups per lane). Up to four
+// bit pair d-2. Digits 2 and 3 are brought into the lane by a 16 x 16 transpose of each 16-lane
+// group through the wave's LDS region and applied there with the same quad step; digits >= 4
+// (G >= 1024) exchange with xor shuffles as y_k = (x_k + x_{k^1}) + (x_{k^2} - x_{k^3}) (rotate16
+// in act_rot.h). Groups never straddle lanes (G % 16 == 0, or G = 4 with four groups per lane). Up to four
 // waves share a row's windows; the rotated row stays in registers while its absmax is reduced
 // (through LDS across the row's waves), then it is quantized and stored with 16-byte stores.
 //

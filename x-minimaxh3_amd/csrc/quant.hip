@@ -8,9 +8,11 @@
 // for every pair; the bf16 kernels therefore take one reciprocal per row and multiply.
 // (The identity is checked exhaustively over all bf16 pairs by the CPU test suite.)
 //
-// Layout: one wavefront per row; each lane owns 16-byte chunks lane, lane+64, ... of the row,
-// held in registers between the absmax reduction and the quantize pass, so x is read from HBM
-// exactly once and q written once (the memory-bound roofline: 2 B read + 1 B written / element).
+// Layout of the row quantizers: one wavefront per row; each lane owns 16-byte chunks lane,
+// lane+64, ... of the row, held in registers between the absmax reduction and the quantize pass,
+// so x is read from HBM exactly once and q written once (the memory-bound roofline: 2 B read +
+// 1 B written / element). The quantizer fed a known row absmax and the adaLN kernels below
+// describe their own layouts.
 
 #include "mxq_common.h"
 
