@@ -13,8 +13,8 @@
 //
 // Kernel (2) layout. A workgroup of 4 wave64s (2 x 2) owns a BM x BN tile; each wave a WM x WN
 // sub-tile of v_mfma_i32_32x32x32_i8 blocks. Per 128-wide K stage:
-//  * A (activations) is staged through LDS, double-buffered, with the same conflict-free
-//    swizzle as the W8A8 GEMM;
+//  * A (activations) is staged through LDS, double-buffered, with a conflict-free XOR
+//    swizzle of its 16-byte chunks (w4_swz);
 //  * B (weights) never touches LDS: lane (column lane%32, half h = lane/32) loads the 32 packed
 //    bytes that hold k in [k0 + 64h, k0 + 64h + 64) of its column and unpacks them in registers.
 //    K-step s of the stage then consumes k in [k0 + 64h + 16s, +16) on both operands (the sum
