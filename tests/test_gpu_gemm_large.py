@@ -1,8 +1,10 @@
 """GPU parity of the 256 x 256-tile INT8 GEMM (the configuration every model-sized shape runs)
 and of the 128 x 128 one at a mid-sized shape with partial edge tiles.
 
-The library runs a GEMM with 256 x 256 tiles once it has at least 256 of them (fewer: 128 x 128
-tiles, which the small-shape tests cover), so these shapes have M x N >= 4100 x 4104. K is chosen
+The library runs a GEMM with 256 x 256 tiles once it has at least 256 of them, unless its rounds of
+128 x 128 tiles (512 per round, ~0.55 of a 256-tile round) would finish first; the small-shape tests
+cover 128 x 128 tiles. These shapes (4100 x 7432: 17 x 30 = 510 tiles of 256, two full rounds,
+both edges partial) keep the 256 x 256 kernel for every epilogue. K is chosen
 at the boundaries of the K loop: a single stage (128), stages that are all full with and without
 steady-state iterations (256, 384, 1024) and a partial last stage after zero, one or two steady
 iterations (144, 400, 528). Every epilogue is covered: int32, dequant (+ bias) to bf16, GELU +
@@ -22,7 +24,7 @@ from oracle.bf16 import bf16_bits
 
 pytestmark = pytest.mark.gpu
 
-M, N = 4100, 4104  # 17 x 17 tiles of 256, both edges partial
+M, N = 4100, 7432  # 17 x 30 tiles of 256, both edges partial
 
 
 def _mx():
@@ -55,7 +57,8 @@ def test_int8_linear_256_tiles(dev, k, bias):
 
 
 def test_ffn_chain_256_tiles(dev):
-    """fc1 (GELU + row absmax epilogue) and fc2 both run 256 x 256 tiles."""
+    """fc1 (GELU + row absmax epilogue) runs 256 x 256 tiles; fc2 (17 x 16 tiles of 256, just over
+    one round) runs 128 x 128 tiles."""
     m, k, hidden, n = M, 400, 4112, 4096  # hidden: a multiple of 16 with a partial edge tile
     print(f"ffn 256-tile m={m} k={k} hidden={hidden} n={n}", flush=True)
     x = activations(m, k, 60)

@@ -583,9 +583,15 @@ __global__ __launch_bounds__(kGemmThreads, kT == 256 ? 1 : 2) void gemm_i8_kerne
 template <int kEpi, int kOut>
 static int launch_gemm(const GemmArgs& args0, hipStream_t stream) {
   GemmArgs args = args0;
-  // Problems with fewer 256-tiles than CUs run 128-tiles (four times as many workgroups).
+  // Problems with fewer 256-tiles than CUs run 128-tiles (four times as many workgroups). Larger
+  // ones run 128-tiles too when their rounds finish first: 256 CUs hold 256 workgroups of 256-tiles
+  // or 512 of 128-tiles, and a round of 128-tiles takes about 0.55 of a round of 256-tiles
+  // (measured at K = 4096-8192), so a last round of 256-tiles that is mostly empty is cheaper as
+  // 128-tiles (4096 x 5120: 1.25 rounds, 0.147 -> 0.117 ms) and a full one is not.
   const int64_t big_tiles = ((args.M + 255) / 256) * ((args.N + 255) / 256);
-  const bool small = kEpi != kEpiGelu && kEpi != kEpiSwiGLU && big_tiles < 256;
+  const int64_t tiles128 = ((args.M + 127) / 128) * ((args.N + 127) / 128);
+  const bool prefer128 = big_tiles < 256 || ((tiles128 + 511) / 512) * 11 < ((big_tiles + 255) / 256) * 20;
+  const bool small = kEpi != kEpiGelu && kEpi != kEpiSwiGLU && prefer128;
   const int kt = small ? 128 : 256;
   args.tiles_m = (int)((args.M + kt - 1) / kt);
   args.tiles_n = (int)((args.N + kt - 1) / kt);
