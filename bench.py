@@ -224,28 +224,56 @@ class QkvWorkload:
         return _cpu_sample(run, budget_s, self.m, "tokens/s", "first {rows} tokens through eager adaln -> int8_linear")
 
 
+def _copies(bytes_per_copy, floor_bytes=1 << 30):
+    """Number of input copies a workload cycles through so that consecutive steps touch more
+    than `floor_bytes` (1 GiB: four times the 256 MB last-level cache) before a copy comes back."""
+    return max(2, -(-floor_bytes // max(int(bytes_per_copy), 1)))
+
+
 class W4A8Workload:
-    def __init__(self, dev, m, n, k, g=128, name="w4a8_gemm"):
+    """Group-scaled W4A8 GEMM. With `from_bf16` (the skinny projection) a step is the per-token
+    quantizer of the bf16 activations and the GEMM; otherwise (the 8192-row GEMM, whose input is
+    the int8 activations) the GEMM alone. Each step takes the next of `copies` sets of activations
+    and weights, so that their bytes come from HBM rather than the last-level cache."""
+
+    def __init__(self, dev, m, n, k, g=128, name="w4a8_gemm", from_bf16=False):
         self.name = name
         self.m, self.n, self.k, self.g = m, n, k, g
-        x = make_activations(m, k, dev, 20)
-        self.xq, xs = mx_qlinear.quantize_int8_rowwise(x)
-        self.xs = xs.reshape(-1)
-        self.x = x
-        self.w = torch.randint(-128, 128, (n, k // 2), generator=_gen(dev, 21), device=dev, dtype=torch.int8)
-        self.gs = (torch.randn(k // g, n, generator=_gen(dev, 22), device=dev).abs() * 0.01).to(torch.float16)
-        self.out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        self.from_bf16 = from_bf16
         self.dev = dev
         # Group 128: the weights are re-laid once for the GEMM (as when a layer loads).
         self.prepared = g == 128 and n % 8 == 0
-        self.wg = mx_qlinear.prepare_w4a8_grouped(self.w).qdata if self.prepared else self.w
+        act_bytes = m * k * (2 if from_bf16 else 1)
+        self.copies = _copies(act_bytes + n * k // 2 + (k // g) * n * 2)
+        self.sets = []
+        for c in range(self.copies):
+            x = make_activations(m, k, dev, 20 + 100 * c)
+            w = torch.randint(-128, 128, (n, k // 2), generator=_gen(dev, 21 + 100 * c), device=dev, dtype=torch.int8)
+            gs = (torch.randn(k // g, n, generator=_gen(dev, 22 + 100 * c), device=dev).abs() * 0.01).to(torch.float16)
+            wg = mx_qlinear.prepare_w4a8_grouped(w).qdata if self.prepared else w
+            if from_bf16:
+                self.sets.append((x, None, None, w, wg, gs))
+            else:
+                xq, xs = mx_qlinear.quantize_int8_rowwise(x)
+                self.sets.append((None, xq, xs.reshape(-1), w, wg, gs))
+        self.xq = torch.empty(m, k, dtype=torch.int8, device=dev)
+        self.xs = torch.empty(m, dtype=torch.float32, device=dev)
+        self.out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        self.calls = 0
 
     def step(self, timer=None):
         st = _stream(self.dev)
         t = timer.span if timer else (lambda name: _Null())
+        x, xq, xs, _, wg, gs = self.sets[self.calls % self.copies]
+        self.calls += 1
+        if self.from_bf16:
+            xq, xs = self.xq, self.xs
+            with t("quant_x"):
+                _lib.call("mxq_quantize_int8_rowwise", _p(x), _lib.DTYPE_BF16, _p(xq), _p(xs), self.m, self.k,
+                          _lib.ACT_NONE, st)
         with t("w4a8_gemm"):
             entry = "mxq_w4a8_gemm_grouped_prepared" if self.prepared else "mxq_w4a8_gemm_grouped"
-            _lib.call(entry, _p(self.xq), _p(self.xs), _p(self.wg), _p(self.gs), None,
+            _lib.call(entry, _p(xq), _p(xs), _p(wg), _p(gs), None,
                       _p(self.out), self.m, self.n, self.k, self.g, self.n, _lib.DTYPE_BF16, st)
 
     def ops_per_step(self):
@@ -254,56 +282,83 @@ class W4A8Workload:
     def units_per_step(self):
         return self.m
 
-    def alg_bytes(self):
+    def gemm_bytes(self):
         return self.m * self.k + self.n * self.k // 2 + (self.k // self.g) * self.n * 2 + self.m * 4 + self.m * self.n * 2
+
+    def alg_bytes(self):
+        """Bytes of the step: from the bf16 activations when the step quantizes them."""
+        if self.from_bf16:
+            return 2 * self.m * self.k + self.n * self.k // 2 + (self.k // self.g) * self.n * 2 + self.m * self.n * 2
+        return self.gemm_bytes()
 
     def dominant(self, timer):
         sym = "w4a8_g128_kernel" if self.g == 128 and self.n % 8 == 0 else "w4a8_grouped_kernel"
         return {"span": "w4a8_gemm", "symbol": sym, "ops": self.ops_per_step(),
-                "bytes": self.alg_bytes()}
+                "bytes": self.gemm_bytes()}
 
     def config(self):
         return {"workload": self.name, "m": self.m, "n": self.n, "k": self.k, "group": self.g,
+                "input": "bf16 activations, per-token quant inside the step" if self.from_bf16
+                else "int8 activations (per-token quantized) with fp32 scales",
                 "weights": "int4 offset-8 packed, fp16 group scales"
-                + ("; nibbles re-laid once at load (prepare_w4a8_grouped)" if self.prepared else "")}
+                + ("; nibbles re-laid once at load (prepare_w4a8_grouped)" if self.prepared else ""),
+                "input_copies_cycled": self.copies}
 
     def cpu_baseline(self, budget_s):
         from oracle import eager_torch
 
-        w, gs = self.w.cpu(), self.gs.cpu()
+        x, xq, xs, w, _, gs = self.sets[0]
+        w, gs = w.cpu(), gs.cpu()
+        if self.from_bf16:
+            xq, xs = mx_qlinear.quantize_int8_rowwise(x)
+            xs = xs.reshape(-1)
 
         def run(rows):
-            a, xs = self.xq[:rows].cpu(), self.xs[:rows].cpu()
+            a, s = xq[:rows].cpu(), xs[:rows].cpu()
+            xb = x[:rows].cpu() if self.from_bf16 else None
             t0 = time.perf_counter()
-            eager_torch.w4a8_grouped_linear(a, xs, w, gs, self.g)
+            if xb is not None:
+                a, s = eager_torch.quantize_int8_rowwise(xb)
+                s = s.reshape(-1)
+            eager_torch.w4a8_grouped_linear(a, s, w, gs, self.g)
             return time.perf_counter() - t0
 
-        return _cpu_sample(run, budget_s, self.m, "tokens/s", "first {rows} rows through eager per-group _int_mm")
+        what = ("first {rows} rows through eager per-token quant + per-group _int_mm" if self.from_bf16
+                else "first {rows} rows through eager per-group _int_mm")
+        return _cpu_sample(run, budget_s, self.m, "tokens/s", what)
 
 
 class LinearC1Workload:
+    """W8A8 single linear 1024 x 3072 x 3072: per-token quant of bf16 X, then the GEMM with the
+    dequant + bias epilogue. Each step takes the next of `copies` sets of X and weights."""
+
     name = "int8_linear_1024x3072x3072"
 
     def __init__(self, dev):
-        self.m = self.k = 3072
-        self.m = 1024
-        self.n = 3072
-        self.x = make_activations(self.m, self.k, dev, 30)
-        self.w, self.s = make_int8_weight(self.n, self.k, dev, 31)
+        self.m, self.n, self.k = 1024, 3072, 3072
+        self.copies = _copies(2 * self.m * self.k + self.n * self.k)
+        self.sets = []
+        for c in range(self.copies):
+            x = make_activations(self.m, self.k, dev, 30 + 100 * c)
+            w, s = make_int8_weight(self.n, self.k, dev, 31 + 100 * c)
+            self.sets.append((x, w, s))
         self.b = make_bias(self.n, dev, 32)
         self.xq = torch.empty(self.m, self.k, dtype=torch.int8, device=dev)
         self.xs = torch.empty(self.m, dtype=torch.float32, device=dev)
         self.out = torch.empty(self.m, self.n, dtype=torch.bfloat16, device=dev)
         self.dev = dev
+        self.calls = 0
 
     def step(self, timer=None):
         st = _stream(self.dev)
         t = timer.span if timer else (lambda name: _Null())
+        x, w, s = self.sets[self.calls % self.copies]
+        self.calls += 1
         with t("quant_x"):
-            _lib.call("mxq_quantize_int8_rowwise", _p(self.x), _lib.DTYPE_BF16, _p(self.xq), _p(self.xs), self.m,
+            _lib.call("mxq_quantize_int8_rowwise", _p(x), _lib.DTYPE_BF16, _p(self.xq), _p(self.xs), self.m,
                       self.k, _lib.ACT_NONE, st)
         with t("gemm"):
-            _lib.call("mxq_int8_gemm_dequant", _p(self.xq), _p(self.w), _p(self.xs), _p(self.s), self.n,
+            _lib.call("mxq_int8_gemm_dequant", _p(self.xq), _p(w), _p(self.xs), _p(s), self.n,
                       _p(self.b), _p(self.out), self.m, self.n, self.k, self.n, _lib.DTYPE_BF16, st)
 
     def ops_per_step(self):
@@ -318,15 +373,17 @@ class LinearC1Workload:
                 "bytes": m * k + n * k + 2 * m * n + 4 * m + 4 * n + 2 * n}
 
     def config(self):
-        return {"workload": self.name, "m": self.m, "n": self.n, "k": self.k}
+        return {"workload": self.name, "m": self.m, "n": self.n, "k": self.k,
+                "input": "bf16 activations, per-token quant inside the step", "input_copies_cycled": self.copies}
 
     def cpu_baseline(self, budget_s):
         from oracle import eager_torch
 
-        w, s, b = self.w.cpu(), self.s.cpu(), self.b.cpu()
+        x0, w, s = self.sets[0]
+        w, s, b = w.cpu(), s.cpu(), self.b.cpu()
 
         def run(rows):
-            x = self.x[:rows].cpu()
+            x = x0[:rows].cpu()
             t0 = time.perf_counter()
             eager_torch.int8_linear(x, w, s, b)
             return time.perf_counter() - t0
@@ -643,9 +700,21 @@ class LinearM1Workload:
             total += time.perf_counter() - t0
             calls += 1
         value = self.alg_bytes() * calls / total / 1e9
-        return {"value": round(value, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        return {"value": round(value, 3), "unit": "GB/s", "cores": threads, "cpu_model": cpu_model(), "kind": "port",
                 "sample": f"{calls} single-token eager int8_linear(convrot=True) calls on the host, "
                           f"{total:.1f} s"}
+
+
+def cpu_model():
+    """The host CPU's model name (first `model name` line of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def _cpu_sample(run, budget_s, max_rows, unit, what):
@@ -665,7 +734,7 @@ def _cpu_sample(run, budget_s, max_rows, unit, what):
     while total < budget_s:
         total += run(rows)
         passes += 1
-    return {"value": rows * passes / total, "unit": unit, "cores": threads, "kind": "port",
+    return {"value": rows * passes / total, "unit": unit, "cores": threads, "cpu_model": cpu_model(), "kind": "port",
             "sample": what.format(rows=rows) + f", {passes} pass(es), {total:.1f} s, torch {torch.__version__} CPU"}
 
 
@@ -754,7 +823,8 @@ WORKLOADS = {
     "ffn": lambda dev: FfnWorkload(dev),
     "qkv_adaln": lambda dev: QkvWorkload(dev),
     "w4a8_gemm": lambda dev: W4A8Workload(dev, 8192, 5120, 5120, name="w4a8_gemm_8192x5120x5120"),
-    "w4a8_skinny": lambda dev: W4A8Workload(dev, 512, 10240, 5120, name="w4a8_skinny_512x10240x5120"),
+    "w4a8_skinny": lambda dev: W4A8Workload(dev, 512, 10240, 5120, name="w4a8_skinny_512x10240x5120",
+                                            from_bf16=True),
     "linear_c1": lambda dev: LinearC1Workload(dev),
     "h3_mlp": lambda dev: H3MlpWorkload(dev),
     "h3_qkv": lambda dev: H3QkvWorkload(dev),

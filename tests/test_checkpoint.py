@@ -49,6 +49,8 @@ def test_roundtrip_read_audit_and_build(tmp_path):
             mx.quant_linear(src, "blocks.0.attn.out_proj", device="cpu")
     assert isinstance(l1, mx.ConvRotInt8Linear) and l1.spec.convrot and l1.spec.convrot_groupsize == 256
     assert torch.equal(l1.qweight, t["blocks.0.attn.qkv_proj.weight"])
+    # the stored INT8 bias is not applied, as in the reference's loader (assembly.py:174-184)
+    assert "blocks.0.attn.qkv_proj.bias" in t and l1.bias is None
     assert isinstance(l2, mx.ConvRotW4A8Linear) and l2.spec.group_size == 16
     assert l2.s_rel.dtype == torch.float8_e4m3fn and l2.codebook is not None
     with pytest.raises(RuntimeError):  # the modules run on the GPU only
@@ -117,8 +119,9 @@ def test_loaded_layers_run_on_the_gpu(tmp_path, dev):
         layer = mx.quant_linear(src, "l", device=dev)
     x = activations(24, 512, 11).to(dev)
     y = layer(x)
-    ref = mx.int8_linear(x, q, s, t["l.bias"].to(dev), convrot=True, convrot_groupsize=256)
+    assert layer.bias is None  # a stored INT8 bias is not applied (assembly.py:174-184)
+    ref = mx.int8_linear(x, q, s, None, convrot=True, convrot_groupsize=256)
     assert torch.equal(y, ref)
     # the stored weights are the rotated, quantized originals: the layer approximates x @ W^T
-    dense = x.float() @ wf.float().to(dev).T + t["l.bias"].float().to(dev)
+    dense = x.float() @ wf.float().to(dev).T
     assert ((y.float() - dense).norm() / dense.norm()).item() < 0.05

@@ -144,9 +144,29 @@ def _check_rms_adaln_bound(y, x, w, scale, shift, rows, eps):
     t = bf16_to_f32(bf16_bits(np.float32(1.0) + bf16_to_f32(bits(scale))[rows]))
     tol = 2 * bf16_ulp(np.abs(n64 * t).astype(np.float32)) + bf16_ulp(np.maximum(np.abs(rv), np.abs(yv)))
     assert np.all(np.abs(yv - rv) <= tol)
-    mismatch = np.mean(bits(y) != ref)
+    mismatch = float(np.mean(bits(y) != ref))
     print(f"rms_adaln bf16 mismatch rate vs torch CPU: {mismatch:.2e}")
-    assert mismatch < 1e-2
+    assert mismatch <= RMS_ADALN_MISMATCH_BOUND
+    return mismatch
+
+
+# Elements of the RMS adaLN bf16 output that differ from torch's CPU rms_norm composition:
+# RMS_ADALN_MISMATCH_BOUND for any test size, RMS_ADALN_MISMATCH_LARGE (about twice the measured
+# rate) for the large-sample test.
+RMS_ADALN_MISMATCH_BOUND = 1e-4
+RMS_ADALN_MISMATCH_LARGE = 1e-4
+
+
+def test_rms_adaln_mismatch_rate_large_sample(dev):
+    m, d, eps = 4096, 5376, 1e-6
+    print(f"rms_adaln mismatch sample m={m} d={d}", flush=True)
+    x, w, scale, shift = _rms_inputs(m, d, 4343)
+    segs = _segments(m, 3)
+    rows = eager_np.segment_row_map(m, segs)
+    y = _mx().rms_adaln(x.to(dev), (w.to(dev), eps), shift.to(dev), scale.to(dev), segs)
+    rate = _check_rms_adaln_bound(y, x, w, scale, shift, rows, eps)
+    print(f"rms_adaln mismatch vs torch CPU over {m * d} elements: bf16 {rate:.3e}", flush=True)
+    assert rate <= RMS_ADALN_MISMATCH_LARGE
 
 
 @pytest.mark.parametrize("m,d,eps", [(64, 5120, 1e-6), (33, 1024, 1e-5), (7, 3072, 1e-6), (300, 5120, 1e-6)])

@@ -126,15 +126,15 @@ class SafeTensorSource:
 def quant_linear(source: TensorSource, prefix: str, *, device: torch.device | str,
                  int8_kernel=None, w4a8_kernel=None, output_dtype: torch.dtype | None = None):
     """Build the quantized module stored under ``prefix`` (assembly.py:166-228): INT8 ConvRot if
-    ``{p}.weight_scale`` exists, else W4A8 (KeyError if neither layout is present)."""
+    ``{p}.weight_scale`` exists, else W4A8 (KeyError if neither layout is present). As in the
+    reference, an INT8 layer is built from its weight, scale and spec only: a stored
+    ``{p}.bias`` is not applied to it (W4A8 layers do load theirs)."""
     if source.has_tensor(f"{prefix}.weight_scale"):
         state = {
             f"{prefix}.weight": source.tensor(f"{prefix}.weight").to(device),
             f"{prefix}.weight_scale": source.tensor(f"{prefix}.weight_scale").to(device),
             f"{prefix}.comfy_quant": source.tensor(f"{prefix}.comfy_quant"),
         }
-        if source.has_tensor(f"{prefix}.bias"):
-            state[f"{prefix}.bias"] = source.tensor(f"{prefix}.bias").to(device)
         return ConvRotInt8Linear.from_state_dict(state, prefix, kernel=int8_kernel, output_dtype=output_dtype)
     required = (f"{prefix}.weight_s_rel", f"{prefix}.weight_s_channel")
     if not all(source.has_tensor(key) for key in required):

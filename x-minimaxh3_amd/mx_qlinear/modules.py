@@ -144,7 +144,7 @@ class ConvRotInt8Linear(nn.Module):
             raise ValueError("bias does not match qweight output rows")
         if spec.convrot and qweight.shape[1] % spec.convrot_groupsize:
             raise ValueError("qweight input width is not divisible by ConvRot group size")
-        self.register_buffer("qweight", qweight)
+        self.register_buffer("qweight", ops.prepare_int8_weight(qweight))
         self.register_buffer("scale", scale)
         self.register_buffer("bias", bias)
         self.spec = spec
@@ -197,17 +197,22 @@ class ConvRotInt8Linear(nn.Module):
         return self._forward_parameters(value, *self._slice_params(start, stop))
 
     def prepare_output_slices(self, value: torch.Tensor) -> PreparedConvRotInt8Input:
-        """Quantize a 2-D activation once for later output slices (quantization.py:339-371)."""
-        if value.ndim != 2:
-            raise RuntimeError("prepared output slices require a rank-two activation")
-        _gpu_only(value)
+        """Quantize a 2-D activation once for later output slices (quantization.py:339-371), with
+        the reference's contract: this package's INT8 kernel, a rank-two GPU activation, ConvRot
+        group 256 and an input width that is a multiple of 256 in [256, 16384]; RuntimeError
+        otherwise (ValueError for a width that does not match the weight), in the same order."""
+        if self.kernel is not int8_kernel:
+            raise RuntimeError("prepared output slices require the audited HIP INT8 kernel")
+        if not value.is_cuda or value.ndim != 2:
+            raise RuntimeError("prepared output slices require a rank-two GPU activation")
+        if not self.spec.convrot or self.spec.convrot_groupsize != 256:
+            raise RuntimeError("prepared output slices require ConvRot group size 256")
         if value.shape[1] != self.in_features:
             raise ValueError("input width does not match quantized weight")
+        if not 256 <= self.in_features <= 16_384 or self.in_features % 256:
+            raise RuntimeError("prepared output slice width is outside the fused GPU contract")
         contiguous = value if value.is_contiguous() else value.contiguous()
-        if self.spec.convrot:
-            qdata, scale = ops.quantize_int8_rowwise_convrot(contiguous, self.spec.convrot_groupsize)
-        else:
-            qdata, scale = ops.quantize_int8_rowwise(contiguous)
+        qdata, scale = ops.quantize_int8_rowwise_convrot(contiguous, 256)
         return PreparedConvRotInt8Input(qdata=qdata, scale=scale, rows=int(value.shape[0]),
                                         width=int(value.shape[1]), dtype=value.dtype)
 

@@ -295,13 +295,7 @@ def _rms_adaln_call(value, norm, shift, scale, segments, quant: bool, group: int
     if sc.shape[0] != sh.shape[0]:
         raise ValueError("scale and shift must have the same number of rows")
     if isinstance(segments, torch.Tensor):
-        mr = segments.to(device=dev, dtype=torch.int32).reshape(-1).contiguous()
-        if mr.numel() != rows:
-            raise ValueError(f"modulation row map has {mr.numel()} entries, expected {rows}")
-        if rows:
-            lo, hi = torch.aminmax(mr)
-            if int(lo) < 0 or int(hi) >= sc.shape[0]:
-                raise ValueError("modulation row outside the scale/shift tables")
+        mr = _row_map(segments, rows, sc.shape[0], dev, "modulation row map", "modulation row outside the scale/shift tables")
     else:
         mr = segment_row_map(rows, segments, dev)
         if rows and max(int(r) for _, _, r in segments) >= sc.shape[0]:
@@ -323,18 +317,51 @@ def _rms_adaln_call(value, norm, shift, scale, segments, quant: bool, group: int
 # INT8 GEMMs
 # ---------------------------------------------------------------------------------------
 
+def _gemm_weight(w: torch.Tensor, kp: int, transpose: bool = False) -> torch.Tensor:
+    """The int8 weight as the GEMM reads it: ``[N, kp]`` row-major (``w.t()`` with ``transpose``),
+    K zero-padded to ``kp`` (zero terms leave the int32 sums unchanged, as the reference's own K
+    padding, CK/backends/eager/quantization.py:770-775) and 16-byte aligned. A weight that already
+    has that form is used as it is; otherwise the copy is made once and kept on the weight tensor
+    (rebuilt only if the weight is modified in place), so repeated calls do not copy it."""
+    src = w.t() if transpose else w
+    if not transpose and src.is_contiguous() and src.shape[1] == kp and src.data_ptr() % 16 == 0:
+        return src
+    key = (w._version, w.data_ptr(), tuple(w.shape), tuple(w.stride()), kp, transpose)
+    cached = getattr(w, "_mxq_gemm_weight", None)
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    wp = torch.zeros((src.shape[0], kp), dtype=torch.int8, device=w.device)
+    wp[:, : src.shape[1]] = src
+    try:
+        w._mxq_gemm_weight = (key, wp)
+    except (AttributeError, RuntimeError):  # tensors that take no attributes: copy per call
+        pass
+    return wp
+
+
+def _gemm_activation(q: torch.Tensor, kp: int) -> torch.Tensor:
+    """The int8 activation ``[M, kp]``: zero-padded K and 16-byte aligned (copied only when needed)."""
+    if q.shape[1] == kp:
+        return _aligned16(q)
+    qp = torch.zeros((q.shape[0], kp), dtype=torch.int8, device=q.device)
+    qp[:, : q.shape[1]] = q
+    return qp
+
+
 def _pad_k(q: torch.Tensor, w: torch.Tensor):
-    """Zero-pad K to a multiple of 16 (zero terms leave the int32 sums unchanged,
-    as the reference's own K padding, CK/backends/eager/quantization.py:770-775)."""
+    """Activation and weight for the GEMM with K rounded up to a multiple of 16; the weight's
+    padded or realigned form is built once per weight tensor (:func:`_gemm_weight`)."""
     k = q.shape[1]
     kp = (k + 15) // 16 * 16
-    if kp == k:
-        return _aligned16(q), _aligned16(w), k
-    qp = torch.zeros((q.shape[0], kp), dtype=torch.int8, device=q.device)
-    qp[:, :k] = q
-    wp = torch.zeros((w.shape[0], kp), dtype=torch.int8, device=w.device)
-    wp[:, :k] = w
-    return qp, wp, kp
+    return _gemm_activation(q, kp), _gemm_weight(w, kp), kp
+
+
+def prepare_int8_weight(qweight: torch.Tensor) -> torch.Tensor:
+    """Build, once (at load), the GEMM form of an int8 ``[N, K]`` weight when it differs from the
+    stored tensor (K not a multiple of 16, or a misaligned start), so later calls do not copy it."""
+    if qweight.dim() == 2 and qweight.dtype == torch.int8 and qweight.is_cuda:
+        _gemm_weight(qweight, (qweight.shape[1] + 15) // 16 * 16)
+    return qweight
 
 
 def mm_int8(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
@@ -350,7 +377,10 @@ def mm_int8(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
         return out
     if a.shape[1] == 0:
         return out.zero_()
-    a2, w2, k = _pad_k(a.contiguous(), b.t().contiguous())
+    k = a.shape[1]
+    kp = (k + 15) // 16 * 16
+    a2, w2 = _gemm_activation(a.contiguous(), kp), _gemm_weight(b, kp, transpose=True)
+    k = kp
     with torch.cuda.device(dev):
         call("mxq_int8_gemm_i32", _p(a2), _p(w2), _p(out), m, n, k, n, _stream(dev))
     return out
@@ -428,10 +458,10 @@ def int8_linear_prequantized(x_qdata: torch.Tensor, x_scale: torch.Tensor, weigh
     k = x_qdata.shape[1]
     if m == 1 and _m1_ok(k):
         with torch.cuda.device(dev):
-            call("mxq_int8_gemv_dequant", _p(_aligned16(x_qdata)), _p(xs), _p(_aligned16(weight)), _p(ws),
+            call("mxq_int8_gemv_dequant", _p(_aligned16(x_qdata)), _p(xs), _p(_gemm_weight(weight, k)), _p(ws),
                  ws.numel(), _p(b), _p(out), n, k, code, _stream(dev))
         return out
-    q2, w2, k = _pad_k(x_qdata.contiguous(), weight.contiguous())
+    q2, w2, k = _pad_k(x_qdata.contiguous(), weight)
     with torch.cuda.device(dev):
         call("mxq_int8_gemm_dequant", _p(q2), _p(w2), _p(xs), _p(ws), ws.numel(), _p(b), _p(out),
              m, n, k, n, code, _stream(dev))
@@ -478,7 +508,7 @@ def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tenso
         xq = torch.empty((1, width), dtype=torch.int8, device=dev)
         xs = torch.empty((1, 1), dtype=torch.float32, device=dev)
         with torch.cuda.device(dev):
-            call("mxq_int8_linear_m1", _p(_aligned16(x2)), _p(_aligned16(weight)), _p(ws), ws.numel(), _p(b),
+            call("mxq_int8_linear_m1", _p(_aligned16(x2)), _p(_gemm_weight(weight, width)), _p(ws), ws.numel(), _p(b),
                  _p(out), n, width, convrot_groupsize if convrot else 0, act, _out_code(out_dtype), _p(xq), _p(xs),
                  _stream(dev))
         return out.reshape(*lead, n)
@@ -539,8 +569,8 @@ def int8_ffn_gelu(x: torch.Tensor, fc1_weight: torch.Tensor, fc1_scale: torch.Te
         return out.reshape(*x.shape[:-1], n)
     reuse = workspace is not None and workspace.shape == (m, k, hidden) and workspace.xq.device == dev
     ws = workspace if reuse else FfnWorkspace(m, k, hidden, dev)
-    w1 = fc1_weight.contiguous()
-    w2 = fc2_weight.contiguous()
+    w1 = _gemm_weight(fc1_weight, k)
+    w2 = _gemm_weight(fc2_weight, hidden)
     st = _stream(dev)
     with torch.cuda.device(dev):
         call("mxq_quantize_int8_rowwise", _p(x2), _lib.DTYPE_BF16, _p(ws.xq), _p(ws.xs), m, k,
@@ -563,6 +593,29 @@ def int8_ffn_gelu(x: torch.Tensor, fc1_weight: torch.Tensor, fc1_scale: torch.Te
 _ROW_MAP_CACHE: dict[tuple, torch.Tensor] = {}
 
 
+def _row_map(t: torch.Tensor, rows: int, count: int, dev, what: str, range_error: str) -> torch.Tensor:
+    """An int32 [rows] row map on ``dev`` whose entries index a table of ``count`` rows. The range
+    check reads the map back to the host, so it runs once per map tensor (and again only if the
+    tensor is modified in place): later calls, including ones under graph capture, do not
+    synchronise. The kernels clamp every index into the table, so even an unchecked map cannot
+    read out of bounds."""
+    m = t.to(device=dev, dtype=torch.int32).reshape(-1).contiguous()
+    if m.numel() != rows:
+        raise ValueError(f"{what} has {m.numel()} entries, expected {rows}")
+    key = (t._version, t.data_ptr(), rows, str(dev))
+    checked = getattr(t, "_mxq_row_map_checked", None)
+    if rows and not (checked is not None and checked[0] == key and checked[1] <= count):
+        lo, hi = torch.aminmax(m)
+        lo, hi = int(lo), int(hi)
+        if lo < 0 or hi >= count:
+            raise ValueError(range_error)
+        try:
+            t._mxq_row_map_checked = (key, hi + 1)
+        except (AttributeError, RuntimeError):
+            pass
+    return m
+
+
 def segment_row_map(length: int, segments, device) -> torch.Tensor:
     """int32 [length] modulation row of every token, from ordered ``(start, stop, row)``
     segments that partition ``[0, length)``; cached per device and segmentation
@@ -583,6 +636,9 @@ def segment_row_map(length: int, segments, device) -> torch.Tensor:
     if previous != length:
         raise ValueError("modulation segments do not cover the packed sequence")
     cached = host.to(device=device)
+    if length:
+        cached._mxq_row_map_checked = ((cached._version, cached.data_ptr(), int(length), str(device)),
+                                       max(r for _, _, r in normalized) + 1)
     _ROW_MAP_CACHE[key] = cached
     return cached
 
@@ -616,13 +672,7 @@ def int8_linear_gated_residual_(residual: torch.Tensor, x: torch.Tensor, weight:
         raise ValueError(f"gate must be [rows, {n}], got {tuple(gate.shape)}")
     g = gate.to(device=dev, dtype=torch.bfloat16).contiguous()
     if isinstance(gate_rows, torch.Tensor):
-        gr = gate_rows.to(device=dev, dtype=torch.int32).reshape(-1).contiguous()
-        if gr.numel() != rows:
-            raise ValueError(f"gate_rows has {gr.numel()} entries, expected {rows}")
-        if rows:
-            lo, hi = torch.aminmax(gr)
-            if int(lo) < 0 or int(hi) >= g.shape[0]:
-                raise ValueError("gate_rows index outside the gate")
+        gr = _row_map(gate_rows, rows, g.shape[0], dev, "gate_rows", "gate_rows index outside the gate")
     else:
         gr = segment_row_map(rows, gate_rows, dev)
         if rows and max(int(r) for _, _, r in gate_rows) >= g.shape[0]:
@@ -645,7 +695,7 @@ def int8_linear_gated_residual_(residual: torch.Tensor, x: torch.Tensor, weight:
         q, xs = quantize_int8_rowwise_convrot(x2, convrot_groupsize, input_act)
     else:
         q, xs = quantize_int8_rowwise(x2, input_act=input_act)
-    q2, w2, k = _pad_k(q, weight.contiguous())
+    q2, w2, k = _pad_k(q, weight)
     with torch.cuda.device(dev):
         call("mxq_int8_gemm_gated_residual", _p(q2), _p(w2), _p(xs), _p(ws), ws.numel(), _p(b), _p(res2),
              res2.stride(0), _p(g), g.stride(0), g.shape[0], _p(gr), rows, n, k, _stream(dev))
