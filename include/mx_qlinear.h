@@ -3,9 +3,9 @@
  *
  * One shared library, libmx_qlinear.so, built by hipcc for gfx950 only. Every entry
  * point takes raw device pointers, element counts and a hipStream_t passed as void*,
- * enqueues its kernels on that stream and returns without synchronising. Nothing
- * allocates device memory except mxq_w4a8_codebook_gemm's caller-provided workspace
- * contract (the caller allocates it). Return value: MXQ_OK (0) or a negative error
+ * enqueues its kernels on that stream and returns without synchronising. No entry point
+ * allocates device memory: workspaces are the caller's (mxq_w4a8_codebook_gemm) or a static
+ * device array of the library (mxq_w4a8_codebook_gemm_noalloc). Return value: MXQ_OK (0) or a negative error
  * code; mxq_last_error() then describes the failure (thread-local string).
  *
  * Reference paths are relative to the reference tree; CK stands for
@@ -264,6 +264,21 @@ int mxq_w4a8_codebook_gemm(const int8_t* xq, const int8_t* qdata, const void* s_
                            const float* xs, const void* bias, int8_t* workspace, void* out,
                            int64_t M, int64_t N, int64_t K, int64_t group_size,
                            int64_t chunk_cols, int out_dtype, void* stream);
+
+/*
+ * mxq_w4a8_codebook_gemm without the caller's workspace: the decoded chunk lives in a static
+ * device array of the library (32 MiB per GPU, held until the process ends), so the call
+ * allocates nothing. No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments and results (bit for bit) as mxq_w4a8_codebook_gemm, less
+ * `workspace`; min(chunk_cols, N) * K must not exceed 32 MiB (MXQ_ERR_INVALID otherwise).
+ * Calls share the GPU's array: two calls that overlap on one GPU (different streams) race.
+ */
+int mxq_w4a8_codebook_gemm_noalloc(const int8_t* xq, const int8_t* qdata, const void* s_rel,
+                                   int s_rel_dtype, const float* codebook, const float* s_channel,
+                                   const float* xs, const void* bias, void* out, int64_t M, int64_t N,
+                                   int64_t K, int64_t group_size, int64_t chunk_cols, int out_dtype,
+                                   void* stream);
 
 /*
  * Grouped-scale W4A8 GEMM (int4 weights with one fp16 scale per K-group and output channel):

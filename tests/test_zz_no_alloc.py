@@ -1,0 +1,68 @@
+"""GPU parity of the allocation-free W4A8 entry point (mxq_w4a8_codebook_gemm_noalloc) against
+the entry point it varies (mxq_w4a8_codebook_gemm with a caller workspace), called through the
+C ABI: two calls in a row, the second smaller, then a chunk too large for the static workspace.
+
+Bar: outputs bit-identical to the workspace entry point's on every call.
+"""
+
+import pytest
+import torch
+
+from _util import activations, bf16_vec, gen, packed_int4
+
+pytestmark = pytest.mark.gpu
+
+
+def _call_pair(dev, m, n, k, g, e4m3, codebook, bias, chunk, seed):
+    import mx_qlinear
+    from mx_qlinear import _lib
+    from mx_qlinear.ops import _p, _stream
+
+    print(f"no-alloc w4a8 m={m} n={n} k={k} g={g} e4m3={e4m3} codebook={codebook} chunk={chunk}", flush=True)
+    x = activations(m, k, seed).to(dev)
+    xq, xs = mx_qlinear.quantize_int8_rowwise(x)
+    qd = packed_int4(n, k, seed + 1).to(dev)
+    srel = torch.rand(n, k // g, generator=gen(seed + 2)) * 0.75 + 0.25
+    if e4m3:
+        sr, code = srel.to(torch.float8_e4m3fn).view(torch.uint8).to(dev), _lib.DTYPE_E4M3
+    else:
+        sr, code = srel.to(dev), _lib.DTYPE_F32
+    cb = (torch.randn(16, generator=gen(seed + 3)) * 4).to(dev) if codebook else None
+    sch = (torch.rand(n, generator=gen(seed + 4)) * 0.5 + 0.5).to(dev) * (0.06 / 127)
+    b = bf16_vec(n, seed + 5, 0.01).to(dev) if bias else None
+    want = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=dev)
+    got = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=dev)
+    work = torch.empty((min(chunk, n), k), dtype=torch.int8, device=dev)
+    st = _stream(dev)
+    _lib.call("mxq_w4a8_codebook_gemm", _p(xq), _p(qd), _p(sr), code, _p(cb), _p(sch), _p(xs), _p(b), _p(work),
+              _p(want), m, n, k, g, chunk, _lib.DTYPE_BF16, st)
+    _lib.call("mxq_w4a8_codebook_gemm_noalloc", _p(xq), _p(qd), _p(sr), code, _p(cb), _p(sch), _p(xs), _p(b),
+              _p(got), m, n, k, g, chunk, _lib.DTYPE_BF16, st)
+    torch.cuda.synchronize()
+    assert not bool(torch.isnan(want).any())
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_noalloc_matches_workspace_entry_two_calls(dev):
+    # first call: several chunks, e4m3 scales, codebook, bias
+    _call_pair(dev, 300, 5000, 1024, 16, True, True, True, 2048, 7001)
+    # second call, smaller: one chunk, fp32 scales, no codebook, no bias; the array keeps the
+    # first call's decode beyond this one's chunk, which must not leak into the result
+    _call_pair(dev, 64, 700, 512, 16, False, False, False, 4096, 7002)
+
+
+def test_noalloc_rejects_a_chunk_beyond_the_static_workspace(dev):
+    from mx_qlinear import _lib
+    from mx_qlinear.ops import _p, _stream
+
+    m, n, k, g = 8, 8192, 8192, 16
+    xq = torch.zeros((m, k), dtype=torch.int8, device=dev)
+    xs = torch.ones(m, dtype=torch.float32, device=dev)
+    qd = torch.zeros((n, k // 2), dtype=torch.int8, device=dev)
+    sr = torch.ones((n, k // g), dtype=torch.float32, device=dev)
+    sch = torch.ones(n, dtype=torch.float32, device=dev)
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    # 4096 x 8192 = 32 MiB fits; 4097 columns do not (the check runs before any launch)
+    with pytest.raises(ValueError, match="static workspace"):
+        _lib.call("mxq_w4a8_codebook_gemm_noalloc", _p(xq), _p(qd), _p(sr), _lib.DTYPE_F32, None, _p(sch), _p(xs),
+                  None, _p(out), m, n, k, g, 4097, _lib.DTYPE_BF16, _stream(dev))

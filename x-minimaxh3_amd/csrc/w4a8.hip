@@ -25,6 +25,7 @@
 //    unscaled recipe while the unpack costs 6 ALU ops per 8 weights.
 
 #include <algorithm>
+#include <mutex>
 
 #include "w4a8_common.h"
 
@@ -305,26 +306,21 @@ extern "C" int mxq_int8_gemm_dequant(const int8_t* a, const int8_t* b, const flo
                                      int64_t M, int64_t N, int64_t K, int64_t ldd, int out_dtype,
                                      void* stream);
 
-extern "C" int mxq_w4a8_codebook_gemm(const int8_t* xq, const int8_t* qdata, const void* s_rel,
-                                      int s_rel_dtype, const float* codebook,
-                                      const float* s_channel, const float* xs, const void* bias,
-                                      int8_t* workspace, void* out, int64_t M, int64_t N,
-                                      int64_t K, int64_t group_size, int64_t chunk_cols,
-                                      int out_dtype, void* stream) {
-  int rc = check_decode_args(qdata, s_rel, s_rel_dtype, N, K, group_size);
-  if (rc) return rc;
-  if (M < 0) return mxq_set_error(MXQ_ERR_INVALID, "negative M");
-  if (M == 0 || N == 0) return MXQ_OK;
-  if (chunk_cols <= 0) return mxq_set_error(MXQ_ERR_INVALID, "chunk_cols must be positive");
-  if (!workspace || !out || !s_channel || !xs) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+// Decode-then-GEMM over column chunks of chunk_cols weights rows, the decoded chunk in
+// `workspace` ([chunk_cols, K] int8). Arguments are validated by the callers.
+static int codebook_gemm_chunks(const int8_t* xq, const int8_t* qdata, const void* s_rel, int s_rel_dtype,
+                                const float* codebook, const float* s_channel, const float* xs,
+                                const void* bias, int8_t* workspace, void* out, int64_t M, int64_t N,
+                                int64_t K, int64_t group_size, int64_t chunk_cols, int out_dtype,
+                                void* stream) {
   const int osz = out_dtype == MXQ_DTYPE_F32 ? 4 : 2;
   const int64_t groups = K / group_size;
   const int sbytes = s_rel_dtype == MXQ_DTYPE_E4M3 ? 1 : 4;
   hipStream_t st = (hipStream_t)stream;
   for (int64_t n0 = 0; n0 < N; n0 += chunk_cols) {
     const int64_t cols = chunk_cols < N - n0 ? chunk_cols : N - n0;
-    rc = decode_launch(qdata + n0 * (K / 2), (const char*)s_rel + n0 * groups * sbytes,
-                       s_rel_dtype, codebook, workspace, cols, K, group_size, st);
+    int rc = decode_launch(qdata + n0 * (K / 2), (const char*)s_rel + n0 * groups * sbytes,
+                           s_rel_dtype, codebook, workspace, cols, K, group_size, st);
     if (rc) return rc;
     const void* bias_chunk = bias ? (const char*)bias + n0 * osz : nullptr;
     rc = mxq_int8_gemm_dequant(xq, workspace, xs, s_channel + n0, cols, bias_chunk,
@@ -332,6 +328,90 @@ extern "C" int mxq_w4a8_codebook_gemm(const int8_t* xq, const int8_t* qdata, con
     if (rc) return rc;
   }
   return MXQ_OK;
+}
+
+static int check_codebook_gemm(const int8_t* qdata, const void* s_rel, int s_rel_dtype,
+                               const float* s_channel, const float* xs, const void* out, int64_t M,
+                               int64_t N, int64_t K, int64_t group_size, int64_t chunk_cols) {
+  int rc = check_decode_args(qdata, s_rel, s_rel_dtype, N, K, group_size);
+  if (rc) return rc;
+  if (M < 0) return mxq_set_error(MXQ_ERR_INVALID, "negative M");
+  if (M == 0 || N == 0) return MXQ_OK;
+  if (chunk_cols <= 0) return mxq_set_error(MXQ_ERR_INVALID, "chunk_cols must be positive");
+  if (!out || !s_channel || !xs) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  return MXQ_OK;
+}
+
+extern "C" int mxq_w4a8_codebook_gemm(const int8_t* xq, const int8_t* qdata, const void* s_rel,
+                                      int s_rel_dtype, const float* codebook,
+                                      const float* s_channel, const float* xs, const void* bias,
+                                      int8_t* workspace, void* out, int64_t M, int64_t N,
+                                      int64_t K, int64_t group_size, int64_t chunk_cols,
+                                      int out_dtype, void* stream) {
+  int rc = check_codebook_gemm(qdata, s_rel, s_rel_dtype, s_channel, xs, out, M, N, K, group_size, chunk_cols);
+  if (rc || M == 0 || N == 0) return rc;
+  if (!workspace) return mxq_set_error(MXQ_ERR_INVALID, "null workspace");
+  return codebook_gemm_chunks(xq, qdata, s_rel, s_rel_dtype, codebook, s_channel, xs, bias, workspace, out, M, N,
+                              K, group_size, chunk_cols, out_dtype, stream);
+}
+
+// ---- allocation-free variant ----------------------------------------------------------
+// The decode workspace of mxq_w4a8_codebook_gemm_noalloc is this file-scope array: each GPU the
+// library runs on holds its own copy (kNoAllocScratchBytes) until the process ends. Host code
+// never passes `scratch` itself to a kernel (in host code the name is a host-side stand-in, not a
+// device address): the device address is looked up once per device with hipGetSymbolAddress and
+// kept in g_scratch_ptr. Every call on one GPU reuses that GPU's array; the decode overwrites
+// every byte a GEMM reads, so nothing needs clearing between calls, and two calls that overlap on
+// one GPU (two streams) race on it.
+constexpr int64_t kNoAllocScratchBytes = int64_t(32) << 20;
+static __device__ __attribute__((aligned(256))) int8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+int8_t* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of the current device's scratch array (looked up on the first call per device).
+int current_device_scratch(int8_t** ptr) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return mxq_set_error(MXQ_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(err));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return mxq_set_error(MXQ_ERR_UNSUPPORTED, "device ordinal %d outside the %d the library tracks", dev,
+                         kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr)
+      return mxq_set_error(MXQ_ERR_HIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                           hipGetErrorString(err));
+    g_scratch_ptr[dev] = static_cast<int8_t*>(p);
+  }
+  *ptr = g_scratch_ptr[dev];
+  return MXQ_OK;
+}
+}  // namespace
+
+extern "C" int mxq_w4a8_codebook_gemm_noalloc(const int8_t* xq, const int8_t* qdata, const void* s_rel,
+                                              int s_rel_dtype, const float* codebook,
+                                              const float* s_channel, const float* xs, const void* bias,
+                                              void* out, int64_t M, int64_t N, int64_t K, int64_t group_size,
+                                              int64_t chunk_cols, int out_dtype, void* stream) {
+  int rc = check_codebook_gemm(qdata, s_rel, s_rel_dtype, s_channel, xs, out, M, N, K, group_size, chunk_cols);
+  if (rc || M == 0 || N == 0) return rc;
+  const int64_t cols = chunk_cols < N ? chunk_cols : N;
+  if (cols > kNoAllocScratchBytes / K)
+    return mxq_set_error(MXQ_ERR_INVALID,
+                         "decode chunk of %lld x %lld int8 exceeds the %lld-byte static workspace; use at most "
+                         "%lld columns per chunk",
+                         (long long)cols, (long long)K, (long long)kNoAllocScratchBytes,
+                         (long long)(kNoAllocScratchBytes / K));
+  int8_t* ws = nullptr;
+  rc = current_device_scratch(&ws);
+  if (rc) return rc;
+  return codebook_gemm_chunks(xq, qdata, s_rel, s_rel_dtype, codebook, s_channel, xs, bias, ws, out, M, N, K,
+                              group_size, chunk_cols, out_dtype, stream);
 }
 
 static int check_grouped(const int8_t* a, const float* xs, const int8_t* qdata, const uint16_t* group_scale,
