@@ -43,6 +43,34 @@ MXQ_DEVICE v2u quant8_bf16(v4u w, float r) {
   return o;
 }
 
+// The same for a row whose absmax is finite. Then |bf16(v * r)| <= 127.5 (r = 1 / bf16(s) and
+// bf16(s) is within 2^-8 of amax / 127), so the lower clamp never acts and the upper one is a
+// min with 127 before rounding; the rounding to an integer is one fp32 addition of 1.5 * 2^23
+// (an exact sum rounded half to even) whose low byte is the two's complement int8.
+MXQ_DEVICE uint32_t quant_byte_finite(float v) {
+  return __float_as_uint(fminf(v, 127.0f) + 12582912.0f);
+}
+
+MXQ_DEVICE v2u quant8_bf16_finite(v4u w, float r) {
+  uint32_t b[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t p = pack_bf16x2(bf16_lo(w[i]) * r, bf16_hi(w[i]) * r);
+    b[2 * i] = quant_byte_finite(bf16_lo(p));
+    b[2 * i + 1] = quant_byte_finite(bf16_hi(p));
+  }
+  v2u o;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t lo = __builtin_amdgcn_perm(b[4 * h + 1], b[4 * h], 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(b[4 * h + 3], b[4 * h + 2], 0x0c0c0400u);
+    o[h] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+  }
+  return o;
+}
+
+MXQ_DEVICE bool finite_absmax(float amax) { return __float_as_uint(amax) < 0x7F800000u; }
+
 MXQ_DEVICE uint32_t gelu_pair(uint32_t w) {
   return gelu_bf16(w & 0xFFFFu) | (gelu_bf16(w >> 16) << 16);
 }
@@ -60,27 +88,37 @@ __global__ __launch_bounds__(kQuantBlock) void quant_rows_bf16_reg(
     const v4u* src = reinterpret_cast<const v4u*>(x + row * cols);
     v4u v[NCH];
     uint32_t m = 0;
+    // All of the row's loads are issued before any is used (a chunk past the row end re-reads
+    // the row's last chunk and is masked below): with a load inside a branch the compiler waited
+    // for each load before issuing the next.
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) v[j] = __builtin_nontemporal_load(src + min(lane + j * kWave, nchunk - 1));
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
-      const int c = lane + j * kWave;
-      if (c < nchunk) {
-        v[j] = __builtin_nontemporal_load(src + c);
-        if (kGelu) {
+      const bool ok = lane + j * kWave < nchunk;
+      if (kGelu) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) v[j][i] = gelu_pair(v[j][i]);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) m = absmax_acc_bf16x2(m, v[j][i]);
+        for (int i = 0; i < 4; ++i) v[j][i] = gelu_pair(v[j][i]);
       }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m = ok ? absmax_acc_bf16x2(m, v[j][i]) : m;
     }
     const float amax = wave_absmax(absmax_bits_of_bf16x2(m));
     const float s = row_scale_from_absmax(amax);
     const float r = 1.0f / round_bf16(s);
     v2u* dst = reinterpret_cast<v2u*>(q + row * cols);
+    if (finite_absmax(amax)) {
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int c = lane + j * kWave;
-      if (c < nchunk) __builtin_nontemporal_store(quant8_bf16(v[j], r), dst + c);
+      for (int j = 0; j < NCH; ++j) {
+        const int c = lane + j * kWave;
+        if (c < nchunk) __builtin_nontemporal_store(quant8_bf16_finite(v[j], r), dst + c);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int c = lane + j * kWave;
+        if (c < nchunk) __builtin_nontemporal_store(quant8_bf16(v[j], r), dst + c);
+      }
     }
     if (lane == 0) scales[row] = s;
   }
@@ -137,24 +175,35 @@ __global__ __launch_bounds__(kQuantBlock) void quant_rows_generic(
 // issuing kBatch loads before their stores so that up to kBatch x 4 KB of a row are in flight.
 constexpr int kAbsmaxBatch = 10;
 
+// One row's pass: kFinite selects the quantization of a row whose absmax is finite.
+template <bool kFinite>
+MXQ_DEVICE void absmax_row_pass(const v4u* __restrict__ src, v2u* __restrict__ dst, int chunks, float r, int t) {
+  auto quant = [&](v4u w) { return kFinite ? quant8_bf16_finite(w, r) : quant8_bf16(w, r); };
+  int c = t;
+  for (; c + (kAbsmaxBatch - 1) * 256 < chunks; c += kAbsmaxBatch * 256) {
+    v4u w[kAbsmaxBatch];
+#pragma unroll
+    for (int u = 0; u < kAbsmaxBatch; ++u) w[u] = __builtin_nontemporal_load(src + c + u * 256);
+#pragma unroll
+    for (int u = 0; u < kAbsmaxBatch; ++u) __builtin_nontemporal_store(quant(w[u]), dst + c + u * 256);
+  }
+  for (; c < chunks; c += 256) __builtin_nontemporal_store(quant(__builtin_nontemporal_load(src + c)), dst + c);
+}
+
 __global__ __launch_bounds__(256) void quant_rows_bf16_absmax(
     const uint16_t* __restrict__ x, const float* __restrict__ row_absmax,
     int8_t* __restrict__ q, float* __restrict__ scales, int64_t rows, int chunks_per_row) {
   const int t = threadIdx.x;
   for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
-    const float s = row_scale_from_absmax(row_absmax[row]);
+    const float amax = row_absmax[row];
+    const float s = row_scale_from_absmax(amax);
     const float r = 1.0f / round_bf16(s);
     const v4u* src = reinterpret_cast<const v4u*>(x + row * (int64_t)chunks_per_row * 8);
     v2u* dst = reinterpret_cast<v2u*>(q + row * (int64_t)chunks_per_row * 8);
-    int c = t;
-    for (; c + (kAbsmaxBatch - 1) * 256 < chunks_per_row; c += kAbsmaxBatch * 256) {
-      v4u w[kAbsmaxBatch];
-#pragma unroll
-      for (int u = 0; u < kAbsmaxBatch; ++u) w[u] = __builtin_nontemporal_load(src + c + u * 256);
-#pragma unroll
-      for (int u = 0; u < kAbsmaxBatch; ++u) __builtin_nontemporal_store(quant8_bf16(w[u], r), dst + c + u * 256);
-    }
-    for (; c < chunks_per_row; c += 256) __builtin_nontemporal_store(quant8_bf16(__builtin_nontemporal_load(src + c), r), dst + c);
+    if (finite_absmax(amax))
+      absmax_row_pass<true>(src, dst, chunks_per_row, r, t);
+    else
+      absmax_row_pass<false>(src, dst, chunks_per_row, r, t);
     if (t == 0) scales[row] = s;
   }
 }
@@ -292,6 +341,134 @@ __global__ __launch_bounds__(kQuantBlock) void adaln_rows_reg(
                                       reinterpret_cast<const v4u*>(shift + (row / shift_group) * cols), eps, q,
                                       scales, y_out, row, cols, lane);
     }
+  }
+}
+
+// adaLN with one modulation row for every row (the common case: one sample per launch). One wave
+// per row, rows taken grid-stride by the launch's waves; each wave loads its next row into a
+// second register buffer before it processes the current one, so a row's HBM latency overlaps
+// the previous row's arithmetic. t = bf16(1 + scale) and shift are staged once per workgroup in
+// LDS as fp32 (cols * 8 bytes of dynamic LDS). The statistics and the modulation are the same
+// operations, in the same order, as adaln_row's; rows whose absmax is finite are quantized by
+// the finite-row path.
+// Both bf16 halves of w as fp32, as an inline-asm pair: the compiler cannot reuse an earlier
+// unpack of the same word, which would keep a row's unpacked values live (twice the registers of
+// the packed row) from one pass to the next.
+MXQ_DEVICE void unpack_fresh(uint32_t w, float& lo, float& hi) {
+  __asm__ volatile("v_lshlrev_b32 %0, 16, %2\n\tv_and_b32 %1, 0xffff0000, %2" : "=&v"(lo), "=v"(hi) : "v"(w));
+}
+
+template <int NCH, bool kQuant, bool kExact>
+__global__ __launch_bounds__(kQuantBlock) __attribute__((amdgpu_waves_per_eu(kExact && NCH <= 10 ? 3 : 2))) void adaln_uniform_rows(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ scale, const uint16_t* __restrict__ shift,
+    float eps, int8_t* __restrict__ q, float* __restrict__ scales, uint16_t* __restrict__ y_out, int64_t rows,
+    int cols) {
+  extern __shared__ __attribute__((aligned(16))) float s_mod[];
+  float* s_t = s_mod;
+  float* s_sh = s_mod + cols;
+  for (int c = threadIdx.x; c < cols; c += kQuantBlock) {
+    s_t[c] = round_bf16(1.0f + bf16_to_f32(scale[c]));
+    s_sh[c] = bf16_to_f32(shift[c]);
+  }
+  __syncthreads();
+  const int lane = threadIdx.x % kWave;
+  const int nchunk = kExact ? NCH * kWave : cols / 8;  // kExact: cols == NCH * 512
+  const int64_t stride = (int64_t)gridDim.x * (kQuantBlock / kWave);
+  int64_t row = (int64_t)blockIdx.x * (kQuantBlock / kWave) + threadIdx.x / kWave;
+
+  // Loads are unconditional (a chunk past the row end re-reads the row's last chunk and is masked
+  // out of the statistics, the absmax and the stores): a load inside a branch made the compiler
+  // wait for every earlier load before issuing it.
+  auto load = [&](v4u (&v)[NCH], int64_t r) {
+    const v4u* src = reinterpret_cast<const v4u*>(x + r * cols);
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) v[j] = __builtin_nontemporal_load(src + min(lane + j * kWave, nchunk - 1));
+  };
+  auto process = [&](v4u (&v)[NCH], int64_t r) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const bool ok = kExact || lane + j * kWave < nchunk;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sum += ok ? bf16_lo(v[j][i]) + bf16_hi(v[j][i]) : 0.0f;
+    }
+    const float mean = wave_sum(sum) / (float)cols;
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const bool ok = kExact || lane + j * kWave < nchunk;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float xl, xh;
+        unpack_fresh(v[j][i], xl, xh);
+        const float a = ok ? xl - mean : 0.0f, b = ok ? xh - mean : 0.0f;
+        ss += a * a;
+        ss += b * b;
+      }
+    }
+    const float var = wave_sum(ss) / (float)cols;
+    const float rstd = 1.0f / sqrtf(var + eps);
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = min(lane + j * kWave, nchunk - 1);
+      const bool ok = kExact || lane + j * kWave < nchunk;
+      {
+        const v4f t0 = reinterpret_cast<const v4f*>(s_t)[2 * c], t1 = reinterpret_cast<const v4f*>(s_t)[2 * c + 1];
+        const v4f h0 = reinterpret_cast<const v4f*>(s_sh)[2 * c], h1 = reinterpret_cast<const v4f*>(s_sh)[2 * c + 1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float tl = i < 2 ? t0[2 * i] : t1[2 * i - 4], th = i < 2 ? t0[2 * i + 1] : t1[2 * i - 3];
+          const float hl = i < 2 ? h0[2 * i] : h1[2 * i - 4], hh = i < 2 ? h0[2 * i + 1] : h1[2 * i - 3];
+          float xl, xh;
+          unpack_fresh(v[j][i], xl, xh);
+          const uint32_t n = pack_bf16x2((xl - mean) * rstd, (xh - mean) * rstd);
+          const uint32_t p = pack_bf16x2(bf16_lo(n) * tl, bf16_hi(n) * th);
+          v[j][i] = pack_bf16x2(bf16_lo(p) + hl, bf16_hi(p) + hh);
+          m = ok ? absmax_acc_bf16x2(m, v[j][i]) : m;
+        }
+        if (y_out != nullptr && ok) __builtin_nontemporal_store(v[j], reinterpret_cast<v4u*>(y_out + r * cols) + c);
+      }
+      // one chunk's modulation at a time: the LDS reads of later chunks are not hoisted, which
+      // would hold every chunk's t and shift in registers at once
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (kQuant) {
+      const float amax = wave_absmax(absmax_bits_of_bf16x2(m));
+      const float s = row_scale_from_absmax(amax);
+      const float rcp = 1.0f / round_bf16(s);
+      v2u* dst = reinterpret_cast<v2u*>(q + r * cols);
+      if (finite_absmax(amax)) {
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) {
+          const int c = lane + j * kWave;
+          if (c < nchunk) __builtin_nontemporal_store(quant8_bf16_finite(v[j], rcp), dst + c);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) {
+          const int c = lane + j * kWave;
+          if (c < nchunk) __builtin_nontemporal_store(quant8_bf16(v[j], rcp), dst + c);
+        }
+      }
+      if (lane == 0) scales[r] = s;
+    }
+  };
+
+  // The next row's loads are unconditional (past the last row they re-read row rows - 1), so the
+  // compiler's wait for the current row counts exactly the next row's loads as still in flight.
+  v4u a[NCH], b[NCH];
+  if (row < rows) load(a, row);
+  while (row < rows) {
+    const int64_t r1 = row + stride;
+    load(b, min(r1, rows - 1));
+    process(a, row);
+    row = r1;
+    if (row >= rows) break;
+    const int64_t r2 = row + stride;
+    load(a, min(r2, rows - 1));
+    process(b, row);
+    row = r2;
   }
 }
 
@@ -441,6 +618,39 @@ static int adaln_launch(const void* x, const void* scale, const void* shift, int
     return mxq_set_error(MXQ_ERR_UNSUPPORTED,
                          "adaLN needs cols %% 8 == 0, cols <= 8192 and 16-byte aligned rows");
   hipStream_t st = (hipStream_t)stream;
+  const int64_t need = (cols / 8 + kWave - 1) / kWave;
+  const int uch = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : need <= 6 ? 6 : need <= 8 ? 8 : need <= 10 ? 10
+                : need <= 11 ? 11 : need <= 12 ? 12 : need <= 14 ? 14 : 16;
+  if (scale_group >= rows && shift_group >= rows && cols <= kAdalnMaxCols && (cols == uch * 512 || uch <= 12)) {
+    // one modulation row: the two-buffer kernel (widths whose register budget it fits)
+    const size_t lds = (size_t)cols * 2 * sizeof(float);
+    const int64_t wg = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    const unsigned grid = (unsigned)(wg < 1024 ? wg : 1024);
+#define MXQ_ADALN_UNIFORM_K(N_, E_)                                                                              \
+  (quant ? (void)(adaln_uniform_rows<N_, true, E_><<<grid, kQuantBlock, lds, st>>>(                              \
+               (const uint16_t*)x, (const uint16_t*)scale, (const uint16_t*)shift, eps, q, scales,              \
+               (uint16_t*)y_out, rows, (int)cols))                                                               \
+         : (void)(adaln_uniform_rows<N_, false, E_><<<grid, kQuantBlock, lds, st>>>(                             \
+               (const uint16_t*)x, (const uint16_t*)scale, (const uint16_t*)shift, eps, nullptr, nullptr,        \
+               (uint16_t*)y_out, rows, (int)cols)))
+#define MXQ_ADALN_UNIFORM(N_) \
+  (cols == (N_) * 512 ? MXQ_ADALN_UNIFORM_K(N_, true) : MXQ_ADALN_UNIFORM_K(N_, false))
+    switch (uch) {
+      case 1: MXQ_ADALN_UNIFORM(1); break;
+      case 2: MXQ_ADALN_UNIFORM(2); break;
+      case 4: MXQ_ADALN_UNIFORM(4); break;
+      case 6: MXQ_ADALN_UNIFORM(6); break;
+      case 8: MXQ_ADALN_UNIFORM(8); break;
+      case 10: MXQ_ADALN_UNIFORM(10); break;
+      case 11: MXQ_ADALN_UNIFORM(11); break;
+      case 12: MXQ_ADALN_UNIFORM(12); break;
+      case 14: MXQ_ADALN_UNIFORM(14); break;
+      default: MXQ_ADALN_UNIFORM(16); break;
+    }
+#undef MXQ_ADALN_UNIFORM
+#undef MXQ_ADALN_UNIFORM_K
+    return mxq_check_launch("adaln_uniform_rows");
+  }
   if (quant) {
     MXQ_NCH_SWITCH_16(nch, (adaln_rows_reg<N_, true><<<adaln_grid(rows), kQuantBlock, 0, st>>>(
                              (const uint16_t*)x, (const uint16_t*)scale, (const uint16_t*)shift,
