@@ -95,6 +95,44 @@ class Timer:
 # ----------------------------------------------------------------------------------------
 # workloads
 # ----------------------------------------------------------------------------------------
+def mfma_ceiling(a, b, dev, workgroups=256, iters=100000):
+    """Sustained v_mfma_i32_32x32x32_i8 rate on the workload's own int8 operands with registers
+    only (mxq_probe_mfma_i8: one workgroup of four waves per CU, no memory traffic), and the
+    shader clock it ran at. The board power limit lowers the clock as the operand bits toggle,
+    so this is the MFMA peak a GEMM on this data can reach on this GPU."""
+    a = a.reshape(-1)[: 1 << 20].contiguous()
+    b = b.reshape(-1)[: 1 << 20].contiguous()
+    sink = torch.empty(workgroups * 256, dtype=torch.int32, device=dev)
+    clocks = torch.zeros(workgroups * 2, dtype=torch.int64, device=dev)
+    st = _stream(dev)
+
+    def launch(n):
+        _lib.call("mxq_probe_mfma_i8", _p(a), a.numel(), _p(b), b.numel(), _p(sink), _p(clocks), workgroups, n, st)
+
+    launch(iters // 5)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    launch(iters)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    c = clocks.view(-1, 2).double()
+    ops = 2.0 * 32 * 32 * 32 * 8 * iters * 4 * workgroups
+    return {"value": round(ops / (ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s",
+            "clock_mhz": round((c[:, 0].sum() / c[:, 1].sum()).item() * 100.0),
+            "what": "register-only v_mfma_i32_32x32x32_i8 loop on this kernel's own int8 operands "
+                    "(mxq_probe_mfma_i8, 256 workgroups x 4 waves): the power-limited MFMA ceiling for this data"}
+
+
+def _w4_mfma_operand(qdata_prepared):
+    """The int8 values the group-128 W4A8 kernel feeds the MFMAs: each nibble of the prepared
+    layout as 16 * (c - 8) (the high half of a byte)."""
+    w = qdata_prepared.reshape(-1)[: 1 << 19].view(torch.uint8).to(torch.int32)
+    lo, hi = (w << 4) & 0xF0, w & 0xF0
+    return torch.stack([lo, hi], dim=-1).reshape(-1).to(torch.uint8).view(torch.int8)
+
+
 
 class FfnWorkload:
     name = "int8_ffn_gelu_720p"
@@ -141,6 +179,9 @@ class FfnWorkload:
         fc2 = {"span": "fc2_gemm", "symbol": "gemm_i8_kernel<1, 2, 256>", "ops": 2 * m * k * h,
                "bytes": m * h + k * h + 2 * m * k + 4 * m + 4 * k + 2 * k}
         return max((fc1, fc2), key=lambda d: timer.mean_ms(d["span"]))
+
+    def probe_operands(self, span):
+        return (self.ws.xq, self.w1) if span == "fc1_gemm" else (self.ws.hq, self.w2)
 
     def config(self):
         return {"workload": self.name, "tokens": self.m, "d_model": self.k, "d_ff": self.hidden,
@@ -205,6 +246,9 @@ class QkvWorkload:
         m, k, n = self.m, self.k, self.n
         return {"span": "qkv_gemm", "symbol": "gemm_i8_kernel<1, 2, 256>", "ops": 2 * m * n * k,
                 "bytes": m * k + n * k + 2 * m * n + 4 * m + 4 * n + 2 * n}
+
+    def probe_operands(self, span):
+        return self.xq, self.w
 
     def config(self):
         return {"workload": self.name, "tokens": self.m, "d_model": self.k, "qkv_out": self.n,
@@ -296,6 +340,12 @@ class W4A8Workload:
         return {"span": "w4a8_gemm", "symbol": sym, "ops": self.ops_per_step(),
                 "bytes": self.gemm_bytes()}
 
+    def probe_operands(self, span):
+        x, xq, _, _, wg, _ = self.sets[0]
+        if xq is None:
+            xq, _ = mx_qlinear.quantize_int8_rowwise(x)
+        return xq, (_w4_mfma_operand(wg) if self.prepared else None)
+
     def config(self):
         return {"workload": self.name, "m": self.m, "n": self.n, "k": self.k, "group": self.g,
                 "input": "bf16 activations, per-token quant inside the step" if self.from_bf16
@@ -371,6 +421,9 @@ class LinearC1Workload:
         m, k, n = self.m, self.k, self.n
         return {"span": "gemm", "symbol": "gemm_i8_kernel<1, 2, 128>", "ops": 2 * m * n * k,
                 "bytes": m * k + n * k + 2 * m * n + 4 * m + 4 * n + 2 * n}
+
+    def probe_operands(self, span):
+        return self.xq, self.sets[0][1]
 
     def config(self):
         return {"workload": self.name, "m": self.m, "n": self.n, "k": self.k,
@@ -471,6 +524,9 @@ class H3MlpWorkload:
                "bytes": m * f + d * f + 4 * m * d + 4 * m + 4 * m + 4 * d + 2 * d + 6 * d}
         return max((fc1, fc2), key=lambda x: timer.mean_ms(x["span"]))
 
+    def probe_operands(self, span):
+        return (self.q1, self.fc1.qweight) if span == "fc1_swiglu_gemm" else (self.q2, self.w2)
+
     def config(self):
         return {"workload": self.name, "tokens": self.m, "d_model": self.d, "swiglu_inner": self.inner,
                 "norm": "rms_adaln eps 1e-6, 3 segments", "convrot_group": 256,
@@ -532,6 +588,9 @@ class H3QkvWorkload:
         return {"span": "qkv_gemm", "symbol": "gemm_i8_kernel<1, 2, 256>", "ops": 2 * m * n * d,
                 "bytes": m * d + n * d + 2 * m * n + 4 * m + 4 * n + 2 * n}
 
+    def probe_operands(self, span):
+        return self.q, self.w
+
     def config(self):
         return {"workload": self.name, "tokens": self.m, "d_model": self.d, "qkv_out": self.n,
                 "norm": "rms_adaln eps 1e-6, 3 segments", "convrot_group": 256}
@@ -569,10 +628,12 @@ class W4A8RefQkvWorkload:
     def __init__(self, dev, m=75600, d=H3_D, n=3 * H3_ATTN, g=16):
         self.m, self.d, self.n, self.g = m, d, n, g
         self.x = make_activations(m, d, dev, 60)
-        self.qdata = torch.randint(-128, 128, (n, d // 2), generator=_gen(dev, 61), device=dev, dtype=torch.int8)
-        srel = torch.rand(n, d // g, generator=_gen(dev, 62), device=dev) * 0.75 + 0.25
-        self.s_rel = srel.to(torch.float8_e4m3fn).view(torch.uint8)
-        self.s_ch = (torch.rand(n, generator=_gen(dev, 63), device=dev) * 0.5 + 0.5) * (0.06 / 127)
+        # W4A8 storage made the way the reference makes it: an N(0, 0.02) bf16 weight rotated and
+        # quantized by quantize_w4a8_int8_weight (group 16, the 16-level codebook, e4m3 s_rel)
+        wf = (torch.randn(n, d, generator=_gen(dev, 61), device=dev) * 0.02).to(torch.bfloat16)
+        self.qdata, s_rel, self.s_ch, _, self.codebook = mx_qlinear.quantize_w4a8_int8_weight(wf, g, 256)
+        self.s_rel = s_rel.view(torch.uint8)
+        del wf
         self.b = make_bias(n, dev, 64)
         self.q = torch.empty(m, d, dtype=torch.int8, device=dev)
         self.xs = torch.empty(m, dtype=torch.float32, device=dev)
@@ -586,9 +647,9 @@ class W4A8RefQkvWorkload:
         if timer is None:
             _lib.call("mxq_quantize_int8_rowwise_convrot", _p(self.x), _lib.DTYPE_BF16, _p(self.q), _p(self.xs), m, d,
                       256, _lib.ACT_NONE, st)
-            _lib.call("mxq_w4a8_codebook_gemm", _p(self.q), _p(self.qdata), _p(self.s_rel), _lib.DTYPE_E4M3, None,
-                      _p(self.s_ch), _p(self.xs), _p(self.b), _p(self.work), _p(self.out), m, n, d, g, self.chunk,
-                      _lib.DTYPE_BF16, st)
+            _lib.call("mxq_w4a8_codebook_gemm", _p(self.q), _p(self.qdata), _p(self.s_rel), _lib.DTYPE_E4M3,
+                      _p(self.codebook), _p(self.s_ch), _p(self.xs), _p(self.b), _p(self.work), _p(self.out), m, n, d,
+                      g, self.chunk, _lib.DTYPE_BF16, st)
             return
         with timer.span("convrot_quant"):
             _lib.call("mxq_quantize_int8_rowwise_convrot", _p(self.x), _lib.DTYPE_BF16, _p(self.q), _p(self.xs), m, d,
@@ -597,7 +658,7 @@ class W4A8RefQkvWorkload:
             cols = min(self.chunk, n - n0)
             with timer.span("decode"):
                 _lib.call("mxq_dequant_int4_grouped_to_int8", _p(self.qdata[n0:]), _p(self.s_rel[n0:]), _lib.DTYPE_E4M3,
-                          None, _p(self.work), cols, d, g, st)
+                          _p(self.codebook), _p(self.work), cols, d, g, st)
             with timer.span("gemm"):
                 _lib.call("mxq_int8_gemm_dequant", _p(self.q), _p(self.work), _p(self.xs), _p(self.s_ch[n0:]), cols,
                           _p(self.b[n0:]), _p(self.out[:, n0:]), m, cols, d, n, _lib.DTYPE_BF16, st)
@@ -613,9 +674,13 @@ class W4A8RefQkvWorkload:
         return {"span": "gemm", "symbol": "gemm_i8_kernel<1, 2, 256>", "ops": 2 * m * c * d,
                 "bytes": m * d + c * d + 2 * m * c + 4 * m + 4 * c + 2 * c}
 
+    def probe_operands(self, span):
+        return self.q, self.work
+
     def config(self):
         return {"workload": self.name, "tokens": self.m, "d_model": self.d, "qkv_out": self.n,
-                "weights": "int4 codes, e4m3 s_rel per 16, fp32 s_channel (the reference's W4A8 format)",
+                "weights": "int4 codes, e4m3 s_rel per 16, fp32 s_channel, 16-level codebook (the reference's W4A8 "
+                           "format), made from an N(0,0.02) bf16 weight by quantize_w4a8_int8_weight",
                 "convrot_group": 256, "decode_chunk_cols": self.chunk}
 
     def cpu_baseline(self, budget_s):
@@ -624,11 +689,12 @@ class W4A8RefQkvWorkload:
         qd, b = self.qdata.cpu(), self.b.cpu()
         sr = self.s_rel.cpu().view(torch.float8_e4m3fn).float()
         sc = self.s_ch.cpu()
+        cb = self.codebook.cpu()
 
         def run(rows):
             x = self.x[:rows].cpu()
             t0 = time.perf_counter()
-            w8 = eager_torch.dequant_int4_grouped_to_int8(qd, sr, None, self.g)
+            w8 = eager_torch.dequant_int4_grouped_to_int8(qd, sr, cb, self.g)
             eager_torch.int8_linear(x, w8, sc, b, convrot=True)
             return time.perf_counter() - t0
 
@@ -913,6 +979,12 @@ def main():
     roof = {"bound": dom.get("bound", "mfma"), "kernel": f"{dom['symbol']} ({dom['span']})",
             "achieved": round(achieved, 2), "peak": peak, "unit": runit, "frac": round(achieved / peak, 4),
             "traffic": None, "alg_bytes": dom["bytes"], "launch_ms": round(kms, 4)}
+    if roof["bound"] == "mfma" and hasattr(wl, "probe_operands"):
+        a_op, b_op = wl.probe_operands(dom["span"])
+        if a_op is not None and b_op is not None:
+            ceiling = mfma_ceiling(a_op, b_op, dev)
+            roof["measured_peak"] = ceiling
+            roof["frac_of_measured_peak"] = round(achieved / ceiling["value"], 4)
     if not args.no_traffic:
         try:
             traffic, detail = pmc_traffic(args.workload, dom["symbol"])

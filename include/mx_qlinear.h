@@ -327,6 +327,46 @@ int mxq_w4a8_gemm_grouped_prepared(const int8_t* a, const float* xs, const int8_
                                    int64_t N, int64_t K, int64_t group_size, int64_t ldd, int out_dtype,
                                    void* stream);
 
+/* Storage modes of mxq_w4a8_quantize_weight. */
+#define MXQ_W4_CODEBOOK 0     /* symmetric, 16-level codebook (the reference's default) */
+#define MXQ_W4_SYMMETRIC 1    /* symmetric uniform codes c - 8 */
+#define MXQ_W4_ASYMMETRIC 2   /* min/max codes with a correction term */
+#define MXQ_W4_ROTATE_ONLY 3  /* only the ConvRot rotation, written to rotated_out */
+
+/*
+ * Offline W4A8 weight preparation, one launch: ConvRot rotation of each weight row (group
+ * convrot_groupsize, a power of 4, or 0 for none; the exact product rounded once to the weight's
+ * dtype) and the grouped int4 storage of the rotated row:
+ *   w bf16 or fp32 [N, K] (w_dtype); K % 16 == 0, K <= 16384; group_size >= 4 dividing 16 or a
+ *   multiple of 16, at most 128; codebook fp32 [16] (MXQ_W4_CODEBOOK);
+ *   packed int8 [N, K/2] (two codes per byte, even k in the low nibble); s_rel [N, K/G] fp32 or
+ *   float8_e4m3fn bits (s_rel_dtype 0 or 5); s_channel fp32 [N]; correction [K/G, N] of w_dtype
+ *   (MXQ_W4_ASYMMETRIC); rotated_out [N, K] of w_dtype or NULL (the rotated rows).
+ * Semantics: _quantize_rotated_w4a8_int8_weight after the weight rotation,
+ * CK/backends/eager/w4a8_int8.py:122-209 (group sums in torch's CPU order for groups of <= 32).
+ * Replaces: the per-element part of quantize_w4a8_int8_weight (w4a8_int8.py:243-341) and
+ * rotate_int8_convrot_weight (CK/backends/eager/quantization.py:909-912); the codebook choice
+ * (w4a8_int8.py:24-32, 221-240) stays with the caller.
+ */
+int mxq_w4a8_quantize_weight(const void* w, int w_dtype, int64_t N, int64_t K, int64_t group_size,
+                             int64_t convrot_groupsize, int mode, const float* codebook, int s_rel_dtype,
+                             int8_t* packed, void* s_rel, float* s_channel, void* correction, void* rotated_out,
+                             void* stream);
+
+/*
+ * Measurement helper (no counterpart in the reference; it calibrates the roofline): runs
+ * `workgroups` x 256 threads, each lane cycling eight v_mfma_i32_32x32x32_i8 accumulators over
+ * four A and two B 16-byte fragments read from a / b (wrapping within a_bytes / b_bytes), for
+ * `iters` iterations of 8 MFMAs with no memory traffic. sink int32 [workgroups * 256] receives
+ * each lane's accumulator sum; clocks uint64 [workgroups * 2] the shader-clock cycles and the
+ * 100 MHz reference-clock ticks of the loop per workgroup. Operands 16-byte aligned.
+ * Throughput = 2 * 32768 * 8 * iters * 4 waves * workgroups / elapsed; the clock = cycles /
+ * ticks * 100 MHz. With a GEMM's own operands this is the MFMA ceiling for that data: the board
+ * power limit lowers the clock as the operand bits toggle more.
+ */
+int mxq_probe_mfma_i8(const int8_t* a, int64_t a_bytes, const int8_t* b, int64_t b_bytes, int32_t* sink,
+                      uint64_t* clocks, int64_t workgroups, int64_t iters, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

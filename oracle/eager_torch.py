@@ -177,3 +177,58 @@ def h3_mlp_(residual, norm_weight, eps, shift, scale, gate, segments, w1, s1, b1
     raw = int8_linear(hidden, w1, s1, b1, convrot=True)
     projected = int8_linear(raw, w2, s2, b2, input_act="swiglu", convrot=True)
     return gated_residual_(residual, projected, gate, segments)
+
+
+def quantize_rotated_w4a8(weight: torch.Tensor, group_size: int = 16, symmetric: bool = True,
+                          scale_dtype: torch.dtype = torch.float8_e4m3fn,
+                          codebook: torch.Tensor | None = None):
+    """The reference's storage of an already rotated weight as torch CPU ops
+    (CK/backends/eager/w4a8_int8.py:122-209; nearest-level search 35-63): ``codebook`` given
+    selects the symmetric codebook mode, None the uniform symmetric mode (or the asymmetric one
+    when ``symmetric`` is False). Returns (packed, s_rel, s_channel, correction)."""
+    n, k = weight.shape
+    groups = k // group_size
+    gw = weight.float().view(n, groups, group_size)
+
+    def nearest(values, levels):  # first index of the smallest |values - level|
+        best = (values - levels[..., 0]).abs()
+        idx = torch.zeros_like(values, dtype=torch.int32)
+        for i in range(1, 16):
+            d = (values - levels[..., i]).abs()
+            closer = d < best
+            best = torch.where(closer, d, best)
+            idx = torch.where(closer, i, idx)
+        return idx
+
+    correction = None
+    if symmetric and codebook is not None:
+        cb = codebook.float()
+        gs = gw.abs().amax(dim=-1, keepdim=True).clamp(min=1e-8)
+        q = nearest(gw / gs, cb)
+        for _ in range(3):
+            qc = cb[q]
+            gs = ((gw * qc).sum(-1, keepdim=True) / (qc * qc).sum(-1, keepdim=True).clamp(min=1e-8)).clamp(min=1e-8)
+            q = nearest(gw / gs, cb)
+        shifted = cb[q] * gs
+    elif symmetric:
+        gs = (gw.abs().amax(dim=-1, keepdim=True) / 7.0).clamp(min=1e-8)
+        signed = (gw / gs).round().clamp(-8, 7).to(torch.int32)
+        q = signed + 8
+        shifted = signed * gs
+    else:
+        mn = gw.amin(dim=-1, keepdim=True)
+        gs = ((gw.amax(dim=-1, keepdim=True) - mn) / 15.0).clamp(min=1e-8)
+        q = ((gw - mn) / gs).round().clamp(0, 15).to(torch.int32)
+        shifted = (q - 8) * gs
+        correction = (8.0 * gs + mn).squeeze(-1).t().contiguous().to(weight.dtype)
+    s_channel = (shifted.abs().amax(dim=(1, 2)) / 127.0).clamp(min=1e-8)
+    s_rel = (gs.squeeze(-1) / s_channel.unsqueeze(1)).float()
+    if scale_dtype != torch.float32:
+        s_rel = s_rel.to(scale_dtype)
+    if symmetric and codebook is not None:
+        levels = (cb.view(1, 1, 16) * s_rel.float().unsqueeze(-1)).round_().clamp_(-127, 127)
+        target = gw / s_channel.view(-1, 1, 1)
+        q = nearest(target, levels.unsqueeze(2))
+    u = q.reshape(n, k)
+    packed = ((u[:, 0::2] & 0xF) | ((u[:, 1::2] & 0xF) << 4)).to(torch.int8)
+    return packed, s_rel, s_channel.float(), correction

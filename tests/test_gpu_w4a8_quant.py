@@ -1,0 +1,154 @@
+"""GPU parity of the offline W4A8 weight preparation (mxq_w4a8_quantize_weight and the Python
+functions around it) against the oracle (oracle/w4a8_quant.py, pinned on the CPU against torch's
+own routines and the reference's torch op sequence), and of the reference-format W4A8 linear
+on weights it prepared.
+
+Bar: rotated weights, codes, relative and channel scales and the correction bit-exact; the
+linear's bf16 output bit-exact against the oracle's composition on the same storage.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from _util import activations, bf16_vec, bits, gen
+from oracle import convrot as cr
+from oracle import eager_np
+from oracle import w4a8_quant as wq
+from oracle.bf16 import bf16_bits
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+
+
+def _mx():
+    import mx_qlinear
+
+    return mx_qlinear
+
+
+def _weight(n, k, seed, dtype=torch.bfloat16, tiny_groups=False):
+    w = torch.randn(n, k, generator=gen(seed)) * 0.02
+    if tiny_groups:  # every second 16-group a thousand times smaller: colliding decoded levels
+        w = w.view(n, k // 16, 16)
+        w[:, 1::2] *= 0.001
+        w = w.reshape(n, k)
+    return w.to(dtype)
+
+
+def _np(w):
+    return w.float().numpy()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("g,k", [(4, 256), (16, 512), (64, 2048), (256, 1024), (1024, 2048), (256, 16384)])
+def test_rotation_matches_oracle(dev, dtype, g, k):
+    w = _weight(24, k, g + k, dtype)
+    got = _mx().rotate_int8_convrot_weight(w.to(dev), g)
+    want = wq.rotate_weight(_np(w), "bf16" if dtype == torch.bfloat16 else "fp32", g)
+    assert np.array_equal(got.float().cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("mode", ["codebook", "symmetric", "asymmetric"])
+@pytest.mark.parametrize("sdt", [torch.float8_e4m3fn, torch.float32])
+@pytest.mark.parametrize("g", [4, 16, 32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_storage_matches_oracle(dev, mode, sdt, g, dtype):
+    print(f"w4a8 quant mode={mode} sdt={sdt} g={g} dtype={dtype}", flush=True)
+    n, k = 96, 1024
+    w = _weight(n, k, 40 + g, dtype, tiny_groups=True)
+    sym, cb = mode != "asymmetric", mode == "codebook"
+    lut = torch.from_numpy(wq.FIXED_LUT)
+    p, s, c, corr, table = _mx().quantize_w4a8_int8_weight(w.to(dev), g, 256, sym, sdt, cb, lut if cb else None)
+    rp, rs, rc, rcorr, _ = wq.quantize_w4a8_int8_weight(_np(w), "bf16" if dtype == torch.bfloat16 else "fp32", g, 256,
+                                                        sym, "e4m3" if sdt != torch.float32 else "f32", cb,
+                                                        wq.FIXED_LUT if cb else None)
+    assert np.array_equal(p.cpu().numpy(), rp)
+    assert np.array_equal(s.cpu().view(torch.uint8).numpy() if sdt != torch.float32 else s.cpu().numpy(), rs)
+    assert np.array_equal(c.cpu().numpy(), rc)
+    if mode == "asymmetric":
+        assert np.array_equal(corr.float().cpu().numpy(), rcorr)
+    else:
+        assert corr is None
+    assert (table is not None) == cb
+
+
+def test_gaussian_weight_takes_the_fixed_table(dev):
+    w = _weight(512, 2048, 5)
+    _, _, _, _, table = _mx().quantize_w4a8_int8_weight(w.to(dev))
+    assert np.array_equal(table.cpu().numpy(), wq.FIXED_LUT)
+
+
+def test_heavy_tailed_weight_gets_a_fitted_table(dev):
+    """A heavy-tailed rotated weight (excess kurtosis above the gate) gets a 16-level fit; the
+    storage for that table equals the oracle's."""
+    n, k = 256, 1024
+    # heavy-tailed in the rotated basis (a cubed Gaussian), then rotated back: the rotation is its
+    # own inverse, so the quantizer's rotation recovers the heavy-tailed groups
+    heavy = (torch.randn(n, k, generator=gen(6)) ** 3 * 0.02).numpy().astype(F32)
+    w = torch.from_numpy(wq.rotate_weight(heavy, "fp32", 256))
+    rot = wq.rotate_weight(_np(w), "fp32", 256).reshape(n, k // 16, 16)
+    norm = rot / np.maximum(np.abs(rot).max(-1, keepdims=True), F32(1e-8))
+    x = torch.from_numpy(norm.astype(F32)).flatten()
+    assert (((x - x.mean()) / (x.std() + 1e-9)).pow(4).mean() - 3.0).item() > wq.GATE_KURTOSIS
+    p, s, c, _, table = _mx().quantize_w4a8_int8_weight(w.to(dev))
+    t = table.cpu().numpy()
+    assert t.shape == (16,) and not np.array_equal(t, wq.FIXED_LUT) and np.all(np.diff(t) > 0)
+    rp, rs, rc, _, _ = wq.quantize_rotated(rot.reshape(n, k), 16, True, "e4m3", t)
+    assert np.array_equal(p.cpu().numpy(), rp) and np.array_equal(s.cpu().view(torch.uint8).numpy(), rs)
+    assert np.array_equal(c.cpu().numpy(), rc)
+
+
+@pytest.mark.parametrize("sym,cb", [(True, True), (True, False), (False, False)])
+def test_dequantize_matches_oracle(dev, sym, cb):
+    w = _weight(64, 512, 8)
+    p, s, c, corr, table = _mx().quantize_w4a8_int8_weight(w.to(dev), 16, 256, sym, torch.float8_e4m3fn, cb)
+    back = _mx().dequantize_w4a8_int8_weight(p, s, c, table, corr, 16, 256)
+    want = wq.dequantize_w4a8_int8_weight(p.cpu().numpy(), s.cpu().view(torch.uint8).numpy(), c.cpu().numpy(),
+                                          None if table is None else table.cpu().numpy(),
+                                          None if corr is None else corr.float().cpu().numpy(), 16, 256, True, "bf16")
+    assert np.array_equal(back.float().cpu().numpy(), want)
+    assert ((back.float() - w.to(dev).float()).norm() / w.float().norm()).item() < 0.2
+
+
+def test_reference_format_linear_on_prepared_weights(dev):
+    """The reference's W4A8 linear (ConvRot 256 activations, group-16 codebook storage, e4m3
+    s_rel) on weights prepared by the library: bit-exact against the oracle's composition (the
+    rotated row quantizer, the int4 decode, the int8 GEMM and the dequant epilogue)."""
+    m, n, k = 300, 1024, 2048
+    w = _weight(n, k, 9)
+    x = activations(m, k, 10)
+    bias = bf16_vec(n, 11, 0.01)
+    p, s, c, corr, table = _mx().quantize_w4a8_int8_weight(w.to(dev))
+    y = _mx().w4a8_int8_linear(x.to(dev), p, s, c, codebook=table, bias=bias.to(dev))
+    q, xs, _ = cr.convrot_quantize_bf16(bits(x), 256)
+    w8 = eager_np.dequant_int4_grouped_to_int8(p.cpu().numpy(), s.cpu().view(torch.uint8).numpy(),
+                                               table.cpu().numpy(), 16, s_rel_is_e4m3=True)
+    ref = eager_np.dequant_epilogue(eager_np.int8_matmul(q, w8), xs, c.cpu().numpy(), bits(bias), "bf16")
+    assert np.array_equal(bits(y), bf16_bits(ref))
+    # the layer approximates x @ W^T + bias in the original basis
+    dense = x.float() @ w.float().T + bias.float()
+    assert ((y.float().cpu() - dense).norm() / dense.norm()).item() < 0.1
+
+
+def test_module_from_prepared_asymmetric_weights(dev):
+    """ConvRotW4A8Linear on asymmetric storage (with its correction term) prepared by the library
+    approximates the dense layer."""
+    m, n, k = 64, 512, 1024
+    w = _weight(n, k, 12)
+    x = activations(m, k, 13, outlier_frac=0.0)
+    p, s, c, corr, _ = _mx().quantize_w4a8_int8_weight(w.to(dev), 16, 256, False, torch.float8_e4m3fn, False)
+    layer = _mx().ConvRotW4A8Linear(p, s, c, correction=corr)
+    y = layer(x.to(dev))
+    dense = x.float() @ w.float().T
+    assert ((y.float().cpu() - dense).norm() / dense.norm()).item() < 0.15
+
+
+def test_preparation_rejects_what_the_reference_rejects(dev):
+    w = _weight(8, 520, 14).to(dev)
+    with pytest.raises(ValueError, match="must be divisible by 16"):
+        _mx().quantize_w4a8_int8_weight(w)
+    with pytest.raises(ValueError, match="scale_dtype"):
+        _mx().quantize_w4a8_int8_weight(_weight(8, 512, 15).to(dev), scale_dtype=torch.float16)
+    with pytest.raises(ValueError, match="2D"):
+        _mx().quantize_w4a8_int8_weight(torch.zeros(4, 4, 4, device=dev))

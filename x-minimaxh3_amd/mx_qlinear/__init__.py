@@ -15,6 +15,7 @@ from .ops import (  # noqa: F401
     adaln_quantize_int8,
     apply_input_act,
     dequantize_int4_grouped_to_int8,
+    dequantize_w4a8_int8_weight,
     fused_down_gated_residual,
     h3_mlp_,
     int8_ffn_gelu,
@@ -28,8 +29,10 @@ from .ops import (  # noqa: F401
     quantize_int8_convrot_weight,
     quantize_int8_rowwise,
     quantize_int8_rowwise_convrot,
+    quantize_w4a8_int8_weight,
     rms_adaln,
     rms_adaln_quantize_int8,
+    rotate_int8_convrot_weight,
     segment_row_map,
     swiglu_mlp_gated_residual_,
     w4a8_grouped_linear,

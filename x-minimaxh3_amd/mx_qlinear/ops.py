@@ -977,3 +977,180 @@ def w4a8_grouped_linear(x: torch.Tensor, qdata: torch.Tensor | PreparedW4A8Group
         call(entry, _p(xq), _p(xs), _p(qdata.contiguous()), _p(gs), _p(b), _p(out),
              m, n, k, group_size, n, code, _stream(dev))
     return out.reshape(*lead, n)
+
+
+# ---------------------------------------------------------------------------------------
+# Offline W4A8 weight preparation (the reference's quantize_w4a8_int8_weight)
+# ---------------------------------------------------------------------------------------
+
+# Lloyd-Max levels for a group-normalised Gaussian (CK/backends/eager/w4a8_int8.py:13-16): the
+# codes of the default storage index this table, so the values are the reference's.
+_W4A8_FIXED_LUT = (
+    -0.980602, -0.794529, -0.638165, -0.500986, -0.377321, -0.263187, -0.155210, -0.050720,
+    0.052541, 0.156985, 0.265284, 0.379533, 0.502636, 0.638953, 0.794876, 0.980671,
+)
+_W4A8_GATE_KURTOSIS = -0.1
+_W4A8_KURTOSIS_SAMPLE = 1 << 19
+_W4A8_CODEBOOK_SAMPLE_ELEMS = 1 << 22
+_W4_MODES = {"codebook": 0, "symmetric": 1, "asymmetric": 2, "rotate": 3}
+
+
+def _validate_w4a8_weight(weight: torch.Tensor, group_size: int, convrot_groupsize: int) -> None:
+    """CK/backends/eager/w4a8_int8.py:99-119 (same condition and message)."""
+    if weight.dim() != 2:
+        raise ValueError(f"W4A8 weight must be 2D, got shape {tuple(weight.shape)}")
+    k = weight.shape[1]
+    if (k % 16 != 0 or k % group_size != 0 or k % convrot_groupsize != 0 or group_size < 4
+            or (16 % group_size != 0 and group_size % 16 != 0)):
+        raise ValueError(
+            f"K={k} must be divisible by 16, group_size={group_size}, and "
+            f"convrot_groupsize={convrot_groupsize}; group_size must be >=4 "
+            f"and divide 16 or be a multiple of 16"
+        )
+
+
+def _w4_kernel(weight: torch.Tensor, mode: str, group_size: int, convrot_groupsize: int,
+               codebook: torch.Tensor | None = None, e4m3: bool = True, rotated: torch.Tensor | None = None):
+    dev = weight.device
+    n, k = weight.shape
+    code = _OUT_CODES[weight.dtype]
+    packed = s_rel = s_ch = corr = None
+    if mode != "rotate":
+        packed = torch.empty((n, k // 2), dtype=torch.int8, device=dev)
+        s_rel = torch.empty((n, k // group_size), dtype=torch.uint8 if e4m3 else torch.float32, device=dev)
+        s_ch = torch.empty((n,), dtype=torch.float32, device=dev)
+        if mode == "asymmetric":
+            corr = torch.empty((k // group_size, n), dtype=weight.dtype, device=dev)
+    with torch.cuda.device(dev):
+        call("mxq_w4a8_quantize_weight", _p(weight), code, n, k, group_size, convrot_groupsize, _W4_MODES[mode],
+             _p(codebook), _lib.DTYPE_E4M3 if e4m3 else _lib.DTYPE_F32, _p(packed), _p(s_rel), _p(s_ch), _p(corr),
+             _p(rotated), _stream(dev))
+    if s_rel is not None and e4m3:
+        s_rel = s_rel.view(torch.float8_e4m3fn)
+    return packed, s_rel, s_ch, corr
+
+
+def rotate_int8_convrot_weight(weight: torch.Tensor, group_size: int) -> torch.Tensor:
+    """ConvRot rotation of weight rows, ``W_grouped @ H^T`` per group (CK/backends/eager/
+    quantization.py:909-912), as the exact product rounded once to the weight's dtype (bf16 or
+    fp32). H is symmetric and orthogonal, so the rotation is its own inverse."""
+    _check_power_of_four(group_size)
+    if weight.dim() != 2:
+        raise ValueError("weight must be 2D [out_features, in_features]")
+    if weight.shape[1] % group_size:
+        raise ValueError(f"in_features {weight.shape[1]} not divisible by group_size {group_size}")
+    _require_gpu(weight)
+    if weight.dtype not in (torch.bfloat16, torch.float32):
+        raise NotImplementedError("the weight rotation takes bfloat16 or float32 weights")
+    w = weight.contiguous()
+    out = torch.empty_like(w)
+    if w.numel():
+        _w4_kernel(w, "rotate", 16, group_size, rotated=out)
+    return out
+
+
+def _w4a8_codebook_for(normalized: torch.Tensor) -> torch.Tensor:
+    """The fixed table unless the group-normalised rotated weights are heavy-tailed
+    (CK/backends/eager/w4a8_int8.py:24-32): the excess kurtosis of a seeded sample, drawn with
+    torch's generator on the tensor's device as the reference draws it."""
+    x = normalized.detach().flatten()
+    if x.numel() > _W4A8_KURTOSIS_SAMPLE:
+        gen = torch.Generator(device=x.device).manual_seed(0)
+        x = x[torch.randint(0, x.numel(), (_W4A8_KURTOSIS_SAMPLE,), device=x.device, generator=gen)]
+    x = x.float()
+    excess = ((x - x.mean()) / (x.std() + 1e-9)).pow(4).mean() - 3.0
+    if excess.item() <= _W4A8_GATE_KURTOSIS:
+        return torch.tensor(_W4A8_FIXED_LUT, device=normalized.device, dtype=torch.float32)
+    return _w4a8_fit_codebook(normalized)
+
+
+def _w4a8_fit_codebook(normalized: torch.Tensor, levels: int = 16, iterations: int = 25,
+                       sample_size: int = 300000) -> torch.Tensor:
+    """Lloyd-Max fit of the 16 levels on a seeded sample (CK/backends/eager/w4a8_int8.py:66-97):
+    quantile start, 25 nearest-level / mean updates."""
+    samples = normalized.flatten()
+    if samples.numel() > sample_size:
+        gen = torch.Generator(device=samples.device).manual_seed(0)
+        samples = samples[torch.randint(0, samples.numel(), (sample_size,), device=samples.device, generator=gen)]
+    samples = samples.float()
+    cb = torch.quantile(samples, torch.linspace(0, 1, levels, device=samples.device))
+    for _ in range(iterations):
+        assign = (samples.unsqueeze(-1) - cb).abs().argmin(-1)
+        upd = cb.clone()
+        for i in range(levels):
+            sel = assign == i
+            if sel.any():
+                upd[i] = samples[sel].mean()
+        cb = upd
+    return cb.contiguous()
+
+
+def _w4a8_decide_codebook(weight: torch.Tensor, group_size: int, convrot_groupsize: int) -> torch.Tensor:
+    """One table for the whole tensor from evenly strided rows (CK/backends/eager/w4a8_int8.py:
+    221-240), the rows rotated by the HIP kernel."""
+    n, k = weight.shape
+    max_rows = max(1, _W4A8_CODEBOOK_SAMPLE_ELEMS // max(k, 1))
+    if n > max_rows:
+        idx = torch.linspace(0, n - 1, max_rows, device=weight.device).long()
+        sample = weight.index_select(0, idx).contiguous()
+    else:
+        sample = weight
+    rotated = rotate_int8_convrot_weight(sample, convrot_groupsize)
+    grouped = rotated.float().view(sample.shape[0], k // group_size, group_size)
+    normalized = grouped / grouped.abs().amax(dim=-1, keepdim=True).clamp(min=1e-8)
+    return _w4a8_codebook_for(normalized)
+
+
+def quantize_w4a8_int8_weight(weight: torch.Tensor, group_size: int = 16, convrot_groupsize: int = 256,
+                              symmetric: bool = True, scale_dtype: torch.dtype = torch.float8_e4m3fn,
+                              codebook: bool = True, codebook_tensor: torch.Tensor | None = None):
+    """Rotate and store a floating weight ``[N, K]`` in the grouped W4A8 format
+    (CK/tensor/w4a8_int8.py:29-63, eager backend CK/backends/eager/w4a8_int8.py:122-209,
+    243-341): returns ``(qdata int8 [N, K/2], s_rel [N, K/G] float8_e4m3fn or float32,
+    s_channel float32 [N], correction [K/G, N] or None, codebook float32 [16] or None)`` with the
+    reference's meaning, ready for ``w4a8_int8_linear`` / ``ConvRotW4A8Linear``.
+
+    The rotation, the group and channel scales, the codes and the packing run in one HIP launch
+    (one workgroup per row); the codebook choice (a kurtosis test on a seeded sample and, for
+    heavy-tailed weights, a 16-level fit) is made once per tensor as in the reference, or taken
+    from ``codebook_tensor``. bf16 or fp32 weights on the GPU, K <= 16384."""
+    if scale_dtype not in (torch.float32, torch.float8_e4m3fn):
+        raise ValueError(f"scale_dtype must be float32 or float8_e4m3fn, got {scale_dtype}")
+    _validate_w4a8_weight(weight, group_size, convrot_groupsize)
+    dev = _require_gpu(weight)
+    if weight.dtype not in (torch.bfloat16, torch.float32):
+        raise NotImplementedError("W4A8 preparation takes bfloat16 or float32 weights")
+    w = weight.contiguous()
+    table = None
+    if symmetric and codebook:
+        table = (codebook_tensor.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+                 if codebook_tensor is not None else _w4a8_decide_codebook(w, group_size, convrot_groupsize))
+        if table.numel() != 16:
+            raise ValueError(f"codebook must have 16 entries, got {table.numel()}")
+        mode = "codebook"
+    else:
+        mode = "symmetric" if symmetric else "asymmetric"
+    packed, s_rel, s_ch, corr = _w4_kernel(w, mode, group_size, convrot_groupsize, table,
+                                           e4m3=scale_dtype == torch.float8_e4m3fn)
+    return packed, s_rel, s_ch, corr, table
+
+
+def dequantize_w4a8_int8_weight(qdata: torch.Tensor, s_rel: torch.Tensor, s_channel: torch.Tensor,
+                                codebook: torch.Tensor | None = None, correction: torch.Tensor | None = None,
+                                group_size: int = 16, convrot_groupsize: int = 256,
+                                output_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """The physical ``[N, K]`` weight of W4A8 storage (CK/backends/eager/w4a8_int8.py:404-437):
+    the int8 grid (``dequantize_int4_grouped_to_int8``), times ``s_channel`` plus the correction
+    in float32, rounded to ``output_dtype``, rotated back to the original basis."""
+    _check_power_of_four(convrot_groupsize)
+    w8 = dequantize_int4_grouped_to_int8(qdata, s_rel, codebook, group_size)
+    n, k = w8.shape
+    groups = k // group_size
+    if tuple(s_channel.shape) != (n,):
+        raise ValueError(f"s_channel must have shape {(n,)}, got {tuple(s_channel.shape)}")
+    if correction is not None and tuple(correction.shape) != (groups, n):
+        raise ValueError(f"correction must have shape {(groups, n)}, got {tuple(correction.shape)}")
+    v = w8.float().view(n, groups, group_size) * s_channel.to(device=w8.device, dtype=torch.float32).view(n, 1, 1)
+    if correction is not None:
+        v = v + correction.to(w8.device).t().unsqueeze(-1).float()
+    return rotate_int8_convrot_weight(v.view(n, k).to(output_dtype), convrot_groupsize)
