@@ -34,10 +34,11 @@ pytestmark = pytest.mark.gpu
 M = 75600
 SEED = 20261202
 
-# Measured on MI355X (torch CPU LayerNorm on the host as the oracle) and bounded at about twice
-# the measured rate; see test_c2_adaln_qkv_chain_full_size.
-ADALN_BF16_MISMATCH_BOUND = 1e-4
-ADALN_INT8_MISMATCH_BOUND = 1e-4
+# Measured on MI355X (torch's CPU LayerNorm on the host as the oracle) over the 819,200 sampled
+# elements: 2 bf16 elements (2.4e-6) and no int8 value differ. Bounds: twice that bf16 rate, and
+# at most one int8 value in 10^6.
+ADALN_BF16_MISMATCH_BOUND = 5e-6
+ADALN_INT8_MISMATCH_BOUND = 1e-6
 
 
 def _mx():

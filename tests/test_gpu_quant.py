@@ -117,13 +117,15 @@ def test_quant_with_known_absmax(dev):
     assert np.array_equal(s.cpu().numpy(), s_ref.reshape(-1))
 
 
-# Elements of the modulated bf16 output that differ from torch's CPU LayerNorm composition. The
-# kernel's statistics are exact to within a few fp32 ulps; torch's own are off by up to ~1000 ulps
-# of the mean, and with exact statistics the rate against torch is already ~1.1e-5 (probed on
-# the CPU). ADALN_MISMATCH_BOUND holds for any test size; the large-sample test bounds the
-# measured rate at about twice its value.
-ADALN_MISMATCH_BOUND = 1e-4
-ADALN_MISMATCH_LARGE = 1e-4
+# Elements of the modulated bf16 output that differ from torch's CPU LayerNorm composition (its
+# statistics are reductions in an order of its own). Measured on MI355X against the host's torch:
+# 4.9e-6 of 21 M elements (bf16) and no int8 value over 4096 x 5120 rows; 2.4e-6 (bf16) and no
+# int8 value over the 160 sampled rows of the 75600 x 5120 chain. The large-sample bounds are
+# about twice those rates; ADALN_MISMATCH_BOUND covers the small tests, where one element is
+# already ~3e-6.
+ADALN_MISMATCH_BOUND = 5e-5
+ADALN_MISMATCH_LARGE = 1e-5
+ADALN_INT8_MISMATCH_LARGE = 1e-6
 
 
 def test_adaln_mismatch_rate_large_sample(dev):
@@ -139,7 +141,7 @@ def test_adaln_mismatch_rate_large_sample(dev):
     int8_rate = float(np.mean(q.cpu().numpy() != q_ref))
     print(f"adaLN mismatch vs torch CPU over {m * d} elements: bf16 {bf16_rate:.3e}, int8 {int8_rate:.3e}", flush=True)
     assert bf16_rate <= ADALN_MISMATCH_LARGE
-    assert int8_rate <= ADALN_MISMATCH_LARGE
+    assert int8_rate <= ADALN_INT8_MISMATCH_LARGE
 
 
 def _adaln_inputs(m, d, seed):

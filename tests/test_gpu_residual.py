@@ -150,11 +150,11 @@ def _check_rms_adaln_bound(y, x, w, scale, shift, rows, eps):
     return mismatch
 
 
-# Elements of the RMS adaLN bf16 output that differ from torch's CPU rms_norm composition:
-# RMS_ADALN_MISMATCH_BOUND for any test size, RMS_ADALN_MISMATCH_LARGE (about twice the measured
-# rate) for the large-sample test.
-RMS_ADALN_MISMATCH_BOUND = 1e-4
-RMS_ADALN_MISMATCH_LARGE = 1e-4
+# Elements of the RMS adaLN bf16 output that differ from torch's CPU rms_norm composition.
+# Measured on MI355X against the host's torch: 3.5e-6 of 22 M elements (4096 x 5376). The
+# large-sample bound is about twice that; RMS_ADALN_MISMATCH_BOUND covers the small tests.
+RMS_ADALN_MISMATCH_BOUND = 5e-5
+RMS_ADALN_MISMATCH_LARGE = 7e-6
 
 
 def test_rms_adaln_mismatch_rate_large_sample(dev):

@@ -55,7 +55,12 @@ struct TileCfg {
   static constexpr int kLds = kSlots * kSlotBytes;
   static constexpr int kEpiLds = kT == 256 ? 131072 : 4 * kSlotBytes;  // per-column factors
 };
-constexpr int kGroupM = 8;
+// Tile-rows per group: with 2, the ~32 tiles an XCD runs at once are 2 tile-rows x 16 tile-columns,
+// so an activation panel is read from HBM once and then served from that XCD's L2 to the whole
+// row sweep, and the weight panels (the smaller operand) come back from the last-level cache.
+// Measured against 1, 3, 4, 8, 16 and 32 on the FFN and QKV shapes at 720p: 2 was fastest
+// (fc1 -2.8 %, fc2 -3.2 %, QKV -2 % against 8).
+constexpr int kGroupM = 2;
 
 enum { kEpiI32 = 0, kEpiDequant = 1, kEpiGelu = 2, kEpiGatedRes = 3, kEpiSwiGLU = 4 };
 
