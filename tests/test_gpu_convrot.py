@@ -122,12 +122,20 @@ def test_convrot_module_forward_slices_and_prepared_inputs(dev):
     assert torch.equal(r, full[3:29, 64:250])
 
 
-def test_w4a8_reference_format_with_convrot(dev):
+@pytest.mark.parametrize("source", ["random", "prepared"])
+def test_w4a8_reference_format_with_convrot(dev, source):
+    """Random storage, or storage that quantize_w4a8_int8_weight made from an N(0, 0.02) bf16
+    weight in the uniform symmetric mode (no codebook)."""
     mx = _mx()
     n, k, gsz = 256, 1024, 16
-    qd = packed_int4(n, k, 81)
-    s_rel = (torch.rand(n, k // gsz, generator=gen(82)) * 1.5 + 0.25).to(torch.float8_e4m3fn)
-    s_ch = (torch.rand(n, generator=gen(83)) * 0.01 + 0.001)
+    if source == "prepared":
+        w = (torch.randn(n, k, generator=gen(85)) * 0.02).to(torch.bfloat16)
+        qd, s_rel, s_ch, _, _ = mx.quantize_w4a8_int8_weight(w.to(dev), gsz, 256, codebook=False)
+        qd, s_rel, s_ch = qd.cpu(), s_rel.cpu(), s_ch.cpu()
+    else:
+        qd = packed_int4(n, k, 81)
+        s_rel = (torch.rand(n, k // gsz, generator=gen(82)) * 1.5 + 0.25).to(torch.float8_e4m3fn)
+        s_ch = (torch.rand(n, generator=gen(83)) * 0.01 + 0.001)
     x = activations(33, k, 84)
     y = mx.w4a8_int8_linear(x.to(dev), qd.to(dev), s_rel.to(dev), s_ch.to(dev), group_size=gsz,
                             convrot_groupsize=256)

@@ -47,15 +47,26 @@ def test_decode_unit_scale_is_code_minus_8(dev):
     assert np.array_equal(w8.cpu().numpy(), codes - 8)
 
 
-# N = 4232 decodes in two chunks (4096 + 136 columns) into the GEMM's output column slices.
-@pytest.mark.parametrize("m,n,k,use_codebook", [(200, 300, 1024, True), (64, 4232, 256, False)])
-def test_w4a8_reference_format_linear(dev, m, n, k, use_codebook):
-    g = 16
-    x = activations(m, k, 31)
+def _format_r_storage(n, k, g, use_codebook, source):
+    """Random codes and scales, or storage made by quantize_w4a8_int8_weight from an N(0, 0.02)
+    bf16 weight (the reference's codebook or uniform symmetric mode, e4m3 s_rel)."""
+    if source == "prepared":
+        w = (torch.randn(n, k, generator=gen(36)) * 0.02).to(torch.bfloat16)
+        qd, s_rel, s_ch, _, cb = _mx().quantize_w4a8_int8_weight(w.cuda(), g, 256, codebook=use_codebook)
+        return qd.cpu(), s_rel.cpu(), s_ch.cpu(), None if cb is None else cb.cpu()
     qd = packed_int4(n, k, 32)
     s_rel = (torch.rand(n, k // g, generator=gen(33)) * 15 + 1).to(torch.float8_e4m3fn)
     s_ch = torch.rand(n, generator=gen(34)) * 1e-3
-    cb = torch.linspace(-7.5, 7.5, 16) if use_codebook else None
+    return qd, s_rel, s_ch, torch.linspace(-7.5, 7.5, 16) if use_codebook else None
+
+
+# N = 4232 decodes in two chunks (4096 + 136 columns) into the GEMM's output column slices.
+@pytest.mark.parametrize("source", ["random", "prepared"])
+@pytest.mark.parametrize("m,n,k,use_codebook", [(200, 300, 1024, True), (64, 4232, 256, False)])
+def test_w4a8_reference_format_linear(dev, m, n, k, use_codebook, source):
+    g = 16
+    x = activations(m, k, 31)
+    qd, s_rel, s_ch, cb = _format_r_storage(n, k, g, use_codebook, source)
     bias = bf16_vec(n, 35, 0.01)
     y = _mx().w4a8_int8_linear(x.to(dev), qd.to(dev), s_rel.to(dev), s_ch.to(dev),
                                codebook=None if cb is None else cb.to(dev),

@@ -74,7 +74,8 @@ struct GemmArgs {
   float* row_absmax;
   int64_t M, N, K, ldd;
   int ws_per_channel;
-  int vec_store;  // run stores allowed (d aligned to 4 elements and ldd % 4 == 0)
+  int vec_store;   // run stores allowed (d aligned to 4 elements and ldd % 4 == 0)
+  int line_store;  // 16-byte row pieces allowed (every row of d, and of res / gate, 16-byte aligned)
   int tiles_m, tiles_n;
   // kEpiGatedRes: bf16 residual [M, ldr] (read and written), bf16 gate [*, ldg], gate_rows [M]
   uint16_t* res;
@@ -319,6 +320,94 @@ MXQ_DEVICE void gated_block_row(const GemmArgs& p, bool full, int64_t row, int64
   }
 }
 
+// ---- whole-line stores through LDS ----
+// Stored straight from the accumulator layout, every store instruction writes 8- or 16-byte
+// pieces of 32 different rows. Interior tiles instead pass 32-row x 128-byte pieces of a wave's
+// output through a private 4 KB LDS buffer: written in the accumulator layout, read back by rows
+// (read t gives lane l 16 bytes of row 8 t + l / 8), so that eight lanes store one whole
+// 128-byte line. Chunk c (16 bytes) of row r sits at chunk c ^ ((r >> 1) & 7) of the row: the
+// writes (32 rows at one chunk) and the reads (8 rows x 8 chunks) then use every bank equally.
+constexpr int kStageBytes = 32 * 128;
+
+MXQ_DEVICE char* stage_at(char* buf, int r, int c) { return buf + r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
+
+// Lanes exchange data through the buffer: this orders the wave's LDS accesses before the call
+// against those after it (one wave's LDS instructions execute in order).
+MXQ_DEVICE void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The 8 bytes of half h of chunk c of row r.
+MXQ_DEVICE void stage_put8(char* buf, int r, int c, int h, uint32_t w0, uint32_t w1) {
+  *reinterpret_cast<v2u*>(stage_at(buf, r, c) + h * 8) = v2u{w0, w1};
+}
+
+MXQ_DEVICE void stage_put16(char* buf, int r, int c, const uint32_t* w) {
+  *reinterpret_cast<v4u*>(stage_at(buf, r, c)) = v4u{w[0], w[1], w[2], w[3]};
+}
+
+MXQ_DEVICE v4u stage_get(char* buf, int t) {
+  const int lane = threadIdx.x & 63;
+  return *reinterpret_cast<const v4u*>(stage_at(buf, t * 8 + (lane >> 3), lane & 7));
+}
+
+// Stores the staged piece as bytes [byte0, byte0 + 128) of rows row0 .. row0 + 31 of d.
+MXQ_DEVICE void stage_store(const GemmArgs& p, char* buf, int64_t row0, int64_t byte0, int64_t pitch) {
+  const int lane = threadIdx.x & 63;
+  wave_lds_sync();
+  v4u v[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) v[t] = stage_get(buf, t);
+  char* base = reinterpret_cast<char*>(p.d) + (row0 + (lane >> 3)) * pitch + byte0 + (lane & 7) * 16;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) *reinterpret_cast<v4u*>(base + t * 8 * pitch) = v[t];
+}
+
+// Two 32 x 32 blocks of 16-bit words (jj = 0, 1: 8 words each, as epi_run gives them), or one
+// block of 32-bit words, as one piece.
+MXQ_DEVICE void stage_blocks16(char* buf, const uint32_t (&w)[2][8]) {
+  const int lane = threadIdx.x & 63;
+  wave_lds_sync();  // the previous piece has been read
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) stage_put8(buf, lane & 31, jj * 4 + q, lane >> 5, w[jj][2 * q], w[jj][2 * q + 1]);
+}
+
+MXQ_DEVICE void stage_block32(char* buf, const uint32_t* w) {
+  const int lane = threadIdx.x & 63;
+  wave_lds_sync();
+#pragma unroll
+  for (int q = 0; q < 4; ++q) stage_put16(buf, lane & 31, q * 2 + (lane >> 5), w + q * 4);
+}
+
+// Gated residual update of a staged piece (bf16 y of rows row0 .. row0 + 31, columns
+// col0 .. col0 + 63): res = bf16(res + y * gate[grow]) with 16-byte accesses; grow[t] is the
+// gate row of row row0 + 8 t + lane / 8. The residual and gate reads are issued before the
+// staging so that their latency overlaps it.
+MXQ_DEVICE void gated_lines(const GemmArgs& p, char* buf, int64_t row0, int64_t col0, const int64_t (&grow)[4],
+                            const uint32_t (&w)[2][8]) {
+  const int lane = threadIdx.x & 63;
+  uint16_t* res = p.res + (row0 + (lane >> 3)) * p.ldr + col0 + (lane & 7) * 8;
+  v4u r[4], g[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    r[t] = *reinterpret_cast<const v4u*>(res + t * 8 * p.ldr);
+    g[t] = *reinterpret_cast<const v4u*>(p.gate + grow[t] * p.ldg + col0 + (lane & 7) * 8);
+  }
+  stage_blocks16(buf, w);
+  wave_lds_sync();
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const v4u y = stage_get(buf, t);
+    *reinterpret_cast<v4u*>(res + t * 8 * p.ldr) =
+        v4u{gated_pair(r[t][0], y[0], g[t][0]), gated_pair(r[t][1], y[1], g[t][1]),
+            gated_pair(r[t][2], y[2], g[t][2]), gated_pair(r[t][3], y[3], g[t][3])};
+  }
+}
+
 template <int kEpi, int kOut, int kT>
 __global__ __launch_bounds__(kGemmThreads, kT == 256 ? 1 : 2) void gemm_i8_kernel(GemmArgs p) {
   typedef TileCfg<kT> C;
@@ -463,47 +552,99 @@ __global__ __launch_bounds__(kGemmThreads, kT == 256 ? 1 : 2) void gemm_i8_kerne
     barrier_no_drain();
   }
   const bool full = p.vec_store && m0 + kBM <= p.M && n0 + kBN <= p.N;
-  int64_t grow[kBI] = {};  // kEpiGatedRes: the gate row of each of this lane's rows
+  // Interior tiles of a line-aligned output leave through LDS as whole lines (stage_store); the
+  // staging buffers sit behind the per-column factors when a table fills the ring, else at 0.
+  constexpr bool kTable = kEpi == kEpiGelu || kEpi == kEpiSwiGLU;
+  const bool lines = full && p.line_store;
+  char* sbuf = lds + (kTable ? C::kEpiLds + 2 * kBN * 4 : 0) + wave * kStageBytes;
+  static_assert((kTable ? C::kEpiLds + 2 * kBN * 4 : 0) + 4 * kStageBytes <= (kTable ? C::kLds : C::kEpiLds),
+                "staging buffers overlap the table, the factors or the end of LDS");
+  const int64_t pitch = p.ldd * kElem;
+  int64_t grow[kBI] = {};     // kEpiGatedRes: the gate row of each of this lane's rows
+  int64_t grow_rm[kBI][4] = {};  // ... and of the rows it updates in the whole-line form
   if constexpr (kEpi == kEpiGatedRes) {
+    auto gate_row = [&](int64_t m) {  // clamped into the gate so a bad row index cannot fault
+      const int64_t gr = p.gate_rows[min(m, p.M - 1)];
+      return gr < 0 ? (int64_t)0 : (gr >= p.gate_count ? p.gate_count - 1 : gr);
+    };
 #pragma unroll
-    for (int i = 0; i < kBI; ++i) {  // clamped into the gate so a bad row index cannot fault
-      const int64_t gr = p.gate_rows[min(m0 + wm * kWaveM + i * 32 + lr, p.M - 1)];
-      grow[i] = gr < 0 ? 0 : (gr >= p.gate_count ? p.gate_count - 1 : gr);
+    for (int i = 0; i < kBI; ++i) {
+      grow[i] = gate_row(m0 + wm * kWaveM + i * 32 + lr);
+      if (lines)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) grow_rm[i][t] = gate_row(m0 + wm * kWaveM + i * 32 + t * 8 + (lane >> 3));
     }
   }
 
+  // The blocks go by pairs of 32-column blocks (jp), the factors of a pair held in registers.
   // GELU / SwiGLU: pre-activation bf16 pairs, kept until the table has landed.
-  constexpr bool kTable = kEpi == kEpiGelu || kEpi == kEpiSwiGLU;
   uint32_t yp[kTable ? kBI : 1][kTable ? kBJ : 1][8];
-  static_for<kBJ>([&](auto J) {
-    constexpr int j = decltype(J)::value;
-    const int cl0 = wn * kWaveN + j * 32 + lh * 4;  // tile column of run q = 0
-    float wsv[16], bsv[16];
+  static_for<kBJ / 2>([&](auto JP) {
+    constexpr int jp = decltype(JP)::value;
+    float wsv[2][16], bsv[2][16];
     if constexpr (kEpi != kEpiI32) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const v4f w4 = *reinterpret_cast<const v4f*>(s_ws + cl0 + q * 8);
-        const v4f b4 = *reinterpret_cast<const v4f*>(s_bias + cl0 + q * 8);
+      for (int jj = 0; jj < 2; ++jj) {
+        const int cl0 = wn * kWaveN + (2 * jp + jj) * 32 + lh * 4;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          wsv[q * 4 + e] = w4[e];
-          bsv[q * 4 + e] = b4[e];
+        for (int q = 0; q < 4; ++q) {
+          const v4f w4 = *reinterpret_cast<const v4f*>(s_ws + cl0 + q * 8);
+          const v4f b4 = *reinterpret_cast<const v4f*>(s_bias + cl0 + q * 8);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            wsv[jj][q * 4 + e] = w4[e];
+            bsv[jj][q * 4 + e] = b4[e];
+          }
         }
       }
     }
     static_for<kBI>([&](auto I) {
       constexpr int i = decltype(I)::value;
       constexpr int kWords = kElem == 4 ? 4 : 2;
-      uint32_t w[4 * kWords];
+      const int64_t row0 = m0 + wm * kWaveM + i * 32;  // the block row's first row
+      const int64_t col0 = n0 + wn * kWaveN + jp * 64;  // the pair's first column
+      uint32_t w[2][8];
+      uint32_t w32[2][16];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) epi_run<kEpi, kOut>(acc[i][j], q, xsv[i], wsv + q * 4, bsv + q * 4, w + q * kWords);
+      for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if constexpr (kElem == 4)
+            epi_run<kEpi, kOut>(acc[i][2 * jp + jj], q, xsv[i], wsv[jj] + q * 4, bsv[jj] + q * 4, w32[jj] + q * kWords);
+          else
+            epi_run<kEpi, kOut>(acc[i][2 * jp + jj], q, xsv[i], wsv[jj] + q * 4, bsv[jj] + q * 4, w[jj] + q * kWords);
+        }
       if constexpr (kTable) {
 #pragma unroll
-        for (int r = 0; r < 8; ++r) yp[i][j][r] = w[r];
+        for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+          for (int r = 0; r < 8; ++r) yp[i][2 * jp + jj][r] = w[jj][r];
       } else if constexpr (kEpi == kEpiGatedRes) {
-        gated_block_row(p, full, m0 + wm * kWaveM + i * 32 + lr, grow[i], n0 + cl0, w);
+        if (lines) {
+          gated_lines(p, sbuf, row0, col0, grow_rm[i], w);
+        } else {
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) gated_block_row(p, full, row0 + lr, grow[i], col0 + jj * 32 + lh * 4, w[jj]);
+        }
+      } else if constexpr (kElem == 4) {
+        if (lines) {
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) {
+            stage_block32(sbuf, w32[jj]);
+            stage_store(p, sbuf, row0, (col0 + jj * 32) * 4, pitch);
+          }
+        } else {
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) store_block_row<4>(p, full, row0 + lr, col0 + jj * 32 + lh * 4, w32[jj]);
+        }
       } else {
-        store_block_row<kElem>(p, full, m0 + wm * kWaveM + i * 32 + lr, n0 + cl0, w);
+        if (lines) {
+          stage_blocks16(sbuf, w);
+          stage_store(p, sbuf, row0, col0 * 2, pitch);
+        } else {
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) store_block_row<2>(p, full, row0 + lr, col0 + jj * 32 + lh * 4, w[jj]);
+        }
       }
     });
   });
@@ -514,37 +655,50 @@ __global__ __launch_bounds__(kGemmThreads, kT == 256 ? 1 : 2) void gemm_i8_kerne
     // |h| as bf16 bits: non-negative values order like their bit patterns (NaN above +inf), so
     // the row maximum is an integer maximum, kept for both halves of a word at once.
     us2 rmax[kBI] = {};
-    // Interior tiles run a copy of the pass without column masks or store guards.
-    auto gelu_pass = [&](auto FullC) {
-      constexpr bool kFull = decltype(FullC)::value;
-      static_for<kBJ>([&](auto J) {
-        constexpr int j = decltype(J)::value;
-        const int cl0 = wn * kWaveN + j * 32 + lh * 4;
-        static_for<kBI>([&](auto I) {
-          constexpr int i = decltype(I)::value;
-          uint32_t g[8];
+    // kMode 2: interior tile, whole-line stores; 1: interior tile, run stores; 0: edge tile,
+    // column masks and store guards.
+    auto gelu_pass = [&](auto ModeC) {
+      constexpr int kMode = decltype(ModeC)::value;
+      static_for<kBI>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        const int64_t row0 = m0 + wm * kWaveM + i * 32;
+        static_for<kBJ / 2>([&](auto JP) {
+          constexpr int jp = decltype(JP)::value;
+          const int64_t col0 = n0 + wn * kWaveN + jp * 64;
+          uint32_t g[2][8];
 #pragma unroll
-          for (int r = 0; r < 8; ++r) {
-            const uint32_t h = yp[i][j][r];
-            g[r] = (uint32_t)s_gelu[h & 0xFFFFu] | ((uint32_t)s_gelu[h >> 16] << 16);
-          }
+          for (int jj = 0; jj < 2; ++jj) {
 #pragma unroll
-          for (int r = 0; r < 8; ++r) {
-            uint32_t m = g[r] & 0x7FFF7FFFu;
-            if constexpr (!kFull) {
-              const int64_t col = n0 + cl0 + (r >> 1) * 8 + (r & 1) * 2;
-              m &= (col < p.N ? 0xFFFFu : 0u) | (col + 1 < p.N ? 0xFFFF0000u : 0u);
+            for (int r = 0; r < 8; ++r) {
+              const uint32_t h = yp[i][2 * jp + jj][r];
+              g[jj][r] = (uint32_t)s_gelu[h & 0xFFFFu] | ((uint32_t)s_gelu[h >> 16] << 16);
             }
-            rmax[i] = __builtin_elementwise_max(rmax[i], __builtin_bit_cast(us2, m));
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+              uint32_t m = g[jj][r] & 0x7FFF7FFFu;
+              if constexpr (kMode == 0) {
+                const int64_t col = col0 + jj * 32 + lh * 4 + (r >> 1) * 8 + (r & 1) * 2;
+                m &= (col < p.N ? 0xFFFFu : 0u) | (col + 1 < p.N ? 0xFFFF0000u : 0u);
+              }
+              rmax[i] = __builtin_elementwise_max(rmax[i], __builtin_bit_cast(us2, m));
+            }
           }
-          store_block_row<2>(p, kFull, m0 + wm * kWaveM + i * 32 + lr, n0 + cl0, g);
+          if constexpr (kMode == 2) {
+            stage_blocks16(sbuf, g);
+            stage_store(p, sbuf, row0, col0 * 2, pitch);
+          } else {
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) store_block_row<2>(p, kMode == 1, row0 + lr, col0 + jj * 32 + lh * 4, g[jj]);
+          }
         });
       });
     };
-    if (full)
-      gelu_pass(std::true_type{});
+    if (lines)
+      gelu_pass(std::integral_constant<int, 2>{});
+    else if (full)
+      gelu_pass(std::integral_constant<int, 1>{});
     else
-      gelu_pass(std::false_type{});
+      gelu_pass(std::integral_constant<int, 0>{});
     // Lanes l and l + 32 hold the two halves of each row's columns of this wave.
 #pragma unroll
     for (int i = 0; i < kBI; ++i) {
@@ -558,29 +712,43 @@ __global__ __launch_bounds__(kGemmThreads, kT == 256 ? 1 : 2) void gemm_i8_kerne
     wait_vmcnt<0>();
     barrier_no_drain();  // every wave's part of the SiLU table has landed
     // Runs 0, 1 of a 32 x 32 block are gate columns, runs 2, 3 the matching up columns; output
-    // channel c of block b (tile column t0 = b * 32) is h column t0 / 2 + c.
+    // channel c of block b (tile column t0 = b * 32) is h column t0 / 2 + c. A wave's four
+    // blocks of a block row give 64 h columns: one 128-byte piece for the whole-line form.
     const uint16_t* s_silu = reinterpret_cast<const uint16_t*>(lds);
     const int64_t nh = p.N / 2;
     const bool hfull = p.vec_store && m0 + kBM <= p.M && (n0 + kBN) / 2 <= nh;
-    static_for<kBJ>([&](auto J) {
-      constexpr int j = decltype(J)::value;
-      const int64_t hc0 = (n0 + wn * kWaveN + j * 32) / 2 + lh * 4;
-      static_for<kBI>([&](auto I) {
-        constexpr int i = decltype(I)::value;
-        const int64_t row = m0 + wm * kWaveM + i * 32 + lr;
-        uint32_t hw[4];
+    const bool hlines = hfull && p.line_store;
+    static_for<kBI>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      const int64_t row = m0 + wm * kWaveM + i * 32 + lr;
+      uint32_t hw[kBJ][4];
+#pragma unroll
+      for (int j = 0; j < kBJ; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const uint32_t g = yp[i][j][r], u = yp[i][j][r + 4];
           const float plo = bf16_to_f32(s_silu[g & 0xFFFFu]) * bf16_to_f32(u & 0xFFFFu);
           const float phi = bf16_to_f32(s_silu[g >> 16]) * bf16_to_f32(u >> 16);
-          hw[r] = (plo != plo ? 0x7FC0u : f32_to_bf16_bits(plo)) | ((phi != phi ? 0x7FC0u : f32_to_bf16_bits(phi)) << 16);
+          hw[j][r] = (plo != plo ? 0x7FC0u : f32_to_bf16_bits(plo)) | ((phi != phi ? 0x7FC0u : f32_to_bf16_bits(phi)) << 16);
         }
-        if (hfull || row < p.M) {
-          store_run<2>(p.d, p.ldd, row, hc0, nh, hfull || (p.vec_store && hc0 + 4 <= nh), hw);
-          store_run<2>(p.d, p.ldd, row, hc0 + 8, nh, hfull || (p.vec_store && hc0 + 12 <= nh), hw + 2);
+      if (hlines) {
+        wave_lds_sync();
+#pragma unroll
+        for (int j = 0; j < kBJ; ++j) {
+          stage_put8(sbuf, lr, j * 2, lh, hw[j][0], hw[j][1]);
+          stage_put8(sbuf, lr, j * 2 + 1, lh, hw[j][2], hw[j][3]);
         }
-      });
+        stage_store(p, sbuf, m0 + wm * kWaveM + i * 32, (n0 + wn * kWaveN) / 2 * 2, pitch);
+      } else {
+#pragma unroll
+        for (int j = 0; j < kBJ; ++j) {
+          const int64_t hc0 = (n0 + wn * kWaveN + j * 32) / 2 + lh * 4;
+          if (hfull || row < p.M) {
+            store_run<2>(p.d, p.ldd, row, hc0, nh, hfull || (p.vec_store && hc0 + 4 <= nh), hw[j]);
+            store_run<2>(p.d, p.ldd, row, hc0 + 8, nh, hfull || (p.vec_store && hc0 + 12 <= nh), hw[j] + 2);
+          }
+        }
+      }
     });
   }
 }
@@ -602,8 +770,11 @@ static int launch_gemm(const GemmArgs& args0, hipStream_t stream) {
   args.tiles_n = (int)((args.N + kt - 1) / kt);
   const int elem = (kOut == 0 || kEpi == kEpiI32) ? 4 : 2;
   args.vec_store = ((uintptr_t)args.d % (4 * elem) == 0) && (args.ldd % 4 == 0);
-  if (kEpi == kEpiGatedRes)
+  args.line_store = ((uintptr_t)args.d % 16 == 0) && ((args.ldd * elem) % 16 == 0);
+  if (kEpi == kEpiGatedRes) {
     args.vec_store = args.vec_store && ((uintptr_t)args.gate % 8 == 0) && (args.ldg % 4 == 0);
+    args.line_store = args.line_store && ((uintptr_t)args.gate % 16 == 0) && (args.ldg % 8 == 0);
+  }
   const int64_t tiles = (int64_t)args.tiles_m * args.tiles_n;
   if (tiles > INT32_MAX) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "too many tiles");
   if constexpr (kEpi != kEpiGelu && kEpi != kEpiSwiGLU) {
