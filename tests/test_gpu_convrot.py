@@ -60,6 +60,26 @@ def test_convrot_zero_and_constant_rows(dev):
     assert s[0].item() == np.float32(1e-30) and int(q[0].abs().max()) == 0
 
 
+@pytest.mark.parametrize("k,g", [(512, 256), (512, 4), (1024, 64), (80, 16)])
+def test_convrot_midpoint_rows(dev, k, g):
+    """Rows whose rotated values land on bfloat16 midpoints in float32 while the exact value lies
+    just above or below (1, 2^-8 and +-2^-30 in each group): the rounding must follow the exact
+    value, not the float32 detour. K a multiple of 256 runs the unit form, K = 80 the window form."""
+    x = np.zeros((6, k), np.float32)
+    for r in range(6):
+        for g0 in range(0, k, g):
+            x[r, g0 + (r % 3)] = 1.0 * (1 + r)
+            x[r, g0 + 1 + (r % 2)] = 2.0 ** -8 * (1 + r)
+            x[r, g0 + 3] = (-1) ** r * 2.0 ** -30
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    rot = cr.fht_f64(x.astype(np.float64), g)
+    f = rot.astype(np.float32).view(np.uint32)
+    assert np.any(((f & 0xFFFF) == 0x8000) & (f.view(np.float32).astype(np.float64) != rot))  # the case arises
+    q, s = _mx().quantize_int8_rowwise_convrot(xb.to(dev), g)
+    qr, sr, yr = cr.convrot_quantize_bf16(bits(xb), g)
+    assert np.array_equal(q.cpu().numpy(), qr) and np.array_equal(s.cpu().numpy(), sr)
+
+
 def test_swiglu_all_gate_values(dev):
     """All 65,536 bf16 gate patterns against torch's silu(gate).mul_(up) via the oracle."""
     gate = torch.arange(0, 65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).reshape(64, 1024)

@@ -274,6 +274,309 @@ int launch_convrot(const CrArgs& a, int nw, hipStream_t st) {
   return mxq_check_launch("convrot_quant_kernel");
 }
 
+// ---- unit form: bfloat16 rows, G <= 256, K a multiple of 256 ----
+// A unit is 256 consecutive columns of a row, held by 16 lanes (16 columns each), so every group
+// of G <= 256 columns lies inside one unit (digits 0 and 1 in the lane, digits 2 and 3 across the
+// 16 lanes, rotate16). A 16-lane group takes kNU units of one row (units g, g + gr, g + 2 gr, ...,
+// so the groups of a wave read adjacent units), and a block holds rpb rows of gr groups each; the
+// launcher picks kNU, gr and rpb so that few lanes idle whatever K is (the window form above
+// leaves a third of its lanes idle at K = 5376), preferring small blocks (at most 4 waves: at
+// 720p 4-wave blocks beat 8- and 16-wave ones by 15-35 %). A row's statistics (absmax, and the RMS
+// sum for the adaLN front end) are reduced over its 16 lanes by shuffles and over its groups
+// through LDS, double-buffered by iteration parity. The value path is the window form's, with
+// the float64 -> bfloat16 rounding done in pairs (the midpoint correction of f64_to_bf16_bits
+// runs only for a unit where some float32 value lands on a bfloat16 midpoint) and rows whose
+// absmax is finite quantized by the finite-row path.
+constexpr int kUnitMaxWaves = 4;
+
+// The rotation of one unit up to the transposed layout: digits 0 and 1 in the lane; for
+// kDigits >= 3 each 16-lane group transposes its 16 x 16 float64 values through its LDS region
+// (as rotate16) and applies digits 2 (and 3) in the lane, leaving lane s of the group with the
+// values of columns 16 l + s, l = 0..15. The operations and their order are rotate16's.
+template <int kDigits>
+MXQ_DEVICE void rotate_unit_fwd(double* v, double* tb) {
+  if constexpr (kDigits >= 1) {
+#pragma unroll
+    for (int j = 0; j < 16; j += 4) h4_quad(v[j], v[j + 1], v[j + 2], v[j + 3]);
+  }
+  if constexpr (kDigits >= 2) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) h4_quad(v[j], v[j + 4], v[j + 8], v[j + 12]);
+  }
+  if constexpr (kDigits >= 3) {
+    const int lane = threadIdx.x & 63, s = lane & 15;
+    double* gb = tb + (lane >> 4) * kTGroup;
+    typedef double d2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int c = 0; c < 8; ++c) *reinterpret_cast<d2*>(gb + s * kTRow + 2 * c) = d2{v[2 * c], v[2 * c + 1]};
+    wave_lds_fence();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[r] = gb[r * kTRow + s];
+    wave_lds_fence();
+#pragma unroll
+    for (int j = 0; j < 16; j += 4) h4_quad(v[j], v[j + 1], v[j + 2], v[j + 3]);  // digit 2
+    if constexpr (kDigits >= 4) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) h4_quad(v[j], v[j + 4], v[j + 8], v[j + 12]);  // digit 3
+    }
+  }
+}
+
+// The way back for the rounded values: lane s of a group holds bf16 pairs of columns
+// (16 l + s), l = 0..15 (pair m: l = 2m, 2m + 1). It writes each value as 16 bits to row l,
+// column s of a 16 x 16 matrix (rows of 48 bytes, groups 800 bytes apart, so that both the
+// 16-bit writes and the row reads spread over the banks), and lane l reads its row back as two
+// 16-byte loads: columns 16 l .. 16 l + 15 as pairs again. 16-bit traffic, a quarter of a
+// float64 transpose. (Scattered 16-bit writes rather than 16-bit loads into register halves:
+// with SRAM ECC those loads do not preserve the other half.)
+constexpr int kBRow = 48, kBGroup = 800;
+
+MXQ_DEVICE void unit_back16(uint32_t (&w)[8], double* tb) {
+  const int lane = threadIdx.x & 63, s = lane & 15;
+  char* gb = reinterpret_cast<char*>(tb) + (lane >> 4) * kBGroup;
+  wave_lds_fence();  // the float64 transpose of this region has been read
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    reinterpret_cast<uint16_t*>(gb + (2 * m) * kBRow)[s] = (uint16_t)(w[m] & 0xFFFFu);
+    reinterpret_cast<uint16_t*>(gb + (2 * m + 1) * kBRow)[s] = (uint16_t)(w[m] >> 16);
+  }
+  wave_lds_fence();
+  const v4u lo = *reinterpret_cast<const v4u*>(gb + s * kBRow);
+  const v4u hi = *reinterpret_cast<const v4u*>(gb + s * kBRow + 16);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    w[e] = lo[e];
+    w[4 + e] = hi[e];
+  }
+  wave_lds_fence();  // read before the region's next writes
+}
+
+template <int kAct, int kMod, int kDigits, int kNU>
+__global__ __launch_bounds__(kUnitMaxWaves * 64) void convrot_units_kernel(CrArgs p, int gr, int rpb) {
+  constexpr int kRawWords = kAct == MXQ_ACT_SWIGLU ? 16 : 8;  // dwords per unit and lane
+  constexpr double kInv = 1.0 / (double)(1 << kDigits);     // 1/sqrt(G), exact
+  __shared__ uint32_t red_max[2][4 * kUnitMaxWaves];
+  __shared__ double red_ss[2][4 * kUnitMaxWaves];
+  extern __shared__ __attribute__((aligned(16))) double tbuf[];  // kTWave per wave of the block
+  const int wave = threadIdx.x >> 6;
+  const int grp = threadIdx.x >> 4, gl = threadIdx.x & 15;
+  const int slot = grp / gr, gi = grp - slot * gr;
+  const int units = p.K >> 8;
+  const int64_t xstride = kAct == MXQ_ACT_SWIGLU ? 2 * (int64_t)p.K : p.K;
+  double* tb = tbuf + wave * kTWave;
+  int it = 0;
+  // Raw loads of every unit of this group for the batch starting at r (zeros for units past
+  // the row and rows past the end).
+  auto load_batch = [&](int64_t r, uint32_t (&raw)[kNU][kRawWords]) {
+    const int64_t row = r + slot;
+    const bool row_on = slot < rpb && row < p.rows;
+#pragma unroll
+    for (int k = 0; k < kNU; ++k) {
+      const int u = gi + k * gr;
+      const bool on = row_on && u < units;
+      const uint16_t* xr = reinterpret_cast<const uint16_t*>(p.x) + (on ? row * xstride + u * 256 + gl * 16 : 0);
+#pragma unroll
+      for (int c = 0; c < kRawWords / 4; ++c) {
+        const v4u w = on ? *reinterpret_cast<const v4u*>(xr + (c < 2 ? 0 : p.K) + 8 * (c & 1)) : v4u{0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) raw[k][4 * c + e] = w[e];
+      }
+    }
+  };
+  for (int64_t r0 = (int64_t)blockIdx.x * rpb; r0 < p.rows; r0 += (int64_t)gridDim.x * rpb, it ^= 1) {
+    const int64_t row = r0 + slot;
+    const bool row_on = slot < rpb && row < p.rows;
+    uint32_t raw[kNU][kRawWords];
+    load_batch(r0, raw);
+    // ---- RMS statistic of the row (RMS adaLN front end): squares of bf16 values are exact in
+    // float64, as are their sums (row-independent of the order while the spread allows)
+    float rinv = 0.0f;
+    const uint16_t* msc = nullptr;
+    const uint16_t* msh = nullptr;
+    if constexpr (kMod != kModNone) {
+      double ss = 0.0;
+#pragma unroll
+      for (int k = 0; k < kNU; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const double lo = (double)bf16_lo(raw[k][e]), hi = (double)bf16_hi(raw[k][e]);
+          ss = __builtin_fma(lo, lo, ss);
+          ss = __builtin_fma(hi, hi, ss);
+        }
+#pragma unroll
+      for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, kWave);
+      if (gl == 0) red_ss[it][grp] = ss;
+      __syncthreads();
+      // lane i of each group takes partials i and i + 16 of its row, then the 16 lanes combine
+      double tot = 0.0;
+      for (int i = gl; i < gr; i += 16) tot += red_ss[it][slot * gr + i];
+#pragma unroll
+      for (int m = 1; m < 16; m <<= 1) tot += __shfl_xor(tot, m, kWave);
+      const float mean = (float)tot / (float)p.K;
+      rinv = 1.0f / sqrtf(mean + p.eps);
+      int64_t mr = row_on ? p.mrows[row] : 0;
+      mr = mr < 0 ? 0 : (mr >= p.mod_count ? p.mod_count - 1 : mr);
+      msc = p.mscale + mr * p.ldm;
+      msh = p.mshift + mr * p.ldm;
+    }
+    // ---- activation / modulation, rotation, rounding to bf16 pairs; absmax
+    uint32_t keep[kNU][8];
+    uint32_t amax = 0;  // packed |bf16| pairs
+#pragma unroll
+    for (int k = 0; k < kNU; ++k) {
+      const int u = gi + k * gr;
+      const bool on = row_on && u < units;
+      const int e0 = u * 256 + gl * 16;
+      const v4u* rw = reinterpret_cast<const v4u*>(raw[k]);
+      double v[16];
+      if constexpr (kMod != kModNone) {
+        v4u nw[2], sc[2], sh[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          nw[c] = on ? reinterpret_cast<const v4u*>(p.norm_w + e0)[c] : v4u{0, 0, 0, 0};
+          sc[c] = on ? reinterpret_cast<const v4u*>(msc + e0)[c] : v4u{0, 0, 0, 0};
+          sh[c] = on ? reinterpret_cast<const v4u*>(msh + e0)[c] : v4u{0, 0, 0, 0};
+        }
+        uint32_t ybits[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t xw = rw[i >> 2][i & 3], ww = nw[i >> 2][i & 3];
+          const uint32_t sw = sc[i >> 2][i & 3], hw = sh[i >> 2][i & 3];
+          // t = bf16(1 + scale), n = bf16((x * r) * w), y = bf16(bf16(n * t) + shift), in pairs
+          const uint32_t t = pack_bf16x2(1.0f + bf16_lo(sw), 1.0f + bf16_hi(sw));
+          const uint32_t n = pack_bf16x2((bf16_lo(xw) * rinv) * bf16_lo(ww), (bf16_hi(xw) * rinv) * bf16_hi(ww));
+          const uint32_t nt = pack_bf16x2(bf16_lo(n) * bf16_lo(t), bf16_hi(n) * bf16_hi(t));
+          ybits[i] = pack_bf16x2(bf16_lo(nt) + bf16_lo(hw), bf16_hi(nt) + bf16_hi(hw));
+          v[2 * i] = (double)bf16_lo(ybits[i]);
+          v[2 * i + 1] = (double)bf16_hi(ybits[i]);
+        }
+        if (p.y_out && on) {
+          v4u* dst = reinterpret_cast<v4u*>(p.y_out + row * p.K + e0);
+          dst[0] = v4u{ybits[0], ybits[1], ybits[2], ybits[3]};
+          dst[1] = v4u{ybits[4], ybits[5], ybits[6], ybits[7]};
+        }
+        if constexpr (kMod == kModOnly) continue;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          uint32_t b = half_of(rw, i);
+          if constexpr (kAct == MXQ_ACT_GELU_TANH) b = gelu_bf16(b);
+          if constexpr (kAct == MXQ_ACT_SWIGLU) b = swiglu_bf16(b, half_of(rw + 2, i));
+          v[i] = (double)bf16_to_f32(b);
+        }
+      }
+      rotate_unit_fwd<kDigits>(v, tb);
+      bool mid = false;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float a = (float)(v[2 * i] * kInv), b = (float)(v[2 * i + 1] * kInv);
+        keep[k][i] = pack_bf16x2(a, b);
+        mid |= ((__float_as_uint(a) & 0xFFFFu) == 0x8000u) | ((__float_as_uint(b) & 0xFFFFu) == 0x8000u);
+      }
+      if (mid) {  // a float32 on a bfloat16 midpoint: the exact value decides (f64_to_bf16_bits)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          keep[k][i] = f64_to_bf16_bits(v[2 * i] * kInv) | (f64_to_bf16_bits(v[2 * i + 1] * kInv) << 16);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) amax = absmax_acc_bf16x2(amax, keep[k][i]);
+      if constexpr (kDigits >= 3) unit_back16(keep[k], tb);
+    }
+    if constexpr (kMod == kModOnly) continue;
+    // ---- row absmax over the group's lanes, then over the row's groups
+    uint32_t bits = absmax_bits_of_bf16x2(amax);
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+      const uint32_t o = (uint32_t)__shfl_xor((int)bits, m, kWave);
+      bits = bits > o ? bits : o;
+    }
+    if (gl == 0) red_max[it][grp] = bits;
+    __syncthreads();
+    uint32_t rmax = 0;
+    for (int i = gl; i < gr; i += 16) rmax = max(rmax, red_max[it][slot * gr + i]);
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) rmax = max(rmax, (uint32_t)__shfl_xor((int)rmax, m, kWave));
+    const float amaxf = __uint_as_float(rmax);
+    const float s = row_scale_from_absmax(amaxf);
+    const float r = 1.0f / round_bf16(s);
+    // ---- quantize from registers, 16-byte stores
+    auto store_units = [&](auto finite) {
+#pragma unroll
+      for (int k = 0; k < kNU; ++k) {
+        const int u = gi + k * gr;
+        if (u >= units) continue;
+        const v4u* kw = reinterpret_cast<const v4u*>(keep[k]);
+        const v2u o0 = decltype(finite)::value ? quant8_bf16_finite(kw[0], r) : quant8_bf16(kw[0], r);
+        const v2u o1 = decltype(finite)::value ? quant8_bf16_finite(kw[1], r) : quant8_bf16(kw[1], r);
+        *reinterpret_cast<v4u*>(p.q + row * p.K + u * 256 + gl * 16) = v4u{o0[0], o0[1], o1[0], o1[1]};
+      }
+    };
+    if (row_on) {
+      if (finite_absmax(amaxf))
+        store_units(std::true_type{});
+      else
+        store_units(std::false_type{});
+    }
+    if (row_on && gi == 0 && gl == 0) p.scales[row] = s;
+  }
+}
+
+// Units per group, groups per row and rows per block for a row of K = 256 * units columns: the
+// choice with the fewest idle unit slots in blocks of at most kUnitMaxWaves waves, then the one
+// with fewer units per group (fewer registers).
+struct UnitSplit {
+  int nu, gr, rpb, waves;
+};
+
+UnitSplit unit_split(int units) {
+  UnitSplit best{0, 0, 0, 0};
+  double best_util = -1.0;
+  for (int nu = 1; nu <= 4; ++nu) {
+    const int gr = (units + nu - 1) / nu;
+    if (gr > 4 * kUnitMaxWaves) continue;
+    for (int rpb = 1; rpb * gr <= 4 * kUnitMaxWaves; ++rpb) {
+      const int waves = (rpb * gr + 3) / 4;
+      const double util = (double)(rpb * units) / (double)(waves * 4 * nu);
+      if (util > best_util + 1e-9 || (util > best_util - 1e-9 && waves < best.waves)) {
+        best_util = util;
+        best = UnitSplit{nu, gr, rpb, waves};
+      }
+    }
+  }
+  return best;
+}
+
+template <int kAct, int kMod, int kDigits>
+int launch_units(const CrArgs& a, const UnitSplit& u, hipStream_t st) {
+  // One row batch per block (measured faster at 720p than persistent blocks that prefetch the
+  // next batch); small blocks, many resident per CU, hide the load latency instead.
+  const unsigned grid = (unsigned)std::min<int64_t>((a.rows + u.rpb - 1) / u.rpb, 1 << 20);
+  const unsigned threads = (unsigned)(u.waves * 64);
+  const size_t lds = (size_t)u.waves * kTWave * sizeof(double);
+  switch (u.nu) {
+    case 1: convrot_units_kernel<kAct, kMod, kDigits, 1><<<grid, threads, lds, st>>>(a, u.gr, u.rpb); break;
+    case 2: convrot_units_kernel<kAct, kMod, kDigits, 2><<<grid, threads, lds, st>>>(a, u.gr, u.rpb); break;
+    case 3: convrot_units_kernel<kAct, kMod, kDigits, 3><<<grid, threads, lds, st>>>(a, u.gr, u.rpb); break;
+    default: convrot_units_kernel<kAct, kMod, kDigits, 4><<<grid, threads, lds, st>>>(a, u.gr, u.rpb); break;
+  }
+  return mxq_check_launch("convrot_units_kernel");
+}
+
+template <int kAct, int kMod>
+int launch_units_digits(const CrArgs& a, hipStream_t st) {
+  const UnitSplit u = unit_split(a.K >> 8);
+  switch (a.digits) {
+    case 0: return launch_units<kAct, kMod, 0>(a, u, st);
+    case 1: return launch_units<kAct, kMod, 1>(a, u, st);
+    case 2: return launch_units<kAct, kMod, 2>(a, u, st);
+    case 3: return launch_units<kAct, kMod, 3>(a, u, st);
+    default: return launch_units<kAct, kMod, 4>(a, u, st);
+  }
+}
+
+// The unit form takes bf16 rows with G <= 256 and K a multiple of 256 up to 4 * 32 units.
+bool units_fit(int64_t cols, int digits) { return digits <= 4 && cols % 256 == 0 && cols <= 256 * 4 * 4 * kUnitMaxWaves; }
+
 __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
                                                       int64_t rows, int64_t cols) {
   const int64_t n = rows * cols;
@@ -317,6 +620,13 @@ extern "C" int mxq_quantize_int8_rowwise_convrot(const void* x, int x_dtype, int
   row_split(cols, a.wpr, nw);
   hipStream_t st = (hipStream_t)stream;
   if (x_dtype == MXQ_DTYPE_F32) return launch_convrot<MXQ_ACT_NONE, MXQ_DTYPE_F32, kModNone>(a, nw, st);
+  if (units_fit(cols, digits)) {
+    switch (input_act) {
+      case MXQ_ACT_NONE: return launch_units_digits<MXQ_ACT_NONE, kModNone>(a, st);
+      case MXQ_ACT_GELU_TANH: return launch_units_digits<MXQ_ACT_GELU_TANH, kModNone>(a, st);
+      default: return launch_units_digits<MXQ_ACT_SWIGLU, kModNone>(a, st);
+    }
+  }
   switch (input_act) {
     case MXQ_ACT_NONE: return launch_convrot<MXQ_ACT_NONE, MXQ_DTYPE_BF16, kModNone>(a, nw, st);
     case MXQ_ACT_GELU_TANH: return launch_convrot<MXQ_ACT_GELU_TANH, MXQ_DTYPE_BF16, kModNone>(a, nw, st);
@@ -373,6 +683,10 @@ extern "C" int mxq_rms_adaln_quantize_int8(const void* x, const void* norm_weigh
   a.eps = eps;
   a.y_out = (uint16_t*)y_out;
   hipStream_t st = (hipStream_t)stream;
+  if (units_fit(cols, digits)) {
+    if (q) return launch_units_digits<MXQ_ACT_NONE, kModQuant>(a, st);
+    return launch_units_digits<MXQ_ACT_NONE, kModOnly>(a, st);
+  }
   if (q) return launch_convrot<MXQ_ACT_NONE, MXQ_DTYPE_BF16, kModQuant>(a, nw, st);
   return launch_convrot<MXQ_ACT_NONE, MXQ_DTYPE_BF16, kModOnly>(a, nw, st);
 }

@@ -119,6 +119,57 @@ MXQ_DEVICE int quant_round_clamp(float qf) {
   return (qf != qf) ? 0 : (int)r;
 }
 
+// ---- row quantization of packed bf16 values (8 values in 4 words -> 8 int8 in 2 words) ----
+MXQ_DEVICE float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+MXQ_DEVICE float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+MXQ_DEVICE uint32_t pack_q4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) |
+         ((uint32_t)(d & 0xFF) << 24);
+}
+
+// Quantize 8 bf16 values (4 packed words) with reciprocal r; returns 8 int8 in two words.
+MXQ_DEVICE v2u quant8_bf16(v4u w, float r) {
+  int q[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    q[2 * i] = quant_round_clamp(round_bf16(bf16_lo(w[i]) * r));
+    q[2 * i + 1] = quant_round_clamp(round_bf16(bf16_hi(w[i]) * r));
+  }
+  v2u o;
+  o[0] = pack_q4(q[0], q[1], q[2], q[3]);
+  o[1] = pack_q4(q[4], q[5], q[6], q[7]);
+  return o;
+}
+
+// The same for a row whose absmax is finite. Then |bf16(v * r)| <= 127.5 (r = 1 / bf16(s) and
+// bf16(s) is within 2^-8 of amax / 127), so the lower clamp never acts and the upper one is a
+// min with 127 before rounding; the rounding to an integer is one fp32 addition of 1.5 * 2^23
+// (an exact sum rounded half to even) whose low byte is the two's complement int8.
+MXQ_DEVICE uint32_t quant_byte_finite(float v) {
+  return __float_as_uint(fminf(v, 127.0f) + 12582912.0f);
+}
+
+MXQ_DEVICE v2u quant8_bf16_finite(v4u w, float r) {
+  uint32_t b[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t p = pack_bf16x2(bf16_lo(w[i]) * r, bf16_hi(w[i]) * r);
+    b[2 * i] = quant_byte_finite(bf16_lo(p));
+    b[2 * i + 1] = quant_byte_finite(bf16_hi(p));
+  }
+  v2u o;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t lo = __builtin_amdgcn_perm(b[4 * h + 1], b[4 * h], 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(b[4 * h + 3], b[4 * h + 2], 0x0c0c0400u);
+    o[h] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+  }
+  return o;
+}
+
+MXQ_DEVICE bool finite_absmax(float amax) { return __float_as_uint(amax) < 0x7F800000u; }
+
 // ---- tanh-GELU on bfloat16 ----------------------------------------------------------
 // Bit-exact torch CPU gelu(approximate="tanh") on a bfloat16 input (the routine the reference
 // applies, backends/turbo/vendor/comfy_kitchen/backends/_activations.py:47-48). The function
