@@ -54,10 +54,21 @@ int mxq_abi_version(void);
  *   input_act  MXQ_ACT_NONE or MXQ_ACT_GELU_TANH (bf16 only): apply tanh-GELU to x first
  * Semantics: CK/backends/eager/quantization.py:857-875.
  * Replaces: launch_quantize_int8_rowwise_kernel, CK/backends/cuda/ops/int8_linear.cu:1035-1084
- * (stochastic rounding, off by default there, is not provided).
+ * (stochastic rounding: mxq_quantize_int8_rowwise_stochastic).
  */
 int mxq_quantize_int8_rowwise(const void* x, int x_dtype, int8_t* q, float* scales,
                               int64_t rows, int64_t cols, int input_act, void* stream);
+
+/*
+ * The same quantizer with stochastic rounding: noise [rows, cols] of x_dtype holds the caller's
+ * uniform draws in [0, 1) (the reference draws torch.rand(x.shape, dtype=x.dtype) from a
+ * generator on x's device seeded with the stochastic_rounding seed); then
+ * q = clamp(floor(dt(dt(x / dt(s)) + noise)), -128, 127), dt the input dtype, NaN -> 0.
+ * Semantics: quantize_int8_rowwise(x, stochastic_rounding=seed), CK/__init__.py:702-709 and
+ * CK/backends/eager/quantization.py:803-826, 857-875.
+ */
+int mxq_quantize_int8_rowwise_stochastic(const void* x, int x_dtype, const void* noise, int8_t* q,
+                                         float* scales, int64_t rows, int64_t cols, void* stream);
 
 /*
  * The same quantizer for bf16 rows whose absmax is already known (row_absmax[r] must

@@ -50,6 +50,25 @@ def quantize_int8_rowwise(x_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     return q, scale
 
 
+def quantize_int8_rowwise_stochastic(x_bits: np.ndarray, noise_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """The same quantizer with stochastic rounding on bfloat16 (quantization.py:803-826): the
+    scaled value ``bf16(x / bf16(s))`` gets the uniform draw ``noise`` (bf16, the reference's
+    ``torch.rand`` in the input dtype) added in bfloat16 (``scaled.add_(rng)``: an fp32 sum rounded
+    once), then ``floor``, clamp to [-128, 127]; NaN -> 0 as in the rounding path."""
+    x_bits = np.asarray(x_bits, dtype=np.uint16)
+    xf = bf16_to_f32(x_bits)
+    amax = np.max(np.abs(xf), axis=-1, keepdims=True)
+    scale = np.maximum(amax / F32(127.0), _SCALE_FLOOR).astype(F32)
+    s_math = round_bf16(scale)
+    s_math = np.where(s_math == 0, _BF16_TINY, s_math)
+    qf = round_bf16(xf / s_math)
+    t = round_bf16((qf + bf16_to_f32(np.asarray(noise_bits, dtype=np.uint16))).astype(F32))
+    with np.errstate(invalid="ignore"):
+        q = np.clip(np.floor(t), -128.0, 127.0)
+    q = np.nan_to_num(q, nan=0.0).astype(np.int8)
+    return q, scale
+
+
 def quantize_int8_rowwise_with_absmax(x_bits: np.ndarray, amax: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     """Same quantizer with the row absmax supplied (it must equal max |x|)."""
     xf = bf16_to_f32(np.asarray(x_bits, dtype=np.uint16))

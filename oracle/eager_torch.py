@@ -22,6 +22,23 @@ def quantize_int8_rowwise(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return q, scale
 
 
+def quantize_int8_rowwise_stochastic(x: torch.Tensor, seed: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """The reference's stochastic path, quantization.py:803-826 + 857-875, on x's device: the
+    noise is torch.rand in x's dtype from a generator on x's device seeded with ``seed``. The
+    scale is divided on the CPU, as the eager path computes it there (torch on a GPU divides by
+    a host scalar through its reciprocal, which can differ in the last bit)."""
+    abs_max = x.abs().amax(dim=-1, keepdim=True)
+    scale = (abs_max.float().cpu() / 127.0).clamp(min=1e-30).to(x.device)
+    s = scale.to(dtype=x.dtype)
+    s = torch.where(s == 0, torch.full_like(s, torch.finfo(x.dtype).tiny), s)
+    scaled = x / s
+    gen = torch.Generator(device=x.device)
+    gen.manual_seed(seed)
+    rng = torch.rand(scaled.shape, dtype=scaled.dtype, layout=scaled.layout, device=scaled.device, generator=gen)
+    q = scaled.add_(rng).floor_().clamp_(-128.0, 127.0).to(torch.int8)
+    return q, scale
+
+
 def int8_matmul(a: torch.Tensor, w_nk: torch.Tensor) -> torch.Tensor:
     """``torch._int_mm`` with the K padding of quantization.py:749-782."""
     b = w_nk.t().contiguous()

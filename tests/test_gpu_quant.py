@@ -227,3 +227,37 @@ def test_adaln_quant_nan_row(dev):
     q, s = _mx().adaln_quantize_int8(x.to(dev), sc.to(dev), sh.to(dev), 1e-6)
     assert bool(s[2].isnan()) and int(q[2].abs().max()) == 0
     assert not bool(s[[0, 1, 3, 4]].isnan().any())
+
+
+# ---- stochastic rounding (quantize_int8_rowwise(x, stochastic_rounding=seed)) ---------------
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("seed", [1, 99])
+def test_stochastic_rounding_equals_the_reference_on_device(dev, dtype, seed):
+    """The reference's own op sequence run with torch on the same device and seed draws the same
+    noise (torch.rand from a device generator): outputs identical."""
+    x = (activations(257, 3072, seed) * 3).to(dtype)
+    q, s = _mx().quantize_int8_rowwise(x.to(dev), stochastic_rounding=seed)
+    qr, sr = eager_torch.quantize_int8_rowwise_stochastic(x.to(dev), seed)
+    assert torch.equal(q, qr) and torch.equal(s, sr)
+
+
+def test_stochastic_rounding_matches_the_oracle_with_the_same_draws(dev):
+    x = activations(64, 1024, 11)
+    seed = 5
+    q, s = _mx().quantize_int8_rowwise(x.to(dev), stochastic_rounding=seed)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    noise = torch.rand(x.shape, dtype=torch.bfloat16, device=dev, generator=g).cpu()
+    qr, sr = eager_np.quantize_int8_rowwise_stochastic(bits(x), bits(noise))
+    assert np.array_equal(q.cpu().numpy(), qr) and np.array_equal(s.cpu().numpy(), sr)
+    # the draws change the result: not the rounding quantizer's
+    assert not torch.equal(q, _mx().quantize_int8_rowwise(x.to(dev))[0])
+
+
+def test_stochastic_rounding_off_is_the_rounding_quantizer(dev):
+    x = activations(33, 512, 12).to(dev)
+    q0, s0 = _mx().quantize_int8_rowwise(x)
+    for seed in (0, None, -3):
+        q, s = _mx().quantize_int8_rowwise(x, stochastic_rounding=seed)
+        assert torch.equal(q, q0) and torch.equal(s, s0)

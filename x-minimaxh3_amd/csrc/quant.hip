@@ -75,10 +75,13 @@ __global__ __launch_bounds__(kQuantBlock) void quant_rows_bf16_reg(
 }
 
 // Any dtype, any cols: two passes over the row with scalar loads (second pass hits cache).
-template <int kDtype, bool kGelu>
+// kNoise: stochastic rounding (quantization.py:803-826): the scaled value, rounded to the input
+// dtype, gets noise[row, i] (a uniform draw in the input dtype) added in that dtype, then floor
+// and clamp; NaN -> 0.
+template <int kDtype, bool kGelu, bool kNoise = false>
 __global__ __launch_bounds__(kQuantBlock) void quant_rows_generic(
     const void* __restrict__ xv, int8_t* __restrict__ q, float* __restrict__ scales,
-    int64_t rows, int64_t cols) {
+    int64_t rows, int64_t cols, const void* __restrict__ noise = nullptr) {
   const int lane = threadIdx.x % kWave;
   for (int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave; row < rows;
        row += (int64_t)gridDim.x * kRowsPerBlock) {
@@ -114,7 +117,22 @@ __global__ __launch_bounds__(kQuantBlock) void quant_rows_generic(
       float qf = f / s_math;
       if (kDtype == MXQ_DTYPE_BF16) qf = round_bf16(qf);
       if (kDtype == MXQ_DTYPE_F16) qf = round_f16(qf);
-      q[row * cols + i] = (int8_t)quant_round_clamp(qf);
+      if constexpr (kNoise) {
+        float r;
+        if (kDtype == MXQ_DTYPE_F32) {
+          r = reinterpret_cast<const float*>(noise)[row * cols + i];
+        } else {
+          const uint16_t b = reinterpret_cast<const uint16_t*>(noise)[row * cols + i];
+          r = (kDtype == MXQ_DTYPE_BF16) ? bf16_to_f32(b) : f16_to_f32(b);
+        }
+        float t = qf + r;
+        if (kDtype == MXQ_DTYPE_BF16) t = round_bf16(t);
+        if (kDtype == MXQ_DTYPE_F16) t = round_f16(t);
+        const float fl = fminf(fmaxf(floorf(t), -128.0f), 127.0f);
+        q[row * cols + i] = (int8_t)(t != t ? 0 : (int)fl);
+      } else {
+        q[row * cols + i] = (int8_t)quant_round_clamp(qf);
+      }
     }
     if (lane == 0) scales[row] = s;
   }
@@ -529,6 +547,23 @@ extern "C" int mxq_quantize_int8_rowwise(const void* x, int x_dtype, int8_t* q, 
   } else {
     quant_rows_generic<MXQ_DTYPE_F32, false><<<row_grid(rows), kQuantBlock, 0, st>>>(x, q, scales, rows, cols);
   }
+  return mxq_check_launch("quant_rows_generic");
+}
+
+extern "C" int mxq_quantize_int8_rowwise_stochastic(const void* x, int x_dtype, const void* noise, int8_t* q,
+                                                    float* scales, int64_t rows, int64_t cols, void* stream) {
+  if (rows < 0 || cols <= 0) return mxq_set_error(MXQ_ERR_INVALID, "bad shape [%lld, %lld]", (long long)rows, (long long)cols);
+  if (rows == 0) return MXQ_OK;
+  if (!x || !noise || !q || !scales) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  if (x_dtype != MXQ_DTYPE_BF16 && x_dtype != MXQ_DTYPE_F16 && x_dtype != MXQ_DTYPE_F32)
+    return mxq_set_error(MXQ_ERR_INVALID, "unsupported input dtype code %d", x_dtype);
+  hipStream_t st = (hipStream_t)stream;
+  if (x_dtype == MXQ_DTYPE_BF16)
+    quant_rows_generic<MXQ_DTYPE_BF16, false, true><<<row_grid(rows), kQuantBlock, 0, st>>>(x, q, scales, rows, cols, noise);
+  else if (x_dtype == MXQ_DTYPE_F16)
+    quant_rows_generic<MXQ_DTYPE_F16, false, true><<<row_grid(rows), kQuantBlock, 0, st>>>(x, q, scales, rows, cols, noise);
+  else
+    quant_rows_generic<MXQ_DTYPE_F32, false, true><<<row_grid(rows), kQuantBlock, 0, st>>>(x, q, scales, rows, cols, noise);
   return mxq_check_launch("quant_rows_generic");
 }
 

@@ -29,6 +29,7 @@ _F = ctypes.c_float
 # name -> argument types (every function returns int)
 SIGNATURES: dict[str, list] = {
     "mxq_quantize_int8_rowwise": [_P, _I, _P, _P, _I64, _I64, _I, _P],
+    "mxq_quantize_int8_rowwise_stochastic": [_P, _I, _P, _P, _P, _I64, _I64, _P],
     "mxq_quantize_int8_rowwise_absmax": [_P, _P, _P, _P, _I64, _I64, _P],
     "mxq_adaln": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _P],
     "mxq_adaln_quantize_int8": [_P, _P, _P, _I64, _I64, _F, _P, _P, _P, _I64, _I64, _P],

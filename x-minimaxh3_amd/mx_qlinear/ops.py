@@ -77,14 +77,18 @@ def quantize_int8_rowwise(x: torch.Tensor, stochastic_rounding: int | None = 0,
                           input_act: str | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """Per-row INT8 quantization: ``(q int8 [..., K], scale fp32 [..., 1])``.
 
-    CK/__init__.py:702-709 / CK/backends/eager/quantization.py:857-875. Stochastic rounding
-    is not provided (the reference default, 0, is). ``input_act`` ('gelu_tanh' or 'swiglu',
-    bf16 inputs; CK/backends/_activations.py:40-53) is applied first; with 'swiglu' the
-    input is ``[..., 2K]`` and the result ``[..., K]``.
+    CK/__init__.py:702-709 / CK/backends/eager/quantization.py:857-875. ``stochastic_rounding``
+    > 0 is the reference's seed (quantization.py:803-826): the noise is ``torch.rand`` in x's
+    dtype from a generator on x's device seeded with it, the same draws the reference makes, and
+    the kernel adds it to the scaled value and floors. ``input_act`` ('gelu_tanh' or 'swiglu',
+    bf16 inputs; CK/backends/_activations.py:40-53) is applied first (not with stochastic
+    rounding); with 'swiglu' the input is ``[..., 2K]`` and the result ``[..., K]``.
     """
-    if stochastic_rounding:
-        raise NotImplementedError("stochastic rounding is not provided by mx_qlinear")
     act = _act_code(input_act)
+    if stochastic_rounding is not None and stochastic_rounding > 0:
+        if act:
+            raise NotImplementedError("input_act is not provided together with stochastic rounding")
+        return _quantize_int8_rowwise_stochastic(x, int(stochastic_rounding))
     if act == _lib.ACT_SWIGLU:
         return quantize_int8_rowwise_convrot(x, 0, input_act)
     dev = _require_gpu(x)
@@ -101,6 +105,26 @@ def quantize_int8_rowwise(x: torch.Tensor, stochastic_rounding: int | None = 0,
     s = torch.empty((m, 1), dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
         call("mxq_quantize_int8_rowwise", _p(x2), _OUT_CODES[x.dtype], _p(q), _p(s), m, k, act, _stream(dev))
+    return q.reshape(x.shape), s.reshape(*x.shape[:-1], 1)
+
+
+def _quantize_int8_rowwise_stochastic(x: torch.Tensor, seed: int) -> tuple[torch.Tensor, torch.Tensor]:
+    dev = _require_gpu(x)
+    if x.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise ValueError(f"unsupported input dtype {x.dtype}")
+    k = x.shape[-1]
+    if k == 0:
+        raise ValueError("quantize_int8_rowwise needs a non-empty last dimension")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    noise = torch.rand(x.shape, dtype=x.dtype, layout=x.layout, device=dev, generator=gen)
+    x2 = x.reshape(-1, k).contiguous()
+    m = x2.shape[0]
+    q = torch.empty((m, k), dtype=torch.int8, device=dev)
+    s = torch.empty((m, 1), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        call("mxq_quantize_int8_rowwise_stochastic", _p(x2), _OUT_CODES[x.dtype], _p(noise.reshape(m, k)),
+             _p(q), _p(s), m, k, _stream(dev))
     return q.reshape(x.shape), s.reshape(*x.shape[:-1], 1)
 
 
