@@ -125,3 +125,48 @@ def test_loaded_layers_run_on_the_gpu(tmp_path, dev):
     # the stored weights are the rotated, quantized originals: the layer approximates x @ W^T
     dense = x.float() @ wf.float().to(dev).T
     assert ((y.float() - dense).norm() / dense.norm()).item() < 0.05
+
+
+def test_reads_a_file_written_without_this_package(tmp_path):
+    """A checkpoint written directly with safetensors in the layout the reference's loader and
+    audit read (h3serve/native_engine/model/assembly.py:105-135, checkpoint.py:130-190,
+    quantization.py:105-131): `comfy_quant` as uint8 JSON bytes (here with the nested `params`
+    form), INT8 `[N, 1]` fp32 scales, W4A8 layers with fp32 `s_rel`, a codebook, a correction
+    term, and the per-layer record in the file's `_quantization_metadata`."""
+    from safetensors.torch import save_file
+
+    mx = _mx()
+    n, k, g = 64, 512, 16
+    w8 = torch.randint(-127, 128, (n, k), generator=gen(31), dtype=torch.int8)
+    ws = torch.rand(n, 1, generator=gen(32)) * 1e-3
+    cq = json.dumps({"format": "int8_tensorwise", "params": {"convrot": True, "convrot_groupsize": 64}})
+    qd = packed_int4(n, k, 33)
+    s_rel = torch.rand(n, k // g, generator=gen(34)) * 4 + 0.5
+    s_ch = torch.rand(n, generator=gen(35)) * 1e-3
+    cb = torch.linspace(-1.0, 1.0, 16)
+    corr = (torch.randn(k // g, n, generator=gen(36)) * 1e-3).to(torch.bfloat16)
+    tensors = {
+        "blocks.3.attn.out_proj.weight": w8,
+        "blocks.3.attn.out_proj.weight_scale": ws,
+        "blocks.3.attn.out_proj.comfy_quant": torch.tensor(list(cq.encode()), dtype=torch.uint8),
+        "blocks.3.mlp.fc1.weight": qd,
+        "blocks.3.mlp.fc1.weight_s_rel": s_rel,
+        "blocks.3.mlp.fc1.weight_s_channel": s_ch,
+        "blocks.3.mlp.fc1.weight_codebook": cb,
+        "blocks.3.mlp.fc1.weight_correction": corr,
+    }
+    record = {"format": "asym_w4a8_int8", "group_size": g, "convrot": True, "convrot_groupsize": 256}
+    path = tmp_path / "foreign.safetensors"
+    save_file(tensors, str(path), metadata={"_quantization_metadata": json.dumps({"layers": {"blocks.3.mlp.fc1": record}})})
+    with mx.SafeTensorSource(str(path)) as src:
+        assert src.quantization_spec("blocks.3.mlp.fc1") == record
+        a = mx.audit_quantized_layer(src, "blocks.3.attn.out_proj", (n, k))
+        b = mx.audit_quantized_layer(src, "blocks.3.mlp.fc1", (n, k))
+        assert (a.kind, a.ok, b.kind, b.ok) == ("int8", True, "w4a8", True), (a.issues, b.issues)
+        l1 = mx.quant_linear(src, "blocks.3.attn.out_proj", device="cpu")
+        l2 = mx.quant_linear(src, "blocks.3.mlp.fc1", device="cpu")
+    assert l1.spec.convrot and l1.spec.convrot_groupsize == 64
+    assert torch.equal(l1.qweight, w8) and torch.equal(l1.scale.reshape(-1), ws.reshape(-1))
+    assert l2.spec.group_size == g and l2.spec.convrot_groupsize == 256
+    assert torch.equal(l2.qdata, qd) and torch.equal(l2.s_rel, s_rel) and torch.equal(l2.s_channel, s_ch)
+    assert torch.equal(l2.codebook, cb) and torch.equal(l2.correction, corr)

@@ -128,6 +128,35 @@ def test_rotation_agrees_with_torch_cpu_bf16_matmul():
     assert np.all(np.abs(a - b) <= bf16_ulp(np.abs(a).astype(np.float32)))
 
 
+# The rotated bf16 values differ from the reference's torch matmul on about 1e-5 of the elements
+# (test above); after the row quantizer, measured on 2048 x 5120 and 768 x 14336 samples of these
+# activations, one int8 value in ~1e7 differs (by one step) and no row scale differs. The bound
+# allows a few such values per test sample.
+CONVROT_INT8_MISMATCH_BOUND = 1e-6
+
+
+@pytest.mark.parametrize("k", [5120, 14336])
+def test_int8_difference_against_the_reference_rotation_is_bounded(k):
+    """The quantized row of the exact-product rotation against the reference's composition
+    (torch's CPU bf16 matmul x @ H_256, CK/tensor/int8_utils.py:58-74, then the eager row
+    quantizer, quantization.py:857-875): int8 values differ on a small fraction of elements, by
+    one step, and the row scales agree."""
+    from oracle import eager_torch
+
+    rows = 5 * 2 ** 20 // k
+    x = activations(rows, k, 40 + k)
+    q, s, _ = cr.convrot_quantize_bf16(bits(x), 256)
+    h = torch.from_numpy(cr.hadamard(256)).to(torch.bfloat16)
+    xr = torch.matmul(x.reshape(rows, k // 256, 256), h).reshape(rows, k)
+    qt, st = eager_torch.quantize_int8_rowwise(xr)
+    diff = np.abs(q.astype(np.int32) - qt.numpy().astype(np.int32))
+    rate = float(np.mean(diff != 0))
+    print(f"ConvRot int8 mismatch vs torch-matmul rotation, k={k}: {rate:.2e} (max step {diff.max()})")
+    assert diff.max() <= 1
+    assert rate <= CONVROT_INT8_MISMATCH_BOUND
+    assert np.array_equal(s.reshape(-1), st.numpy().reshape(-1))
+
+
 def test_rotation_equals_torch_where_accumulation_is_exact():
     """Inputs with a narrow exponent range make torch's float32 sums exact: then equality."""
     g = gen(5)
