@@ -258,6 +258,18 @@ MXQ_DEVICE void atomic_max_nonneg(float* addr, float v) {
 typedef const void __attribute__((address_space(1)))* gptr_t;
 typedef void __attribute__((address_space(3)))* lptr_t;
 
+// Direct-to-LDS 16-byte buffer load: lane l's 16 bytes from base + voff + soff land at
+// dst + 16 l (dst wave-uniform). The raw buffer (stride 0) spans `bytes` bytes, so the caller's
+// per-lane offset is a fixed 32-bit register and the advance along K a scalar offset: unlike a
+// global load, no 64-bit address is formed per load. (The buffer intrinsics stay inside device
+// functions: a kernel body naming them directly gets no host-side launch stub.)
+constexpr int kRawBufferWord3 = 0x00020000;  // resource word 3: 32-bit data format, no swizzle
+MXQ_DEVICE void buffer_load_lds16(const void* base, int bytes, lptr_t dst, uint32_t voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, kRawBufferWord3), dst, 16, (int)voff,
+      soff, 0, 0);
+}
+
 // s_waitcnt with vmcnt <= n (lgkmcnt and expcnt left alone); n is a compile-time constant.
 template <int n> MXQ_DEVICE void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));

@@ -13,16 +13,19 @@
 // Workgroup: 4 wave64s side by side along N; a 128 x 128 tile, wave w owning channels
 // w*32 + [0, 32) of all 128 rows as four v_mfma_i32_32x32x32_i8 blocks (activations first:
 // lane l holds channel l % 32, so a lane needs one group scale per group).
-//  * One K stage = one group. Each stage's A (128 rows x 128 B), packed B (128 rows x 64 B) and
-//    the group's 128 fp16 scales are fetched with direct-to-LDS loads into a ring of kNS stages
-//    (scales into a ring of 8 slots), kNS - 1 stages ahead.
+//  * One K stage = one group. Each stage's A (kBM rows x 128 B), packed B (128 rows x 64 B) and
+//    the group's 128 fp16 scales are fetched with direct-to-LDS buffer loads into a ring of kNS
+//    stages, kNS - 1 stages ahead. The lane offsets of the loads are fixed registers and the K
+//    advance is a scalar offset, so a load costs no vector instruction; the stage loop is
+//    unrolled by kNS, so every LDS read is a fixed base register plus an immediate.
 //  * Lane half h = l / 32 consumes k in [64 h, 64 h + 64) of the stage; K-step s the 16 k from
 //    64 h + 16 s on both operands (the int32 sum over a group is order-free).
 //  * At the start of group g each block's int32 accumulators still hold group g-1's sum; the
 //    block is folded into its fp32 accumulators just before its first MFMA of group g, so the
 //    fold of one block issues while the previous block's MFMA executes (a wave issues in order:
-//    MFMAs issued back to back would leave the VALU work serialised behind them). The next
-//    K-step's A fragment reads and nibble unpack are interleaved with the MFMAs the same way.
+//    MFMAs issued back to back would leave the VALU work serialised behind them). The scale of
+//    group g-1 was read from its stage during group g-1. The next K-step's A fragment reads and
+//    nibble unpack are interleaved with the MFMAs the same way.
 // LDS rows: A 128 B with chunk c at slot c ^ ((r >> 1) & 7); B 64 B with chunk c at slot
 // c ^ ((r >> 2) & 3) -- conflict-free for sixteen consecutive rows read at one chunk.
 
@@ -41,11 +44,9 @@ constexpr int kBN = 128, kNS = 3;
 constexpr int kWaves = kBN / 32;
 constexpr int kThreads = kWaves * 64;
 constexpr int kStageB = kBN * 64;   // 8 KB packed
-constexpr int kScaleRing = 8;       // > kNS + 1: a slot is refilled only after its fold
 constexpr int kScaleBytes = kBN * 2;
 constexpr int kBLoads = kStageB / 1024 / kWaves;  // 2
 constexpr int kScaleLanes = kScaleBytes / kWaves / 16;  // lanes per wave fetching scales
-static_assert(kScaleRing >= kNS + 2, "scale slot refilled before it is folded");
 static_assert(kBLoads * kWaves * 16 == kBN, "load split");
 
 template <int kBM_>
@@ -54,12 +55,13 @@ struct W4Cfg {
   static constexpr int kBI = kBM / 32;                         // MFMA blocks per wave along M
   static constexpr int kOcc = kBM == 128 ? 2 : 3;              // workgroups per CU
   static constexpr int kStageA = kBM * 128;
-  static constexpr int kStage = kStageA + kStageB;
-  static constexpr int kLds = kNS * kStage + kScaleRing * kScaleBytes;
+  static constexpr int kStage = kStageA + kStageB + kScaleBytes;  // A | packed B | scales
+  static constexpr int kLds = kNS * kStage;
   static constexpr int kALoads = kStageA / 1024 / kWaves;      // direct-to-LDS loads per wave per stage
   static constexpr int kLoads = kALoads + kBLoads + 1;         // + the wave's share of the scales
   static_assert(kALoads * kWaves * 8 == kBM, "load split");
   static_assert(kOcc * kLds <= 160 * 1024, "LDS per CU");
+  static_assert((kNS - 1) * kStage + (kBI - 1) * 32 * 128 < 65536, "LDS read offsets fit the 16-bit immediate");
 };
 
 struct Tile {
@@ -86,23 +88,33 @@ MXQ_DEVICE Tile tile_of(const W4Args& p) {
   return Tile{(int64_t)(first + in % gm) * kBM, (int64_t)(in / gm) * kBN};
 }
 
+// A 16-bit LDS read issued as inline assembly, like lds_read_b128 (its wait is placed by hand).
+template <int kOff>
+MXQ_DEVICE uint32_t lds_read_u16(uint32_t addr) {
+  uint32_t r;
+  __asm__ volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(kOff));
+  return r;
+}
+
 template <int kOut, bool kPrepared, int kTileM>
 __global__ __launch_bounds__(kThreads, W4Cfg<kTileM>::kOcc) void w4a8_g128_kernel(W4Args p) {
   typedef W4Cfg<kTileM> C;
   constexpr int kBM = C::kBM, kBI = C::kBI, kStageA = C::kStageA, kStage = C::kStage, kLds = C::kLds;
   constexpr int kALoads = C::kALoads, kLoads = C::kLoads;
   __shared__ __attribute__((aligned(16))) char lds[kLds];
-  char* const scale_ring = lds + kNS * kStage;
 
   const Tile tile = tile_of<kBM>(p);
   const int64_t m0 = tile.m0, n0 = tile.n0;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);  // scalar: LDS destinations are scalar arithmetic
   const int lr = lane & 31, lh = lane >> 5;
   const int64_t khalf = p.K / 2;
   const int ktiles = (int)(p.K / 128);
 
-  // ---- direct-to-LDS sources: 32-bit byte offsets of this lane from a wave-uniform base that
-  // advances with K (the launcher guarantees M*K and N*K/2 fit in 31 bits).
+  // ---- direct-to-LDS sources: raw buffers over A, the packed weights and the scales (the
+  // launcher guarantees each spans fewer than 2^31 bytes), a fixed 32-bit byte offset per lane
+  // and load, and the K advance as the scalar offset.
+  const int a_bytes = (int)(p.M * p.K), b_bytes = (int)(p.N * khalf), s_bytes = (int)(p.N * ktiles * 2);
   uint32_t a_off[kALoads], b_off[kBLoads];
 #pragma unroll
   for (int t = 0; t < kALoads; ++t) {
@@ -116,25 +128,23 @@ __global__ __launch_bounds__(kThreads, W4Cfg<kTileM>::kOcc) void w4a8_g128_kerne
     const int c = (lane & 3) ^ ((r >> 2) & 3);
     b_off[t] = (uint32_t)(min(n0 + r, p.N - 1) * khalf + c * 16);
   }
-  // wave w fetches scale bytes [64 w, 64 w + 64) of the group's row of kBN (8 per lane).
+  // wave w fetches scale bytes [64 w, 64 w + 64) of the group's row of kBN (16 per lane).
   const int64_t s_col = n0 + wave * 32 + lane * 8;
   const uint32_t s_off = (uint32_t)((s_col < p.N ? s_col : 0) * 2);
 
-  auto issue_stage = [&](int kt) {
-    char* st = lds + (kt % kNS) * kStage;
-    const int64_t k0 = (int64_t)kt * 128;
-    const char* abase = reinterpret_cast<const char*>(p.a) + k0;
-    const char* bbase = reinterpret_cast<const char*>(p.w) + k0 / 2;
-    const char* sbase = reinterpret_cast<const char*>(p.gs + (int64_t)kt * p.N);
+  // Stage kt into ring slot kSlot (= kt % kNS).
+  auto issue_stage = [&](int kt, auto SlotC) {
+    constexpr int kSlot = decltype(SlotC)::value;
+    char* st = lds + kSlot * kStage;
+    const int ka = kt * 128, kb = kt * 64, ksc = kt * (int)p.N * 2;
 #pragma unroll
     for (int t = 0; t < kALoads; ++t)
-      __builtin_amdgcn_global_load_lds((gptr_t)(abase + a_off[t]), (lptr_t)(st + (wave * kALoads + t) * 1024), 16, 0, 0);
+      buffer_load_lds16(p.a, a_bytes, (lptr_t)(st + (wv * kALoads + t) * 1024), a_off[t], ka);
 #pragma unroll
     for (int t = 0; t < kBLoads; ++t)
-      __builtin_amdgcn_global_load_lds((gptr_t)(bbase + b_off[t]),
-                                       (lptr_t)(st + kStageA + (wave * kBLoads + t) * 1024), 16, 0, 0);
-    char* sd = scale_ring + (kt & (kScaleRing - 1)) * kScaleBytes + wave * (kScaleBytes / kWaves);
-    if (lane < kScaleLanes) __builtin_amdgcn_global_load_lds((gptr_t)(sbase + s_off), (lptr_t)sd, 16, 0, 0);
+      buffer_load_lds16(p.w, b_bytes, (lptr_t)(st + kStageA + (wv * kBLoads + t) * 1024), b_off[t], kb);
+    if (lane < kScaleLanes)
+      buffer_load_lds16(p.gs, s_bytes, (lptr_t)(st + kStageA + kStageB + wv * (kScaleBytes / kWaves)), s_off, ksc);
   };
 
   v16i acc[kBI];
@@ -146,21 +156,27 @@ __global__ __launch_bounds__(kThreads, W4Cfg<kTileM>::kOcc) void w4a8_g128_kerne
     for (int r = 0; r < 16; ++r) facc[i][r] = 0.0f;
   }
 
+  // LDS read bases (the ring slot and the block are immediates): A for K-steps 0..3, the two B
+  // chunks, and this lane's channel scale.
   const uint32_t lds_addr = (uint32_t)(uintptr_t)(lptr_t)lds;
-  const uint32_t a_row = (uint32_t)lr * 128;  // block i adds i * 32 rows
   const int a_f = (lr >> 1) & 7;
-  const uint32_t b_row = (uint32_t)kStageA + (uint32_t)(wave * 32 + lr) * 64;
-  const int b_f = (lr >> 2) & 3;
-  const uint32_t b_lo = (uint32_t)(((2 * lh) ^ b_f) << 4), b_hi = (uint32_t)(((2 * lh + 1) ^ b_f) << 4);
-  const int s_idx = wave * 32 + lr;  // this lane's channel within the tile
-
+  uint32_t a_base[4];
 #pragma unroll
-  for (int s = 0; s < kNS - 1; ++s)
-    if (s < ktiles) issue_stage(s);
-  if (ktiles >= kNS - 1)
-    wait_vmcnt<(kNS - 2) * kLoads>();
-  else
+  for (int s = 0; s < 4; ++s) a_base[s] = lds_addr + (uint32_t)lr * 128 + (uint32_t)(((lh * 4 + s) ^ a_f) << 4);
+  const int b_f = (lr >> 2) & 3;
+  const uint32_t b_row = lds_addr + (uint32_t)kStageA + (uint32_t)(wave * 32 + lr) * 64;
+  const uint32_t b_base0 = b_row + (uint32_t)(((2 * lh) ^ b_f) << 4);
+  const uint32_t b_base1 = b_row + (uint32_t)(((2 * lh + 1) ^ b_f) << 4);
+  const int s_idx = wave * 32 + lr;  // this lane's channel within the tile
+  const uint32_t s_base = lds_addr + (uint32_t)(kStageA + kStageB + s_idx * 2);
+
+  issue_stage(0, std::integral_constant<int, 0>{});
+  if (ktiles > 1) {
+    issue_stage(1, std::integral_constant<int, 1>{});
+    wait_vmcnt<kLoads>();
+  } else {
     wait_vmcnt<0>();
+  }
   barrier_no_drain();
 
   auto unpack_step = [&](const v4i (&bq)[2], int s) {
@@ -175,32 +191,27 @@ __global__ __launch_bounds__(kThreads, W4Cfg<kTileM>::kOcc) void w4a8_g128_kerne
     return v4i{(int)o0, (int)o1, (int)o2, (int)o3};
   };
 
-  // One stage = group kt. At K-step 0, block i's accumulators still hold group kt-1's sum: they
-  // are folded (16 x cvt + fma) right before block i's first MFMA of group kt, so each fold
-  // issues while the previous block's MFMA executes. The A fragment of block i for K-step s+1
-  // is read right after block i's MFMA of step s; the next step's nibble unpack follows the
-  // second MFMA of each step.
-  auto stage = [&](int kt) {
-    const uint32_t st = lds_addr + (uint32_t)((kt % kNS) * kStage);
+  float sc = 0.0f;  // scale of the previous group; zero before the first (an exact no-op fold of zeros)
+  // One stage = group kt, in ring slot kSlot = kt % kNS. At K-step 0, block i's accumulators
+  // still hold group kt-1's sum: they are folded (16 x cvt + fma) right before block i's first
+  // MFMA of group kt, so each fold issues while the previous block's MFMA executes. The A
+  // fragment of block i for K-step s+1 is read right after block i's MFMA of step s; the next
+  // step's nibble unpack follows the second MFMA of each step.
+  auto stage = [&](int kt, auto SlotC) {
+    constexpr int kSlot = decltype(SlotC)::value;
+    constexpr int so = kSlot * kStage;
     v4i bq[2];
-    bq[0] = lds_read_b128<0>(st + b_row + b_lo);
-    bq[1] = lds_read_b128<0>(st + b_row + b_hi);
+    bq[0] = lds_read_b128<so>(b_base0);
+    bq[1] = lds_read_b128<so>(b_base1);
     v4i fa[kBI];
-    {
-      const uint32_t x = (uint32_t)(((lh * 4) ^ a_f) << 4);
-      static_for<kBI>([&](auto I) { fa[decltype(I)::value] = lds_read_b128<decltype(I)::value * 32 * 128>(st + a_row + x); });
-    }
-    // Scale of group kt-1; zero before the first group (an exact no-op fold of zeros).
-    const uint16_t* srow =
-        reinterpret_cast<const uint16_t*>(scale_ring + ((kt - 1) & (kScaleRing - 1)) * kScaleBytes);
-    const float sc = kt > 0 ? f16_to_f32(srow[s_idx]) : 0.0f;
-    if (kt + kNS - 1 < ktiles) issue_stage(kt + kNS - 1);
+    static_for<kBI>([&](auto I) { fa[decltype(I)::value] = lds_read_b128<so + decltype(I)::value * 32 * 128>(a_base[0]); });
+    const uint32_t sraw = lds_read_u16<so>(s_base);  // this group's scale, folded during the next group
+    if (kt + kNS - 1 < ktiles) issue_stage(kt + kNS - 1, std::integral_constant<int, (kSlot + kNS - 1) % kNS>{});
     wait_lgkm<0>();
     __builtin_amdgcn_sched_barrier(0);
     v4i fb = unpack_step(bq, 0);
     static_for<4>([&](auto S) {
       constexpr int s = decltype(S)::value;
-      const uint32_t xn = (uint32_t)(((lh * 4 + s + 1) ^ a_f) << 4);  // chunk of K-step s+1
       v4i fb_next;
       static_for<kBI>([&](auto I) {
         constexpr int i = decltype(I)::value;
@@ -216,13 +227,14 @@ __global__ __launch_bounds__(kThreads, W4Cfg<kTileM>::kOcc) void w4a8_g128_kerne
         __builtin_amdgcn_sched_barrier(0);
         acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb, s == 0 ? v16i{} : acc[i], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (s < 3) fa[i] = lds_read_b128<i * 32 * 128>(st + a_row + xn);
+        if constexpr (s < 3) fa[i] = lds_read_b128<so + i * 32 * 128>(a_base[s + 1]);
         if constexpr (i == 1 && s < 3) fb_next = unpack_step(bq, s + 1);
         __builtin_amdgcn_sched_barrier(0);
       });
       if constexpr (s < 3) fb = fb_next;
     });
-    // Stage kt+1 has landed (later stages may stay in flight); buffer kt % kNS is free.
+    sc = f16_to_f32((uint16_t)sraw);
+    // Stage kt+1 has landed (later stages may stay in flight); slot kSlot is free.
     if (kt + kNS - 1 < ktiles)
       wait_vmcnt<(kNS - 2) * kLoads>();
     else if (kt + kNS - 2 < ktiles)
@@ -234,16 +246,19 @@ __global__ __launch_bounds__(kThreads, W4Cfg<kTileM>::kOcc) void w4a8_g128_kerne
     barrier_no_drain();
   };
 
-  for (int kt = 0; kt < ktiles; ++kt) stage(kt);
-  {
-    const int g = ktiles - 1;
-    const uint16_t* srow = reinterpret_cast<const uint16_t*>(scale_ring + (g & (kScaleRing - 1)) * kScaleBytes);
-    const float sc = f16_to_f32(srow[s_idx]);
-#pragma unroll
-    for (int i = 0; i < kBI; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) facc[i][r] = fmaf((float)acc[i][r], sc, facc[i][r]);
+  static_assert(kNS == 3, "the stage loop is unrolled by the ring depth");
+  int kt = 0;
+  for (; kt + kNS <= ktiles; kt += kNS) {
+    stage(kt, std::integral_constant<int, 0>{});
+    stage(kt + 1, std::integral_constant<int, 1>{});
+    stage(kt + 2, std::integral_constant<int, 2>{});
   }
+  if (kt < ktiles) stage(kt, std::integral_constant<int, 0>{});
+  if (kt + 1 < ktiles) stage(kt + 1, std::integral_constant<int, 1>{});
+#pragma unroll
+  for (int i = 0; i < kBI; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) facc[i][r] = fmaf((float)acc[i][r], sc, facc[i][r]);
 
   // ---- epilogue: y = out(facc * (xs / 16)); y = out(y + bias). The main loop's last barrier
   // left the LDS free: the tile's row scales go there first (every global read of the
@@ -291,9 +306,18 @@ __global__ __launch_bounds__(kThreads, W4Cfg<kTileM>::kOcc) void w4a8_g128_kerne
     if (vec && gcol + kPerElem <= p.N) {
       *reinterpret_cast<v4u*>(dst) = v;
     } else {
-      const char* src = reinterpret_cast<const char*>(&v);
-      for (int e = 0; e < kPerElem && gcol + e < p.N; ++e)
-        for (int b = 0; b < kE; ++b) dst[e * kE + b] = src[e * kE + b];
+      // Element by element from the register words (taking the address of v would place it in
+      // memory, and the compiler then moves such per-thread arrays into LDS).
+#pragma unroll
+      for (int e = 0; e < kPerElem; ++e) {
+        if (gcol + e < p.N) {
+          const uint32_t word = v[e * kE / 4];
+          if constexpr (kE == 4)
+            *reinterpret_cast<uint32_t*>(dst + e * 4) = word;
+          else
+            *reinterpret_cast<uint16_t*>(dst + e * 2) = (uint16_t)(word >> (16 * (e & 1)));
+        }
+      }
     }
   }
 }
