@@ -36,7 +36,7 @@ sys.path.insert(0, os.path.join(ROOT, "x-minimaxh3_amd"))
 
 import mx_qlinear  # noqa: E402
 from mx_qlinear import _lib  # noqa: E402
-from mx_qlinear.ops import _p, _stream  # noqa: E402
+from mx_qlinear.ops import _gemm_ws, _p, _stream  # noqa: E402
 
 INT8_PEAK_TOPS = 5000.0   # MI355X dense INT8 MFMA
 HBM_PEAK_GBS = 8000.0     # MI355X HBM3E
@@ -157,12 +157,12 @@ class FfnWorkload:
         _lib.call("mxq_fill_f32", _p(ws.hmax), 0.0, m, st)
         with t("fc1_gemm"):
             _lib.call("mxq_int8_gemm_dequant_gelu_absmax", _p(ws.xq), _p(self.w1), _p(ws.xs), _p(self.s1),
-                      h, _p(self.b1), _p(ws.h), _p(ws.hmax), m, h, k, h, st)
+                      h, _p(self.b1), _p(ws.h), _p(ws.hmax), m, h, k, h, *_gemm_ws(self.dev), st)
         with t("requant"):
             _lib.call("mxq_quantize_int8_rowwise_absmax", _p(ws.h), _p(ws.hmax), _p(ws.hq), _p(ws.hs), m, h, st)
         with t("fc2_gemm"):
             _lib.call("mxq_int8_gemm_dequant", _p(ws.hq), _p(self.w2), _p(ws.hs), _p(self.s2), k, _p(self.b2),
-                      _p(self.out), m, k, h, k, _lib.DTYPE_BF16, st)
+                      _p(self.out), m, k, h, k, _lib.DTYPE_BF16, *_gemm_ws(self.dev), st)
 
     def ops_per_step(self):
         return 2 * 2 * self.m * self.k * self.hidden
@@ -234,7 +234,8 @@ class QkvWorkload:
                       _p(self.xq), _p(self.xs), None, self.m, self.k, st)
         with t("qkv_gemm"):
             _lib.call("mxq_int8_gemm_dequant", _p(self.xq), _p(self.w), _p(self.xs), _p(self.s), self.n,
-                      _p(self.b), _p(self.out), self.m, self.n, self.k, self.n, _lib.DTYPE_BF16, st)
+                      _p(self.b), _p(self.out), self.m, self.n, self.k, self.n, _lib.DTYPE_BF16,
+                      *_gemm_ws(self.dev), st)
 
     def ops_per_step(self):
         return 2 * self.m * self.n * self.k
@@ -409,7 +410,8 @@ class LinearC1Workload:
                       self.k, _lib.ACT_NONE, st)
         with t("gemm"):
             _lib.call("mxq_int8_gemm_dequant", _p(self.xq), _p(w), _p(self.xs), _p(s), self.n,
-                      _p(self.b), _p(self.out), self.m, self.n, self.k, self.n, _lib.DTYPE_BF16, st)
+                      _p(self.b), _p(self.out), self.m, self.n, self.k, self.n, _lib.DTYPE_BF16,
+                      *_gemm_ws(self.dev), st)
 
     def ops_per_step(self):
         return 2 * self.m * self.n * self.k
@@ -501,13 +503,13 @@ class H3MlpWorkload:
                       _p(mod.rows), mod.eps, None, _p(self.q1), _p(self.xs1), m, d, 256, st)
         with t("fc1_swiglu_gemm"):
             _lib.call("mxq_int8_gemm_dequant_swiglu", _p(self.q1), _p(self.fc1.qweight), _p(self.xs1),
-                      _p(self.fc1.scale), 2 * f, _p(self.fc1.bias), _p(self.h), m, 2 * f, d, f, st)
+                      _p(self.fc1.scale), 2 * f, _p(self.fc1.bias), _p(self.h), m, 2 * f, d, f, *_gemm_ws(self.dev), st)
         with t("convrot_quant"):
             _lib.call("mxq_quantize_int8_rowwise_convrot", _p(self.h), _lib.DTYPE_BF16, _p(self.q2), _p(self.xs2),
                       m, f, 256, _lib.ACT_NONE, st)
         with t("fc2_gated_residual"):
             _lib.call("mxq_int8_gemm_gated_residual", _p(self.q2), _p(self.w2), _p(self.xs2), _p(self.s2), d,
-                      _p(self.b2), _p(self.res), d, _p(mod.gate), d, 3, _p(mod.rows), m, d, f, st)
+                      _p(self.b2), _p(self.res), d, _p(mod.gate), d, 3, _p(mod.rows), m, d, f, *_gemm_ws(self.dev), st)
 
     def ops_per_step(self):
         return 2 * self.m * self.d * 2 * self.inner + 2 * self.m * self.inner * self.d
@@ -575,7 +577,7 @@ class H3QkvWorkload:
                       _p(mod.rows), mod.eps, None, _p(self.q), _p(self.xs), m, d, 256, st)
         with t("qkv_gemm"):
             _lib.call("mxq_int8_gemm_dequant", _p(self.q), _p(self.w), _p(self.xs), _p(self.s), n, _p(self.b),
-                      _p(self.out), m, n, d, n, _lib.DTYPE_BF16, st)
+                      _p(self.out), m, n, d, n, _lib.DTYPE_BF16, *_gemm_ws(self.dev), st)
 
     def ops_per_step(self):
         return 2 * self.m * self.n * self.d
@@ -661,7 +663,7 @@ class W4A8RefQkvWorkload:
                           _p(self.codebook), _p(self.work), cols, d, g, st)
             with timer.span("gemm"):
                 _lib.call("mxq_int8_gemm_dequant", _p(self.q), _p(self.work), _p(self.xs), _p(self.s_ch[n0:]), cols,
-                          _p(self.b[n0:]), _p(self.out[:, n0:]), m, cols, d, n, _lib.DTYPE_BF16, st)
+                          _p(self.b[n0:]), _p(self.out[:, n0:]), m, cols, d, n, _lib.DTYPE_BF16, None, 0, st)
 
     def ops_per_step(self):
         return 2 * self.m * self.n * self.d

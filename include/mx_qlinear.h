@@ -4,8 +4,9 @@
  * One shared library, libmx_qlinear.so, built by hipcc for gfx950 only. Every entry
  * point takes raw device pointers, element counts and a hipStream_t passed as void*,
  * enqueues its kernels on that stream and returns without synchronising. No entry point
- * allocates device memory: workspaces are the caller's (mxq_w4a8_codebook_gemm) or a static
- * device array of the library (mxq_w4a8_codebook_gemm_noalloc). Return value: MXQ_OK (0) or a negative error
+ * allocates device memory: workspaces are the caller's (the INT8 GEMMs' tile-queue counters,
+ * mxq_w4a8_codebook_gemm's decode chunk) or a static device array of the library
+ * (mxq_w4a8_codebook_gemm_noalloc). Return value: MXQ_OK (0) or a negative error
  * code; mxq_last_error() then describes the failure (thread-local string).
  *
  * Reference paths are relative to the reference tree; CK stands for
@@ -22,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MXQ_ABI_VERSION 1
+#define MXQ_ABI_VERSION 2
 
 /* Return codes. */
 #define MXQ_OK 0
@@ -101,13 +102,39 @@ int mxq_adaln_quantize_int8(const void* x, const void* scale, const void* shift,
                             void* stream);
 
 /*
+ * Tile-queue workspace of the INT8 GEMMs below (the `workspace, workspace_bytes` pair before the
+ * stream). The hardware deals workgroups to the 8 XCDs round-robin, so a static tile order gives
+ * every XCD 1/8 of the tiles, and the slowest XCD sets the GEMM's time. With a workspace, the
+ * last eighth of each XCD's tiles is claimed at run time by whichever XCD's workgroups get there
+ * first (counters in the workspace); the tiles and their outputs are the same, bit for bit.
+ * NULL runs the static order. The workspace is MXQ_GEMM_WORKSPACE_BYTES of device memory,
+ * 256-byte aligned and zero before its first use; every call leaves it zero again. Calls that
+ * share a workspace must be ordered (one workspace per stream): overlapping calls race on it.
+ * The reference keeps a per-(device, stream) workspace inside its launchers for the same kind
+ * of state (CK/backends/cuda/ops/cutlass_gemm_int8.cu:39-55); here the caller owns it.
+ */
+#define MXQ_GEMM_WORKSPACE_BYTES ((int64_t)4096)
+
+/*
+ * Launch plan the INT8 GEMMs below choose for an M x N x K problem (table_epilogue: 1 for the
+ * GELU and SwiGLU epilogues, 0 otherwise) given workspace_bytes of tile-queue workspace (0:
+ * none): plan[0] tile edge (256 or 128), plan[1] workgroups, plan[2] tiles, plan[3] tiles per
+ * XCD claimed at run time (0: static order), plan[4] workgroups per XCD. Host only; no
+ * reference counterpart (CUTLASS's Gemm::get_workspace_size is the nearest,
+ * CK/backends/cuda/ops/cutlass_gemm_int8.cu:318); tests and tuning read it.
+ */
+int mxq_int8_gemm_plan(int64_t M, int64_t N, int64_t K, int table_epilogue, int64_t workspace_bytes,
+                       int64_t* plan);
+
+/*
  * Raw INT8 GEMM: C[m, n] = sum_k A[m, k] * B[n, k] in int32.
  *   a [M, K] int8 row-major; b [N, K] int8 row-major (the checkpoint's [out, in] layout);
  *   c [M, ldc] int32. K must be a multiple of 16.
  * Replaces: torch._int_mm in _int8_matmul_accumulate, CK/backends/eager/quantization.py:749-782.
  */
 int mxq_int8_gemm_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M, int64_t N,
-                      int64_t K, int64_t ldc, void* stream);
+                      int64_t K, int64_t ldc, void* workspace, int64_t workspace_bytes,
+                      void* stream);
 
 /*
  * INT8 GEMM with the fused dequant epilogue:
@@ -121,7 +148,8 @@ int mxq_int8_gemm_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M, i
  */
 int mxq_int8_gemm_dequant(const int8_t* a, const int8_t* b, const float* xs, const float* ws,
                           int64_t ws_numel, const void* bias, void* d, int64_t M, int64_t N,
-                          int64_t K, int64_t ldd, int out_dtype, void* stream);
+                          int64_t K, int64_t ldd, int out_dtype, void* workspace,
+                          int64_t workspace_bytes, void* stream);
 
 /*
  * fc1 of the INT8 FFN chain: the bf16 dequant epilogue above, then tanh-GELU in bf16,
@@ -134,7 +162,8 @@ int mxq_int8_gemm_dequant(const int8_t* a, const int8_t* b, const float* xs, con
 int mxq_int8_gemm_dequant_gelu_absmax(const int8_t* a, const int8_t* b, const float* xs,
                                       const float* ws, int64_t ws_numel, const void* bias_bf16,
                                       void* h_bf16, float* row_absmax, int64_t M, int64_t N,
-                                      int64_t K, int64_t ldh, void* stream);
+                                      int64_t K, int64_t ldh, void* workspace,
+                                      int64_t workspace_bytes, void* stream);
 
 /*
  * SwiGLU fc1: INT8 GEMM + the bf16 dequant epilogue of mxq_int8_gemm_dequant, then
@@ -150,7 +179,7 @@ int mxq_int8_gemm_dequant_gelu_absmax(const int8_t* a, const int8_t* b, const fl
 int mxq_int8_gemm_dequant_swiglu(const int8_t* a, const int8_t* b, const float* xs,
                                  const float* ws, int64_t ws_numel, const void* bias_bf16,
                                  void* h_bf16, int64_t M, int64_t N, int64_t K, int64_t ldh,
-                                 void* stream);
+                                 void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * INT8 GEMM + dequant epilogue + gated residual update, in place:
@@ -168,7 +197,8 @@ int mxq_int8_gemm_gated_residual(const int8_t* a, const int8_t* b, const float* 
                                  const float* ws, int64_t ws_numel, const void* bias_bf16,
                                  void* residual_bf16, int64_t ldr, const void* gate_bf16,
                                  int64_t ldg, int64_t gate_count, const int32_t* gate_rows,
-                                 int64_t M, int64_t N, int64_t K, void* stream);
+                                 int64_t M, int64_t N, int64_t K, void* workspace,
+                                 int64_t workspace_bytes, void* stream);
 
 /*
  * M = 1 INT8 linear: the row quantizer of x (after the optional input activation and ConvRot

@@ -61,11 +61,11 @@ def test_library_exports_every_declared_symbol(lib):
 def test_abi_version_and_error_string(lib):
     from mx_qlinear import _lib
 
-    assert lib.mxq_abi_version() == 1
+    assert lib.mxq_abi_version() == _lib.ABI_VERSION == 2
     lib.mxq_last_error.restype = ctypes.c_char_p
     assert isinstance(lib.mxq_last_error(), bytes)
     # a rejected call leaves a message naming the problem
-    rc = _lib.load().mxq_int8_gemm_i32(None, None, None, -1, 4, 16, 4, None)
+    rc = _lib.load().mxq_int8_gemm_i32(None, None, None, -1, 4, 16, 4, None, 0, None)
     assert rc == _lib.MXQ_ERR_INVALID
     assert b"negative" in lib.mxq_last_error()
 
@@ -85,31 +85,77 @@ def test_gemm_shape_checks(lib, args, code):
 
     m, n, k, ldc = args
     dummy = ctypes.c_void_p(16)  # never dereferenced: every case is rejected on the host
-    rc = lib.mxq_int8_gemm_i32(dummy, dummy, dummy, m, n, k, ldc, None)
+    rc = lib.mxq_int8_gemm_i32(dummy, dummy, dummy, m, n, k, ldc, None, 0, None)
     assert rc == getattr(_lib, "MXQ_ERR_" + code)
 
 
 def test_empty_gemm_is_a_no_op(lib):
     from mx_qlinear import _lib
 
-    assert lib.mxq_int8_gemm_i32(None, None, None, 0, 0, 16, 0, None) == _lib.MXQ_OK
+    assert lib.mxq_int8_gemm_i32(None, None, None, 0, 0, 16, 0, None, 0, None) == _lib.MXQ_OK
 
 
 def test_dequant_rejects_bad_scale_count_and_dtype(lib):
     from mx_qlinear import _lib
 
     d = ctypes.c_void_p(256)
-    rc = lib.mxq_int8_gemm_dequant(d, d, d, d, 3, None, d, 16, 16, 16, 16, _lib.DTYPE_BF16, None)
+    rc = lib.mxq_int8_gemm_dequant(d, d, d, d, 3, None, d, 16, 16, 16, 16, _lib.DTYPE_BF16, None, 0, None)
     assert rc == _lib.MXQ_ERR_INVALID
-    rc = lib.mxq_int8_gemm_dequant(d, d, d, d, 16, None, d, 16, 16, 16, 16, 7, None)
+    rc = lib.mxq_int8_gemm_dequant(d, d, d, d, 16, None, d, 16, 16, 16, 16, 7, None, 0, None)
     assert rc == _lib.MXQ_ERR_UNSUPPORTED
+
+
+def test_gemm_rejects_a_misaligned_workspace(lib):
+    from mx_qlinear import _lib
+
+    d = ctypes.c_void_p(256)
+    rc = lib.mxq_int8_gemm_i32(d, d, d, 16, 16, 16, 16, ctypes.c_void_p(4096 + 64), 1 << 20, None)
+    assert rc == _lib.MXQ_ERR_INVALID
+    assert b"256-byte aligned" in lib.mxq_last_error()
+
+
+def test_gemm_workspace_size_matches_the_header():
+    from mx_qlinear import _lib
+
+    text = (ROOT / "include" / "mx_qlinear.h").read_text()
+    assert "#define MXQ_GEMM_WORKSPACE_BYTES ((int64_t)4096)" in text
+    assert _lib.GEMM_WORKSPACE_BYTES == 4096
+    assert f"#define MXQ_ABI_VERSION {_lib.ABI_VERSION}" in text
 
 
 def test_python_maps_codes_to_the_reference_exceptions(lib):
     from mx_qlinear import _lib
 
     with pytest.raises(ValueError):
-        _lib.call("mxq_int8_gemm_i32", None, None, None, -1, 4, 16, 4, None)
+        _lib.call("mxq_int8_gemm_i32", None, None, None, -1, 4, 16, 4, None, 0, None)
     with pytest.raises(RuntimeError):
         d = ctypes.c_void_p(16)
-        _lib.call("mxq_int8_gemm_i32", d, d, d, 16, 16, 24, 16, None)
+        _lib.call("mxq_int8_gemm_i32", d, d, d, 16, 16, 24, 16, None, 0, None)
+
+
+@pytest.mark.parametrize(
+    "m,n,k,table,tile,queued",
+    [
+        (75600, 5120, 20480, False, 256, True),   # FFN fc2 at 720p
+        (75600, 20480, 5120, True, 256, True),    # FFN fc1 (GELU epilogue: 256-tiles always)
+        (75600, 15360, 5120, False, 256, True),   # QKV at 720p
+        (8192, 5120, 5120, False, 128, True),     # 2.5 rounds of 128-tiles
+        (1024, 3072, 3072, False, 128, False),    # under two rounds: static order
+    ],
+)
+def test_gemm_plan_queues_large_problems(lib, m, n, k, table, tile, queued):
+    from mx_qlinear import _lib
+
+    plan = _lib.gemm_plan(m, n, k, table)
+    assert plan["tile"] == tile
+    tiles = -(-m // tile) * -(-n // tile)
+    assert plan["tiles"] == tiles
+    if queued:
+        per = tiles // 8
+        assert plan["pool"] == -(-per // 8)
+        assert plan["wg_per_xcd"] == per + (tiles % 8 > 0) + plan["pool"]
+        assert plan["grid"] == 8 * plan["wg_per_xcd"]
+    else:
+        assert plan["pool"] == 0 and plan["grid"] == tiles
+    static = _lib.gemm_plan(m, n, k, table, workspace_bytes=0)
+    assert static["pool"] == 0 and static["grid"] == tiles

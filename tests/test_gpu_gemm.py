@@ -84,7 +84,7 @@ def test_gemm_i32_strided_output(dev):
     from mx_qlinear.ops import _p, _stream
 
     ad, wd = a.to(dev), w.to(dev)
-    L.call("mxq_int8_gemm_i32", _p(ad), _p(wd), _p(c), m, n, k, ldc, _stream(dev))
+    L.call("mxq_int8_gemm_i32", _p(ad), _p(wd), _p(c), m, n, k, ldc, None, 0, _stream(dev))
     c = c.cpu().numpy()
     assert np.array_equal(c[:, :n], eager_np.int8_matmul(a.numpy(), w.numpy()))
     assert np.all(c[:, n:] == 7)

@@ -82,6 +82,11 @@ struct GemmArgs {
   const uint16_t* gate;
   const int32_t* gate_rows;
   int64_t ldr, ldg, gate_count;
+  // Balanced tile queue: the last `pool` tiles of each XCD's range are claimed at run time, by
+  // that XCD's workgroups first and then by any XCD's (see pick_tile). grid = 8 * wg_per_xcd;
+  // n_claim workgroups claim; counters (the caller's workspace) hold the claim counts.
+  int pool, wg_per_xcd, n_claim;
+  unsigned* counters;
 };
 
 // LDS operand layout: a tile row is 128 bytes = eight 16-byte chunks; chunk c of row r sits at
@@ -96,12 +101,9 @@ static __device__ __attribute__((aligned(16))) uint8_t kZeroChunk[16];
 
 // Tile order: first spread contiguous tile ranges over the 8 XCDs (workgroup ids are dealt to
 // XCDs round-robin), then walk each range in groups of kGroupM tile-rows so that the ~32 tiles
-// resident on one XCD share A and B panels in that XCD's L2.
-MXQ_DEVICE void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
-  const int num = tiles_m * tiles_n;
-  const int per = num / 8;
-  int t = bid;
-  if (bid < per * 8) t = (bid % 8) * per + bid / 8;
+// resident on one XCD share A and B panels in that XCD's L2. tile_walk maps a position t of
+// that order to its tile row and column.
+MXQ_DEVICE void tile_walk(int t, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int group = kGroupM * tiles_n;
   const int g = t / group;
   const int first_m = g * kGroupM;
@@ -109,6 +111,21 @@ MXQ_DEVICE void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn)
   const int in = t % group;
   tm = first_m + in % gm;
   tn = in / gm;
+}
+
+// Static order: workgroup bid takes position (bid % 8) * per + bid / 8, i.e. XCD x runs
+// positions [x * per, (x + 1) * per); the last num % 8 positions are taken in id order.
+MXQ_DEVICE int static_position(int bid, int num) {
+  const int per = num / 8;
+  return bid < per * 8 ? (bid % 8) * per + bid / 8 : bid;
+}
+
+// XCD x's range of positions in the balanced order: [start, start + count), the num % 8
+// leftover positions going one each to the first XCDs.
+MXQ_DEVICE void xcd_range(int x, int num, int& start, int& count) {
+  const int per = num / 8, rem = num % 8;
+  start = x * per + min(x, rem);
+  count = per + (x < rem ? 1 : 0);
 }
 
 // Direct-to-LDS stage loads (global_load_lds_dwordx4). One instruction fills 1 KB of LDS:
@@ -408,6 +425,51 @@ MXQ_DEVICE void gated_lines(const GemmArgs& p, char* buf, int64_t row0, int64_t 
   }
 }
 
+// ---- balanced tile queue ----
+// The hardware deals workgroup ids to the 8 XCDs round-robin, so with a static order each XCD
+// runs exactly 1/8 of the tiles, and the XCDs do not run at one speed: per-workgroup timestamps
+// of a 75600 x 5120 x 20480 GEMM gave mean tile times from 282 to 303 us by XCD, and the last
+// XCD finished 0.5 ms after the first. Here workgroup (x = bid % 8, k = bid / 8) takes position
+// start_x + k of its XCD's range while k < count_x - pool; the rest of the range (the pool) and
+// a few extra workgroups per XCD claim positions at run time: first from their own XCD's pool,
+// then from the other pools in turn. A fast XCD thus takes over the end of a slow one's range;
+// workgroups that find every pool empty exit. Claims are relaxed agent-scope atomics on the
+// pool counters (no data passes between workgroups, so no ordering is needed); the last
+// claiming workgroup of a launch resets the counters for the next one. Thread 0 claims, the
+// workgroup reads the result through lds[0] before the ring is used. Returns the position, or
+// -1 if the workgroup has nothing to do.
+MXQ_DEVICE int pick_tile(const GemmArgs& p, int num, char* lds) {
+  const int bid = blockIdx.x;
+  if (p.pool == 0) return static_position(bid, num);
+  const int x = bid & 7, k = bid >> 3;
+  int start, count;
+  xcd_range(x, num, start, count);
+  if (k < count - p.pool) return start + k;
+  volatile int* shared_pos = reinterpret_cast<volatile int*>(lds);
+  if (threadIdx.x == 0) {
+    int got = -1;
+    for (int j = 0; j < 8 && got < 0; ++j) {
+      const int y = (x + j) & 7;
+      const unsigned i = __hip_atomic_fetch_add(p.counters + y * 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (i < (unsigned)p.pool) {
+        int ys, yc;
+        xcd_range(y, num, ys, yc);
+        got = ys + yc - p.pool + (int)i;
+      }
+    }
+    const unsigned done = __hip_atomic_fetch_add(p.counters + 8 * 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (done == (unsigned)p.n_claim - 1) {  // every claim of this launch has been made
+      for (int y = 0; y < 8; ++y) __hip_atomic_exchange(p.counters + y * 32, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_exchange(p.counters + 8 * 32, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    *shared_pos = got;
+  }
+  __syncthreads();
+  const int pos = *shared_pos;
+  __syncthreads();  // read before the ring's first loads overwrite lds[0]
+  return pos;
+}
+
 template <int kEpi, int kOut, int kT>
 __global__ __launch_bounds__(kGemmThreads, kT == 256 ? 1 : 2) void gemm_i8_kernel(GemmArgs p) {
   typedef TileCfg<kT> C;
@@ -416,8 +478,10 @@ __global__ __launch_bounds__(kGemmThreads, kT == 256 ? 1 : 2) void gemm_i8_kerne
   static_assert(kT == 256 || (kEpi != kEpiGelu && kEpi != kEpiSwiGLU), "table epilogues need the 160 KB ring");
   __shared__ __attribute__((aligned(16))) char lds[C::kLds];
 
+  const int pos = pick_tile(p, p.tiles_m * p.tiles_n, lds);
+  if (pos < 0) return;
   int tm, tn;
-  tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  tile_walk(pos, p.tiles_m, p.tiles_n, tm, tn);
   const int64_t m0 = (int64_t)tm * kBM, n0 = (int64_t)tn * kBN;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int wm = wave >> 1, wn = wave & 1;
@@ -753,21 +817,60 @@ __global__ __launch_bounds__(kGemmThreads, kT == 256 ? 1 : 2) void gemm_i8_kerne
   }
 }
 
-template <int kEpi, int kOut>
-static int launch_gemm(const GemmArgs& args0, hipStream_t stream) {
-  GemmArgs args = args0;
-  // Problems with fewer 256-tiles than CUs run 128-tiles (four times as many workgroups). Larger
-  // ones run 128-tiles too when their rounds finish first: 256 CUs hold 256 workgroups of 256-tiles
-  // or 512 of 128-tiles, and a round of 128-tiles takes about 0.55 of a round of 256-tiles
-  // (measured at K = 4096-8192), so a last round of 256-tiles that is mostly empty is cheaper as
-  // 128-tiles (4096 x 5120: 1.25 rounds, 0.147 -> 0.117 ms) and a full one is not.
-  const int64_t big_tiles = ((args.M + 255) / 256) * ((args.N + 255) / 256);
-  const int64_t tiles128 = ((args.M + 127) / 128) * ((args.N + 127) / 128);
+// Balanced tile queue (pick_tile): each XCD's pool is 1/kPoolDiv of its range and each XCD
+// gets as many extra workgroups as its pool holds tiles; problems of fewer than two rounds of
+// tiles keep the static order.
+constexpr int kPoolDiv = 8;
+constexpr int kTileQueueBytes = 9 * 128;  // 8 pool counters and the claim count, a line each
+static_assert(MXQ_GEMM_WORKSPACE_BYTES >= kTileQueueBytes, "workspace holds the tile queue counters");
+
+// Launch plan of one GEMM: tile size, tile queue and grid.
+struct GemmPlan {
+  int tile;  // 256 or 128
+  int tiles_m, tiles_n;
+  int pool, wg_per_xcd, n_claim;
+  int64_t grid;
+};
+
+// Problems with fewer 256-tiles than CUs run 128-tiles (four times as many workgroups). Larger ones
+// run 128-tiles too when their rounds finish first: 256 CUs hold 256 workgroups of 256-tiles or 512
+// of 128-tiles, and a round of 128-tiles takes about 0.55 of a round of 256-tiles (measured at
+// K = 4096-8192), so a last round of 256-tiles that is mostly empty is cheaper as 128-tiles
+// (4096 x 5120: 1.25 rounds, 0.147 -> 0.117 ms) and a full one is not. The table epilogues (GELU,
+// SwiGLU) need the 256-tile ring. With a workspace, problems of two rounds or more balance their
+// tiles over the XCDs at run time (pick_tile).
+static GemmPlan plan_gemm(int64_t M, int64_t N, bool table, int64_t workspace_bytes) {
+  GemmPlan g{};
+  const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256);
+  const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
   const bool prefer128 = big_tiles < 256 || ((tiles128 + 511) / 512) * 11 < ((big_tiles + 255) / 256) * 20;
-  const bool small = kEpi != kEpiGelu && kEpi != kEpiSwiGLU && prefer128;
-  const int kt = small ? 128 : 256;
-  args.tiles_m = (int)((args.M + kt - 1) / kt);
-  args.tiles_n = (int)((args.N + kt - 1) / kt);
+  g.tile = !table && prefer128 ? 128 : 256;
+  g.tiles_m = (int)std::min<int64_t>((M + g.tile - 1) / g.tile, INT32_MAX);
+  g.tiles_n = (int)std::min<int64_t>((N + g.tile - 1) / g.tile, INT32_MAX);
+  const int64_t tiles = (int64_t)g.tiles_m * g.tiles_n;
+  g.grid = tiles;
+  const int64_t slots = g.tile == 256 ? 256 : 512;
+  if (workspace_bytes >= kTileQueueBytes && tiles >= 2 * slots && tiles <= INT32_MAX / 2) {
+    const int64_t per = tiles / 8, rem = tiles % 8;
+    g.pool = (int)((per + kPoolDiv - 1) / kPoolDiv);
+    g.wg_per_xcd = (int)(per + (rem ? 1 : 0) + g.pool);
+    g.grid = 8 * (int64_t)g.wg_per_xcd;
+    g.n_claim = (int)(g.grid - tiles + 8 * (int64_t)g.pool);
+  }
+  return g;
+}
+
+template <int kEpi, int kOut>
+static int launch_gemm(const GemmArgs& args0, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  GemmArgs args = args0;
+  const GemmPlan g = plan_gemm(args.M, args.N, kEpi == kEpiGelu || kEpi == kEpiSwiGLU, workspace ? workspace_bytes : 0);
+  if ((int64_t)g.tiles_m * g.tiles_n > INT32_MAX / 2) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "too many tiles");
+  args.tiles_m = g.tiles_m;
+  args.tiles_n = g.tiles_n;
+  args.pool = g.pool;
+  args.wg_per_xcd = g.wg_per_xcd;
+  args.n_claim = g.n_claim;
+  args.counters = g.pool ? reinterpret_cast<unsigned*>(workspace) : nullptr;
   const int elem = (kOut == 0 || kEpi == kEpiI32) ? 4 : 2;
   args.vec_store = ((uintptr_t)args.d % (4 * elem) == 0) && (args.ldd % 4 == 0);
   args.line_store = ((uintptr_t)args.d % 16 == 0) && ((args.ldd * elem) % 16 == 0);
@@ -775,16 +878,23 @@ static int launch_gemm(const GemmArgs& args0, hipStream_t stream) {
     args.vec_store = args.vec_store && ((uintptr_t)args.gate % 8 == 0) && (args.ldg % 4 == 0);
     args.line_store = args.line_store && ((uintptr_t)args.gate % 16 == 0) && (args.ldg % 8 == 0);
   }
-  const int64_t tiles = (int64_t)args.tiles_m * args.tiles_n;
-  if (tiles > INT32_MAX) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "too many tiles");
+  const unsigned grid = (unsigned)g.grid;
   if constexpr (kEpi != kEpiGelu && kEpi != kEpiSwiGLU) {
-    if (small) {
-      gemm_i8_kernel<kEpi, kOut, 128><<<(unsigned)tiles, kGemmThreads, 0, stream>>>(args);
+    if (g.tile == 128) {
+      gemm_i8_kernel<kEpi, kOut, 128><<<grid, kGemmThreads, 0, stream>>>(args);
       return mxq_check_launch("gemm_i8_kernel");
     }
   }
-  gemm_i8_kernel<kEpi, kOut, 256><<<(unsigned)tiles, kGemmThreads, 0, stream>>>(args);
+  gemm_i8_kernel<kEpi, kOut, 256><<<grid, kGemmThreads, 0, stream>>>(args);
   return mxq_check_launch("gemm_i8_kernel");
+}
+
+// The tile-queue workspace: NULL (static order) or 256-byte aligned.
+static int check_workspace(const void* workspace, int64_t workspace_bytes) {
+  if (!workspace) return MXQ_OK;
+  if (workspace_bytes < 0) return mxq_set_error(MXQ_ERR_INVALID, "negative workspace size");
+  if ((uintptr_t)workspace % 256) return mxq_set_error(MXQ_ERR_INVALID, "GEMM workspace must be 256-byte aligned");
+  return MXQ_OK;
 }
 
 static int check_gemm_shape(const int8_t* a, const int8_t* b, const void* d, int64_t M, int64_t N,
@@ -803,21 +913,36 @@ static int check_gemm_shape(const int8_t* a, const int8_t* b, const void* d, int
 
 using namespace mxq;
 
+extern "C" int mxq_int8_gemm_plan(int64_t M, int64_t N, int64_t K, int table_epilogue,
+                                  int64_t workspace_bytes, int64_t* plan) {
+  if (M <= 0 || N <= 0 || K <= 0 || !plan) return mxq_set_error(MXQ_ERR_INVALID, "GEMM plan needs a positive shape and an output");
+  const GemmPlan g = plan_gemm(M, N, table_epilogue != 0, workspace_bytes);
+  plan[0] = g.tile;
+  plan[1] = g.grid;
+  plan[2] = (int64_t)g.tiles_m * g.tiles_n;
+  plan[3] = g.pool;
+  plan[4] = g.wg_per_xcd;
+  return MXQ_OK;
+}
+
 extern "C" int mxq_int8_gemm_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M,
-                                 int64_t N, int64_t K, int64_t ldc, void* stream) {
+                                 int64_t N, int64_t K, int64_t ldc, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
   int rc = check_gemm_shape(a, b, c, M, N, K, ldc);
+  if (!rc) rc = check_workspace(workspace, workspace_bytes);
   if (rc) return rc;
   if (M == 0 || N == 0) return MXQ_OK;
   GemmArgs g{};
   g.a = a; g.b = b; g.d = c; g.M = M; g.N = N; g.K = K; g.ldd = ldc;
-  return launch_gemm<kEpiI32, 0>(g, (hipStream_t)stream);
+  return launch_gemm<kEpiI32, 0>(g, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 extern "C" int mxq_int8_gemm_dequant(const int8_t* a, const int8_t* b, const float* xs,
                                      const float* ws, int64_t ws_numel, const void* bias, void* d,
                                      int64_t M, int64_t N, int64_t K, int64_t ldd, int out_dtype,
-                                     void* stream) {
+                                     void* workspace, int64_t workspace_bytes, void* stream) {
   int rc = check_gemm_shape(a, b, d, M, N, K, ldd);
+  if (!rc) rc = check_workspace(workspace, workspace_bytes);
   if (rc) return rc;
   if (M == 0 || N == 0) return MXQ_OK;
   if (!xs || !ws) return mxq_set_error(MXQ_ERR_INVALID, "null scale pointer");
@@ -828,9 +953,9 @@ extern "C" int mxq_int8_gemm_dequant(const int8_t* a, const int8_t* b, const flo
   g.M = M; g.N = N; g.K = K; g.ldd = ldd; g.ws_per_channel = ws_numel == N && N != 1;
   hipStream_t st = (hipStream_t)stream;
   switch (out_dtype) {
-    case MXQ_DTYPE_F32: return launch_gemm<kEpiDequant, 0>(g, st);
-    case MXQ_DTYPE_F16: return launch_gemm<kEpiDequant, 1>(g, st);
-    case MXQ_DTYPE_BF16: return launch_gemm<kEpiDequant, 2>(g, st);
+    case MXQ_DTYPE_F32: return launch_gemm<kEpiDequant, 0>(g, workspace, workspace_bytes, st);
+    case MXQ_DTYPE_F16: return launch_gemm<kEpiDequant, 1>(g, workspace, workspace_bytes, st);
+    case MXQ_DTYPE_BF16: return launch_gemm<kEpiDequant, 2>(g, workspace, workspace_bytes, st);
     default: return mxq_set_error(MXQ_ERR_UNSUPPORTED, "output dtype code %d", out_dtype);
   }
 }
@@ -839,8 +964,10 @@ extern "C" int mxq_int8_gemm_dequant_gelu_absmax(const int8_t* a, const int8_t* 
                                                  const float* ws, int64_t ws_numel,
                                                  const void* bias_bf16, void* h_bf16,
                                                  float* row_absmax, int64_t M, int64_t N,
-                                                 int64_t K, int64_t ldh, void* stream) {
+                                                 int64_t K, int64_t ldh, void* workspace,
+                                                 int64_t workspace_bytes, void* stream) {
   int rc = check_gemm_shape(a, b, h_bf16, M, N, K, ldh);
+  if (!rc) rc = check_workspace(workspace, workspace_bytes);
   if (rc) return rc;
   if (M == 0 || N == 0) return MXQ_OK;
   if (!xs || !ws || !row_absmax) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
@@ -848,15 +975,16 @@ extern "C" int mxq_int8_gemm_dequant_gelu_absmax(const int8_t* a, const int8_t* 
   GemmArgs g{};
   g.a = a; g.b = b; g.xs = xs; g.ws = ws; g.bias = bias_bf16; g.d = h_bf16; g.row_absmax = row_absmax;
   g.M = M; g.N = N; g.K = K; g.ldd = ldh; g.ws_per_channel = ws_numel == N && N != 1;
-  return launch_gemm<kEpiGelu, 2>(g, (hipStream_t)stream);
+  return launch_gemm<kEpiGelu, 2>(g, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 extern "C" int mxq_int8_gemm_dequant_swiglu(const int8_t* a, const int8_t* b, const float* xs,
                                             const float* ws, int64_t ws_numel, const void* bias_bf16,
                                             void* h_bf16, int64_t M, int64_t N, int64_t K, int64_t ldh,
-                                            void* stream) {
+                                            void* workspace, int64_t workspace_bytes, void* stream) {
   if (N % 32) return mxq_set_error(MXQ_ERR_INVALID, "SwiGLU fc1 width %lld must be a multiple of 32", (long long)N);
   int rc = check_gemm_shape(a, b, h_bf16, M, N / 2, K, ldh);
+  if (!rc) rc = check_workspace(workspace, workspace_bytes);
   if (rc) return rc;
   if (M == 0 || N == 0) return MXQ_OK;
   if (!xs || !ws) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
@@ -864,15 +992,17 @@ extern "C" int mxq_int8_gemm_dequant_swiglu(const int8_t* a, const int8_t* b, co
   GemmArgs g{};
   g.a = a; g.b = b; g.xs = xs; g.ws = ws; g.bias = bias_bf16; g.d = h_bf16;
   g.M = M; g.N = N; g.K = K; g.ldd = ldh; g.ws_per_channel = ws_numel == N && N != 1;
-  return launch_gemm<kEpiSwiGLU, 2>(g, (hipStream_t)stream);
+  return launch_gemm<kEpiSwiGLU, 2>(g, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 extern "C" int mxq_int8_gemm_gated_residual(const int8_t* a, const int8_t* b, const float* xs,
                                             const float* ws, int64_t ws_numel, const void* bias_bf16,
                                             void* residual_bf16, int64_t ldr, const void* gate_bf16,
                                             int64_t ldg, int64_t gate_count, const int32_t* gate_rows,
-                                            int64_t M, int64_t N, int64_t K, void* stream) {
+                                            int64_t M, int64_t N, int64_t K, void* workspace,
+                                            int64_t workspace_bytes, void* stream) {
   int rc = check_gemm_shape(a, b, residual_bf16, M, N, K, ldr);
+  if (!rc) rc = check_workspace(workspace, workspace_bytes);
   if (rc) return rc;
   if (M == 0 || N == 0) return MXQ_OK;
   if (!xs || !ws || !gate_bf16 || !gate_rows) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
@@ -884,5 +1014,5 @@ extern "C" int mxq_int8_gemm_gated_residual(const int8_t* a, const int8_t* b, co
   g.res = (uint16_t*)residual_bf16; g.ldr = ldr; g.gate = (const uint16_t*)gate_bf16; g.ldg = ldg;
   g.gate_rows = gate_rows; g.gate_count = gate_count;
   g.M = M; g.N = N; g.K = K; g.ldd = ldr; g.ws_per_channel = ws_numel == N && N != 1;
-  return launch_gemm<kEpiGatedRes, 2>(g, (hipStream_t)stream);
+  return launch_gemm<kEpiGatedRes, 2>(g, workspace, workspace_bytes, (hipStream_t)stream);
 }

@@ -301,11 +301,6 @@ extern "C" int mxq_dequant_int4_grouped_to_int8(const int8_t* qdata, const void*
   return decode_launch(qdata, s_rel, s_rel_dtype, codebook, out, N, K, group_size, (hipStream_t)stream);
 }
 
-extern "C" int mxq_int8_gemm_dequant(const int8_t* a, const int8_t* b, const float* xs,
-                                     const float* ws, int64_t ws_numel, const void* bias, void* d,
-                                     int64_t M, int64_t N, int64_t K, int64_t ldd, int out_dtype,
-                                     void* stream);
-
 // Decode-then-GEMM over column chunks of chunk_cols weights rows, the decoded chunk in
 // `workspace` ([chunk_cols, K] int8). Arguments are validated by the callers.
 static int codebook_gemm_chunks(const int8_t* xq, const int8_t* qdata, const void* s_rel, int s_rel_dtype,
@@ -324,7 +319,7 @@ static int codebook_gemm_chunks(const int8_t* xq, const int8_t* qdata, const voi
     if (rc) return rc;
     const void* bias_chunk = bias ? (const char*)bias + n0 * osz : nullptr;
     rc = mxq_int8_gemm_dequant(xq, workspace, xs, s_channel + n0, cols, bias_chunk,
-                               (char*)out + n0 * osz, M, cols, K, N, out_dtype, stream);
+                               (char*)out + n0 * osz, M, cols, K, N, out_dtype, nullptr, 0, stream);
     if (rc) return rc;
   }
   return MXQ_OK;

@@ -19,6 +19,9 @@ MXQ_ERR_UNSUPPORTED = -2
 MXQ_ERR_HIP = -3
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_E4M3 = 0, 1, 2, 5
+ABI_VERSION = 2
+# MXQ_GEMM_WORKSPACE_BYTES: the INT8 GEMMs' tile-queue workspace (counters)
+GEMM_WORKSPACE_BYTES = 4096
 ACT_NONE, ACT_GELU_TANH, ACT_SWIGLU = 0, 1, 2
 
 _P = ctypes.c_void_p
@@ -33,12 +36,14 @@ SIGNATURES: dict[str, list] = {
     "mxq_quantize_int8_rowwise_absmax": [_P, _P, _P, _P, _I64, _I64, _P],
     "mxq_adaln": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _P],
     "mxq_adaln_quantize_int8": [_P, _P, _P, _I64, _I64, _F, _P, _P, _P, _I64, _I64, _P],
-    "mxq_int8_gemm_i32": [_P, _P, _P, _I64, _I64, _I64, _I64, _P],
-    "mxq_int8_gemm_dequant": [_P, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I, _P],
-    "mxq_int8_gemm_dequant_gelu_absmax": [_P, _P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
-    "mxq_int8_gemm_dequant_swiglu": [_P, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "mxq_int8_gemm_plan": [_I64, _I64, _I64, _I, _I64, _P],
+    "mxq_int8_gemm_i32": [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
+    "mxq_int8_gemm_dequant": [_P, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _I64, _P],
+    "mxq_int8_gemm_dequant_gelu_absmax": [_P, _P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64,
+                                          _P],
+    "mxq_int8_gemm_dequant_swiglu": [_P, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
     "mxq_int8_gemm_gated_residual": [_P, _P, _P, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64,
-                                     _P],
+                                     _P, _I64, _P],
     "mxq_fill_f32": [_P, _F, _I64, _P],
     "mxq_quantize_int8_rowwise_convrot": [_P, _I, _P, _P, _I64, _I64, _I64, _I, _P],
     "mxq_swiglu_bf16": [_P, _P, _I64, _I64, _P],
@@ -88,6 +93,14 @@ def load() -> ctypes.CDLL:
                 fn.argtypes = args
             _lib = lib
     return _lib
+
+
+def gemm_plan(m: int, n: int, k: int, table: bool = False, workspace_bytes: int = GEMM_WORKSPACE_BYTES) -> dict:
+    """The INT8 GEMM launch plan (mxq_int8_gemm_plan): tile edge, workgroups, tiles, tiles per XCD
+    claimed at run time (0: static order) and workgroups per XCD."""
+    out = (ctypes.c_int64 * 5)()
+    call("mxq_int8_gemm_plan", m, n, k, int(table), workspace_bytes, out)
+    return {"tile": out[0], "grid": out[1], "tiles": out[2], "pool": out[3], "wg_per_xcd": out[4]}
 
 
 def call(name: str, *args) -> None:

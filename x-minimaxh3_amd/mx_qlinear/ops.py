@@ -29,6 +29,30 @@ def _stream(device: torch.device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+_GEMM_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _gemm_ws(device: torch.device):
+    """The INT8 GEMMs' tile-queue workspace for the current stream on ``device``, as the two
+    trailing arguments (pointer, bytes) the GEMM entry points take before the stream: the
+    counters with which the XCDs share out the last tiles at run time. One zero-filled workspace
+    per (device, stream), made on that stream's first GEMM and kept for the process, as the
+    reference keeps one per (device, stream) inside its launchers
+    (CK/backends/cuda/ops/cutlass_gemm_int8.cu:39-55); the kernels leave it zero after every call.
+    Under graph capture no workspace is passed (the static tile order, the same outputs), so a
+    captured graph shares no memory with eager calls."""
+    with torch.cuda.device(device):
+        if torch.cuda.is_current_stream_capturing():
+            return None, 0
+    stream = torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream)
+    ws = _GEMM_WORKSPACES.get(key)
+    if ws is None:
+        ws = torch.zeros(_lib.GEMM_WORKSPACE_BYTES, dtype=torch.uint8, device=device)
+        _GEMM_WORKSPACES[key] = ws
+    return _p(ws), ws.numel()
+
+
 def _require_gpu(*tensors: torch.Tensor | None) -> torch.device:
     dev = None
     for t in tensors:
@@ -406,7 +430,7 @@ def mm_int8(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     a2, w2 = _gemm_activation(a.contiguous(), kp), _gemm_weight(b, kp, transpose=True)
     k = kp
     with torch.cuda.device(dev):
-        call("mxq_int8_gemm_i32", _p(a2), _p(w2), _p(out), m, n, k, n, _stream(dev))
+        call("mxq_int8_gemm_i32", _p(a2), _p(w2), _p(out), m, n, k, n, *_gemm_ws(dev), _stream(dev))
     return out
 
 
@@ -488,7 +512,7 @@ def int8_linear_prequantized(x_qdata: torch.Tensor, x_scale: torch.Tensor, weigh
     q2, w2, k = _pad_k(x_qdata.contiguous(), weight)
     with torch.cuda.device(dev):
         call("mxq_int8_gemm_dequant", _p(q2), _p(w2), _p(xs), _p(ws), ws.numel(), _p(b), _p(out),
-             m, n, k, n, code, _stream(dev))
+             m, n, k, n, code, *_gemm_ws(dev), _stream(dev))
     return out
 
 
@@ -596,16 +620,17 @@ def int8_ffn_gelu(x: torch.Tensor, fc1_weight: torch.Tensor, fc1_scale: torch.Te
     w1 = _gemm_weight(fc1_weight, k)
     w2 = _gemm_weight(fc2_weight, hidden)
     st = _stream(dev)
+    gws = _gemm_ws(dev)
     with torch.cuda.device(dev):
         call("mxq_quantize_int8_rowwise", _p(x2), _lib.DTYPE_BF16, _p(ws.xq), _p(ws.xs), m, k,
              _lib.ACT_NONE, st)
         call("mxq_fill_f32", _p(ws.hmax), 0.0, m, st)
         call("mxq_int8_gemm_dequant_gelu_absmax", _p(ws.xq), _p(w1), _p(ws.xs), _p(s1), s1.numel(),
-             _p(b1), _p(ws.h), _p(ws.hmax), m, hidden, k, hidden, st)
+             _p(b1), _p(ws.h), _p(ws.hmax), m, hidden, k, hidden, *gws, st)
         call("mxq_quantize_int8_rowwise_absmax", _p(ws.h), _p(ws.hmax), _p(ws.hq), _p(ws.hs), m,
              hidden, st)
         call("mxq_int8_gemm_dequant", _p(ws.hq), _p(w2), _p(ws.hs), _p(s2), s2.numel(), _p(b2),
-             _p(out), m, n, hidden, n, _lib.DTYPE_BF16, st)
+             _p(out), m, n, hidden, n, _lib.DTYPE_BF16, *gws, st)
     out = out.reshape(*x.shape[:-1], n)
     return (out, ws.h.reshape(*x.shape[:-1], hidden)) if return_hidden else out
 
@@ -722,7 +747,7 @@ def int8_linear_gated_residual_(residual: torch.Tensor, x: torch.Tensor, weight:
     q2, w2, k = _pad_k(q, weight)
     with torch.cuda.device(dev):
         call("mxq_int8_gemm_gated_residual", _p(q2), _p(w2), _p(xs), _p(ws), ws.numel(), _p(b), _p(res2),
-             res2.stride(0), _p(g), g.stride(0), g.shape[0], _p(gr), rows, n, k, _stream(dev))
+             res2.stride(0), _p(g), g.stride(0), g.shape[0], _p(gr), rows, n, k, *_gemm_ws(dev), _stream(dev))
     return residual
 
 
@@ -802,7 +827,7 @@ def int8_swiglu_fc1(x_qdata: torch.Tensor, x_scale: torch.Tensor, fc1: PreparedS
     q2, w2, k = _pad_k(x_qdata.contiguous(), fc1.qweight)
     with torch.cuda.device(dev):
         call("mxq_int8_gemm_dequant_swiglu", _p(q2), _p(w2), _p(xs), _p(fc1.scale), fc1.scale.numel(),
-             _p(fc1.bias), _p(h), m, n2, k, h.stride(0), _stream(dev))
+             _p(fc1.bias), _p(h), m, n2, k, h.stride(0), *_gemm_ws(dev), _stream(dev))
     return h
 
 
