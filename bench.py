@@ -2,8 +2,8 @@
 
 Default workload (the headline "DiT FFN tokens/s at 720p"): the full INT8 FFN chain at
 720p x 5 s, M = 75600 tokens (21 latent frames x 45 x 80 patches), d_model 5120, d_ff 20480:
-per-token int8 quant -> fc1 int8 GEMM + bias + tanh-GELU (+ row absmax) -> per-token re-quant
--> fc2 int8 GEMM + bias -> bf16. One step = one pass over the 75600 tokens with all inputs
+per-token int8 quant -> fc1 int8 GEMM + bias -> tanh-GELU + per-token re-quant (one pass) -> fc2
+int8 GEMM + bias -> bf16. One step = one pass over the 75600 tokens with all inputs
 resident in HBM. Synthetic data: X ~ N(0, 1) with 0.5% outlier channels x20, weights
 N(0, 0.02) row-quantized to int8 with fp32 per-channel scales, biases N(0, 0.01), seeded.
 
@@ -154,12 +154,11 @@ class FfnWorkload:
         with t("quant_x"):
             _lib.call("mxq_quantize_int8_rowwise", _p(self.x), _lib.DTYPE_BF16, _p(ws.xq), _p(ws.xs), m, k,
                       _lib.ACT_NONE, st)
-        _lib.call("mxq_fill_f32", _p(ws.hmax), 0.0, m, st)
         with t("fc1_gemm"):
-            _lib.call("mxq_int8_gemm_dequant_gelu_absmax", _p(ws.xq), _p(self.w1), _p(ws.xs), _p(self.s1),
-                      h, _p(self.b1), _p(ws.h), _p(ws.hmax), m, h, k, h, *_gemm_ws(self.dev), st)
+            _lib.call("mxq_int8_gemm_dequant", _p(ws.xq), _p(self.w1), _p(ws.xs), _p(self.s1), h, _p(self.b1),
+                      _p(ws.h), m, h, k, h, _lib.DTYPE_BF16, *_gemm_ws(self.dev), st)
         with t("requant"):
-            _lib.call("mxq_quantize_int8_rowwise_absmax", _p(ws.h), _p(ws.hmax), _p(ws.hq), _p(ws.hs), m, h, st)
+            _lib.call("mxq_quantize_int8_rowwise_gelu", _p(ws.h), None, _p(ws.hq), _p(ws.hs), m, h, st)
         with t("fc2_gemm"):
             _lib.call("mxq_int8_gemm_dequant", _p(ws.hq), _p(self.w2), _p(ws.hs), _p(self.s2), k, _p(self.b2),
                       _p(self.out), m, k, h, k, _lib.DTYPE_BF16, *_gemm_ws(self.dev), st)
@@ -173,10 +172,11 @@ class FfnWorkload:
     def dominant(self, timer):
         """The slower GEMM launch: label, kernel symbol, ops and algorithmic bytes per launch, mean ms."""
         m, k, h = self.m, self.k, self.hidden
-        fc1 = {"span": "fc1_gemm", "symbol": "gemm_i8_kernel<2, 2, 256>", "ops": 2 * m * k * h,
-               # A, W1, out H (bf16), xs, ws, bias, row absmax
-               "bytes": m * k + h * k + 2 * m * h + 4 * m + 4 * h + 2 * h + 4 * m}
-        fc2 = {"span": "fc2_gemm", "symbol": "gemm_i8_kernel<1, 2, 256>", "ops": 2 * m * k * h,
+        # fc1 and fc2 are launches of the same kernel: the first and the second of each step.
+        fc1 = {"span": "fc1_gemm", "symbol": "gemm_i8_kernel<1, 2, 256>", "nth": (0, 2), "ops": 2 * m * k * h,
+               # A, W1, out Y (bf16), xs, ws, bias
+               "bytes": m * k + h * k + 2 * m * h + 4 * m + 4 * h + 2 * h}
+        fc2 = {"span": "fc2_gemm", "symbol": "gemm_i8_kernel<1, 2, 256>", "nth": (1, 2), "ops": 2 * m * k * h,
                "bytes": m * h + k * h + 2 * m * k + 4 * m + 4 * k + 2 * k}
         return max((fc1, fc2), key=lambda d: timer.mean_ms(d["span"]))
 
@@ -826,9 +826,10 @@ def _pmc_child(wl):
     torch.cuda.synchronize()
 
 
-def _counter_pass(workload, counter, symbol, out_root):
+def _counter_pass(workload, counter, symbol, out_root, nth=(0, 1)):
     """Runs `rocprofv3 --pmc <counter>` over a child bench process; returns (KiB per launch of
-    `symbol`, KiB of the calibration copy) or raises."""
+    `symbol` -- its dispatches nth[0], nth[0] + nth[1], ... when a step launches it nth[1]
+    times for different operands --, KiB of the calibration copy) or raises."""
     import csv
     import glob
     import shutil
@@ -863,22 +864,23 @@ def _counter_pass(workload, counter, symbol, out_root):
                 continue
             name, val = row["Kernel_Name"], float(row["Counter_Value"])
             if symbol in name:
-                kern.append(val)
+                kern.append((int(row.get("Dispatch_Id", len(kern))), val))
             elif "neg_kernel" in name:
                 copy.append(val)
+    kern = [v for _, v in sorted(kern)][nth[0]::nth[1]]
     if not kern or not copy:
         raise RuntimeError(f"{counter} pass: kernel or calibration copy not found")
     return statistics.median(kern), max(copy)
 
 
-def pmc_traffic(workload, symbol):
+def pmc_traffic(workload, symbol, nth=(0, 1)):
     """HBM bytes per launch of `symbol`: FETCH_SIZE and WRITE_SIZE (KiB per dispatch, one
     rocprofv3 pass each), each scaled by the ratio of the true size of a 1 GiB copy to what the
     same counter reads for it."""
     out_root = os.path.join(ROOT, "gpurun_out")
     os.makedirs(out_root, exist_ok=True)
-    fetch, cf = _counter_pass(workload, "FETCH_SIZE", symbol, out_root)
-    write, cw = _counter_pass(workload, "WRITE_SIZE", symbol, out_root)
+    fetch, cf = _counter_pass(workload, "FETCH_SIZE", symbol, out_root, nth)
+    write, cw = _counter_pass(workload, "WRITE_SIZE", symbol, out_root, nth)
     kib = CALIB_BYTES / 1024
     f_scale, w_scale = kib / cf, kib / cw
     total = fetch * 1024 * f_scale + write * 1024 * w_scale
@@ -989,7 +991,7 @@ def main():
             roof["frac_of_measured_peak"] = round(achieved / ceiling["value"], 4)
     if not args.no_traffic:
         try:
-            traffic, detail = pmc_traffic(args.workload, dom["symbol"])
+            traffic, detail = pmc_traffic(args.workload, dom["symbol"], dom.get("nth", (0, 1)))
             roof["traffic"] = int(traffic)
             roof["traffic_detail"] = detail
         except Exception as e:  # counters unavailable: traffic stays null, with the reason

@@ -80,6 +80,17 @@ int mxq_quantize_int8_rowwise_absmax(const void* x_bf16, const float* row_absmax
                                      float* scales, int64_t rows, int64_t cols, void* stream);
 
 /*
+ * The FFN intermediate's quantizer: h = gelu_tanh(y) in bf16, then the per-token quantizer of h
+ * (q, scales as mxq_quantize_int8_rowwise). y bf16 [rows, cols], cols % 8 == 0, cols <= 32768,
+ * 16-byte aligned; h_bf16 receives h when not NULL (it may be y itself: the update is in
+ * place). Equals mxq_quantize_int8_rowwise(y, ..., MXQ_ACT_GELU_TANH) bit for bit.
+ * Replaces: apply_input_act("gelu_tanh") + quantize_int8_rowwise inside fc2's int8_linear,
+ * CK/backends/_activations.py:40-53 and CK/backends/eager/quantization.py:857-875.
+ */
+int mxq_quantize_int8_rowwise_gelu(const void* y_bf16, void* h_bf16, int8_t* q, float* scales,
+                                   int64_t rows, int64_t cols, void* stream);
+
+/*
  * adaLN: layer_norm(x, no affine, eps) * (1 + scale) + shift, bf16 in and out.
  *   scale, shift  [rows / scale_group, cols] and [rows / shift_group, cols] bf16: row r uses
  *                 modulation row r / scale_group (r / shift_group); a single [cols] vector

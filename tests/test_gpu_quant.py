@@ -101,6 +101,85 @@ def test_quant_gelu_input_act_matches_oracle(dev):
     assert np.array_equal(s.cpu().numpy(), s_ref)
 
 
+def _gelu_quant_call(y, h=None):
+    """mxq_quantize_int8_rowwise_gelu through the C ABI: (q, scales) of gelu(y); h (a bf16
+    buffer, possibly y itself) receives gelu(y)."""
+    from mx_qlinear import _lib
+    from mx_qlinear.ops import _p, _stream
+
+    m, k = y.shape
+    q = torch.empty(m, k, dtype=torch.int8, device=y.device)
+    s = torch.empty(m, dtype=torch.float32, device=y.device)
+    _lib.call("mxq_quantize_int8_rowwise_gelu", _p(y), _p(h), _p(q), _p(s), m, k, _stream(y.device))
+    return q, s
+
+
+@pytest.mark.parametrize("m,k", [(1, 8), (7, 4104), (300, 2048), (1000, 20480), (40, 32768), (257, 20480)])
+def test_gelu_quantizer_matches_oracle(dev, m, k):
+    """The FFN intermediate's one-pass GELU + per-token quantizer: q and scales bit-exact against
+    the oracle's quantizer of gelu(y); h bit-exact against the GELU table, written to a separate
+    buffer and in place over y. Row counts below and above the 256-workgroup grid, rows whose
+    chunks do not fill the last round of threads (4104 = 513 chunks), and the widest row."""
+    print(f"gelu quant m={m} k={k}", flush=True)
+    y = (torch.randn(m, k, generator=gen(m * 31 + k)) * 2).to(torch.bfloat16)
+    y[:, :: max(k // 7, 1)] *= 20
+    hb_ref = eager_np.gelu_tanh_bf16(bits(y))
+    q_ref, s_ref = eager_np.quantize_int8_rowwise(hb_ref)
+    yd = y.to(dev)
+    q, s = _gelu_quant_call(yd)
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.reshape(-1).view(np.uint32))
+    assert np.array_equal(bits(yd), bits(y))  # no h requested: y untouched
+    h = torch.empty_like(yd)
+    q2, s2 = _gelu_quant_call(yd, h)
+    assert np.array_equal(bits(h), hb_ref)
+    assert torch.equal(q2, q) and torch.equal(s2, s)
+    q3, s3 = _gelu_quant_call(yd, yd)  # in place
+    assert np.array_equal(bits(yd), hb_ref)
+    assert torch.equal(q3, q) and torch.equal(s3, s)
+
+
+def test_gelu_quantizer_nan_and_inf_rows(dev):
+    """gelu(NaN) = NaN makes the row's scale NaN and every q 0; gelu(+inf) = +inf makes the scale
+    inf and q 0; torch's tanh-GELU of -inf is NaN too (-inf * (1 + tanh(-inf)) = -inf * 0), so
+    that row's scale is NaN (torch's amax and division rules)."""
+    m, k = 6, 20480
+    y = (torch.randn(m, k, generator=gen(77))).to(torch.bfloat16)
+    y[1, 100] = float("nan")
+    y[2, 5] = float("inf")
+    y[3, 9] = float("-inf")
+    hb = eager_np.gelu_tanh_bf16(bits(y))
+    q, s = _gelu_quant_call(y.to(dev))
+    q_ref, s_ref = eager_torch.quantize_int8_rowwise(from_bits(hb))
+    assert torch.equal(q.cpu(), q_ref.reshape(m, k))
+    s_ref = s_ref.reshape(-1)
+    assert torch.equal(s.cpu().isnan(), s_ref.isnan())
+    assert torch.equal(torch.nan_to_num(s.cpu()), torch.nan_to_num(s_ref))
+    assert bool(s[1].isnan()) and bool(s[2].isinf()) and int(q[1:3].abs().max()) == 0
+    assert (int(hb[3, 9]) & 0x7FFF) > 0x7F80 and bool(s[3].isnan()) and int(q[3].abs().max()) == 0
+
+
+def test_gelu_input_act_routes_large_inputs_through_the_wide_quantizer(dev):
+    """quantize_int8_rowwise(input_act="gelu_tanh") on a large input (the one-pass kernel) equals
+    the oracle, as the register kernel does on small ones."""
+    y = (torch.randn(1000, 20480, generator=gen(5)) * 2).to(torch.bfloat16)
+    q, s = _mx().quantize_int8_rowwise(y.to(dev), input_act="gelu_tanh")
+    q_ref, s_ref = eager_np.quantize_int8_rowwise(eager_np.gelu_tanh_bf16(bits(y)))
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy().reshape(-1), s_ref.reshape(-1))
+
+
+def test_gelu_quantizer_rejects_what_it_cannot_hold(dev):
+    from mx_qlinear import _lib
+
+    y = torch.zeros(2, 32776, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(RuntimeError, match="exceeds"):
+        _gelu_quant_call(y)
+    with pytest.raises(RuntimeError, match="cols % 8"):
+        _gelu_quant_call(torch.zeros(2, 20, dtype=torch.bfloat16, device=dev))
+    assert _lib.MXQ_ERR_UNSUPPORTED == -2
+
+
 def test_quant_with_known_absmax(dev):
     import mx_qlinear._lib as L
     from mx_qlinear.ops import _p, _stream

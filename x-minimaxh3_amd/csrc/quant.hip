@@ -176,6 +176,108 @@ __global__ __launch_bounds__(256) void quant_rows_bf16_absmax(
   }
 }
 
+// ---- tanh-GELU + per-token quantizer of wide rows (the FFN intermediate) ----------------
+// fc2's quantizer with input_act="gelu_tanh" (CK/backends/_activations.py:40-53 then
+// CK/backends/eager/quantization.py:857-875) on fc1's bf16 output y: h = gelu(y), the row's
+// absmax of h, q = quantize(h). A persistent grid of one 512-thread workgroup per CU copies the
+// 128 KB bf16 -> bf16 GELU table into LDS once (direct-to-LDS loads), then walks rows: thread t
+// holds the row's 16-byte chunks t, t + 512, ... in registers (kC of them), with the next row's
+// loads in flight behind the current row's work; GELU is one 16-bit LDS read per element; the
+// absmax is an integer max over |h| bit patterns (NaN above +inf), reduced over each wave by
+// shuffles and over the eight waves through LDS (double-buffered by row parity, so one barrier
+// per row); the row is quantized from registers with its scale formed once. With kStoreH, h is
+// also written (in place over y is allowed: every element is read before it is written, by the
+// same thread, and the prefetched row is a later one).
+constexpr int kGeluRowThreads = 512;
+constexpr int kGeluRowWaves = kGeluRowThreads / kWave;
+
+template <int kC, bool kStoreH>
+__global__ __launch_bounds__(kGeluRowThreads) void quant_rows_gelu_wide(
+    const uint16_t* y, int8_t* __restrict__ q, float* __restrict__ scales, uint16_t* h,
+    int64_t rows, int chunks) {
+  __shared__ __attribute__((aligned(16))) uint16_t tab[65536];
+  __shared__ uint32_t red[2][kGeluRowWaves];
+  const int t = threadIdx.x, lane = t & (kWave - 1), wave = t >> 6;
+  {
+    const char* src = reinterpret_cast<const char*>(&kGeluFull) + lane * 16;
+    for (int b = wave; b < 128; b += kGeluRowWaves)
+      __builtin_amdgcn_global_load_lds((gptr_t)(src + b * 1024), (lptr_t)(reinterpret_cast<char*>(tab) + b * 1024), 16, 0, 0);
+  }
+  const int64_t stride = gridDim.x;
+  // Rows past the end re-read the last row (never used), so every load is issued unconditionally.
+  auto load_row = [&](int64_t r, v4u (&v)[kC]) {
+    const v4u* src = reinterpret_cast<const v4u*>(y + min(r, rows - 1) * (int64_t)chunks * 8);
+#pragma unroll
+    for (int j = 0; j < kC; ++j) v[j] = __builtin_nontemporal_load(src + min(t + j * kGeluRowThreads, chunks - 1));
+  };
+  auto do_row = [&](int64_t r, v4u (&v)[kC], int parity) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < kC; ++j) {
+      const bool ok = t + j * kGeluRowThreads < chunks;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t w = v[j][i];
+        const uint32_t g = (uint32_t)tab[w & 0xFFFFu] | ((uint32_t)tab[w >> 16] << 16);
+        v[j][i] = g;
+        m = ok ? absmax_acc_bf16x2(m, g) : m;
+      }
+    }
+    uint32_t bits = absmax_bits_of_bf16x2(m);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const uint32_t other = (uint32_t)__shfl_xor((int)bits, o, kWave);
+      bits = bits > other ? bits : other;
+    }
+    if (lane == 0) red[parity][wave] = bits;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kGeluRowWaves; ++w) bits = max(bits, red[parity][w]);
+    const float amax = __uint_as_float(bits);
+    const float s = row_scale_from_absmax(amax);
+    const float rcp = 1.0f / round_bf16(s);
+    v2u* dq = reinterpret_cast<v2u*>(q + r * (int64_t)chunks * 8);
+    v4u* dh = reinterpret_cast<v4u*>(h + r * (int64_t)chunks * 8);
+    if (finite_absmax(amax)) {
+#pragma unroll
+      for (int j = 0; j < kC; ++j) {
+        const int c = t + j * kGeluRowThreads;
+        if (c < chunks) {
+          __builtin_nontemporal_store(quant8_bf16_finite(v[j], rcp), dq + c);
+          if (kStoreH) __builtin_nontemporal_store(v[j], dh + c);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kC; ++j) {
+        const int c = t + j * kGeluRowThreads;
+        if (c < chunks) {
+          __builtin_nontemporal_store(quant8_bf16(v[j], rcp), dq + c);
+          if (kStoreH) __builtin_nontemporal_store(v[j], dh + c);
+        }
+      }
+    }
+    if (t == 0) scales[r] = s;
+  };
+  v4u a[kC], b[kC];
+  int64_t row = blockIdx.x;
+  load_row(row, a);
+  wait_vmcnt<0>();  // the table (and the first row) have landed in this wave
+  __syncthreads();  // ... in every wave
+  int parity = 0;
+  while (row < rows) {
+    load_row(row + stride, b);
+    do_row(row, a, parity);
+    row += stride;
+    parity ^= 1;
+    if (row >= rows) break;
+    load_row(row + stride, a);
+    do_row(row, b, parity);
+    row += stride;
+    parity ^= 1;
+  }
+}
+
 // ---- adaLN ------------------------------------------------------------------------
 // y = bf16(bf16(bf16(n) * bf16(1 + scale)) + shift), n = (x - mean) * rstd in fp32,
 // rstd = 1 / sqrt(var + eps), var the biased variance (CK/backends/eager/adaln.py:11-14 on
@@ -510,6 +612,52 @@ using namespace mxq;
     default: break;                                  \
   }
 
+// Chunks per thread of the wide GELU quantizer; 0 beyond its register budget.
+static int pick_gelu_chunks(int64_t cols) {
+  const int64_t need = (cols / 8 + kGeluRowThreads - 1) / kGeluRowThreads;
+  return need <= 8 ? (int)need : 0;
+}
+
+#define MXQ_GELU_CHUNK_SWITCH(c, BODY)                                          \
+  switch (c) {                                                                  \
+    case 1: { constexpr int C_ = 1; BODY; } break;                              \
+    case 2: { constexpr int C_ = 2; BODY; } break;                              \
+    case 3: { constexpr int C_ = 3; BODY; } break;                              \
+    case 4: { constexpr int C_ = 4; BODY; } break;                              \
+    case 5: { constexpr int C_ = 5; BODY; } break;                              \
+    case 6: { constexpr int C_ = 6; BODY; } break;                              \
+    case 7: { constexpr int C_ = 7; BODY; } break;                              \
+    case 8: { constexpr int C_ = 8; BODY; } break;                              \
+    default: break;                                                             \
+  }
+
+static int gelu_wide_launch(const void* y, void* h, int8_t* q, float* scales, int64_t rows, int64_t cols,
+                            hipStream_t st) {
+  const int c = pick_gelu_chunks(cols);
+  const int64_t grid = rows < 256 ? rows : 256;  // one workgroup per CU (the table fills 128 KB of LDS)
+  if (h) {
+    MXQ_GELU_CHUNK_SWITCH(c, (quant_rows_gelu_wide<C_, true><<<(unsigned)grid, kGeluRowThreads, 0, st>>>(
+                                  (const uint16_t*)y, q, scales, (uint16_t*)h, rows, (int)(cols / 8))));
+  } else {
+    MXQ_GELU_CHUNK_SWITCH(c, (quant_rows_gelu_wide<C_, false><<<(unsigned)grid, kGeluRowThreads, 0, st>>>(
+                                  (const uint16_t*)y, q, scales, nullptr, rows, (int)(cols / 8))));
+  }
+  return mxq_check_launch("quant_rows_gelu_wide");
+}
+
+extern "C" int mxq_quantize_int8_rowwise_gelu(const void* y_bf16, void* h_bf16, int8_t* q, float* scales,
+                                              int64_t rows, int64_t cols, void* stream) {
+  if (rows < 0 || cols <= 0) return mxq_set_error(MXQ_ERR_INVALID, "bad shape [%lld, %lld]", (long long)rows, (long long)cols);
+  if (rows == 0) return MXQ_OK;
+  if (!y_bf16 || !q || !scales) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  if (cols % 8 != 0 || (uintptr_t)y_bf16 % 16 != 0 || (uintptr_t)q % 8 != 0 || (uintptr_t)h_bf16 % 16 != 0)
+    return mxq_set_error(MXQ_ERR_UNSUPPORTED, "GELU quantizer needs cols %% 8 == 0 and 16-byte aligned rows");
+  if (pick_gelu_chunks(cols) == 0)
+    return mxq_set_error(MXQ_ERR_UNSUPPORTED, "GELU quantizer row of %lld columns exceeds %d", (long long)cols,
+                         8 * 8 * kGeluRowThreads);
+  return gelu_wide_launch(y_bf16, h_bf16, q, scales, rows, cols, (hipStream_t)stream);
+}
+
 extern "C" int mxq_quantize_int8_rowwise(const void* x, int x_dtype, int8_t* q, float* scales,
                                          int64_t rows, int64_t cols, int input_act,
                                          void* stream) {
@@ -527,6 +675,11 @@ extern "C" int mxq_quantize_int8_rowwise(const void* x, int x_dtype, int8_t* q, 
   const bool gelu = input_act == MXQ_ACT_GELU_TANH;
   const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 8 == 0);
   const int nch = pick_nch(cols);
+  // Large GELU inputs take the wide kernel (the GELU table in LDS, loaded once per CU); the
+  // register kernels below gather GELU values from the table in global memory.
+  if (gelu && x_dtype == MXQ_DTYPE_BF16 && cols % 8 == 0 && aligned && pick_gelu_chunks(cols) > 0 &&
+      rows * cols >= ((int64_t)1 << 24))
+    return gelu_wide_launch(x, nullptr, q, scales, rows, cols, st);
   if (x_dtype == MXQ_DTYPE_BF16 && cols % 8 == 0 && aligned && nch > 0 && cols <= INT32_MAX) {
     if (gelu) {
       MXQ_NCH_SWITCH(nch, (quant_rows_bf16_reg<N_, true><<<row_grid(rows), kQuantBlock, 0, st>>>(

@@ -34,6 +34,7 @@ SIGNATURES: dict[str, list] = {
     "mxq_quantize_int8_rowwise": [_P, _I, _P, _P, _I64, _I64, _I, _P],
     "mxq_quantize_int8_rowwise_stochastic": [_P, _I, _P, _P, _P, _I64, _I64, _P],
     "mxq_quantize_int8_rowwise_absmax": [_P, _P, _P, _P, _I64, _I64, _P],
+    "mxq_quantize_int8_rowwise_gelu": [_P, _P, _P, _P, _I64, _I64, _P],
     "mxq_adaln": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _P],
     "mxq_adaln_quantize_int8": [_P, _P, _P, _I64, _I64, _F, _P, _P, _P, _I64, _I64, _P],
     "mxq_int8_gemm_plan": [_I64, _I64, _I64, _I, _I64, _P],

@@ -572,6 +572,10 @@ def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tenso
 # The INT8 FFN chain: fc1 -> tanh-GELU -> per-token re-quant -> fc2
 # ---------------------------------------------------------------------------------------
 
+# Widest row the single-pass GELU quantizer (mxq_quantize_int8_rowwise_gelu) holds in registers.
+_GELU_QUANT_MAX_COLS = 32768
+
+
 class FfnWorkspace:
     """Reusable device buffers of :func:`int8_ffn_gelu` for a given (M, K, hidden) shape."""
 
@@ -593,9 +597,12 @@ def int8_ffn_gelu(x: torch.Tensor, fc1_weight: torch.Tensor, fc1_scale: torch.Te
 
     The reference composes two ``int8_linear`` calls with the activation applied before the
     second quantizer (CK/backends/eager/quantization.py:971-1056,
-    CK/backends/_activations.py:40-53). Here fc1's epilogue applies GELU and accumulates each
-    row's absmax, so the intermediate is read once by a single-pass quantizer. Results are
-    identical to the two-call composition. bf16 in and out.
+    CK/backends/_activations.py:40-53). Here fc1 writes its bf16 output and one pass over it
+    applies GELU, takes each row's absmax and quantizes (the GELU table in LDS, loaded once per
+    CU, its lookups hidden under that pass's HBM traffic); with ``return_hidden`` the same pass
+    writes the GELU output over fc1's. Hidden widths beyond that pass's register budget (32768)
+    apply GELU and the row absmax in fc1's epilogue instead. Results are identical to the
+    two-call composition. bf16 in and out.
     """
     if x.dtype != torch.bfloat16:
         raise NotImplementedError("int8_ffn_gelu takes a bfloat16 input")
@@ -624,11 +631,17 @@ def int8_ffn_gelu(x: torch.Tensor, fc1_weight: torch.Tensor, fc1_scale: torch.Te
     with torch.cuda.device(dev):
         call("mxq_quantize_int8_rowwise", _p(x2), _lib.DTYPE_BF16, _p(ws.xq), _p(ws.xs), m, k,
              _lib.ACT_NONE, st)
-        call("mxq_fill_f32", _p(ws.hmax), 0.0, m, st)
-        call("mxq_int8_gemm_dequant_gelu_absmax", _p(ws.xq), _p(w1), _p(ws.xs), _p(s1), s1.numel(),
-             _p(b1), _p(ws.h), _p(ws.hmax), m, hidden, k, hidden, *gws, st)
-        call("mxq_quantize_int8_rowwise_absmax", _p(ws.h), _p(ws.hmax), _p(ws.hq), _p(ws.hs), m,
-             hidden, st)
+        if hidden <= _GELU_QUANT_MAX_COLS:
+            call("mxq_int8_gemm_dequant", _p(ws.xq), _p(w1), _p(ws.xs), _p(s1), s1.numel(), _p(b1),
+                 _p(ws.h), m, hidden, k, hidden, _lib.DTYPE_BF16, *gws, st)
+            call("mxq_quantize_int8_rowwise_gelu", _p(ws.h), _p(ws.h) if return_hidden else None,
+                 _p(ws.hq), _p(ws.hs), m, hidden, st)
+        else:
+            call("mxq_fill_f32", _p(ws.hmax), 0.0, m, st)
+            call("mxq_int8_gemm_dequant_gelu_absmax", _p(ws.xq), _p(w1), _p(ws.xs), _p(s1), s1.numel(),
+                 _p(b1), _p(ws.h), _p(ws.hmax), m, hidden, k, hidden, *gws, st)
+            call("mxq_quantize_int8_rowwise_absmax", _p(ws.h), _p(ws.hmax), _p(ws.hq), _p(ws.hs), m,
+                 hidden, st)
         call("mxq_int8_gemm_dequant", _p(ws.hq), _p(w2), _p(ws.hs), _p(s2), s2.numel(), _p(b2),
              _p(out), m, n, hidden, n, _lib.DTYPE_BF16, *gws, st)
     out = out.reshape(*x.shape[:-1], n)
