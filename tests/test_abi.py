@@ -159,3 +159,51 @@ def test_gemm_plan_queues_large_problems(lib, m, n, k, table, tile, queued):
         assert plan["pool"] == 0 and plan["grid"] == tiles
     static = _lib.gemm_plan(m, n, k, table, workspace_bytes=0)
     assert static["pool"] == 0 and static["grid"] == tiles
+
+
+def _queue_cover(tiles, pool, wg_per_xcd, order):
+    """Positions the balanced tile queue hands out, for workgroups arriving in `order`: the rule
+    the GEMM kernel's pick_tile applies (XCD x = bid % 8 takes position start_x + bid / 8 of its
+    range while that is below count_x - pool; later workgroups claim pool slots, their own XCD's
+    first, then the others' in turn, and leave when all are gone)."""
+    per, rem = tiles // 8, tiles % 8
+
+    def rng(x):
+        return x * per + min(x, rem), per + (1 if x < rem else 0)
+
+    taken, claims = [], [0] * 8
+    for bid in order:
+        x, k = bid % 8, bid // 8
+        start, count = rng(x)
+        if k < count - pool:
+            taken.append(start + k)
+            continue
+        for j in range(8):
+            y = (x + j) % 8
+            i = claims[y]
+            claims[y] += 1
+            if i < pool:
+                ys, yc = rng(y)
+                taken.append(ys + yc - pool + i)
+                break
+    return taken
+
+
+@pytest.mark.parametrize("m,n,table", [(75600, 5120, False), (75600, 20480, True), (10496, 8408, False),
+                                       (8060, 4990, False), (75600, 28672, True)])
+def test_tile_queue_plan_covers_every_tile_once(lib, m, n, table):
+    """With the launch plan's pool and grid, every tile is taken exactly once whatever order the
+    workgroups arrive in (here: dispatch order, reversed, and seeded shuffles)."""
+    import random
+
+    from mx_qlinear import _lib
+
+    plan = _lib.gemm_plan(m, n, 1024, table)
+    assert plan["pool"] > 0 and plan["grid"] == 8 * plan["wg_per_xcd"]
+    orders = [list(range(plan["grid"])), list(range(plan["grid"]))[::-1]]
+    for seed in range(3):
+        o = list(range(plan["grid"]))
+        random.Random(seed).shuffle(o)
+        orders.append(o)
+    for order in orders:
+        assert sorted(_queue_cover(plan["tiles"], plan["pool"], plan["wg_per_xcd"], order)) == list(range(plan["tiles"]))

@@ -61,7 +61,11 @@ def _counters_zero(dev):
     assert int(ws.count_nonzero()) == 0
 
 
-@pytest.mark.parametrize("m,n,k", [(10496, 8192, 2048), (10459, 8144, 2000), (8187, 5120, 5120)])
+@pytest.mark.parametrize(
+    "m,n,k",
+    [(10496, 8192, 2048), (10459, 8144, 2000), (8187, 5120, 5120),
+     (10496, 8408, 1040), (8060, 4990, 1024)],  # tile counts 1353 and 2457: XCD ranges of unequal length
+)
 def test_queue_i32_equals_static_order_and_oracle(dev, m, n, k):
     plan = _assert_queued(m, n, k)
     print(f"queue i32 m={m} n={n} k={k} plan={plan}", flush=True)
@@ -80,7 +84,7 @@ def test_queue_i32_equals_static_order_and_oracle(dev, m, n, k):
 
 
 @pytest.mark.parametrize("out_dtype,code", [(torch.bfloat16, 2), (torch.float16, 1), (torch.float32, 0)])
-@pytest.mark.parametrize("m,n,k", [(10459, 8144, 2000), (8187, 5120, 5120)])
+@pytest.mark.parametrize("m,n,k", [(10459, 8144, 2000), (8187, 5120, 5120), (8060, 4990, 2000)])
 def test_queue_dequant_equals_static_order_and_oracle(dev, out_dtype, code, m, n, k):
     _assert_queued(m, n, k)
     print(f"queue dequant {out_dtype} m={m} n={n} k={k}", flush=True)
