@@ -137,7 +137,7 @@ def test_python_maps_codes_to_the_reference_exceptions(lib):
     "m,n,k,table,tile,queued",
     [
         (75600, 5120, 20480, False, 256, True),   # FFN fc2 at 720p
-        (75600, 20480, 5120, True, 256, True),    # FFN fc1 (GELU epilogue: 256-tiles always)
+        (75600, 20480, 5120, True, 256, True),    # FFN fc1 (planned as a table epilogue)
         (75600, 15360, 5120, False, 256, True),   # QKV at 720p
         (8192, 5120, 5120, False, 128, True),     # 2.5 rounds of 128-tiles
         (1024, 3072, 3072, False, 128, False),    # under two rounds: static order

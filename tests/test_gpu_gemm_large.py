@@ -7,8 +7,9 @@ cover 128 x 128 tiles. These shapes (4100 x 7432: 17 x 30 = 510 tiles of 256, tw
 both edges partial) keep the 256 x 256 kernel for every epilogue. K is chosen
 at the boundaries of the K loop: a single stage (128), stages that are all full with and without
 steady-state iterations (256, 384, 1024) and a partial last stage after zero, one or two steady
-iterations (144, 400, 528). Every epilogue is covered: int32, dequant (+ bias) to bf16, GELU +
-row absmax (in the FFN chain), SwiGLU and the gated residual.
+iterations (144, 400, 528). Every epilogue is covered: int32, dequant (+ bias) to bf16 (alone
+and as the FFN chain's fc1 and fc2), GELU + row absmax (the FFN chain's path for hidden widths
+beyond 32768), SwiGLU and the gated residual.
 
 Bar: int32 and every bf16 output bit-exact against the oracle.
 """
@@ -57,8 +58,8 @@ def test_int8_linear_256_tiles(dev, k, bias):
 
 
 def test_ffn_chain_256_tiles(dev):
-    """fc1 (GELU + row absmax epilogue) runs 256 x 256 tiles; fc2 (17 x 16 tiles of 256, just over
-    one round) runs 128 x 128 tiles."""
+    """fc1 (the bf16 dequant GEMM, then the one-pass GELU quantizer) runs 256 x 256 tiles; fc2
+    (17 x 16 tiles of 256, just over one round) runs 128 x 128 tiles."""
     m, k, hidden, n = M, 400, 4112, 4096  # hidden: a multiple of 16 with a partial edge tile
     print(f"ffn 256-tile m={m} k={k} hidden={hidden} n={n}", flush=True)
     x = activations(m, k, 60)
@@ -68,6 +69,29 @@ def test_ffn_chain_256_tiles(dev):
     out = _mx().int8_ffn_gelu(x.to(dev), w1.to(dev), s1.to(dev), b1.to(dev), w2.to(dev), s2.to(dev), b2.to(dev))
     ref, _ = eager_np.ffn_gelu_int8(bits(x), w1.numpy(), s1.numpy(), bits(b1), w2.numpy(), s2.numpy(), bits(b2))
     assert np.array_equal(bits(out), bf16_bits(ref))
+
+
+@pytest.mark.parametrize("k", [144, 400])
+def test_gelu_absmax_epilogue_256_tiles(dev, k):
+    import mx_qlinear._lib as L
+    from mx_qlinear import ops
+
+    assert L.gemm_plan(M, N, k, True)["tile"] == 256
+    print(f"gelu+absmax 256-tile m={M} n={N} k={k}", flush=True)
+    a, w = _i8((M, k), 90 + k), _i8((N, k), 91 + k)
+    xs = torch.rand(M, generator=gen(92)) * 1e-3
+    ws = torch.rand(N, generator=gen(93)) * 1e-2
+    b = bf16_vec(N, 94, 0.5)
+    dv = [t.to(dev) for t in (a, w, xs, ws, b)]
+    h = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    amax = torch.zeros(M, dtype=torch.float32, device=dev)
+    L.call("mxq_int8_gemm_dequant_gelu_absmax", *map(ops._p, dv[:4]), N, ops._p(dv[4]), ops._p(h),
+           ops._p(amax), M, N, k, N, *ops._gemm_ws(dev), ops._stream(dev))
+    y = eager_np.dequant_epilogue(eager_np.int8_matmul(a.numpy(), w.numpy()), xs.numpy(), ws.numpy(), bits(b), "bf16")
+    hb = eager_np.gelu_tanh_bf16(bf16_bits(y))
+    assert np.array_equal(bits(h), hb)
+    amax_bits = (hb & np.uint16(0x7FFF)).max(axis=1).astype(np.uint32) << np.uint32(16)
+    assert np.array_equal(amax.cpu().numpy().view(np.uint32), amax_bits)
 
 
 def test_swiglu_fc1_256_tiles(dev):
