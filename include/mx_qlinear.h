@@ -130,7 +130,10 @@ int mxq_adaln_quantize_int8(const void* x, const void* scale, const void* shift,
  * Launch plan the INT8 GEMMs below choose for an M x N x K problem (table_epilogue: 1 for the
  * GELU and SwiGLU epilogues, 0 otherwise) given workspace_bytes of tile-queue workspace (0:
  * none): plan[0] tile edge (256 or 128), plan[1] workgroups, plan[2] tiles, plan[3] tiles per
- * XCD claimed at run time (0: static order), plan[4] workgroups per XCD. Host only; no
+ * XCD claimed at run time (0: static order), plan[4] workgroups per XCD, plan[5] stages of
+ * operands requested ahead of the MFMAs (4 when the 128-tiles all fit on the CUs at once, one
+ * workgroup per CU; else 2), plan[6] tile-rows per group of the tile order. plan holds 7
+ * entries. Host only; no
  * reference counterpart (CUTLASS's Gemm::get_workspace_size is the nearest,
  * CK/backends/cuda/ops/cutlass_gemm_int8.cu:318); tests and tuning read it.
  */

@@ -161,6 +161,57 @@ def test_gemm_plan_queues_large_problems(lib, m, n, k, table, tile, queued):
     assert static["pool"] == 0 and static["grid"] == tiles
 
 
+@pytest.mark.parametrize(
+    "m,n,table,tile,ahead",
+    [
+        (1024, 3072, False, 128, 4),    # 192 tiles of 128: one workgroup per CU, deep ring
+        (1100, 1800, False, 128, 4),    # 135 tiles of 128, both edges partial
+        (2048, 2048, False, 128, 4),    # exactly 256 tiles of 128
+        (2050, 2056, False, 128, 2),    # 289 tiles of 128: two workgroups per CU
+        (75600, 5120, False, 256, 2),
+        (1024, 3072, True, 256, 2),     # table epilogues always take 256-tiles
+    ],
+)
+def test_gemm_plan_ring_depth(lib, m, n, table, tile, ahead):
+    from mx_qlinear import _lib
+
+    plan = _lib.gemm_plan(m, n, 1024, table)
+    assert (plan["tile"], plan["ahead"]) == (tile, ahead)
+
+
+def _tile_walk(t, tiles_m, tiles_n, group_m):
+    """Tile (row, column) at position t of the GEMM's tile order (gemm_i8.hip tile_walk): groups
+    of group_m tile-rows, walked column by column."""
+    group = group_m * tiles_n
+    first_m = (t // group) * group_m
+    gm = min(tiles_m - first_m, group_m)
+    return first_m + (t % group) % gm, (t % group) // gm
+
+
+@pytest.mark.parametrize("m,n,group_m", [(1024, 3072, 4), (2048, 2048, 4), (1100, 1800, None), (2050, 2056, 2),
+                                         (300, 5000, None), (75600, 5120, 2), (8192, 5120, 2)])
+def test_tile_order_visits_every_tile_once(lib, m, n, group_m):
+    """Deep-ring problems (every tile on its own CU at once) group their tile order so that each
+    XCD's range of tiles is nearly square (fewer operand panels per XCD); every order is a
+    permutation of the tiles."""
+    from mx_qlinear import _lib
+
+    plan = _lib.gemm_plan(m, n, 1024)
+    if group_m is not None:
+        assert plan["group_m"] == group_m
+    tm, tn = -(-m // plan["tile"]), -(-n // plan["tile"])
+    seen = {_tile_walk(t, tm, tn, plan["group_m"]) for t in range(tm * tn)}
+    assert seen == {(i, j) for i in range(tm) for j in range(tn)}
+    if plan["ahead"] == 4:
+        # each XCD's range spans no more panels than the two-row order would
+        per = -(-tm * tn // 8)
+        for x in range(8):
+            cells = [_tile_walk(t, tm, tn, plan["group_m"]) for t in range(x * per, min((x + 1) * per, tm * tn))]
+            two = [_tile_walk(t, tm, tn, 2) for t in range(x * per, min((x + 1) * per, tm * tn))]
+            panels = lambda c: len({i for i, _ in c}) + len({j for _, j in c})
+            assert panels(cells) <= panels(two) + 1
+
+
 def _queue_cover(tiles, pool, wg_per_xcd, order):
     """Positions the balanced tile queue hands out, for workgroups arriving in `order`: the rule
     the GEMM kernel's pick_tile applies (XCD x = bid % 8 takes position start_x + bid / 8 of its

@@ -1,5 +1,7 @@
-"""GPU parity of the 256 x 256-tile INT8 GEMM (the configuration every model-sized shape runs)
-and of the 128 x 128 one at a mid-sized shape with partial edge tiles.
+"""GPU parity of the 256 x 256-tile INT8 GEMM (the configuration every model-sized shape runs),
+of the 128 x 128 one at a mid-sized shape with partial edge tiles, and of the 128 x 128 one with
+the deep operand ring (one workgroup per CU, four stages in flight) that problems of at most 256
+such tiles run.
 
 The library runs a GEMM with 256 x 256 tiles once it has at least 256 of them, unless its rounds of
 128 x 128 tiles (512 per round, ~0.55 of a 256-tile round) would finish first; the small-shape tests
@@ -121,6 +123,60 @@ def test_gated_residual_256_tiles(dev):
     q, s = eager_np.quantize_int8_rowwise(bits(x))
     y = eager_np.dequant_epilogue(eager_np.int8_matmul(q, w.numpy()), s, ws.numpy(), bits(b), "bf16")
     want = eager_np.gated_residual_bf16(bits(res), bf16_bits(y), bits(gate), eager_np.segment_row_map(M, segs))
+    assert np.array_equal(bits(out), want)
+
+
+# ---- the deep-ring 128-tile configuration: at most 256 tiles of 128, one workgroup per CU with
+# four stages in flight. K covers one partial stage (16), one full (128), the loop's tail with
+# three, two and one stages left after a partial last stage (144 .. 656), steady iterations
+# (1024) and a long loop ending in a partial stage (3088).
+
+MD, ND = 1100, 1800  # 9 x 15 = 135 tiles of 128, both edges partial
+
+
+def _assert_deep(m, n, k):
+    import mx_qlinear._lib as L
+
+    plan = L.gemm_plan(m, n, k)
+    assert (plan["tile"], plan["ahead"]) == (128, 4), plan
+
+
+@pytest.mark.parametrize("k", [16, 128, 144, 400, 528, 656, 1024, 3088])
+def test_gemm_i32_deep_ring(dev, k):
+    _assert_deep(MD, ND, k)
+    print(f"gemm i32 deep-ring m={MD} n={ND} k={k}", flush=True)
+    a, w = _i8((MD, k), 240 + k), _i8((ND, k), 241 + k)
+    c = _mx().mm_int8(a.to(dev), w.to(dev).t())
+    assert np.array_equal(c.cpu().numpy(), eager_np.int8_matmul(a.numpy(), w.numpy()))
+
+
+@pytest.mark.parametrize("k,bias", [(400, True), (3072, False)])
+def test_int8_linear_deep_ring(dev, k, bias):
+    _assert_deep(1024, 3072, k)
+    print(f"int8_linear deep-ring m=1024 n=3072 k={k} bias={bias}", flush=True)
+    x = activations(1024, k, 250 + k)
+    w, ws = int8_weight(3072, k, 251 + k)
+    b = bf16_vec(3072, 252, 0.01) if bias else None
+    y = _mx().int8_linear(x.to(dev), w.to(dev), ws.to(dev), None if b is None else b.to(dev))
+    ref = eager_np.int8_linear(bits(x), w.numpy(), ws.numpy(), None if b is None else bits(b), "bf16")
+    assert np.array_equal(bits(y), bf16_bits(ref))
+
+
+def test_gated_residual_deep_ring(dev):
+    k = 528
+    _assert_deep(MD, ND, k)
+    print(f"gated residual deep-ring m={MD} n={ND} k={k}", flush=True)
+    x = activations(MD, k, 260)
+    w, ws = int8_weight(ND, k, 261)
+    b = bf16_vec(ND, 262, 0.02)
+    gate = torch.randn(2, ND, generator=gen(263)).to(torch.bfloat16)
+    res = activations(MD, ND, 264) * 3
+    segs = ((0, 600, 1), (600, MD, 0))
+    out = res.to(dev)
+    _mx().int8_linear_gated_residual_(out, x.to(dev), w.to(dev), ws.to(dev), b.to(dev), gate.to(dev), segs)
+    q, s = eager_np.quantize_int8_rowwise(bits(x))
+    y = eager_np.dequant_epilogue(eager_np.int8_matmul(q, w.numpy()), s, ws.numpy(), bits(b), "bf16")
+    want = eager_np.gated_residual_bf16(bits(res), bf16_bits(y), bits(gate), eager_np.segment_row_map(MD, segs))
     assert np.array_equal(bits(out), want)
 
 

@@ -12,7 +12,8 @@
 // matrix work and no VGPRs stage data. Fragment reads are inline-asm ds_read_b128 with explicit
 // lgkmcnt waits; vmcnt waits and barriers are issued by hand too (s_waitcnt + s_barrier) so that
 // the prefetches stay in flight across the barrier that publishes the next stage. Problems with
-// fewer 256-tiles than CUs run the same code on 128 x 128 tiles, two workgroups per CU.
+// fewer 256-tiles than CUs run the same code on 128 x 128 tiles: two workgroups per CU, or, when
+// all the 128-tiles fit on the CUs at once, one per CU with a nine-slot ring four stages deep.
 //
 // Epilogue: the MFMAs run with the weights as first operand, so each lane's accumulators are
 // one output row in four runs of four consecutive columns. Every output type is converted in
@@ -40,26 +41,35 @@ namespace mxq {
 
 constexpr int kBK = 128;                                // K bytes per stage
 constexpr int kGemmThreads = 256;                       // 4 waves as 2 x 2
-constexpr int kSlots = 5;                               // LDS ring of operand slots
 
 // Tile shapes: kT x kT outputs per workgroup, each wave (kT/2)^2 as kBI x kBJ MFMA blocks of
 // 32 x 32. 256: one workgroup per CU, 160 KB ring, the GEMM of large problems. 128: two
-// workgroups per CU, 80 KB ring, for problems with fewer 256-tiles than CUs.
-template <int kT>
+// workgroups per CU, 80 KB ring, for problems with fewer 256-tiles than CUs. 128 with kDeep:
+// one workgroup per CU with a 144 KB ring that holds four stages in flight instead of two, for
+// problems whose 128-tiles all fit on the CUs at once (one workgroup per CU then leaves the
+// main loop waiting on operand latency, not on other workgroups).
+template <int kT, bool kDeep = false>
 struct TileCfg {
+  static_assert(kT == 128 || !kDeep, "the deep ring exists for 128-tiles only");
   static constexpr int kBM = kT, kBN = kT;
   static constexpr int kWaveM = kT / 2, kWaveN = kT / 2;
   static constexpr int kBI = kWaveM / 32, kBJ = kWaveN / 32;
   static constexpr int kSlotBytes = kT * kBK;                  // one operand chunk of a stage
   static constexpr int kLoads = kSlotBytes / 1024 / 4;          // direct-to-LDS loads per wave per slot
+  static constexpr int kAhead = kDeep ? 4 : 2;                  // stages requested ahead of the MFMAs
+  static constexpr int kSlots = 2 * kAhead + 1;                 // LDS ring of operand chunks
   static constexpr int kLds = kSlots * kSlotBytes;
   static constexpr int kEpiLds = kT == 256 ? 131072 : 4 * kSlotBytes;  // per-column factors
+  static constexpr int kPerCu = kT == 256 || kDeep ? 1 : 2;     // workgroups per CU
+  static_assert(kLds <= 160 * 1024, "the ring exceeds the CU's LDS");
+  static_assert(2 * kAhead * kLoads < 64, "loads in flight exceed the vmcnt counter");
 };
-// Tile-rows per group: with 2, the ~32 tiles an XCD runs at once are 2 tile-rows x 16 tile-columns,
-// so an activation panel is read from HBM once and then served from that XCD's L2 to the whole
-// row sweep, and the weight panels (the smaller operand) come back from the last-level cache.
-// Measured against 1, 3, 4, 8, 16 and 32 on the FFN and QKV shapes at 720p: 2 was fastest
-// (fc1 -2.8 %, fc2 -3.2 %, QKV -2 % against 8).
+// Tile-rows per group for problems of several rounds: with 2, the ~32 tiles an XCD runs at once are
+// 2 tile-rows x 16 tile-columns, so an activation panel is read from HBM once and then served
+// from that XCD's L2 to the whole row sweep, and the weight panels (the smaller operand) come
+// back from the last-level cache. Measured against 1, 3, 4, 8, 16 and 32 on the FFN and QKV
+// shapes at 720p: 2 was fastest (fc1 -2.8 %, fc2 -3.2 %, QKV -2 % against 8). Problems of one
+// round choose their own (plan_gemm).
 constexpr int kGroupM = 2;
 
 enum { kEpiI32 = 0, kEpiDequant = 1, kEpiGelu = 2, kEpiGatedRes = 3, kEpiSwiGLU = 4 };
@@ -87,6 +97,7 @@ struct GemmArgs {
   // n_claim workgroups claim; counters (the caller's workspace) hold the claim counts.
   int pool, wg_per_xcd, n_claim;
   unsigned* counters;
+  int group_m;  // tile-rows per group of the tile order (tile_walk)
 };
 
 // LDS operand layout: a tile row is 128 bytes = eight 16-byte chunks; chunk c of row r sits at
@@ -100,14 +111,14 @@ MXQ_DEVICE int swz(int r, int c) { return r * kBK + ((c ^ swz_f(r)) << 4); }
 static __device__ __attribute__((aligned(16))) uint8_t kZeroChunk[16];
 
 // Tile order: first spread contiguous tile ranges over the 8 XCDs (workgroup ids are dealt to
-// XCDs round-robin), then walk each range in groups of kGroupM tile-rows so that the ~32 tiles
+// XCDs round-robin), then walk each range in groups of group_m tile-rows so that the tiles
 // resident on one XCD share A and B panels in that XCD's L2. tile_walk maps a position t of
 // that order to its tile row and column.
-MXQ_DEVICE void tile_walk(int t, int tiles_m, int tiles_n, int& tm, int& tn) {
-  const int group = kGroupM * tiles_n;
+MXQ_DEVICE void tile_walk(int t, int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
+  const int group = group_m * tiles_n;
   const int g = t / group;
-  const int first_m = g * kGroupM;
-  const int gm = min(tiles_m - first_m, kGroupM);
+  const int first_m = g * group_m;
+  const int gm = min(tiles_m - first_m, group_m);
   const int in = t % group;
   tm = first_m + in % gm;
   tn = in / gm;
@@ -470,18 +481,19 @@ MXQ_DEVICE int pick_tile(const GemmArgs& p, int num, char* lds) {
   return pos;
 }
 
-template <int kEpi, int kOut, int kT>
-__global__ __launch_bounds__(kGemmThreads, kT == 256 ? 1 : 2) void gemm_i8_kernel(GemmArgs p) {
-  typedef TileCfg<kT> C;
+template <int kEpi, int kOut, int kT, bool kDeep>
+__global__ __launch_bounds__(kGemmThreads, (TileCfg<kT, kDeep>::kPerCu)) void gemm_i8_kernel(GemmArgs p) {
+  typedef TileCfg<kT, kDeep> C;
   constexpr int kBM = C::kBM, kBN = C::kBN, kWaveM = C::kWaveM, kWaveN = C::kWaveN;
   constexpr int kBI = C::kBI, kBJ = C::kBJ, kSlotBytes = C::kSlotBytes, kLoads = C::kLoads;
+  constexpr int kSlots = C::kSlots, kAhead = C::kAhead;
   static_assert(kT == 256 || (kEpi != kEpiGelu && kEpi != kEpiSwiGLU), "table epilogues need the 160 KB ring");
   __shared__ __attribute__((aligned(16))) char lds[C::kLds];
 
   const int pos = pick_tile(p, p.tiles_m * p.tiles_n, lds);
   if (pos < 0) return;
   int tm, tn;
-  tile_walk(pos, p.tiles_m, p.tiles_n, tm, tn);
+  tile_walk(pos, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
   const int64_t m0 = (int64_t)tm * kBM, n0 = (int64_t)tn * kBN;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int wm = wave >> 1, wn = wave & 1;
@@ -492,28 +504,30 @@ __global__ __launch_bounds__(kGemmThreads, kT == 256 ? 1 : 2) void gemm_i8_kerne
 #pragma unroll
     for (int j = 0; j < kBJ; ++j) acc[i][j] = v16i{};
 
-  // Pipeline: a ring of five slots (one operand chunk each) receives the operand chunks in the order A0 B0 A1 B1
-  // A2 ..., chunk i (A_j = 2j, B_j = 2j + 1) into slot i % 5; stage j (128 K-bytes) reads A_j
-  // and B_j. Entering iteration kt, A_kt and B_kt are complete and visible, B_kt+1 is in flight
-  // and F0 holds the fragments of (stage kt, K-step 0). The iteration runs K-steps 0..3, each
-  // step's fragments read behind the previous step's MFMAs. A_kt+2 goes into the slot of
-  // B_kt-1 (free since the previous barrier) with its loads spread over the MFMAs of K-steps 0
-  // and 1; before the MFMAs of K-step 3 the wave waits for B_kt+1, passes the barrier that
-  // frees the slots of A_kt and B_kt, reads (kt+1, 0), and spreads the loads of B_kt+2 over
-  // those MFMAs. A chunk is thus requested one to two stages before it is used, and no wave
-  // issues a burst of loads while its matrix pipe sits idle.
+  // Pipeline (D = kAhead stages ahead, a ring of S = 2D + 1 slots of one operand chunk each):
+  // the operand chunks arrive in the order A0 B0 A1 B1 A2 ..., chunk i (A_j = 2j, B_j = 2j + 1)
+  // into slot i % S; stage j (128 K-bytes) reads A_j and B_j. Entering iteration kt, A_kt and
+  // B_kt are complete and visible, stages kt+1 .. kt+D-1 are in flight and F0 holds the
+  // fragments of (stage kt, K-step 0). The iteration runs K-steps 0..3, each step's fragments
+  // read behind the previous step's MFMAs. A_kt+D goes into the slot of B_kt-1 (free since the
+  // previous barrier) with its loads spread over the MFMAs of K-steps 0 and 1; before the MFMAs
+  // of K-step 3 the wave waits for stage kt+1, passes the barrier that frees the slots of A_kt
+  // and B_kt, reads (kt+1, 0), and spreads the loads of B_kt+D over those MFMAs (into A_kt's
+  // slot). A chunk is thus requested D-1 to D stages before it is used, and no wave issues a
+  // burst of loads while its matrix pipe sits idle.
   const int ktiles = (int)((p.K + kBK - 1) / kBK);
   Loader<kLoads> ld;
   make_loader(ld, p, m0, n0);
-  issue_slot<false>(ld, lds, 0, p.K);
-  issue_slot<true>(ld, lds + kSlotBytes, 0, p.K);
-  if (ktiles > 1) {
-    issue_slot<false>(ld, lds + 2 * kSlotBytes, kBK, p.K);
-    issue_slot<true>(ld, lds + 3 * kSlotBytes, kBK, p.K);
-    wait_vmcnt<2 * kLoads>();
-  } else {
-    wait_vmcnt<0>();
+  const int pre = min(ktiles, kAhead);  // stages requested before the loop
+  for (int s = 0; s < pre; ++s) {
+    issue_slot<false>(ld, lds + 2 * s * kSlotBytes, (int64_t)s * kBK, p.K);
+    issue_slot<true>(ld, lds + (2 * s + 1) * kSlotBytes, (int64_t)s * kBK, p.K);
   }
+  // wait for stage 0: every load but those of stages 1 .. pre-1 has completed
+  static_for<kAhead>([&](auto P) {
+    constexpr int np = decltype(P)::value + 1;
+    if (pre == np) wait_vmcnt<2 * (np - 1) * kLoads>();
+  });
   barrier_no_drain();
 
   const uint32_t lds_addr = (uint32_t)(uintptr_t)(lptr_t)lds;
@@ -530,11 +544,11 @@ __global__ __launch_bounds__(kGemmThreads, kT == 256 ? 1 : 2) void gemm_i8_kerne
     const int sb = sa == kSlots - 1 ? 0 : sa + 1;
     const int na = sb == kSlots - 1 ? 0 : sb + 1;  // A_kt+1
     const int nb = na == kSlots - 1 ? 0 : na + 1;  // B_kt+1
-    const int pa = nb == kSlots - 1 ? 0 : nb + 1;  // A_kt+2 (slot of B_kt-1)
+    const int pa = sa == 0 ? kSlots - 1 : sa - 1;  // A_kt+D (slot of B_kt-1)
     const uint32_t cur_a = lds_addr + (uint32_t)(sa * kSlotBytes), cur_b = lds_addr + (uint32_t)(sb * kSlotBytes);
-    const bool more2 = kSteady || kt + 2 < ktiles;
+    const bool more2 = kSteady || kt + kAhead < ktiles;  // stage kt+D exists
     const bool more1 = kSteady || kt + 1 < ktiles;
-    const int64_t k2 = (int64_t)(kt + 2) * kBK;
+    const int64_t k2 = (int64_t)(kt + kAhead) * kBK;
     load_frags<C>(cur_a, cur_b, wm, wn, 1, f1a, f1b);
     wait_lgkm<kBI + kBJ>();
     __builtin_amdgcn_sched_barrier(0);
@@ -550,8 +564,19 @@ __global__ __launch_bounds__(kGemmThreads, kT == 256 ? 1 : 2) void gemm_i8_kerne
     __builtin_amdgcn_sched_barrier(0);
     mma_step<C>(f0a, f0b, acc);
     __builtin_amdgcn_sched_barrier(0);
+    // Stage kt+1 has landed when only the loads issued after B_kt+1 are outstanding: stages
+    // kt+2 .. kt+D-1 and A_kt+D where they exist (2 (r - 1) chunks when only r < D stages remain).
     if (more2) {
-      __builtin_amdgcn_s_waitcnt((kLoads & 0xF) | (0x7 << 4));  // vmcnt(kLoads) lgkmcnt(0)
+      wait_vm_lgkm0<(2 * kAhead - 3) * kLoads>();
+    } else if constexpr (kAhead > 2) {
+      const int r = ktiles - 1 - kt;
+      if (r == 3) {
+        wait_vm_lgkm0<4 * kLoads>();
+      } else if (r == 2) {
+        wait_vm_lgkm0<2 * kLoads>();
+      } else {
+        wait_all();
+      }
     } else {
       wait_all();
     }
@@ -568,7 +593,7 @@ __global__ __launch_bounds__(kGemmThreads, kT == 256 ? 1 : 2) void gemm_i8_kerne
   // steady < ktiles always (ktiles >= 1): written as do-while, the tail is seen to run at least
   // once, so no path leaves the steady loop with fragment reads in flight straight into the
   // epilogue (whose register copies would otherwise race those reads).
-  const int steady = (int)max<int64_t>(p.K / kBK - 2, 0);  // iterations whose stage kt+2 is full
+  const int steady = (int)max<int64_t>(p.K / kBK - kAhead, 0);  // iterations whose stage kt+D is full
   int kt = 0;
   for (; kt < steady; ++kt) iteration(kt, std::true_type{});
   do {
@@ -827,8 +852,10 @@ static_assert(MXQ_GEMM_WORKSPACE_BYTES >= kTileQueueBytes, "workspace holds the 
 // Launch plan of one GEMM: tile size, tile queue and grid.
 struct GemmPlan {
   int tile;  // 256 or 128
+  bool deep;  // 128-tiles with the deep ring: every tile on its own CU at once
   int tiles_m, tiles_n;
   int pool, wg_per_xcd, n_claim;
+  int group_m;
   int64_t grid;
 };
 
@@ -848,8 +875,25 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, bool table, int64_t workspace_by
   g.tiles_m = (int)std::min<int64_t>((M + g.tile - 1) / g.tile, INT32_MAX);
   g.tiles_n = (int)std::min<int64_t>((N + g.tile - 1) / g.tile, INT32_MAX);
   const int64_t tiles = (int64_t)g.tiles_m * g.tiles_n;
+  g.deep = g.tile == 128 && tiles <= 256;
   g.grid = tiles;
+  // Deep-ring problems run every tile at once, one per CU: each XCD fetches the A and B panels
+  // of its range once, so the range is made as square as the groups allow (1024 x 3072, 24
+  // tiles per XCD: 4 x 6 tiles read 10 panels where 2 x 12 read 14; 17.8 against 18.5 us per
+  // launch with operands from HBM). Two workgroups per CU measured no better this way.
+  g.group_m = kGroupM;
   const int64_t slots = g.tile == 256 ? 256 : 512;
+  if (g.deep) {
+    const int64_t per = (tiles + 7) / 8;
+    int64_t best = INT64_MAX;
+    for (int64_t gm = 1; gm <= std::min<int64_t>(g.tiles_m, per); ++gm) {
+      const int64_t panels = gm + (per + gm - 1) / gm;
+      if (panels < best) {
+        best = panels;
+        g.group_m = (int)gm;
+      }
+    }
+  }
   if (workspace_bytes >= kTileQueueBytes && tiles >= 2 * slots && tiles <= INT32_MAX / 2) {
     const int64_t per = tiles / 8, rem = tiles % 8;
     g.pool = (int)((per + kPoolDiv - 1) / kPoolDiv);
@@ -871,6 +915,7 @@ static int launch_gemm(const GemmArgs& args0, void* workspace, int64_t workspace
   args.wg_per_xcd = g.wg_per_xcd;
   args.n_claim = g.n_claim;
   args.counters = g.pool ? reinterpret_cast<unsigned*>(workspace) : nullptr;
+  args.group_m = g.group_m;
   const int elem = (kOut == 0 || kEpi == kEpiI32) ? 4 : 2;
   args.vec_store = ((uintptr_t)args.d % (4 * elem) == 0) && (args.ldd % 4 == 0);
   args.line_store = ((uintptr_t)args.d % 16 == 0) && ((args.ldd * elem) % 16 == 0);
@@ -881,11 +926,14 @@ static int launch_gemm(const GemmArgs& args0, void* workspace, int64_t workspace
   const unsigned grid = (unsigned)g.grid;
   if constexpr (kEpi != kEpiGelu && kEpi != kEpiSwiGLU) {
     if (g.tile == 128) {
-      gemm_i8_kernel<kEpi, kOut, 128><<<grid, kGemmThreads, 0, stream>>>(args);
+      if (g.deep)
+        gemm_i8_kernel<kEpi, kOut, 128, true><<<grid, kGemmThreads, 0, stream>>>(args);
+      else
+        gemm_i8_kernel<kEpi, kOut, 128, false><<<grid, kGemmThreads, 0, stream>>>(args);
       return mxq_check_launch("gemm_i8_kernel");
     }
   }
-  gemm_i8_kernel<kEpi, kOut, 256><<<grid, kGemmThreads, 0, stream>>>(args);
+  gemm_i8_kernel<kEpi, kOut, 256, false><<<grid, kGemmThreads, 0, stream>>>(args);
   return mxq_check_launch("gemm_i8_kernel");
 }
 
@@ -922,6 +970,8 @@ extern "C" int mxq_int8_gemm_plan(int64_t M, int64_t N, int64_t K, int table_epi
   plan[2] = (int64_t)g.tiles_m * g.tiles_n;
   plan[3] = g.pool;
   plan[4] = g.wg_per_xcd;
+  plan[5] = g.tile == 256 ? TileCfg<256>::kAhead : g.deep ? TileCfg<128, true>::kAhead : TileCfg<128>::kAhead;
+  plan[6] = g.group_m;
   return MXQ_OK;
 }
 

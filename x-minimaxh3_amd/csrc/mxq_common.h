@@ -275,6 +275,12 @@ template <int n> MXQ_DEVICE void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// s_waitcnt vmcnt(n) lgkmcnt(0).
+template <int n> MXQ_DEVICE void wait_vm_lgkm0() {
+  static_assert(n >= 0 && n < 64, "vmcnt is six bits");
+  __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4));
+}
+
 // s_waitcnt vmcnt(0) lgkmcnt(0).
 MXQ_DEVICE void wait_all() { __builtin_amdgcn_s_waitcnt(0x0070); }
 

@@ -98,10 +98,12 @@ def load() -> ctypes.CDLL:
 
 def gemm_plan(m: int, n: int, k: int, table: bool = False, workspace_bytes: int = GEMM_WORKSPACE_BYTES) -> dict:
     """The INT8 GEMM launch plan (mxq_int8_gemm_plan): tile edge, workgroups, tiles, tiles per XCD
-    claimed at run time (0: static order) and workgroups per XCD."""
-    out = (ctypes.c_int64 * 5)()
+    claimed at run time (0: static order), workgroups per XCD, operand stages requested ahead and
+    tile-rows per group of the tile order."""
+    out = (ctypes.c_int64 * 7)()
     call("mxq_int8_gemm_plan", m, n, k, int(table), workspace_bytes, out)
-    return {"tile": out[0], "grid": out[1], "tiles": out[2], "pool": out[3], "wg_per_xcd": out[4]}
+    return {"tile": out[0], "grid": out[1], "tiles": out[2], "pool": out[3], "wg_per_xcd": out[4],
+            "ahead": out[5], "group_m": out[6]}
 
 
 def call(name: str, *args) -> None:
