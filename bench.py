@@ -826,6 +826,13 @@ def _pmc_child(wl):
     torch.cuda.synchronize()
 
 
+def _symbol_matches(symbol, name):
+    """Whether the profiler's kernel name `name` is an instance of `symbol`: a plain name, or a
+    template prefix such as "gemm_i8_kernel<1, 2, 256>" that also matches instances with further
+    template arguments ("gemm_i8_kernel<1, 2, 256, false>")."""
+    return symbol in name or (symbol.endswith(">") and symbol[:-1] + "," in name)
+
+
 def _counter_pass(workload, counter, symbol, out_root, nth=(0, 1)):
     """Runs `rocprofv3 --pmc <counter>` over a child bench process; returns (KiB per launch of
     `symbol` -- its dispatches nth[0], nth[0] + nth[1], ... when a step launches it nth[1]
@@ -863,7 +870,7 @@ def _counter_pass(workload, counter, symbol, out_root, nth=(0, 1)):
             if row["Counter_Name"] != counter:
                 continue
             name, val = row["Kernel_Name"], float(row["Counter_Value"])
-            if symbol in name:
+            if _symbol_matches(symbol, name):
                 kern.append((int(row.get("Dispatch_Id", len(kern))), val))
             elif "neg_kernel" in name:
                 copy.append(val)

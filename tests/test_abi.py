@@ -258,3 +258,20 @@ def test_tile_queue_plan_covers_every_tile_once(lib, m, n, table):
         orders.append(o)
     for order in orders:
         assert sorted(_queue_cover(plan["tiles"], plan["pool"], plan["wg_per_xcd"], order)) == list(range(plan["tiles"]))
+
+
+def test_bench_matches_kernel_instances_by_template_prefix():
+    """bench.py's counter passes find the dominant kernel by its symbol; GEMM instances carry a
+    trailing tile-configuration template argument that the symbol leaves out."""
+    import importlib.util
+    import pathlib
+
+    spec = importlib.util.spec_from_file_location("bench", pathlib.Path(__file__).resolve().parents[1] / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    m = bench._symbol_matches
+    assert m("gemm_i8_kernel<1, 2, 256>", "void mxq::gemm_i8_kernel<1, 2, 256, false>(mxq::GemmArgs)")
+    assert m("gemm_i8_kernel<1, 2, 128>", "void mxq::gemm_i8_kernel<1, 2, 128, true>(mxq::GemmArgs)")
+    assert not m("gemm_i8_kernel<1, 2, 128>", "void mxq::gemm_i8_kernel<1, 2, 256, false>(mxq::GemmArgs)")
+    assert not m("gemm_i8_kernel<1, 2, 256>", "void mxq::gemm_i8_kernel<4, 2, 256, false>(mxq::GemmArgs)")
+    assert m("w4a8_g128_kernel", "void mxq::w4a8_g128_kernel<128, 3>(mxq::G128Args)")
