@@ -21,6 +21,18 @@ int mxq_check_launch(const char* what) {
   return MXQ_OK;
 }
 
+// Compute units of the current device, cached per device (256 when the query fails).
+int mxq_cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cached[dev];
+}
+
 extern "C" const char* mxq_last_error(void) { return g_last_error; }
 
 extern "C" int mxq_abi_version(void) { return MXQ_ABI_VERSION; }

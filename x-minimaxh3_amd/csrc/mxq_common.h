@@ -319,3 +319,15 @@ MXQ_DEVICE v4i lds_read_b128(uint32_t addr) {
 // ---- host-side error plumbing (defined in capi.hip) -------------------------------
 int mxq_set_error(int code, const char* fmt, ...);
 int mxq_check_launch(const char* what);
+int mxq_cu_count();  // compute units of the current device
+
+// Workgroups of `kernel` that are resident at once on the current device (for grid-stride
+// kernels whose workgroups each take an equal share of the rows: a grid larger than this leaves
+// its last workgroups to start when the first have finished), capped at `want`.
+template <class K>
+inline unsigned mxq_resident_grid(K kernel, int block, size_t lds, int64_t want) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, lds) != hipSuccess || per_cu < 1) per_cu = 1;
+  const int64_t cap = (int64_t)per_cu * mxq_cu_count();
+  return (unsigned)(want < cap ? want : cap);
+}

@@ -761,14 +761,19 @@ static int adaln_launch(const void* x, const void* scale, const void* shift, int
                 : need <= 11 ? 11 : need <= 12 ? 12 : need <= 14 ? 14 : 16;
   if (scale_group >= rows && shift_group >= rows && cols <= kAdalnMaxCols && (cols == uch * 512 || uch <= 12)) {
     // one modulation row: the two-buffer kernel (widths whose register budget it fits)
+    // Every workgroup takes an equal share of the rows, so the grid is what fits on the device at
+    // once: a larger one left its last workgroups to start after the first had finished.
     const size_t lds = (size_t)cols * 2 * sizeof(float);
     const int64_t wg = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-    const unsigned grid = (unsigned)(wg < 1024 ? wg : 1024);
 #define MXQ_ADALN_UNIFORM_K(N_, E_)                                                                              \
-  (quant ? (void)(adaln_uniform_rows<N_, true, E_><<<grid, kQuantBlock, lds, st>>>(                              \
+  (quant ? (void)(adaln_uniform_rows<N_, true, E_><<<mxq_resident_grid(adaln_uniform_rows<N_, true, E_>,          \
+                                                                       kQuantBlock, lds, wg),                    \
+                                                     kQuantBlock, lds, st>>>(                                    \
                (const uint16_t*)x, (const uint16_t*)scale, (const uint16_t*)shift, eps, q, scales,              \
                (uint16_t*)y_out, rows, (int)cols))                                                               \
-         : (void)(adaln_uniform_rows<N_, false, E_><<<grid, kQuantBlock, lds, st>>>(                             \
+         : (void)(adaln_uniform_rows<N_, false, E_><<<mxq_resident_grid(adaln_uniform_rows<N_, false, E_>,        \
+                                                                        kQuantBlock, lds, wg),                   \
+                                                      kQuantBlock, lds, st>>>(                                   \
                (const uint16_t*)x, (const uint16_t*)scale, (const uint16_t*)shift, eps, nullptr, nullptr,        \
                (uint16_t*)y_out, rows, (int)cols)))
 #define MXQ_ADALN_UNIFORM(N_) \
