@@ -210,6 +210,20 @@ __global__ __launch_bounds__(kGeluRowThreads) void quant_rows_gelu_wide(
 #pragma unroll
     for (int j = 0; j < kC; ++j) v[j] = __builtin_nontemporal_load(src + min(t + j * kGeluRowThreads, chunks - 1));
   };
+  // A row's int8 results stay in registers until the next row's data has landed: its stores are
+  // issued then, a whole row of work before the next wait, rather than right before it (waits on
+  // the vector-memory counter cover every older access, stores included).
+  v2u qv[kC];
+  float qs = 0.0f;
+  auto store_q = [&](int64_t r) {
+    v2u* dq = reinterpret_cast<v2u*>(q + r * (int64_t)chunks * 8);
+#pragma unroll
+    for (int j = 0; j < kC; ++j) {
+      const int c = t + j * kGeluRowThreads;
+      if (c < chunks) __builtin_nontemporal_store(qv[j], dq + c);
+    }
+    if (t == 0) scales[r] = qs;
+  };
   auto do_row = [&](int64_t r, v4u (&v)[kC], int parity) {
     uint32_t m = 0;
 #pragma unroll
@@ -236,46 +250,47 @@ __global__ __launch_bounds__(kGeluRowThreads) void quant_rows_gelu_wide(
     const float amax = __uint_as_float(bits);
     const float s = row_scale_from_absmax(amax);
     const float rcp = 1.0f / round_bf16(s);
-    v2u* dq = reinterpret_cast<v2u*>(q + r * (int64_t)chunks * 8);
     v4u* dh = reinterpret_cast<v4u*>(h + r * (int64_t)chunks * 8);
     if (finite_absmax(amax)) {
 #pragma unroll
-      for (int j = 0; j < kC; ++j) {
-        const int c = t + j * kGeluRowThreads;
-        if (c < chunks) {
-          __builtin_nontemporal_store(quant8_bf16_finite(v[j], rcp), dq + c);
-          if (kStoreH) __builtin_nontemporal_store(v[j], dh + c);
-        }
-      }
+      for (int j = 0; j < kC; ++j) qv[j] = quant8_bf16_finite(v[j], rcp);
     } else {
+#pragma unroll
+      for (int j = 0; j < kC; ++j) qv[j] = quant8_bf16(v[j], rcp);
+    }
+    qs = s;
+    if (kStoreH) {
 #pragma unroll
       for (int j = 0; j < kC; ++j) {
         const int c = t + j * kGeluRowThreads;
-        if (c < chunks) {
-          __builtin_nontemporal_store(quant8_bf16(v[j], rcp), dq + c);
-          if (kStoreH) __builtin_nontemporal_store(v[j], dh + c);
-        }
+        if (c < chunks) __builtin_nontemporal_store(v[j], dh + c);
       }
     }
-    if (t == 0) scales[r] = s;
   };
   v4u a[kC], b[kC];
   int64_t row = blockIdx.x;
   load_row(row, a);
-  wait_vmcnt<0>();  // the table (and the first row) have landed in this wave
-  __syncthreads();  // ... in every wave
   int parity = 0;
+  int64_t prev = -1;  // the row whose int8 results wait in qv
+  // One step: the current row has landed (and every older access has completed: the previous
+  // row's prefetch a row of work ago, the stores before it), the held results are stored, the
+  // next row's loads go out, and the current row is processed.
+  auto step = [&](v4u (&cur)[kC], v4u (&nxt)[kC]) {
+    wait_vmcnt<0>();
+    if (prev < 0) __syncthreads();  // the table has landed in every wave
+    if (prev >= 0) store_q(prev);
+    load_row(row + stride, nxt);
+    do_row(row, cur, parity);
+    prev = row;
+    row += stride;
+    parity ^= 1;
+  };
   while (row < rows) {
-    load_row(row + stride, b);
-    do_row(row, a, parity);
-    row += stride;
-    parity ^= 1;
+    step(a, b);
     if (row >= rows) break;
-    load_row(row + stride, a);
-    do_row(row, b, parity);
-    row += stride;
-    parity ^= 1;
+    step(b, a);
   }
+  if (prev >= 0) store_q(prev);
 }
 
 // ---- adaLN ------------------------------------------------------------------------
