@@ -651,7 +651,7 @@ class W4A8RefQkvWorkload:
                       256, _lib.ACT_NONE, st)
             _lib.call("mxq_w4a8_codebook_gemm", _p(self.q), _p(self.qdata), _p(self.s_rel), _lib.DTYPE_E4M3,
                       _p(self.codebook), _p(self.s_ch), _p(self.xs), _p(self.b), _p(self.work), _p(self.out), m, n, d,
-                      g, self.chunk, _lib.DTYPE_BF16, st)
+                      g, self.chunk, _lib.DTYPE_BF16, *_gemm_ws(self.dev), st)
             return
         with timer.span("convrot_quant"):
             _lib.call("mxq_quantize_int8_rowwise_convrot", _p(self.x), _lib.DTYPE_BF16, _p(self.q), _p(self.xs), m, d,
@@ -663,7 +663,8 @@ class W4A8RefQkvWorkload:
                           _p(self.codebook), _p(self.work), cols, d, g, st)
             with timer.span("gemm"):
                 _lib.call("mxq_int8_gemm_dequant", _p(self.q), _p(self.work), _p(self.xs), _p(self.s_ch[n0:]), cols,
-                          _p(self.b[n0:]), _p(self.out[:, n0:]), m, cols, d, n, _lib.DTYPE_BF16, None, 0, st)
+                          _p(self.b[n0:]), _p(self.out[:, n0:]), m, cols, d, n, _lib.DTYPE_BF16, *_gemm_ws(self.dev),
+                          st)
 
     def ops_per_step(self):
         return 2 * self.m * self.n * self.d

@@ -311,14 +311,16 @@ int mxq_dequant_int4_grouped_to_int8(const int8_t* qdata, const void* s_rel, int
  * Reference-format W4A8 linear on an already quantized activation: decode the packed weight
  * chunk by chunk into `workspace` ([chunk_cols, K] int8) and run the dequant GEMM with
  * ws = s_channel. Arguments as mxq_dequant_int4_grouped_to_int8 and mxq_int8_gemm_dequant;
- * out [M, N] of out_dtype, bias [N] of out_dtype or NULL.
+ * out [M, N] of out_dtype, bias [N] of out_dtype or NULL; gemm_workspace / gemm_workspace_bytes
+ * are the chunk GEMMs' tile-queue workspace, as for the INT8 GEMMs (NULL, 0: static order).
  * Replaces: launch_w4a8_codebook_gemm_chunked, CK/backends/cuda/ops/w4a8_gemm.cu:133-164.
  */
 int mxq_w4a8_codebook_gemm(const int8_t* xq, const int8_t* qdata, const void* s_rel,
                            int s_rel_dtype, const float* codebook, const float* s_channel,
                            const float* xs, const void* bias, int8_t* workspace, void* out,
                            int64_t M, int64_t N, int64_t K, int64_t group_size,
-                           int64_t chunk_cols, int out_dtype, void* stream);
+                           int64_t chunk_cols, int out_dtype, void* gemm_workspace,
+                           int64_t gemm_workspace_bytes, void* stream);
 
 /*
  * mxq_w4a8_codebook_gemm without the caller's workspace: the decoded chunk lives in a static
@@ -326,8 +328,9 @@ int mxq_w4a8_codebook_gemm(const int8_t* xq, const int8_t* qdata, const void* s_
  * allocates nothing. No counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). Same arguments and results (bit for bit) as mxq_w4a8_codebook_gemm, less
- * `workspace`; min(chunk_cols, N) * K must not exceed 32 MiB (MXQ_ERR_INVALID otherwise).
- * Calls share the GPU's array: two calls that overlap on one GPU (different streams) race.
+ * `workspace` and the GEMM workspace (a second static array, 4 KiB, holds the tile-queue
+ * counters); min(chunk_cols, N) * K must not exceed 32 MiB (MXQ_ERR_INVALID otherwise).
+ * Calls share the GPU's arrays: two calls that overlap on one GPU (different streams) race.
  */
 int mxq_w4a8_codebook_gemm_noalloc(const int8_t* xq, const int8_t* qdata, const void* s_rel,
                                    int s_rel_dtype, const float* codebook, const float* s_channel,

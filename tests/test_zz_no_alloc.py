@@ -1,6 +1,8 @@
 """GPU parity of the allocation-free W4A8 entry point (mxq_w4a8_codebook_gemm_noalloc) against
 the entry point it varies (mxq_w4a8_codebook_gemm with a caller workspace), called through the
-C ABI: two calls in a row, the second smaller, then a chunk too large for the static workspace.
+C ABI: two calls in a row, the second smaller, then a chunk too large for the static workspace;
+and two calls whose chunk GEMMs are large enough to claim tiles at run time (the workspace entry
+with a per-stream tile-queue workspace, the allocation-free one with its static counters).
 
 Bar: outputs bit-identical to the workspace entry point's on every call.
 """
@@ -13,10 +15,14 @@ from _util import activations, bf16_vec, gen, packed_int4
 pytestmark = pytest.mark.gpu
 
 
-def _call_pair(dev, m, n, k, g, e4m3, codebook, bias, chunk, seed):
+def _call_pair(dev, m, n, k, g, e4m3, codebook, bias, chunk, seed, queued=False):
     import mx_qlinear
     from mx_qlinear import _lib
-    from mx_qlinear.ops import _p, _stream
+    from mx_qlinear.ops import _gemm_ws, _p, _stream
+
+    if queued:  # each chunk GEMM claims tiles at run time
+        plan = _lib.gemm_plan(m, min(chunk, n), k)
+        assert plan["pool"] > 0, plan
 
     print(f"no-alloc w4a8 m={m} n={n} k={k} g={g} e4m3={e4m3} codebook={codebook} chunk={chunk}", flush=True)
     x = activations(m, k, seed).to(dev)
@@ -34,8 +40,9 @@ def _call_pair(dev, m, n, k, g, e4m3, codebook, bias, chunk, seed):
     got = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=dev)
     work = torch.empty((min(chunk, n), k), dtype=torch.int8, device=dev)
     st = _stream(dev)
+    gws = _gemm_ws(dev) if queued else (None, 0)
     _lib.call("mxq_w4a8_codebook_gemm", _p(xq), _p(qd), _p(sr), code, _p(cb), _p(sch), _p(xs), _p(b), _p(work),
-              _p(want), m, n, k, g, chunk, _lib.DTYPE_BF16, st)
+              _p(want), m, n, k, g, chunk, _lib.DTYPE_BF16, *gws, st)
     _lib.call("mxq_w4a8_codebook_gemm_noalloc", _p(xq), _p(qd), _p(sr), code, _p(cb), _p(sch), _p(xs), _p(b),
               _p(got), m, n, k, g, chunk, _lib.DTYPE_BF16, st)
     torch.cuda.synchronize()
@@ -49,6 +56,13 @@ def test_noalloc_matches_workspace_entry_two_calls(dev):
     # second call, smaller: one chunk, fp32 scales, no codebook, no bias; the array keeps the
     # first call's decode beyond this one's chunk, which must not leak into the result
     _call_pair(dev, 64, 700, 512, 16, False, False, False, 4096, 7002)
+
+
+def test_noalloc_chunk_gemms_claim_tiles_like_the_workspace_entry(dev):
+    # 8192 x 4096 chunks (512 tiles of 256) and 8000 x 4500 (576): the static counters must be
+    # back at zero after the first call for the second to match
+    _call_pair(dev, 8192, 8192, 1024, 16, True, True, True, 4096, 7101, queued=True)
+    _call_pair(dev, 8000, 4500, 512, 16, False, True, False, 4500, 7102, queued=True)
 
 
 def test_noalloc_rejects_a_chunk_beyond_the_static_workspace(dev):

@@ -302,12 +302,13 @@ extern "C" int mxq_dequant_int4_grouped_to_int8(const int8_t* qdata, const void*
 }
 
 // Decode-then-GEMM over column chunks of chunk_cols weights rows, the decoded chunk in
-// `workspace` ([chunk_cols, K] int8). Arguments are validated by the callers.
+// `workspace` ([chunk_cols, K] int8), each chunk's GEMM with the tile-queue workspace `queue`
+// (NULL: static tile order). Arguments are validated by the callers.
 static int codebook_gemm_chunks(const int8_t* xq, const int8_t* qdata, const void* s_rel, int s_rel_dtype,
                                 const float* codebook, const float* s_channel, const float* xs,
                                 const void* bias, int8_t* workspace, void* out, int64_t M, int64_t N,
                                 int64_t K, int64_t group_size, int64_t chunk_cols, int out_dtype,
-                                void* stream) {
+                                void* queue, int64_t queue_bytes, void* stream) {
   const int osz = out_dtype == MXQ_DTYPE_F32 ? 4 : 2;
   const int64_t groups = K / group_size;
   const int sbytes = s_rel_dtype == MXQ_DTYPE_E4M3 ? 1 : 4;
@@ -319,7 +320,7 @@ static int codebook_gemm_chunks(const int8_t* xq, const int8_t* qdata, const voi
     if (rc) return rc;
     const void* bias_chunk = bias ? (const char*)bias + n0 * osz : nullptr;
     rc = mxq_int8_gemm_dequant(xq, workspace, xs, s_channel + n0, cols, bias_chunk,
-                               (char*)out + n0 * osz, M, cols, K, N, out_dtype, nullptr, 0, stream);
+                               (char*)out + n0 * osz, M, cols, K, N, out_dtype, queue, queue_bytes, stream);
     if (rc) return rc;
   }
   return MXQ_OK;
@@ -342,12 +343,13 @@ extern "C" int mxq_w4a8_codebook_gemm(const int8_t* xq, const int8_t* qdata, con
                                       const float* s_channel, const float* xs, const void* bias,
                                       int8_t* workspace, void* out, int64_t M, int64_t N,
                                       int64_t K, int64_t group_size, int64_t chunk_cols,
-                                      int out_dtype, void* stream) {
+                                      int out_dtype, void* gemm_workspace, int64_t gemm_workspace_bytes,
+                                      void* stream) {
   int rc = check_codebook_gemm(qdata, s_rel, s_rel_dtype, s_channel, xs, out, M, N, K, group_size, chunk_cols);
   if (rc || M == 0 || N == 0) return rc;
   if (!workspace) return mxq_set_error(MXQ_ERR_INVALID, "null workspace");
   return codebook_gemm_chunks(xq, qdata, s_rel, s_rel_dtype, codebook, s_channel, xs, bias, workspace, out, M, N,
-                              K, group_size, chunk_cols, out_dtype, stream);
+                              K, group_size, chunk_cols, out_dtype, gemm_workspace, gemm_workspace_bytes, stream);
 }
 
 // ---- allocation-free variant ----------------------------------------------------------
@@ -357,17 +359,21 @@ extern "C" int mxq_w4a8_codebook_gemm(const int8_t* xq, const int8_t* qdata, con
 // device address): the device address is looked up once per device with hipGetSymbolAddress and
 // kept in g_scratch_ptr. Every call on one GPU reuses that GPU's array; the decode overwrites
 // every byte a GEMM reads, so nothing needs clearing between calls, and two calls that overlap on
-// one GPU (two streams) race on it.
+// one GPU (two streams) race on it. The chunk GEMMs' tile-queue counters are a second, small
+// array of the same kind (zero when the library loads; every GEMM leaves them zero).
 constexpr int64_t kNoAllocScratchBytes = int64_t(32) << 20;
 static __device__ __attribute__((aligned(256))) int8_t scratch[kNoAllocScratchBytes];
+static __device__ __attribute__((aligned(256))) uint32_t queue_scratch[MXQ_GEMM_WORKSPACE_BYTES / 4];
 
 namespace {
 constexpr int kMaxScratchDevices = 64;
 std::mutex g_scratch_mutex;
 int8_t* g_scratch_ptr[kMaxScratchDevices] = {};
+void* g_queue_ptr[kMaxScratchDevices] = {};
 
-// Device address of the current device's scratch array (looked up on the first call per device).
-int current_device_scratch(int8_t** ptr) {
+// Device addresses of the current device's scratch and queue arrays (looked up on the first call
+// per device).
+int current_device_scratch(int8_t** ptr, void** queue) {
   int dev = -1;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return mxq_set_error(MXQ_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(err));
@@ -381,9 +387,16 @@ int current_device_scratch(int8_t** ptr) {
     if (err != hipSuccess || p == nullptr)
       return mxq_set_error(MXQ_ERR_HIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
                            hipGetErrorString(err));
+    void* qp = nullptr;
+    err = hipGetSymbolAddress(&qp, HIP_SYMBOL(queue_scratch));
+    if (err != hipSuccess || qp == nullptr)
+      return mxq_set_error(MXQ_ERR_HIP, "hipGetSymbolAddress(queue_scratch) failed on device %d: %s", dev,
+                           hipGetErrorString(err));
     g_scratch_ptr[dev] = static_cast<int8_t*>(p);
+    g_queue_ptr[dev] = qp;
   }
   *ptr = g_scratch_ptr[dev];
+  *queue = g_queue_ptr[dev];
   return MXQ_OK;
 }
 }  // namespace
@@ -403,10 +416,11 @@ extern "C" int mxq_w4a8_codebook_gemm_noalloc(const int8_t* xq, const int8_t* qd
                          (long long)cols, (long long)K, (long long)kNoAllocScratchBytes,
                          (long long)(kNoAllocScratchBytes / K));
   int8_t* ws = nullptr;
-  rc = current_device_scratch(&ws);
+  void* queue = nullptr;
+  rc = current_device_scratch(&ws, &queue);
   if (rc) return rc;
   return codebook_gemm_chunks(xq, qdata, s_rel, s_rel_dtype, codebook, s_channel, xs, bias, ws, out, M, N, K,
-                              group_size, chunk_cols, out_dtype, stream);
+                              group_size, chunk_cols, out_dtype, queue, MXQ_GEMM_WORKSPACE_BYTES, stream);
 }
 
 static int check_grouped(const int8_t* a, const float* xs, const int8_t* qdata, const uint16_t* group_scale,

@@ -53,7 +53,8 @@ SIGNATURES: dict[str, list] = {
     "mxq_rms_adaln_quantize_int8": [_P, _P, _P, _P, _I64, _I64, _P, _F, _P, _P, _P, _I64, _I64, _I64, _P],
     "mxq_gelu_tanh_bf16": [_P, _P, _I64, _P],
     "mxq_dequant_int4_grouped_to_int8": [_P, _P, _I, _P, _P, _I64, _I64, _I64, _P],
-    "mxq_w4a8_codebook_gemm": [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P],
+    "mxq_w4a8_codebook_gemm": [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P, _I64,
+                               _P],
     "mxq_w4a8_codebook_gemm_noalloc": [_P, _P, _P, _I, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "mxq_w4a8_gemm_grouped": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "mxq_w4a8_gemm_grouped_prepared": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P],

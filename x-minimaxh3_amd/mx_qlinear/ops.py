@@ -957,7 +957,7 @@ def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, 
     work = torch.empty((chunk, k), dtype=torch.int8, device=dev)
     with torch.cuda.device(dev):
         call("mxq_w4a8_codebook_gemm", _p(xq), _p(qdata.contiguous()), _p(sr), scode, _p(cb), _p(sch),
-             _p(xs), _p(b), _p(work), _p(out), m, n, k, group_size, chunk, code, _stream(dev))
+             _p(xs), _p(b), _p(work), _p(out), m, n, k, group_size, chunk, code, *_gemm_ws(dev), _stream(dev))
         if correction is not None:
             sx = torch.empty((m, k // group_size), dtype=out_dtype, device=dev)
             call("mxq_int8_group_sums", _p(xq), _p(xs), _p(sx), m, k, group_size, code, _stream(dev))
