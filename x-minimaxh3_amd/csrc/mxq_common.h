@@ -22,6 +22,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
 namespace mxq {
@@ -143,28 +144,27 @@ MXQ_DEVICE v2u quant8_bf16(v4u w, float r) {
 }
 
 // The same for a row whose absmax is finite. Then |bf16(v * r)| <= 127.5 (r = 1 / bf16(s) and
-// bf16(s) is within 2^-8 of amax / 127), so the lower clamp never acts and the upper one is a
-// min with 127 before rounding; the rounding to an integer is one fp32 addition of 1.5 * 2^23
-// (an exact sum rounded half to even) whose low byte is the two's complement int8.
-MXQ_DEVICE uint32_t quant_byte_finite(float v) {
-  return __float_as_uint(fminf(v, 127.0f) + 12582912.0f);
+// bf16(s) is within 2^-8 of amax / 127), so the integer n = rne(bf16(v * r)) lies in
+// [-128, 128] and only the upper clamp can act. n comes from one fp32 addition of 1.5 * 2^23 (an
+// exact sum rounded half to even): the sum's bits are 0x4B400000 + n, so their low 16 bits are n
+// as int16. Two such halves share a word, one v_pk_min_i16 clamps both to 127, and the low
+// bytes are the two's complement int8 values.
+typedef short mxq_s2 __attribute__((ext_vector_type(2)));
+
+MXQ_DEVICE uint32_t quant_pair_finite(uint32_t p) {
+  constexpr float kRound = 12582912.0f;
+  const uint32_t lo = __float_as_uint(bf16_lo(p) + kRound), hi = __float_as_uint(bf16_hi(p) + kRound);
+  const mxq_s2 n = __builtin_bit_cast(mxq_s2, __builtin_amdgcn_perm(hi, lo, 0x05040100u));
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(n, mxq_s2{127, 127}));
 }
 
 MXQ_DEVICE v2u quant8_bf16_finite(v4u w, float r) {
-  uint32_t b[8];
+  uint32_t n[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t p = pack_bf16x2(bf16_lo(w[i]) * r, bf16_hi(w[i]) * r);
-    b[2 * i] = quant_byte_finite(bf16_lo(p));
-    b[2 * i + 1] = quant_byte_finite(bf16_hi(p));
-  }
+  for (int i = 0; i < 4; ++i) n[i] = quant_pair_finite(pack_bf16x2(bf16_lo(w[i]) * r, bf16_hi(w[i]) * r));
   v2u o;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const uint32_t lo = __builtin_amdgcn_perm(b[4 * h + 1], b[4 * h], 0x0c0c0400u);
-    const uint32_t hi = __builtin_amdgcn_perm(b[4 * h + 3], b[4 * h + 2], 0x0c0c0400u);
-    o[h] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
-  }
+  o[0] = __builtin_amdgcn_perm(n[1], n[0], 0x06040200u);
+  o[1] = __builtin_amdgcn_perm(n[3], n[2], 0x06040200u);
   return o;
 }
 
@@ -211,10 +211,63 @@ MXQ_DEVICE uint32_t gelu_bf16(uint32_t b) { return kGeluFull.v[b & 0xFFFFu]; }
 
 // ---- wave reductions ----------------------------------------------------------------
 
+// Every reduction below needs all 64 lanes active. The exchanges stay inside the VALU (no LDS
+// round trip): v_permlane32_swap / v_permlane16_swap of a register with itself leave the two
+// halves (rows) in the two results, so their sum is v[i] + v[i ^ 32] (v[i ^ 16]) on every lane;
+// the 16-lane steps are DPP operands (row_ror:8 is lane i ^ 8 within a row; lane i ^ 4 is
+// row_ror:4 in banks 0 and 2 and row_ror:12 in banks 1 and 3; quad_perm gives i ^ 2 and i ^ 1).
+constexpr int kDppRowRor4 = 0x124, kDppRowRor8 = 0x128, kDppRowRor12 = 0x12C;
+constexpr int kDppQuadXor2 = 0x4E, kDppQuadXor1 = 0xB1;  // quad_perm [2,3,0,1], [1,0,3,2]
+
+template <int ctrl>
+MXQ_DEVICE uint32_t dpp_lane(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, ctrl, 0xF, 0xF, false);
+}
+MXQ_DEVICE uint32_t lane_xor4(uint32_t v) {
+  const int t = __builtin_amdgcn_update_dpp((int)v, (int)v, kDppRowRor4, 0xF, 0x5, false);
+  return (uint32_t)__builtin_amdgcn_update_dpp(t, (int)v, kDppRowRor12, 0xF, 0xA, false);
+}
+
+// Sum over the wave with the butterfly pairing i ^ 32, 16, 8, 4, 2, 1 in that order: every lane
+// gets the same bits.
 MXQ_DEVICE float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  v += __uint_as_float(dpp_lane<kDppRowRor8>(__float_as_uint(v)));
+  v += __uint_as_float(lane_xor4(__float_as_uint(v)));
+  v += __uint_as_float(dpp_lane<kDppQuadXor2>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_lane<kDppQuadXor1>(__float_as_uint(v)));
   return v;
+}
+
+// v + v[i ^ 16] + v[i ^ 32] + v[i ^ 48] on every lane (the four 16-lane rows of the wave).
+MXQ_DEVICE float sum_lane_rows(float v) {
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Unsigned maximum over the wave (order does not matter for a maximum).
+MXQ_DEVICE uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_lane<kDppRowRor8>(v));
+  v = max(v, dpp_lane<kDppRowRor4>(v));
+  v = max(v, dpp_lane<kDppQuadXor2>(v));
+  v = max(v, dpp_lane<kDppQuadXor1>(v));
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = max(r[0], r[1]);
+  }
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max(r[0], r[1]);
 }
 
 // ---- absolute maxima with torch's NaN propagation ----------------------------------------
@@ -239,14 +292,7 @@ MXQ_DEVICE uint32_t absmax_bits_of_bf16x2(uint32_t acc) {
 }
 
 // Maximum of absolute-value bits across the wave, returned as the float.
-MXQ_DEVICE float wave_absmax(uint32_t bits) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint32_t other = (uint32_t)__shfl_xor((int)bits, o, kWave);
-    bits = bits > other ? bits : other;
-  }
-  return __uint_as_float(bits);
-}
+MXQ_DEVICE float wave_absmax(uint32_t bits) { return __uint_as_float(wave_max_u32(bits)); }
 
 // Non-negative floats order like their bit patterns; NaN (0x7FC00000) sorts above +inf.
 MXQ_DEVICE void atomic_max_nonneg(float* addr, float v) {

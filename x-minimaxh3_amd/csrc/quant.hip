@@ -296,7 +296,28 @@ __global__ __launch_bounds__(kGeluRowThreads) void quant_rows_gelu_wide(
 // ---- adaLN ------------------------------------------------------------------------
 // y = bf16(bf16(bf16(n) * bf16(1 + scale)) + shift), n = (x - mean) * rstd in fp32,
 // rstd = 1 / sqrt(var + eps), var the biased variance (CK/backends/eager/adaln.py:11-14 on
-// torch's CPU layer_norm). Statistics are two-pass over the register-resident row.
+// torch's CPU layer_norm). Statistics are two-pass over the register-resident row: the sum on
+// the matrix cores (adaln_row_sum), the squared deviations as fp32 fmas. Every adaLN kernel
+// forms them with the same operations on the same lane layout (chunk c of 8 values in lane
+// c % 64, register c / 64), so a row's result does not depend on which kernel ran it.
+
+// Sum of a row held as chunks v[j] = row chunk lane + 64 j (chunks at or past nchunk are
+// zeroed here). Each chunk is a lane's A operand of a 16x16x32 bf16 product with a ones matrix,
+// so every output column accumulates the sum of all the wave's values (a zero chunk leaves the
+// fp32 accumulator unchanged, so the result does not depend on NCH); lanes l, l ^ 16, l ^ 32 and
+// l ^ 48 hold one column's 16 rows. The matrix cores are otherwise idle in these kernels, and
+// the VALU, which bounds them, is spared the unpack and two additions per pair.
+template <int NCH, bool kAll>
+MXQ_DEVICE float adaln_row_sum(v4u (&v)[NCH], int lane, int nchunk) {
+  const v8bf ones = __builtin_bit_cast(v8bf, v4u{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+  v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    if (!kAll && lane + j * kWave >= nchunk) v[j] = v4u{0u, 0u, 0u, 0u};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, v[j]), ones, acc, 0, 0, 0);
+  }
+  return sum_lane_rows((acc[0] + acc[1]) + (acc[2] + acc[3]));
+}
 
 MXQ_DEVICE uint32_t modulate(float xv, float mean, float rstd, uint32_t sc, uint32_t sh) {
   const float n = round_bf16((xv - mean) * rstd);
@@ -321,17 +342,12 @@ MXQ_DEVICE void adaln_row(const uint16_t* __restrict__ x, const v4u* scv, const 
   const int nchunk = cols / 8;
   const v4u* src = reinterpret_cast<const v4u*>(x + row * cols);
   v4u v[NCH];
-  float sum = 0.0f;
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     const int c = lane + j * kWave;
-    if (c < nchunk) {
-      v[j] = __builtin_nontemporal_load(src + c);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sum += bf16_lo(v[j][i]) + bf16_hi(v[j][i]);
-    }
+    if (c < nchunk) v[j] = __builtin_nontemporal_load(src + c);
   }
-  const float mean = wave_sum(sum) / (float)cols;
+  const float mean = adaln_row_sum<NCH, false>(v, lane, nchunk) / (float)cols;
   float ss = 0.0f;
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
@@ -340,8 +356,8 @@ MXQ_DEVICE void adaln_row(const uint16_t* __restrict__ x, const v4u* scv, const 
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float a = bf16_lo(v[j][i]) - mean, b = bf16_hi(v[j][i]) - mean;
-        ss += a * a;
-        ss += b * b;
+        ss = __builtin_fmaf(a, a, ss);
+        ss = __builtin_fmaf(b, b, ss);
       }
     }
   }
@@ -434,8 +450,8 @@ __global__ __launch_bounds__(kQuantBlock) void adaln_rows_reg(
 // second register buffer before it processes the current one, so a row's HBM latency overlaps
 // the previous row's arithmetic. t = bf16(1 + scale) and shift are staged once per workgroup in
 // LDS as fp32 (cols * 8 bytes of dynamic LDS). The statistics and the modulation are the same
-// operations, in the same order, as adaln_row's; rows whose absmax is finite are quantized by
-// the finite-row path.
+// operations, in the same order, as adaln_row's (the chunks past the row end are zeroed before
+// the sum); rows whose absmax is finite are quantized by the finite-row path.
 // Both bf16 halves of w as fp32, as an inline-asm pair: the compiler cannot reuse an earlier
 // unpack of the same word, which would keep a row's unpacked values live (twice the registers of
 // the packed row) from one pass to the next.
@@ -470,14 +486,7 @@ __global__ __launch_bounds__(kQuantBlock) __attribute__((amdgpu_waves_per_eu(kEx
     for (int j = 0; j < NCH; ++j) v[j] = __builtin_nontemporal_load(src + min(lane + j * kWave, nchunk - 1));
   };
   auto process = [&](v4u (&v)[NCH], int64_t r) {
-    float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const bool ok = kExact || lane + j * kWave < nchunk;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sum += ok ? bf16_lo(v[j][i]) + bf16_hi(v[j][i]) : 0.0f;
-    }
-    const float mean = wave_sum(sum) / (float)cols;
+    const float mean = adaln_row_sum<NCH, kExact>(v, lane, nchunk) / (float)cols;
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
@@ -487,8 +496,8 @@ __global__ __launch_bounds__(kQuantBlock) __attribute__((amdgpu_waves_per_eu(kEx
         float xl, xh;
         unpack_fresh(v[j][i], xl, xh);
         const float a = ok ? xl - mean : 0.0f, b = ok ? xh - mean : 0.0f;
-        ss += a * a;
-        ss += b * b;
+        ss = __builtin_fmaf(a, a, ss);
+        ss = __builtin_fmaf(b, b, ss);
       }
     }
     const float var = wave_sum(ss) / (float)cols;
