@@ -60,12 +60,6 @@ struct CrArgs {
 
 enum { kModNone = 0, kModQuant = 1, kModOnly = 2 };  // kModOnly: store y, no rotation / quantizer
 
-MXQ_DEVICE double wave_sum_f64(double v) {
-#pragma unroll
-  for (int m = 1; m < kWave; m <<= 1) v += __shfl_xor(v, m, kWave);
-  return v;
-}
-
 MXQ_DEVICE uint32_t half_of(const v4u* w, int i) {  // bf16 i of 16 packed in two v4u
   const uint32_t word = w[i >> 3][(i >> 1) & 3];
   return (i & 1) ? (word >> 16) : (word & 0xFFFFu);
@@ -403,15 +397,13 @@ __global__ __launch_bounds__(kUnitMaxWaves * 64) void convrot_units_kernel(CrArg
           ss = __builtin_fma(lo, lo, ss);
           ss = __builtin_fma(hi, hi, ss);
         }
-#pragma unroll
-      for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, kWave);
+      ss = row16_sum_f64(ss);
       if (gl == 0) red_ss[it][grp] = ss;
       __syncthreads();
       // lane i of each group takes partials i and i + 16 of its row, then the 16 lanes combine
       double tot = 0.0;
       for (int i = gl; i < gr; i += 16) tot += red_ss[it][slot * gr + i];
-#pragma unroll
-      for (int m = 1; m < 16; m <<= 1) tot += __shfl_xor(tot, m, kWave);
+      tot = row16_sum_f64(tot);
       const float mean = (float)tot / (float)p.K;
       rinv = 1.0f / sqrtf(mean + p.eps);
       int64_t mr = row_on ? p.mrows[row] : 0;
@@ -484,18 +476,12 @@ __global__ __launch_bounds__(kUnitMaxWaves * 64) void convrot_units_kernel(CrArg
     }
     if constexpr (kMod == kModOnly) continue;
     // ---- row absmax over the group's lanes, then over the row's groups
-    uint32_t bits = absmax_bits_of_bf16x2(amax);
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) {
-      const uint32_t o = (uint32_t)__shfl_xor((int)bits, m, kWave);
-      bits = bits > o ? bits : o;
-    }
+    const uint32_t bits = row16_max_u32(absmax_bits_of_bf16x2(amax));
     if (gl == 0) red_max[it][grp] = bits;
     __syncthreads();
     uint32_t rmax = 0;
     for (int i = gl; i < gr; i += 16) rmax = max(rmax, red_max[it][slot * gr + i]);
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) rmax = max(rmax, (uint32_t)__shfl_xor((int)rmax, m, kWave));
+    rmax = row16_max_u32(rmax);
     const float amaxf = __uint_as_float(rmax);
     const float s = row_scale_from_absmax(amaxf);
     const float r = 1.0f / round_bf16(s);

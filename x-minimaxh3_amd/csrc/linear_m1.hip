@@ -41,12 +41,6 @@ struct GvArgs {
   int K, ws_per_channel;
 };
 
-MXQ_DEVICE int wave_sum_i32(int v) {
-#pragma unroll
-  for (int m = 1; m < kWave; m <<= 1) v += __shfl_xor(v, m, kWave);
-  return v;
-}
-
 // kChunks: 16-byte chunks per lane per row (K <= 1024 kChunks); kCols: columns per wave.
 template <int kOut, int kChunks, int kCols>
 __global__ __launch_bounds__(kGvThreads) void gemv_i8_kernel(GvArgs p) {

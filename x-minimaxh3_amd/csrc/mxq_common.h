@@ -256,6 +256,66 @@ MXQ_DEVICE float sum_lane_rows(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Maximum over each 16-lane row.
+MXQ_DEVICE uint32_t row16_max_u32(uint32_t v) {
+  v = max(v, dpp_lane<kDppRowRor8>(v));
+  v = max(v, dpp_lane<kDppRowRor4>(v));
+  v = max(v, dpp_lane<kDppQuadXor2>(v));
+  return max(v, dpp_lane<kDppQuadXor1>(v));
+}
+
+// float64 operands: both words take the same lane.
+template <int ctrl>
+MXQ_DEVICE double dpp_lane_f64(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint64_t lo = dpp_lane<ctrl>((uint32_t)b), hi = dpp_lane<ctrl>((uint32_t)(b >> 32));
+  return __builtin_bit_cast(double, lo | (hi << 32));
+}
+MXQ_DEVICE double lane_xor4_f64(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint64_t lo = lane_xor4((uint32_t)b), hi = lane_xor4((uint32_t)(b >> 32));
+  return __builtin_bit_cast(double, lo | (hi << 32));
+}
+
+// Sum over each 16-lane row with the pairing i ^ 1, 2, 4, 8 in that order.
+MXQ_DEVICE double row16_sum_f64(double v) {
+  v += dpp_lane_f64<kDppQuadXor1>(v);
+  v += dpp_lane_f64<kDppQuadXor2>(v);
+  v += lane_xor4_f64(v);
+  return v + dpp_lane_f64<kDppRowRor8>(v);
+}
+
+// Sum over the wave with the pairing i ^ 1, 2, 4, 8, 16, 32 in that order.
+MXQ_DEVICE double wave_sum_f64(double v) {
+  v = row16_sum_f64(v);
+  {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)b, (uint32_t)b, false, false);
+    const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(b >> 32), (uint32_t)(b >> 32), false, false);
+    v = __builtin_bit_cast(double, (uint64_t)lo[0] | ((uint64_t)hi[0] << 32)) +
+        __builtin_bit_cast(double, (uint64_t)lo[1] | ((uint64_t)hi[1] << 32));
+  }
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)b, (uint32_t)b, false, false);
+  const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(b >> 32), (uint32_t)(b >> 32), false, false);
+  return __builtin_bit_cast(double, (uint64_t)lo[0] | ((uint64_t)hi[0] << 32)) +
+         __builtin_bit_cast(double, (uint64_t)lo[1] | ((uint64_t)hi[1] << 32));
+}
+
+// Integer sum over the wave (exact in any order).
+MXQ_DEVICE int wave_sum_i32(int v) {
+  v += (int)dpp_lane<kDppRowRor8>((uint32_t)v);
+  v += (int)dpp_lane<kDppRowRor4>((uint32_t)v);
+  v += (int)dpp_lane<kDppQuadXor2>((uint32_t)v);
+  v += (int)dpp_lane<kDppQuadXor1>((uint32_t)v);
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+    v = (int)(r[0] + r[1]);
+  }
+  const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+  return (int)(r[0] + r[1]);
+}
+
 // Unsigned maximum over the wave (order does not matter for a maximum).
 MXQ_DEVICE uint32_t wave_max_u32(uint32_t v) {
   v = max(v, dpp_lane<kDppRowRor8>(v));

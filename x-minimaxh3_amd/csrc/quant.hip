@@ -237,12 +237,7 @@ __global__ __launch_bounds__(kGeluRowThreads) void quant_rows_gelu_wide(
         m = ok ? absmax_acc_bf16x2(m, g) : m;
       }
     }
-    uint32_t bits = absmax_bits_of_bf16x2(m);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const uint32_t other = (uint32_t)__shfl_xor((int)bits, o, kWave);
-      bits = bits > other ? bits : other;
-    }
+    uint32_t bits = wave_max_u32(absmax_bits_of_bf16x2(m));
     if (lane == 0) red[parity][wave] = bits;
     __syncthreads();
 #pragma unroll
