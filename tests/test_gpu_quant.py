@@ -230,7 +230,10 @@ def _adaln_inputs(m, d, seed):
     return x, sc, sh
 
 
-@pytest.mark.parametrize("m,d", [(64, 5120), (33, 1024), (7, 8192)])
+# Widths off a multiple of 512 take the masked forms: chunks past the row end are zeroed before
+# the row sum (1000, 3000: the uniform kernel; 6200: the general kernel; 72: one partial chunk
+# per lane). Row counts keep one differing element under ADALN_MISMATCH_BOUND.
+@pytest.mark.parametrize("m,d", [(64, 5120), (33, 1024), (7, 8192), (64, 1000), (24, 3000), (12, 6200), (800, 72)])
 def test_adaln_matches_oracle(dev, m, d):
     """Modulated bf16 within 2 ulp(n·t) + ulp(y) of the oracle.
 
@@ -261,10 +264,10 @@ def test_adaln_matches_oracle(dev, m, d):
 
 # The kernel takes 16-row runs: with groups of 4 every run spans several groups (modulation read
 # per row); with groups of 10 some runs lie in one group (modulation staged once in LDS).
-@pytest.mark.parametrize("m,rows_per_group", [(16, 4), (40, 10)])
-def test_adaln_modulation_groups(dev, m, rows_per_group):
+@pytest.mark.parametrize("m,rows_per_group,d", [(16, 4, 512), (40, 10, 512), (40, 10, 1000)])
+def test_adaln_modulation_groups(dev, m, rows_per_group, d):
     """scale/shift with one row per group of consecutive x rows, against per-group calls."""
-    d, groups = 512, m // rows_per_group
+    groups = m // rows_per_group
     x = activations(m, d, 77)
     sc = (torch.randn(groups, d, generator=gen(1)) * 0.1).to(torch.bfloat16)
     sh = (torch.randn(groups, d, generator=gen(2)) * 0.1).to(torch.bfloat16)
