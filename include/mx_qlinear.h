@@ -425,6 +425,15 @@ int mxq_w4a8_quantize_weight(const void* w, int w_dtype, int64_t N, int64_t K, i
 int mxq_probe_mfma_i8(const int8_t* a, int64_t a_bytes, const int8_t* b, int64_t b_bytes, int32_t* sink,
                       uint64_t* clocks, int64_t workgroups, int64_t iters, void* stream);
 
+/*
+ * Test helper (no counterpart in the reference; it pins the lane pairings the row reductions of
+ * the quantizers rely on): one wave64 writes xor4[i] = the value lane_xor4 hands lane i when
+ * every lane offers its own index (i ^ 4 by construction), row16[i] = the 16-lane float64 sum of
+ * in[] with the pairing i ^ 1, 2, 4, 8 in that order, and wsum[i] = the float32 wave sum of
+ * (float)in[] with the pairing i ^ 32, 16, 8, 4, 2, 1. in: 64 doubles; outputs 64 each.
+ */
+int mxq_probe_lane_exchange(const double* in, uint32_t* xor4, double* row16, float* wsum, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,6 +19,15 @@ tile: 75600 = 295 x 256 + 80) and 64 drawn at random.
       bit-exact against the oracle's GEMM + epilogue on that q;
     - end to end against the oracle's whole chain (its own adaLN): bit-exact on every sampled row
       whose modulated row equals torch's, and the rate of int8 values that differ bounded.
+* The group-128 W4A8 GEMMs at their full sizes (format B: int4 codes packed two per byte, fp16
+  group scales [K/128, N], y = bf16(xs * sum_g fp32(s_g) * P_g)); the launches the reference's
+  w4a8_gemm.cu:133-164 would make for these shapes:
+    - 8192 x 5120 x 5120 on weights re-laid at load (prepare_w4a8_grouped): the 128-row tile
+      form, its K loop running 40 groups (13 turns of its 3-stage ring and one extra stage);
+    - 512 x 10240 x 5120 from bf16 activations (the per-token quantizer in front): the 64-row
+      tile form at its full width, on the prepared and on the checkpoint layout.
+  Sampled rows bit-exact against the oracle's restatement of the summation order, and within
+  1 ulp + the float32 accumulation bound of the float64 value.
 """
 
 import numpy as np
@@ -70,9 +79,9 @@ def _bias(n, dev, i):
     return (torch.randn(n, generator=_gen(dev, i), device=dev) * 0.01).to(torch.bfloat16)
 
 
-def _sample_rows(m):
-    rnd = np.random.default_rng(SEED).choice(np.arange(16, m - 80), size=64, replace=False)
-    return np.unique(np.concatenate([np.arange(16), np.arange(m - 80, m), rnd]))
+def _sample_rows(m, last=80, n_random=64):
+    rnd = np.random.default_rng(SEED).choice(np.arange(16, m - last), size=n_random, replace=False)
+    return np.unique(np.concatenate([np.arange(16), np.arange(m - last, m), rnd]))
 
 
 def _rows(t, rows):
@@ -134,3 +143,53 @@ def test_c2_adaln_qkv_chain_full_size(dev):
           f"int8 {int8_rate:.2e}; rows with any bf16 difference {rows_off}", flush=True)
     assert bf16_rate <= ADALN_BF16_MISMATCH_BOUND
     assert int8_rate <= ADALN_INT8_MISMATCH_BOUND
+
+
+def _w4a8_check(y_rows, a_rows, xs_rows, qd, gs, k):
+    """Sampled output rows against the oracle: bit-exact, and within 1 ulp + the float32
+    accumulation bound of the float64 value."""
+    ref = eager_np.w4a8_grouped_linear(a_rows, xs_rows, qd, gs, 128)
+    assert np.array_equal(bits(y_rows), bf16_bits(ref))
+    exact, mag = eager_np.w4a8_grouped_linear_f64(a_rows, xs_rows, qd, gs, 128)
+    yv = y_rows.float().numpy().astype(np.float64)
+    bound = bf16_ulp(np.abs(exact).astype(np.float32)).astype(np.float64) + (k // 128 + 2) * 2.0 ** -24 * mag
+    assert np.all(np.abs(yv - exact) <= bound)
+
+
+def _w4a8_weights(n, k, dev, i):
+    qd = torch.randint(-128, 128, (n, k // 2), generator=_gen(dev, i), device=dev, dtype=torch.int8)
+    gs = (torch.randn(k // 128, n, generator=_gen(dev, i + 1), device=dev).abs() * 0.01).to(torch.float16)
+    return qd, gs
+
+
+def test_c3_w4a8_group128_full_size(dev):
+    m, n, k = 8192, 5120, 5120
+    mx = _mx()
+    tiles128 = (m // 128) * (n // 128)
+    print(f"C3 W4A8 group-128 m={m} n={n} k={k} prepared ({tiles128} tiles of 128 rows)", flush=True)
+    assert tiles128 >= 512  # the launcher's threshold for the 128-row tile form
+    x = torch.randn(m, k, generator=_gen(dev, 30), device=dev).to(torch.bfloat16)
+    a, xs = mx.quantize_int8_rowwise(x)
+    qd, gs = _w4a8_weights(n, k, dev, 31)
+    y = mx.w4a8_grouped_linear(a, mx.prepare_w4a8_grouped(qd), gs, 128, x_scale=xs.reshape(-1))
+    rows = _sample_rows(m, last=128)
+    yr, ar, xsr = _rows(y, rows), _rows(a, rows).numpy(), _rows(xs.reshape(-1), rows).numpy()
+    del y
+    # the int8 activations themselves are the pinned quantizer's
+    q_own, s_own = eager_np.quantize_int8_rowwise(bits(_rows(x, rows)))
+    assert np.array_equal(ar, q_own) and np.array_equal(xsr.view(np.uint32), s_own.reshape(-1).view(np.uint32))
+    _w4a8_check(yr, ar, xsr, qd.cpu().numpy(), gs.cpu().numpy(), k)
+
+
+@pytest.mark.parametrize("prepared", [True, False])
+def test_c4_w4a8_skinny_full_width(dev, prepared):
+    m, n, k = 512, 10240, 5120
+    mx = _mx()
+    print(f"C4 W4A8 skinny m={m} n={n} k={k} prepared={prepared}", flush=True)
+    x = torch.randn(m, k, generator=_gen(dev, 40), device=dev).to(torch.bfloat16)
+    qd, gs = _w4a8_weights(n, k, dev, 41)
+    y = mx.w4a8_grouped_linear(x, mx.prepare_w4a8_grouped(qd) if prepared else qd, gs, 128)
+    rows = _sample_rows(m, last=64, n_random=32)
+    yr = _rows(y, rows)
+    a, xs = eager_np.quantize_int8_rowwise(bits(_rows(x, rows)))
+    _w4a8_check(yr, a, xs.reshape(-1), qd.cpu().numpy(), gs.cpu().numpy(), k)

@@ -139,6 +139,43 @@ def test_int8_linear_k_not_multiple_of_16(dev):
     assert np.array_equal(bits(y), bf16_bits(ref))
 
 
+def test_padded_weight_form_follows_updates(dev):
+    """A weight whose K needs padding has its GEMM form cached on the tensor: an in-place update
+    through the tensor, a prepare_int8_weight call after a write through .data, and a
+    load_state_dict into a module all make later calls use the new contents; mm_int8's generic
+    right operand is never cached."""
+    from mx_qlinear.modules import ComfyQuantSpec, ConvRotInt8Linear
+
+    x = activations(40, 100, 14)
+    w0, ws = int8_weight(48, 100, 15)
+    w1, _ = int8_weight(48, 100, 16)
+    wd = w0.to(dev)
+    xd, wsd = x.to(dev), ws.to(dev)
+
+    def want(w):
+        return bf16_bits(eager_np.int8_linear(bits(x), w.numpy(), ws.numpy(), None, "bf16"))
+
+    assert np.array_equal(bits(_mx().int8_linear(xd, wd, wsd)), want(w0))
+    wd.copy_(w1.to(dev))  # through the tensor: its version moves
+    assert np.array_equal(bits(_mx().int8_linear(xd, wd, wsd)), want(w1))
+    wd.data.copy_(w0.to(dev))  # through .data: the caller re-prepares
+    _mx().prepare_int8_weight(wd)
+    assert np.array_equal(bits(_mx().int8_linear(xd, wd, wsd)), want(w0))
+    spec = ComfyQuantSpec(format="int8_tensorwise", convrot=False)
+    layer = ConvRotInt8Linear(w1.to(dev), ws.reshape(-1, 1).to(dev), spec=spec)
+    assert np.array_equal(bits(layer(xd)), want(w1))
+    layer.load_state_dict({"qweight": w0.to(dev), "scale": ws.reshape(-1, 1).to(dev)})
+    assert np.array_equal(bits(layer(xd)), want(w0))
+    a = _i8((33, 100), 17)
+    b = _i8((100, 24), 18)
+    bd = b.to(dev)
+    assert np.array_equal(_mx().mm_int8(a.to(dev), bd).cpu().numpy(), eager_np.int8_matmul(a.numpy(), b.numpy().T))
+    assert not hasattr(bd, "_mxq_gemm_weight")
+    bd.copy_(_i8((100, 24), 19).to(dev))
+    assert np.array_equal(_mx().mm_int8(a.to(dev), bd).cpu().numpy(),
+                          eager_np.int8_matmul(a.numpy(), bd.cpu().numpy().T))
+
+
 def test_int8_linear_gelu_input_act(dev):
     x = (torch.randn(96, 512, generator=gen(21)) * 2).to(torch.bfloat16)
     w, ws = int8_weight(256, 512, 22)

@@ -131,6 +131,32 @@ def test_grouped_matches_oracle(dev, m, n, k, g):
     assert np.all(np.abs(yv - exact) <= bound)
 
 
+# The 128-row tile form over K loops that wrap its 3-stage ring several times, with a group count
+# that is not a multiple of 3 (10 and 40 groups: the unrolled-by-three stage loop plus one leftover
+# stage), on both edges partial (2056 x 4104: 17 x 33 = 561 tiles, above the 512 that select the
+# form), on the checkpoint and the prepared layout. Sampled rows (first, last, random) against the
+# oracle, which computes per-group partials of every sampled row.
+@pytest.mark.parametrize("k", [1280, 5120])
+@pytest.mark.parametrize("prepared", [False, True])
+def test_grouped_128_row_tiles_deep_k(dev, k, prepared):
+    m, n, g = 2056, 4104, 128
+    assert ((m + 127) // 128) * ((n + 127) // 128) >= 512 and (k // g) % 3 != 0
+    print(f"w4a8 grouped 128-row tiles m={m} n={n} k={k} prepared={prepared}", flush=True)
+    x = activations(m, k, 1100 + k, outlier_frac=0.0)
+    qd = packed_int4(n, k, 1101 + k)
+    gs = group_scales(k, n, g, 1102 + k)
+    bias = bf16_vec(n, 1103, 0.01)
+    qdd = qd.to(dev)
+    y = _mx().w4a8_grouped_linear(x.to(dev), _mx().prepare_w4a8_grouped(qdd) if prepared else qdd, gs.to(dev), g,
+                                  bias=bias.to(dev))
+    rnd = np.random.default_rng(k).choice(np.arange(8, m - 8), size=48, replace=False)
+    rows = np.unique(np.concatenate([np.arange(8), np.arange(m - 8, m), rnd]))
+    a, xs = eager_np.quantize_int8_rowwise(bits(x[torch.from_numpy(rows)]))
+    ref = eager_np.w4a8_grouped_linear(a, xs, qd.numpy(), gs.numpy(), g, bits(bias))
+    got = y[torch.from_numpy(rows).to(dev)]
+    assert np.array_equal(bits(got), bf16_bits(ref))
+
+
 @pytest.mark.parametrize("m,n", [(64, 256), (130, 200)])
 def test_grouped_with_bias(dev, m, n):
     k, g = 512, 128

@@ -1,8 +1,10 @@
-// Error reporting shared by every C-ABI entry point of libmx_qlinear.so.
+// Error reporting and host-side launch helpers shared by every C-ABI entry point of libmx_qlinear.so.
 #include <stdarg.h>
 #include <stdio.h>
 
 #include "mxq_common.h"
+
+#include <mutex>
 
 static thread_local char g_last_error[512] = "";
 
@@ -31,6 +33,31 @@ int mxq_cu_count() {
     cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
   }
   return cached[dev];
+}
+
+int mxq_blocks_per_cu(const void* kernel, int block, size_t lds) {
+  struct Entry {
+    const void* kernel;
+    int dev, block;
+    size_t lds;
+    int per_cu;
+  };
+  static std::mutex mu;
+  static Entry cache[64];
+  static int used = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < used; ++i)
+      if (cache[i].kernel == kernel && cache[i].dev == dev && cache[i].block == block && cache[i].lds == lds)
+        return cache[i].per_cu;
+  }
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, lds) != hipSuccess || per_cu < 1) per_cu = 1;
+  std::lock_guard<std::mutex> lock(mu);
+  if (used < 64) cache[used++] = Entry{kernel, dev, block, lds, per_cu};
+  return per_cu;
 }
 
 extern "C" const char* mxq_last_error(void) { return g_last_error; }

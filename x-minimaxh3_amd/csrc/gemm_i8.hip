@@ -445,8 +445,9 @@ MXQ_DEVICE void gated_lines(const GemmArgs& p, char* buf, int64_t row0, int64_t 
 // a few extra workgroups per XCD claim positions at run time: first from their own XCD's pool,
 // then from the other pools in turn. A fast XCD thus takes over the end of a slow one's range;
 // workgroups that find every pool empty exit. Claims are relaxed agent-scope atomics on the
-// pool counters (no data passes between workgroups, so no ordering is needed); the last
-// claiming workgroup of a launch resets the counters for the next one. Thread 0 claims, the
+// pool counters (no data passes between workgroups); each claiming workgroup then counts itself
+// with an acquire-release increment, and the one that makes the count complete resets the
+// counters for the next launch, after every claim of this one. Thread 0 claims, the
 // workgroup reads the result through lds[0] before the ring is used. Returns the position, or
 // -1 if the workgroup has nothing to do.
 MXQ_DEVICE int pick_tile(const GemmArgs& p, int num, char* lds) {
@@ -468,7 +469,10 @@ MXQ_DEVICE int pick_tile(const GemmArgs& p, int num, char* lds) {
         got = ys + yc - p.pool + (int)i;
       }
     }
-    const unsigned done = __hip_atomic_fetch_add(p.counters + 8 * 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Release: this workgroup's claims above are ordered before its count; acquire: the last
+    // claimer sees every claim of the launch (the counts form one release sequence) before it
+    // resets the pools, so no claim can land on a counter after its reset.
+    const unsigned done = __hip_atomic_fetch_add(p.counters + 8 * 32, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     if (done == (unsigned)p.n_claim - 1) {  // every claim of this launch has been made
       for (int y = 0; y < 8; ++y) __hip_atomic_exchange(p.counters + y * 32, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_exchange(p.counters + 8 * 32, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

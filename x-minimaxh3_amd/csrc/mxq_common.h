@@ -214,8 +214,10 @@ MXQ_DEVICE uint32_t gelu_bf16(uint32_t b) { return kGeluFull.v[b & 0xFFFFu]; }
 // Every reduction below needs all 64 lanes active. The exchanges stay inside the VALU (no LDS
 // round trip): v_permlane32_swap / v_permlane16_swap of a register with itself leave the two
 // halves (rows) in the two results, so their sum is v[i] + v[i ^ 32] (v[i ^ 16]) on every lane;
-// the 16-lane steps are DPP operands (row_ror:8 is lane i ^ 8 within a row; lane i ^ 4 is
-// row_ror:4 in banks 0 and 2 and row_ror:12 in banks 1 and 3; quad_perm gives i ^ 2 and i ^ 1).
+// the 16-lane steps are DPP operands. row_ror:N makes lane i of a row read lane (i - N) mod 16
+// (data rotates towards higher lanes), so row_ror:8 is lane i ^ 8; lane i ^ 4 is lane i + 4 =
+// row_ror:12 in banks 0 and 2 (lanes 0-3, 8-11) and lane i - 4 = row_ror:4 in banks 1 and 3;
+// quad_perm gives i ^ 2 and i ^ 1.
 constexpr int kDppRowRor4 = 0x124, kDppRowRor8 = 0x128, kDppRowRor12 = 0x12C;
 constexpr int kDppQuadXor2 = 0x4E, kDppQuadXor1 = 0xB1;  // quad_perm [2,3,0,1], [1,0,3,2]
 
@@ -224,8 +226,8 @@ MXQ_DEVICE uint32_t dpp_lane(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, ctrl, 0xF, 0xF, false);
 }
 MXQ_DEVICE uint32_t lane_xor4(uint32_t v) {
-  const int t = __builtin_amdgcn_update_dpp((int)v, (int)v, kDppRowRor4, 0xF, 0x5, false);
-  return (uint32_t)__builtin_amdgcn_update_dpp(t, (int)v, kDppRowRor12, 0xF, 0xA, false);
+  const int t = __builtin_amdgcn_update_dpp((int)v, (int)v, kDppRowRor12, 0xF, 0x5, false);
+  return (uint32_t)__builtin_amdgcn_update_dpp(t, (int)v, kDppRowRor4, 0xF, 0xA, false);
 }
 
 // Sum over the wave with the butterfly pairing i ^ 32, 16, 8, 4, 2, 1 in that order: every lane
@@ -427,13 +429,15 @@ int mxq_set_error(int code, const char* fmt, ...);
 int mxq_check_launch(const char* what);
 int mxq_cu_count();  // compute units of the current device
 
+// Workgroups of one kernel resident per CU, from the occupancy query, cached per (kernel,
+// device, block, dynamic LDS): the query costs host time on every launch otherwise.
+int mxq_blocks_per_cu(const void* kernel, int block, size_t lds);
+
 // Workgroups of `kernel` that are resident at once on the current device (for grid-stride
 // kernels whose workgroups each take an equal share of the rows: a grid larger than this leaves
 // its last workgroups to start when the first have finished), capped at `want`.
 template <class K>
 inline unsigned mxq_resident_grid(K kernel, int block, size_t lds, int64_t want) {
-  int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, lds) != hipSuccess || per_cu < 1) per_cu = 1;
-  const int64_t cap = (int64_t)per_cu * mxq_cu_count();
+  const int64_t cap = (int64_t)mxq_blocks_per_cu(reinterpret_cast<const void*>(kernel), block, lds) * mxq_cu_count();
   return (unsigned)(want < cap ? want : cap);
 }

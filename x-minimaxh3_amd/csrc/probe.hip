@@ -44,9 +44,25 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(const int8_t* __restric
   }
 }
 
+// One wave64: the lane pairings of the DPP wave reductions. xor4[i] = lane_xor4(i); row16[i] =
+// row16_sum_f64 of in[]; wsum[i] = wave_sum of float(in[]).
+__global__ __launch_bounds__(64) void lane_exchange_kernel(const double* __restrict__ in, uint32_t* __restrict__ xor4,
+                                                           double* __restrict__ row16, float* __restrict__ wsum) {
+  const int i = threadIdx.x;
+  xor4[i] = lane_xor4((uint32_t)i);
+  row16[i] = row16_sum_f64(in[i]);
+  wsum[i] = wave_sum((float)in[i]);
+}
+
 }  // namespace mxq
 
 using namespace mxq;
+
+extern "C" int mxq_probe_lane_exchange(const double* in, uint32_t* xor4, double* row16, float* wsum, void* stream) {
+  if (!in || !xor4 || !row16 || !wsum) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  lane_exchange_kernel<<<1, 64, 0, (hipStream_t)stream>>>(in, xor4, row16, wsum);
+  return mxq_check_launch("lane_exchange_kernel");
+}
 
 extern "C" int mxq_probe_mfma_i8(const int8_t* a, int64_t a_bytes, const int8_t* b, int64_t b_bytes,
                                  int32_t* sink, uint64_t* clocks, int64_t workgroups, int64_t iters,

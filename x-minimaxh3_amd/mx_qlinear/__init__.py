@@ -25,6 +25,7 @@ from .ops import (  # noqa: F401
     int8_linear_gated_residual_,
     int8_linear_prequantized,
     mm_int8,
+    prepare_int8_weight,
     prepare_swiglu_fc1,
     quantize_int8_convrot_weight,
     quantize_int8_rowwise,

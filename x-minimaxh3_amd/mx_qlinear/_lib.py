@@ -60,6 +60,7 @@ SIGNATURES: dict[str, list] = {
     "mxq_w4a8_gemm_grouped_prepared": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "mxq_w4a8_prepare_grouped": [_P, _P, _I64, _I64, _P],
     "mxq_probe_mfma_i8": [_P, _I64, _P, _I64, _P, _P, _I64, _I64, _P],
+    "mxq_probe_lane_exchange": [_P, _P, _P, _P, _P],
     "mxq_w4a8_quantize_weight": [_P, _I, _I64, _I64, _I64, _I64, _I, _P, _I, _P, _P, _P, _P, _P, _P],
     "mxq_int8_group_sums": [_P, _P, _P, _I64, _I64, _I64, _I, _P],
 }

@@ -164,6 +164,12 @@ class ConvRotInt8Linear(nn.Module):
         return cls(qweight, scale, state.get(f"{prefix}.bias"), spec=spec, kernel=kernel,
                    output_dtype=output_dtype)
 
+    def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
+        super()._load_from_state_dict(state_dict, prefix, *args, **kwargs)
+        # the GEMM form of a weight that needs padding or realignment is rebuilt from the loaded
+        # contents (load_state_dict may also have written through .data, which it cannot see)
+        ops.prepare_int8_weight(self.qweight)
+
     @property
     def in_features(self) -> int:
         return int(self.qweight.shape[1])

@@ -369,21 +369,26 @@ def _gemm_weight(w: torch.Tensor, kp: int, transpose: bool = False) -> torch.Ten
     """The int8 weight as the GEMM reads it: ``[N, kp]`` row-major (``w.t()`` with ``transpose``),
     K zero-padded to ``kp`` (zero terms leave the int32 sums unchanged, as the reference's own K
     padding, CK/backends/eager/quantization.py:770-775) and 16-byte aligned. A weight that already
-    has that form is used as it is; otherwise the copy is made once and kept on the weight tensor
-    (rebuilt only if the weight is modified in place), so repeated calls do not copy it."""
+    has that form is used as it is. Otherwise a weight (``transpose`` False: a layer's ``[N, K]``
+    parameter or buffer) has the copy made once and kept on the tensor, rebuilt when the tensor's
+    version counter moves; an in-place write through ``w.data`` does not move that counter, so a
+    weight updated that way must be passed to :func:`prepare_int8_weight` again (or updated through
+    the tensor itself). ``transpose`` (mm_int8's generic right operand, which can be any
+    activation-like tensor) copies per call and caches nothing."""
     src = w.t() if transpose else w
     if not transpose and src.is_contiguous() and src.shape[1] == kp and src.data_ptr() % 16 == 0:
         return src
-    key = (w._version, w.data_ptr(), tuple(w.shape), tuple(w.stride()), kp, transpose)
-    cached = getattr(w, "_mxq_gemm_weight", None)
+    key = (w._version, w.data_ptr(), tuple(w.shape), tuple(w.stride()), kp)
+    cached = None if transpose else getattr(w, "_mxq_gemm_weight", None)
     if cached is not None and cached[0] == key:
         return cached[1]
     wp = torch.zeros((src.shape[0], kp), dtype=torch.int8, device=w.device)
     wp[:, : src.shape[1]] = src
-    try:
-        w._mxq_gemm_weight = (key, wp)
-    except (AttributeError, RuntimeError):  # tensors that take no attributes: copy per call
-        pass
+    if not transpose:
+        try:
+            w._mxq_gemm_weight = (key, wp)
+        except (AttributeError, RuntimeError):  # tensors that take no attributes: copy per call
+            pass
     return wp
 
 
@@ -406,8 +411,15 @@ def _pad_k(q: torch.Tensor, w: torch.Tensor):
 
 def prepare_int8_weight(qweight: torch.Tensor) -> torch.Tensor:
     """Build, once (at load), the GEMM form of an int8 ``[N, K]`` weight when it differs from the
-    stored tensor (K not a multiple of 16, or a misaligned start), so later calls do not copy it."""
+    stored tensor (K not a multiple of 16, or a misaligned start), so later calls do not copy it.
+    Calling it again rebuilds that form from the tensor's current contents (after an update
+    through ``qweight.data``, which the cache cannot see)."""
     if qweight.dim() == 2 and qweight.dtype == torch.int8 and qweight.is_cuda:
+        if hasattr(qweight, "_mxq_gemm_weight"):
+            try:
+                del qweight._mxq_gemm_weight
+            except (AttributeError, RuntimeError):
+                pass
         _gemm_weight(qweight, (qweight.shape[1] + 15) // 16 * 16)
     return qweight
 
