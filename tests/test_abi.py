@@ -189,7 +189,7 @@ def _tile_walk(t, tiles_m, tiles_n, group_m):
 
 
 @pytest.mark.parametrize("m,n,group_m", [(1024, 3072, 4), (2048, 2048, 4), (1100, 1800, None), (2050, 2056, 2),
-                                         (300, 5000, None), (75600, 5120, 2), (8192, 5120, 2)])
+                                         (300, 5000, None), (75600, 5120, 4), (8192, 5120, 2)])
 def test_tile_order_visits_every_tile_once(lib, m, n, group_m):
     """Deep-ring problems (every tile on its own CU at once) group their tile order so that each
     XCD's range of tiles is nearly square (fewer operand panels per XCD); every order is a

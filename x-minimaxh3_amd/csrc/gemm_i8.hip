@@ -4,16 +4,23 @@
 // (the reference's torch._int_mm(x_8, weight.T) / CUTLASS RowMajor x ColumnMajor,
 // backends/turbo/vendor/comfy_kitchen/backends/cuda/ops/cutlass_gemm_int8.cu:245-283).
 //
-// Main loop: a 256-thread workgroup (4 wave64s, 2 x 2) owns a 256 x 256 output tile; each wave
-// owns 128 x 128 as a 4 x 4 grid of v_mfma_i32_32x32x32_i8 blocks (256 int32 accumulators per
-// lane, held in AGPRs). K advances 128 bytes per stage; a stage's A and B chunks (32 KB each) are
-// fetched with gfx950's direct-to-LDS 16-byte loads into a ring of five 32 KB slots, one to two
-// stages ahead of the MFMAs, the loads interleaved one per MFMA, so global latency hides behind
+// Main loop: one workgroup per CU owns a 256 x 256 output tile. K advances 128 bytes per stage; a
+// stage's A and B chunks (32 KB each) are fetched with gfx950's direct-to-LDS 16-byte loads into
+// a ring of five 32 KB slots, one to two stages ahead of the MFMAs, so global latency hides behind
 // matrix work and no VGPRs stage data. Fragment reads are inline-asm ds_read_b128 with explicit
 // lgkmcnt waits; vmcnt waits and barriers are issued by hand too (s_waitcnt + s_barrier) so that
-// the prefetches stay in flight across the barrier that publishes the next stage. Problems with
-// fewer 256-tiles than CUs run the same code on 128 x 128 tiles: two workgroups per CU, or, when
-// all the 128-tiles fit on the CUs at once, one per CU with a nine-slot ring four stages deep.
+// the prefetches stay in flight across the barrier that publishes the next stage.
+//  * Ping-pong (the plain epilogues): 512 threads, two waves per SIMD, each owning 128 x 64 as a
+//    4 x 2 grid of v_mfma_i32_32x32x32_i8 blocks (128 int32 accumulators per lane). The SIMD's
+//    two waves take turns: one issues a half stage of MFMAs while the other reads its next
+//    fragments and issues operand loads, a barrier between turns (pp_main_loop).
+//  * Four waves (the table epilogues, whose 128 KB table leaves no LDS for eight waves' output
+//    staging): 256 threads, one wave per SIMD owning 128 x 128 as 4 x 4 blocks (256 accumulators
+//    per lane, in AGPRs), each K-step's fragment reads issued behind the previous step's MFMAs and
+//    the operand loads interleaved one per MFMA.
+// Problems with fewer 256-tiles than CUs run the four-wave code on 128 x 128 tiles: two
+// workgroups per CU, or, when all the 128-tiles fit on the CUs at once, one per CU with a
+// nine-slot ring four stages deep.
 //
 // Epilogue: the MFMAs run with the weights as first operand, so each lane's accumulators are
 // one output row in four runs of four consecutive columns. Every output type is converted in
@@ -48,14 +55,18 @@ constexpr int kGemmThreads = 256;                       // 4 waves as 2 x 2
 // one workgroup per CU with a 144 KB ring that holds four stages in flight instead of two, for
 // problems whose 128-tiles all fit on the CUs at once (one workgroup per CU then leaves the
 // main loop waiting on operand latency, not on other workgroups).
-template <int kT, bool kDeep = false>
+template <int kT, bool kDeep = false, bool kPP = false>
 struct TileCfg {
   static_assert(kT == 128 || !kDeep, "the deep ring exists for 128-tiles only");
+  static_assert(kT == 256 || !kPP, "the ping-pong schedule exists for 256-tiles only");
+  static constexpr bool kPingPong = kPP;
+  static constexpr int kWaves = kPP ? 8 : 4;                    // two per SIMD with kPP
+  static constexpr int kThreads = kWaves * 64;
   static constexpr int kBM = kT, kBN = kT;
-  static constexpr int kWaveM = kT / 2, kWaveN = kT / 2;
+  static constexpr int kWaveM = kT / 2, kWaveN = kPP ? kT / 4 : kT / 2;
   static constexpr int kBI = kWaveM / 32, kBJ = kWaveN / 32;
   static constexpr int kSlotBytes = kT * kBK;                  // one operand chunk of a stage
-  static constexpr int kLoads = kSlotBytes / 1024 / 4;          // direct-to-LDS loads per wave per slot
+  static constexpr int kLoads = kSlotBytes / 1024 / kWaves;     // direct-to-LDS loads per wave per slot
   static constexpr int kAhead = kDeep ? 4 : 2;                  // stages requested ahead of the MFMAs
   static constexpr int kSlots = 2 * kAhead + 1;                 // LDS ring of operand chunks
   static constexpr int kLds = kSlots * kSlotBytes;
@@ -67,10 +78,12 @@ struct TileCfg {
 // Tile-rows per group for problems of several rounds: with 2, the ~32 tiles an XCD runs at once are
 // 2 tile-rows x 16 tile-columns, so an activation panel is read from HBM once and then served
 // from that XCD's L2 to the whole row sweep, and the weight panels (the smaller operand) come
-// back from the last-level cache. Measured against 1, 3, 4, 8, 16 and 32 on the FFN and QKV
-// shapes at 720p: 2 was fastest (fc1 -2.8 %, fc2 -3.2 %, QKV -2 % against 8). Problems of one
-// round choose their own (plan_gemm).
-constexpr int kGroupM = 2;
+// back from the last-level cache. For the four-wave kernels, measured against 1, 3, 4, 8, 16 and
+// 32 on the FFN and QKV shapes at 720p, 2 was fastest (fc1 -2.8 %, fc2 -3.2 %, QKV -2 % against
+// 8). The ping-pong kernel (a third more LDS traffic per MFMA, so a lower clock under the board's
+// power limit) does better with the fewer L2 fills of 4-row groups (QKV -1 to -2 %, FFN -0.3 %
+// against 2; 1, 6 and 8 slower). Problems of one round choose their own (plan_gemm).
+constexpr int kGroupM = 2, kGroupMPingPong = 4;
 
 enum { kEpiI32 = 0, kEpiDequant = 1, kEpiGelu = 2, kEpiGatedRes = 3, kEpiSwiGLU = 4 };
 
@@ -190,16 +203,17 @@ MXQ_DEVICE void issue_slot(const Loader<kL>& L, char* slot, int64_t k0, int64_t 
   for (int t = 0; t < kL; ++t) issue_one<kB, true>(L, slot, k0, K, t);
 }
 
-// Fragments of K-step ks (32 K-bytes) of a stage: A rows wm*kWaveM + i*32 + l%32 and B rows
-// wn*kWaveN + j*32 + l%32, chunk ks*2 + l/32. Every row a lane touches has the same swizzle
-// f = ((l % 32) >> 1) & 7, so one base address per operand serves all its blocks.
+// Fragments of K-step ks (32 K-bytes) of a stage: A rows wrow + i*32 + l%32 and B rows
+// wcol + j*32 + l%32 (the wave's first row and column in the tile, multiples of 16), chunk
+// ks*2 + l/32. Every row a lane touches has the same swizzle f = ((l % 32) >> 1) & 7, so one base
+// address per operand serves all its blocks.
 template <class C>
-MXQ_DEVICE void load_frags(uint32_t slot_a, uint32_t slot_b, int wm, int wn, int ks, v4i fa[C::kBI], v4i fb[C::kBJ]) {
+MXQ_DEVICE void load_frags(uint32_t slot_a, uint32_t slot_b, int wrow, int wcol, int ks, v4i fa[C::kBI], v4i fb[C::kBJ]) {
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31;
   const uint32_t x = (uint32_t)(((ks * 2 + (lane >> 5)) ^ swz_f(lr)) << 4);
-  const uint32_t ba = slot_a + (uint32_t)(wm * C::kWaveM + lr) * kBK + x;
-  const uint32_t bb = slot_b + (uint32_t)(wn * C::kWaveN + lr) * kBK + x;
+  const uint32_t ba = slot_a + (uint32_t)(wrow + lr) * kBK + x;
+  const uint32_t bb = slot_b + (uint32_t)(wcol + lr) * kBK + x;
   static_for<C::kBI>([&](auto I) { fa[decltype(I)::value] = lds_read_b128<decltype(I)::value * 32 * kBK>(ba); });
   static_for<C::kBJ>([&](auto J) { fb[decltype(J)::value] = lds_read_b128<decltype(J)::value * 32 * kBK>(bb); });
 }
@@ -485,9 +499,162 @@ MXQ_DEVICE int pick_tile(const GemmArgs& p, int num, char* lds) {
   return pos;
 }
 
-template <int kEpi, int kOut, int kT, bool kDeep>
-__global__ __launch_bounds__(kGemmThreads, (TileCfg<kT, kDeep>::kPerCu)) void gemm_i8_kernel(GemmArgs p) {
-  typedef TileCfg<kT, kDeep> C;
+// ---- ping-pong main loop (kPP: eight waves, two per SIMD) ----
+// Waves w and w + 4 share a SIMD and a 128 x 128 quadrant of the 256 x 256 tile, one 64-column
+// half each (128 accumulators per lane, so two waves fit a SIMD's registers). They alternate: in
+// every phase one group of four waves (one per SIMD) issues the 16 MFMAs of a half stage (two
+// K-steps) from fragments already in registers, while the other group reads its fragments of the
+// next half stage from LDS and issues its share of the direct-to-LDS operand loads; a workgroup
+// barrier ends each phase. A wave's stalls on LDS latency, load issue or the barrier thus fall in
+// the phases where the other wave of its SIMD keeps the matrix pipe busy.
+//
+// Ring: the operand chunks A_0 B_0 A_1 B_1 ... go to slot (chunk index) % 5 as in the four-wave
+// loop. Iteration kt (stage kt in slots sa, sb) has four phases; group g computes in phases
+// 2q + g and reads in the others:
+//   P0  g0: MFMAs of (kt, K-steps 0-1)     g1: reads (kt, 0-1), loads A_kt+2 into B_kt-1's slot
+//   P1  g1: MFMAs of (kt, 0-1)             g0: reads (kt, 2-3), loads A_kt+2
+//   P2  g0: MFMAs of (kt, 2-3)             g1: reads (kt, 2-3)        both then wait for stage kt+1
+//   P3  g1: MFMAs of (kt, 2-3) + loads     g0: reads (kt+1, 0-1), loads B_kt+2 into A_kt's slot
+//       of B_kt+2 into A_kt's slot
+// A_kt+2's slot was last read in P2 of iteration kt-1 and A_kt's in P2 of this one, so every
+// load goes to a slot no wave reads any more; stage kt+1 is complete (each wave waited for its
+// own loads of it, vmcnt) before the barrier that opens P3, its first reader.
+template <class C>
+MXQ_DEVICE void pp_frags(uint32_t slot_a, uint32_t slot_b, int wrow, int wcol, int ks0, v4i (&fa)[2][C::kBI],
+                         v4i (&fb)[2][C::kBJ]) {
+  load_frags<C>(slot_a, slot_b, wrow, wcol, ks0, fa[0], fb[0]);
+  load_frags<C>(slot_a, slot_b, wrow, wcol, ks0 + 1, fa[1], fb[1]);
+}
+
+// The 16 MFMAs of a half stage; with kLoadsB > 0 one direct-to-LDS load (t = 0 .. kLoadsB-1 of a
+// B slot) follows each of the first kLoadsB MFMAs when `on`.
+template <class C, int kLoadsB, bool kCheck>
+MXQ_DEVICE void pp_mma(const v4i (&fa)[2][C::kBI], const v4i (&fb)[2][C::kBJ], v16i (&acc)[C::kBI][C::kBJ],
+                       const Loader<C::kLoads>& L, char* slot, int64_t k0, int64_t K, bool on) {
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int q = 0; q < C::kBI * C::kBJ; ++q) {
+      const int i = q / C::kBJ, j = q % C::kBJ;
+      acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[kk][j], fa[kk][i], acc[i][j], 0, 0, 0);
+      if (kk == 0 && q < kLoadsB && on) issue_one<true, kCheck>(L, slot, k0, K, q);
+    }
+}
+
+template <bool kB, bool kCheck, int kL>
+MXQ_DEVICE void pp_issue(const Loader<kL>& L, char* slot, int64_t k0, int64_t K, bool on) {
+  if (on) {
+#pragma unroll
+    for (int t = 0; t < kL; ++t) issue_one<kB, kCheck>(L, slot, k0, K, t);
+  }
+}
+
+MXQ_DEVICE void pp_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  barrier_no_drain();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// One group's whole main loop (kG = 0: waves 0-3, 1: waves 4-7). The two groups run separate
+// straight-line code with the same barriers, so no accumulator or fragment value depends on a
+// branch (a branch per phase made the compiler copy and spill them).
+template <class C, int kG>
+MXQ_DEVICE void pp_loop(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][C::kBJ], int wrow, int wcol,
+                        const Loader<C::kLoads>& ld) {
+  constexpr int kSlotBytes = C::kSlotBytes, kSlots = C::kSlots, kL = C::kLoads;
+  const int ktiles = (int)((p.K + kBK - 1) / kBK);
+  const uint32_t lds_addr = (uint32_t)(uintptr_t)(lptr_t)lds;
+  auto slot_addr = [&](int sl) { return lds_addr + (uint32_t)(sl * kSlotBytes); };
+
+  // prologue: stages 0 and 1 into slots 0-3; stage 0 complete; group 0 reads (0, 0-1)
+  pp_issue<false, true>(ld, lds, 0, p.K, true);
+  pp_issue<true, true>(ld, lds + kSlotBytes, 0, p.K, true);
+  pp_issue<false, true>(ld, lds + 2 * kSlotBytes, kBK, p.K, ktiles > 1);
+  pp_issue<true, true>(ld, lds + 3 * kSlotBytes, kBK, p.K, ktiles > 1);
+  if (ktiles > 1)
+    wait_vmcnt<2 * kL>();
+  else
+    wait_vmcnt<0>();
+  pp_barrier();
+  v4i fa[2][C::kBI], fb[2][C::kBJ];
+  if constexpr (kG == 0) {
+    pp_frags<C>(slot_addr(0), slot_addr(1), wrow, wcol, 0, fa, fb);
+    wait_lgkm<0>();
+  }
+  pp_barrier();
+
+  int sa = 0;  // slot of A_kt; B_kt is in the next one
+  // kSteady: stage kt+2 exists and lies wholly below K (every load issued, none checked)
+  auto iteration = [&](int kt, auto SteadyC) {
+    constexpr bool kSteady = decltype(SteadyC)::value;
+    const int sb = sa == kSlots - 1 ? 0 : sa + 1;
+    const int na = sb == kSlots - 1 ? 0 : sb + 1;
+    const int nb = na == kSlots - 1 ? 0 : na + 1;
+    const int pa = sa == 0 ? kSlots - 1 : sa - 1;
+    const bool more1 = kSteady || kt + 1 < ktiles, more2 = kSteady || kt + 2 < ktiles;
+    const int64_t k2 = (int64_t)(kt + 2) * kBK;
+    char* slot_pa = lds + pa * kSlotBytes;
+    char* slot_sa = lds + sa * kSlotBytes;
+    if constexpr (kG == 0) {
+      pp_mma<C, 0, false>(fa, fb, acc, ld, nullptr, 0, 0, false);                       // P0
+      pp_barrier();
+      pp_frags<C>(slot_addr(sa), slot_addr(sb), wrow, wcol, 2, fa, fb);                  // P1
+      pp_issue<false, !kSteady>(ld, slot_pa, k2, p.K, more2);
+      wait_lgkm<0>();
+      pp_barrier();
+      pp_mma<C, 0, false>(fa, fb, acc, ld, nullptr, 0, 0, false);                       // P2
+    } else {
+      pp_frags<C>(slot_addr(sa), slot_addr(sb), wrow, wcol, 0, fa, fb);                  // P0
+      pp_issue<false, !kSteady>(ld, slot_pa, k2, p.K, more2);
+      wait_lgkm<0>();
+      pp_barrier();
+      pp_mma<C, 0, false>(fa, fb, acc, ld, nullptr, 0, 0, false);                       // P1
+      pp_barrier();
+      pp_frags<C>(slot_addr(sa), slot_addr(sb), wrow, wcol, 2, fa, fb);                  // P2
+      wait_lgkm<0>();
+    }
+    // stage kt+1 has landed: only A_kt+2 (when it exists) was issued after it
+    if (kSteady || more2)
+      wait_vmcnt<kL>();
+    else
+      wait_vmcnt<0>();
+    pp_barrier();
+    if constexpr (kG == 0) {
+      // P3 (at the last stage these reads fetch slots nobody uses; they keep the code branch-free)
+      pp_frags<C>(slot_addr(na), slot_addr(nb), wrow, wcol, 0, fa, fb);
+      pp_issue<true, !kSteady>(ld, slot_sa, k2, p.K, more2);
+      wait_lgkm<0>();
+    } else {
+      pp_mma<C, kL, !kSteady>(fa, fb, acc, ld, slot_sa, k2, p.K, more2);                 // P3
+    }
+    pp_barrier();
+    (void)more1;
+    sa = na;
+  };
+  const int steady = (int)max<int64_t>(p.K / kBK - 2, 0);
+  int kt = 0;
+  for (; kt < steady; ++kt) iteration(kt, std::true_type{});
+  for (; kt < ktiles; ++kt) iteration(kt, std::false_type{});
+  // every load has completed and no wave reads the ring any more: the epilogue may reuse the LDS
+  wait_all();
+  pp_barrier();
+}
+
+template <class C>
+MXQ_DEVICE void pp_main_loop(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][C::kBJ], int wrow, int wcol,
+                             int64_t m0, int64_t n0) {
+  static_assert(C::kWaves == 8 && C::kSlots == 5 && C::kLoads == 4, "the ping-pong ring");
+  Loader<C::kLoads> ld;
+  make_loader(ld, p, m0, n0);
+  if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8)) == 0)
+    pp_loop<C, 0>(p, lds, acc, wrow, wcol, ld);
+  else
+    pp_loop<C, 1>(p, lds, acc, wrow, wcol, ld);
+}
+
+template <int kEpi, int kOut, int kT, bool kDeep, bool kPP>
+__global__ __launch_bounds__((TileCfg<kT, kDeep, kPP>::kThreads), (TileCfg<kT, kDeep, kPP>::kPerCu)) void gemm_i8_kernel(GemmArgs p) {
+  typedef TileCfg<kT, kDeep, kPP> C;
   constexpr int kBM = C::kBM, kBN = C::kBN, kWaveM = C::kWaveM, kWaveN = C::kWaveN;
   constexpr int kBI = C::kBI, kBJ = C::kBJ, kSlotBytes = C::kSlotBytes, kLoads = C::kLoads;
   constexpr int kSlots = C::kSlots, kAhead = C::kAhead;
@@ -500,7 +667,10 @@ __global__ __launch_bounds__(kGemmThreads, (TileCfg<kT, kDeep>::kPerCu)) void ge
   tile_walk(pos, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
   const int64_t m0 = (int64_t)tm * kBM, n0 = (int64_t)tn * kBN;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int wm = wave >> 1, wn = wave & 1;
+  // The wave's first output row and column in the tile: a 2 x 2 grid of 128 x 128 quadrants;
+  // with kPP the two waves of a SIMD (w and w + 4) take the two 64-column halves of quadrant w.
+  const int wrow = ((wave & 3) >> 1) * kWaveM;
+  const int wcol = kPP ? (wave & 1) * 128 + (wave >> 2) * 64 : (wave & 1) * kWaveN;
 
   v16i acc[kBI][kBJ];
 #pragma unroll
@@ -508,109 +678,113 @@ __global__ __launch_bounds__(kGemmThreads, (TileCfg<kT, kDeep>::kPerCu)) void ge
 #pragma unroll
     for (int j = 0; j < kBJ; ++j) acc[i][j] = v16i{};
 
-  // Pipeline (D = kAhead stages ahead, a ring of S = 2D + 1 slots of one operand chunk each):
-  // the operand chunks arrive in the order A0 B0 A1 B1 A2 ..., chunk i (A_j = 2j, B_j = 2j + 1)
-  // into slot i % S; stage j (128 K-bytes) reads A_j and B_j. Entering iteration kt, A_kt and
-  // B_kt are complete and visible, stages kt+1 .. kt+D-1 are in flight and F0 holds the
-  // fragments of (stage kt, K-step 0). The iteration runs K-steps 0..3, each step's fragments
-  // read behind the previous step's MFMAs. A_kt+D goes into the slot of B_kt-1 (free since the
-  // previous barrier) with its loads spread over the MFMAs of K-steps 0 and 1; before the MFMAs
-  // of K-step 3 the wave waits for stage kt+1, passes the barrier that frees the slots of A_kt
-  // and B_kt, reads (kt+1, 0), and spreads the loads of B_kt+D over those MFMAs (into A_kt's
-  // slot). A chunk is thus requested D-1 to D stages before it is used, and no wave issues a
-  // burst of loads while its matrix pipe sits idle.
-  const int ktiles = (int)((p.K + kBK - 1) / kBK);
-  Loader<kLoads> ld;
-  make_loader(ld, p, m0, n0);
-  const int pre = min(ktiles, kAhead);  // stages requested before the loop
-  for (int s = 0; s < pre; ++s) {
-    issue_slot<false>(ld, lds + 2 * s * kSlotBytes, (int64_t)s * kBK, p.K);
-    issue_slot<true>(ld, lds + (2 * s + 1) * kSlotBytes, (int64_t)s * kBK, p.K);
-  }
-  // wait for stage 0: every load but those of stages 1 .. pre-1 has completed
-  static_for<kAhead>([&](auto P) {
-    constexpr int np = decltype(P)::value + 1;
-    if (pre == np) wait_vmcnt<2 * (np - 1) * kLoads>();
-  });
-  barrier_no_drain();
+  if constexpr (kPP) {
+    pp_main_loop<C>(p, lds, acc, wrow, wcol, m0, n0);
+  } else {
+    // Pipeline (D = kAhead stages ahead, a ring of S = 2D + 1 slots of one operand chunk each):
+    // the operand chunks arrive in the order A0 B0 A1 B1 A2 ..., chunk i (A_j = 2j, B_j = 2j + 1)
+    // into slot i % S; stage j (128 K-bytes) reads A_j and B_j. Entering iteration kt, A_kt and
+    // B_kt are complete and visible, stages kt+1 .. kt+D-1 are in flight and F0 holds the
+    // fragments of (stage kt, K-step 0). The iteration runs K-steps 0..3, each step's fragments
+    // read behind the previous step's MFMAs. A_kt+D goes into the slot of B_kt-1 (free since the
+    // previous barrier) with its loads spread over the MFMAs of K-steps 0 and 1; before the MFMAs
+    // of K-step 3 the wave waits for stage kt+1, passes the barrier that frees the slots of A_kt
+    // and B_kt, reads (kt+1, 0), and spreads the loads of B_kt+D over those MFMAs (into A_kt's
+    // slot). A chunk is thus requested D-1 to D stages before it is used, and no wave issues a
+    // burst of loads while its matrix pipe sits idle.
+    const int ktiles = (int)((p.K + kBK - 1) / kBK);
+    Loader<kLoads> ld;
+    make_loader(ld, p, m0, n0);
+    const int pre = min(ktiles, kAhead);  // stages requested before the loop
+    for (int s = 0; s < pre; ++s) {
+      issue_slot<false>(ld, lds + 2 * s * kSlotBytes, (int64_t)s * kBK, p.K);
+      issue_slot<true>(ld, lds + (2 * s + 1) * kSlotBytes, (int64_t)s * kBK, p.K);
+    }
+    // wait for stage 0: every load but those of stages 1 .. pre-1 has completed
+    static_for<kAhead>([&](auto P) {
+      constexpr int np = decltype(P)::value + 1;
+      if (pre == np) wait_vmcnt<2 * (np - 1) * kLoads>();
+    });
+    barrier_no_drain();
 
-  const uint32_t lds_addr = (uint32_t)(uintptr_t)(lptr_t)lds;
-  v4i f0a[kBI], f0b[kBJ], f1a[kBI], f1b[kBJ];
-  load_frags<C>(lds_addr, lds_addr + kSlotBytes, wm, wn, 0, f0a, f0b);
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-  __builtin_amdgcn_sched_barrier(0);
-  int sa = 0;  // slot of A_kt; B_kt is in (sa + 1) % 5
-  // One iteration. kSteady: stage kt+2 exists and lies wholly below K, so every load of the
-  // iteration is issued and none needs the K-tail check (no per-load compare, select or branch);
-  // the last two or three iterations take the general form.
-  auto iteration = [&](int kt, auto steady) {
-    constexpr bool kSteady = decltype(steady)::value;
-    const int sb = sa == kSlots - 1 ? 0 : sa + 1;
-    const int na = sb == kSlots - 1 ? 0 : sb + 1;  // A_kt+1
-    const int nb = na == kSlots - 1 ? 0 : na + 1;  // B_kt+1
-    const int pa = sa == 0 ? kSlots - 1 : sa - 1;  // A_kt+D (slot of B_kt-1)
-    const uint32_t cur_a = lds_addr + (uint32_t)(sa * kSlotBytes), cur_b = lds_addr + (uint32_t)(sb * kSlotBytes);
-    const bool more2 = kSteady || kt + kAhead < ktiles;  // stage kt+D exists
-    const bool more1 = kSteady || kt + 1 < ktiles;
-    const int64_t k2 = (int64_t)(kt + kAhead) * kBK;
-    load_frags<C>(cur_a, cur_b, wm, wn, 1, f1a, f1b);
-    wait_lgkm<kBI + kBJ>();
+    const uint32_t lds_addr = (uint32_t)(uintptr_t)(lptr_t)lds;
+    v4i f0a[kBI], f0b[kBJ], f1a[kBI], f1b[kBJ];
+    load_frags<C>(lds_addr, lds_addr + kSlotBytes, wrow, wcol, 0, f0a, f0b);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_sched_barrier(0);
-    mma_step_dma<C, false, 0, kLoads / 2, !kSteady>(f0a, f0b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
-    __builtin_amdgcn_sched_barrier(0);
-    load_frags<C>(cur_a, cur_b, wm, wn, 2, f0a, f0b);
-    wait_lgkm<kBI + kBJ>();
-    __builtin_amdgcn_sched_barrier(0);
-    mma_step_dma<C, false, kLoads / 2, kLoads / 2, !kSteady>(f1a, f1b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
-    __builtin_amdgcn_sched_barrier(0);
-    load_frags<C>(cur_a, cur_b, wm, wn, 3, f1a, f1b);
-    wait_lgkm<kBI + kBJ>();
-    __builtin_amdgcn_sched_barrier(0);
-    mma_step<C>(f0a, f0b, acc);
-    __builtin_amdgcn_sched_barrier(0);
-    // Stage kt+1 has landed when only the loads issued after B_kt+1 are outstanding: stages
-    // kt+2 .. kt+D-1 and A_kt+D where they exist (2 (r - 1) chunks when only r < D stages remain).
-    if (more2) {
-      wait_vm_lgkm0<(2 * kAhead - 3) * kLoads>();
-    } else if constexpr (kAhead > 2) {
-      const int r = ktiles - 1 - kt;
-      if (r == 3) {
-        wait_vm_lgkm0<4 * kLoads>();
-      } else if (r == 2) {
-        wait_vm_lgkm0<2 * kLoads>();
+    int sa = 0;  // slot of A_kt; B_kt is in (sa + 1) % 5
+    // One iteration. kSteady: stage kt+2 exists and lies wholly below K, so every load of the
+    // iteration is issued and none needs the K-tail check (no per-load compare, select or branch);
+    // the last two or three iterations take the general form.
+    auto iteration = [&](int kt, auto steady) {
+      constexpr bool kSteady = decltype(steady)::value;
+      const int sb = sa == kSlots - 1 ? 0 : sa + 1;
+      const int na = sb == kSlots - 1 ? 0 : sb + 1;  // A_kt+1
+      const int nb = na == kSlots - 1 ? 0 : na + 1;  // B_kt+1
+      const int pa = sa == 0 ? kSlots - 1 : sa - 1;  // A_kt+D (slot of B_kt-1)
+      const uint32_t cur_a = lds_addr + (uint32_t)(sa * kSlotBytes), cur_b = lds_addr + (uint32_t)(sb * kSlotBytes);
+      const bool more2 = kSteady || kt + kAhead < ktiles;  // stage kt+D exists
+      const bool more1 = kSteady || kt + 1 < ktiles;
+      const int64_t k2 = (int64_t)(kt + kAhead) * kBK;
+      load_frags<C>(cur_a, cur_b, wrow, wcol, 1, f1a, f1b);
+      wait_lgkm<kBI + kBJ>();
+      __builtin_amdgcn_sched_barrier(0);
+      mma_step_dma<C, false, 0, kLoads / 2, !kSteady>(f0a, f0b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
+      __builtin_amdgcn_sched_barrier(0);
+      load_frags<C>(cur_a, cur_b, wrow, wcol, 2, f0a, f0b);
+      wait_lgkm<kBI + kBJ>();
+      __builtin_amdgcn_sched_barrier(0);
+      mma_step_dma<C, false, kLoads / 2, kLoads / 2, !kSteady>(f1a, f1b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
+      __builtin_amdgcn_sched_barrier(0);
+      load_frags<C>(cur_a, cur_b, wrow, wcol, 3, f1a, f1b);
+      wait_lgkm<kBI + kBJ>();
+      __builtin_amdgcn_sched_barrier(0);
+      mma_step<C>(f0a, f0b, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      // Stage kt+1 has landed when only the loads issued after B_kt+1 are outstanding: stages
+      // kt+2 .. kt+D-1 and A_kt+D where they exist (2 (r - 1) chunks when only r < D stages remain).
+      if (more2) {
+        wait_vm_lgkm0<(2 * kAhead - 3) * kLoads>();
+      } else if constexpr (kAhead > 2) {
+        const int r = ktiles - 1 - kt;
+        if (r == 3) {
+          wait_vm_lgkm0<4 * kLoads>();
+        } else if (r == 2) {
+          wait_vm_lgkm0<2 * kLoads>();
+        } else {
+          wait_all();
+        }
       } else {
         wait_all();
       }
-    } else {
-      wait_all();
-    }
+      __builtin_amdgcn_sched_barrier(0);
+      if (more1) {
+        barrier_no_drain();
+        load_frags<C>(lds_addr + (uint32_t)(na * kSlotBytes), lds_addr + (uint32_t)(nb * kSlotBytes), wrow, wcol, 0, f0a, f0b);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      mma_step_dma<C, true, 0, kLoads, !kSteady>(f1a, f1b, acc, ld, lds + sa * kSlotBytes, k2, p.K, more2 && more1);
+      __builtin_amdgcn_sched_barrier(0);
+      sa = na;
+    };
+    // steady < ktiles always (ktiles >= 1): written as do-while, the tail is seen to run at least
+    // once, so no path leaves the steady loop with fragment reads in flight straight into the
+    // epilogue (whose register copies would otherwise race those reads).
+    const int steady = (int)max<int64_t>(p.K / kBK - kAhead, 0);  // iterations whose stage kt+D is full
+    int kt = 0;
+    for (; kt < steady; ++kt) iteration(kt, std::true_type{});
+    do {
+      iteration(kt, std::false_type{});
+    } while (++kt < ktiles);
+    // Every wave is done reading the ring before the epilogue reuses it, and the last (unused)
+    // fragment reads have landed before their registers are reused.
+    wait_all();
     __builtin_amdgcn_sched_barrier(0);
-    if (more1) {
-      barrier_no_drain();
-      load_frags<C>(lds_addr + (uint32_t)(na * kSlotBytes), lds_addr + (uint32_t)(nb * kSlotBytes), wm, wn, 0, f0a, f0b);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    mma_step_dma<C, true, 0, kLoads, !kSteady>(f1a, f1b, acc, ld, lds + sa * kSlotBytes, k2, p.K, more2 && more1);
-    __builtin_amdgcn_sched_barrier(0);
-    sa = na;
-  };
-  // steady < ktiles always (ktiles >= 1): written as do-while, the tail is seen to run at least
-  // once, so no path leaves the steady loop with fragment reads in flight straight into the
-  // epilogue (whose register copies would otherwise race those reads).
-  const int steady = (int)max<int64_t>(p.K / kBK - kAhead, 0);  // iterations whose stage kt+D is full
-  int kt = 0;
-  for (; kt < steady; ++kt) iteration(kt, std::true_type{});
-  do {
-    iteration(kt, std::false_type{});
-  } while (++kt < ktiles);
-  // Every wave is done reading the ring before the epilogue reuses it, and the last (unused)
-  // fragment reads have landed before their registers are reused.
-  wait_all();
-  __builtin_amdgcn_sched_barrier(0);
-  barrier_no_drain();
+    barrier_no_drain();
+  }
 
   // ---- epilogue ----
-  // Lane l holds, for m-block i and n-block j, row wm*kWaveM + i*32 + l%32 and the four column
+  // Lane l holds, for m-block i and n-block j, row wrow + i*32 + l%32 and the four column
   // runs j*32 + q*8 + (l/32)*4 + {0..3}, q = 0..3 (see mma_step). The main loop's last barrier
   // left the LDS free: per-column factors go behind the four stage buffers and, for GELU, the
   // 128 KB bf16 -> bf16 table is fetched into the buffers themselves while the dequant runs.
@@ -629,12 +803,12 @@ __global__ __launch_bounds__(kGemmThreads, (TileCfg<kT, kDeep>::kPerCu)) void ge
     const float wsl = p.ws_per_channel ? p.ws[col] : p.ws[0];
     const float bl = has_b ? OutT<kOut>::load(reinterpret_cast<const typename OutT<kOut>::T*>(p.bias) + col) : -0.0f;
 #pragma unroll
-    for (int i = 0; i < kBI; ++i) xsv[i] = p.xs[min(m0 + wm * kWaveM + i * 32 + lr, p.M - 1)];
+    for (int i = 0; i < kBI; ++i) xsv[i] = p.xs[min(m0 + wrow + i * 32 + lr, p.M - 1)];
     if (kEpi == kEpiGelu || kEpi == kEpiSwiGLU) {
       const char* src = reinterpret_cast<const char*>(kEpi == kEpiGelu ? (const void*)&kGeluFull : (const void*)&kSiluFull) +
                         lane * 16;
 #pragma unroll 4
-      for (int q = wave; q < 128; q += 4)
+      for (int q = wave; q < 128; q += C::kWaves)
         __builtin_amdgcn_global_load_lds((gptr_t)(src + q * 1024), (lptr_t)(lds + q * 1024), 16, 0, 0);
     }
     if (t < kBN) {
@@ -650,7 +824,7 @@ __global__ __launch_bounds__(kGemmThreads, (TileCfg<kT, kDeep>::kPerCu)) void ge
   constexpr bool kTable = kEpi == kEpiGelu || kEpi == kEpiSwiGLU;
   const bool lines = full && p.line_store;
   char* sbuf = lds + (kTable ? C::kEpiLds + 2 * kBN * 4 : 0) + wave * kStageBytes;
-  static_assert((kTable ? C::kEpiLds + 2 * kBN * 4 : 0) + 4 * kStageBytes <= (kTable ? C::kLds : C::kEpiLds),
+  static_assert((kTable ? C::kEpiLds + 2 * kBN * 4 : 0) + C::kWaves * kStageBytes <= (kTable ? C::kLds : C::kEpiLds),
                 "staging buffers overlap the table, the factors or the end of LDS");
   const int64_t pitch = p.ldd * kElem;
   int64_t grow[kBI] = {};     // kEpiGatedRes: the gate row of each of this lane's rows
@@ -662,10 +836,10 @@ __global__ __launch_bounds__(kGemmThreads, (TileCfg<kT, kDeep>::kPerCu)) void ge
     };
 #pragma unroll
     for (int i = 0; i < kBI; ++i) {
-      grow[i] = gate_row(m0 + wm * kWaveM + i * 32 + lr);
+      grow[i] = gate_row(m0 + wrow + i * 32 + lr);
       if (lines)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) grow_rm[i][t] = gate_row(m0 + wm * kWaveM + i * 32 + t * 8 + (lane >> 3));
+        for (int t = 0; t < 4; ++t) grow_rm[i][t] = gate_row(m0 + wrow + i * 32 + t * 8 + (lane >> 3));
     }
   }
 
@@ -678,7 +852,7 @@ __global__ __launch_bounds__(kGemmThreads, (TileCfg<kT, kDeep>::kPerCu)) void ge
     if constexpr (kEpi != kEpiI32) {
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
-        const int cl0 = wn * kWaveN + (2 * jp + jj) * 32 + lh * 4;
+        const int cl0 = wcol + (2 * jp + jj) * 32 + lh * 4;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const v4f w4 = *reinterpret_cast<const v4f*>(s_ws + cl0 + q * 8);
@@ -694,8 +868,8 @@ __global__ __launch_bounds__(kGemmThreads, (TileCfg<kT, kDeep>::kPerCu)) void ge
     static_for<kBI>([&](auto I) {
       constexpr int i = decltype(I)::value;
       constexpr int kWords = kElem == 4 ? 4 : 2;
-      const int64_t row0 = m0 + wm * kWaveM + i * 32;  // the block row's first row
-      const int64_t col0 = n0 + wn * kWaveN + jp * 64;  // the pair's first column
+      const int64_t row0 = m0 + wrow + i * 32;  // the block row's first row
+      const int64_t col0 = n0 + wcol + jp * 64;  // the pair's first column
       uint32_t w[2][8];
       uint32_t w32[2][16];
 #pragma unroll
@@ -754,10 +928,10 @@ __global__ __launch_bounds__(kGemmThreads, (TileCfg<kT, kDeep>::kPerCu)) void ge
       constexpr int kMode = decltype(ModeC)::value;
       static_for<kBI>([&](auto I) {
         constexpr int i = decltype(I)::value;
-        const int64_t row0 = m0 + wm * kWaveM + i * 32;
+        const int64_t row0 = m0 + wrow + i * 32;
         static_for<kBJ / 2>([&](auto JP) {
           constexpr int jp = decltype(JP)::value;
-          const int64_t col0 = n0 + wn * kWaveN + jp * 64;
+          const int64_t col0 = n0 + wcol + jp * 64;
           uint32_t g[2][8];
 #pragma unroll
           for (int jj = 0; jj < 2; ++jj) {
@@ -797,7 +971,7 @@ __global__ __launch_bounds__(kGemmThreads, (TileCfg<kT, kDeep>::kPerCu)) void ge
     for (int i = 0; i < kBI; ++i) {
       uint32_t m = max((uint32_t)rmax[i][0], (uint32_t)rmax[i][1]);
       m = max(m, (uint32_t)__shfl_xor((int)m, 32, kWave));
-      const int64_t row = m0 + wm * kWaveM + i * 32 + lr;
+      const int64_t row = m0 + wrow + i * 32 + lr;
       if (lh == 0 && row < p.M) atomicMax(reinterpret_cast<unsigned int*>(p.row_absmax + row), m << 16);
     }
   }
@@ -813,7 +987,7 @@ __global__ __launch_bounds__(kGemmThreads, (TileCfg<kT, kDeep>::kPerCu)) void ge
     const bool hlines = hfull && p.line_store;
     static_for<kBI>([&](auto I) {
       constexpr int i = decltype(I)::value;
-      const int64_t row = m0 + wm * kWaveM + i * 32 + lr;
+      const int64_t row = m0 + wrow + i * 32 + lr;
       uint32_t hw[kBJ][4];
 #pragma unroll
       for (int j = 0; j < kBJ; ++j)
@@ -831,11 +1005,11 @@ __global__ __launch_bounds__(kGemmThreads, (TileCfg<kT, kDeep>::kPerCu)) void ge
           stage_put8(sbuf, lr, j * 2, lh, hw[j][0], hw[j][1]);
           stage_put8(sbuf, lr, j * 2 + 1, lh, hw[j][2], hw[j][3]);
         }
-        stage_store(p, sbuf, m0 + wm * kWaveM + i * 32, (n0 + wn * kWaveN) / 2 * 2, pitch);
+        stage_store(p, sbuf, m0 + wrow + i * 32, (n0 + wcol) / 2 * 2, pitch);
       } else {
 #pragma unroll
         for (int j = 0; j < kBJ; ++j) {
-          const int64_t hc0 = (n0 + wn * kWaveN + j * 32) / 2 + lh * 4;
+          const int64_t hc0 = (n0 + wcol + j * 32) / 2 + lh * 4;
           if (hfull || row < p.M) {
             store_run<2>(p.d, p.ldd, row, hc0, nh, hfull || (p.vec_store && hc0 + 4 <= nh), hw[j]);
             store_run<2>(p.d, p.ldd, row, hc0 + 8, nh, hfull || (p.vec_store && hc0 + 12 <= nh), hw[j] + 2);
@@ -885,7 +1059,7 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, bool table, int64_t workspace_by
   // of its range once, so the range is made as square as the groups allow (1024 x 3072, 24
   // tiles per XCD: 4 x 6 tiles read 10 panels where 2 x 12 read 14; 17.8 against 18.5 us per
   // launch with operands from HBM). Two workgroups per CU measured no better this way.
-  g.group_m = kGroupM;
+  g.group_m = g.tile == 256 && !table ? kGroupMPingPong : kGroupM;
   const int64_t slots = g.tile == 256 ? 256 : 512;
   if (g.deep) {
     const int64_t per = (tiles + 7) / 8;
@@ -931,13 +1105,16 @@ static int launch_gemm(const GemmArgs& args0, void* workspace, int64_t workspace
   if constexpr (kEpi != kEpiGelu && kEpi != kEpiSwiGLU) {
     if (g.tile == 128) {
       if (g.deep)
-        gemm_i8_kernel<kEpi, kOut, 128, true><<<grid, kGemmThreads, 0, stream>>>(args);
+        gemm_i8_kernel<kEpi, kOut, 128, true, false><<<grid, kGemmThreads, 0, stream>>>(args);
       else
-        gemm_i8_kernel<kEpi, kOut, 128, false><<<grid, kGemmThreads, 0, stream>>>(args);
+        gemm_i8_kernel<kEpi, kOut, 128, false, false><<<grid, kGemmThreads, 0, stream>>>(args);
       return mxq_check_launch("gemm_i8_kernel");
     }
+    // 256-tiles without a table epilogue: the ping-pong schedule (eight waves)
+    gemm_i8_kernel<kEpi, kOut, 256, false, true><<<grid, TileCfg<256, false, true>::kThreads, 0, stream>>>(args);
+    return mxq_check_launch("gemm_i8_kernel");
   }
-  gemm_i8_kernel<kEpi, kOut, 256, false><<<grid, kGemmThreads, 0, stream>>>(args);
+  gemm_i8_kernel<kEpi, kOut, 256, false, false><<<grid, kGemmThreads, 0, stream>>>(args);
   return mxq_check_launch("gemm_i8_kernel");
 }
 
