@@ -26,6 +26,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -775,15 +776,34 @@ class LinearM1Workload:
 
 
 def cpu_model():
-    """The host CPU's model name (first `model name` line of /proc/cpuinfo)."""
+    """The host CPU as `lscpu` names it ("Model name"), with the family / model / stepping numbers
+    from /proc/cpuinfo (a virtualised host may report only a generic name)."""
+    name = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name:"):
+                name = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if ":" not in line:
+                    if fields:
+                        break
+                    continue
+                k, v = (x.strip() for x in line.split(":", 1))
+                if k in ("model name", "cpu family", "model", "stepping") and k not in fields:
+                    fields[k] = v
     except OSError:
         pass
-    return "unknown"
+    name = name or fields.get("model name", "unknown")
+    if "cpu family" in fields:
+        name += f" (family {fields['cpu family']}, model {fields.get('model', '?')}, stepping {fields.get('stepping', '?')})"
+    return name
 
 
 def _cpu_sample(run, budget_s, max_rows, unit, what):

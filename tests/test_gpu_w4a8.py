@@ -157,6 +157,32 @@ def test_grouped_128_row_tiles_deep_k(dev, k, prepared):
     assert np.array_equal(bits(got), bf16_bits(ref))
 
 
+# The 128-row tile form on a larger problem (4100 x 4360: 33 x 35 tiles, both edges partial) over
+# K of 1, 3, 5 and 10 groups (its ring holds three), on both weight layouts, with a bias, and
+# fp16 / fp32 outputs. Sampled rows against the oracle.
+@pytest.mark.parametrize("k,prepared,out_dtype", [(128, True, torch.bfloat16), (384, False, torch.bfloat16),
+                                                  (640, True, torch.float16), (1280, False, torch.float32),
+                                                  (1280, True, torch.bfloat16)])
+def test_grouped_128_row_tiles_outputs(dev, k, prepared, out_dtype):
+    m, n, g = 4100, 4360, 128
+    assert -(-m // 128) * -(-n // 128) >= 512
+    print(f"w4a8 grouped 128-row tiles m={m} n={n} k={k} prepared={prepared} out={out_dtype}", flush=True)
+    x = activations(m, k, 1200 + k, outlier_frac=0.0)
+    qd = packed_int4(n, k, 1201 + k)
+    gs = group_scales(k, n, g, 1202 + k)
+    bias = bf16_vec(n, 1203, 0.01)
+    qdd = qd.to(dev)
+    y = _mx().w4a8_grouped_linear(x.to(dev), _mx().prepare_w4a8_grouped(qdd) if prepared else qdd, gs.to(dev), g,
+                                  bias=bias.to(dev), out_dtype=out_dtype)
+    rnd = np.random.default_rng(k).choice(np.arange(8, m - 8), size=40, replace=False)
+    rows = np.unique(np.concatenate([np.arange(8), np.arange(m - 8, m), rnd]))
+    a, xs = eager_np.quantize_int8_rowwise(bits(x[torch.from_numpy(rows)]))
+    code = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[out_dtype]
+    ref = eager_np.w4a8_grouped_linear(a, xs, qd.numpy(), gs.numpy(), g, bits(bias), code)
+    got = y[torch.from_numpy(rows).to(dev)].float().cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.astype(np.float32).view(np.uint32))
+
+
 @pytest.mark.parametrize("m,n", [(64, 256), (130, 200)])
 def test_grouped_with_bias(dev, m, n):
     k, g = 512, 128
