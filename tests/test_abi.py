@@ -61,7 +61,7 @@ def test_library_exports_every_declared_symbol(lib):
 def test_abi_version_and_error_string(lib):
     from mx_qlinear import _lib
 
-    assert lib.mxq_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.mxq_abi_version() == _lib.ABI_VERSION == 3
     lib.mxq_last_error.restype = ctypes.c_char_p
     assert isinstance(lib.mxq_last_error(), bytes)
     # a rejected call leaves a message naming the problem
@@ -153,12 +153,18 @@ def test_gemm_plan_queues_large_problems(lib, m, n, k, table, tile, queued):
     if queued:
         per = tiles // 8
         assert plan["pool"] == -(-per // 8)
-        assert plan["wg_per_xcd"] == per + (tiles % 8 > 0) + plan["pool"]
+        # 256-tiles without a table epilogue: one looping workgroup per CU (this host has no GPU,
+        # so the library plans for 256 CUs); otherwise one workgroup per tile plus claimers
+        assert plan["persistent"] == (tile == 256 and not table)
+        if plan["persistent"]:
+            assert plan["wg_per_xcd"] == 256 // 8
+        else:
+            assert plan["wg_per_xcd"] == per + (tiles % 8 > 0) + plan["pool"]
         assert plan["grid"] == 8 * plan["wg_per_xcd"]
     else:
-        assert plan["pool"] == 0 and plan["grid"] == tiles
+        assert plan["pool"] == 0 and plan["grid"] == tiles and not plan["persistent"]
     static = _lib.gemm_plan(m, n, k, table, workspace_bytes=0)
-    assert static["pool"] == 0 and static["grid"] == tiles
+    assert static["pool"] == 0 and static["grid"] == tiles and not static["persistent"]
 
 
 @pytest.mark.parametrize(
@@ -240,17 +246,72 @@ def _queue_cover(tiles, pool, wg_per_xcd, order):
     return taken
 
 
+def _persistent_cover(tiles, pool, wg_per_xcd, seed):
+    """Positions the looping ping-pong workgroups take (gemm_i8.hip pp_tiles / pp_claim): workgroup
+    (x = bid % 8, k = bid / 8) walks start_x + k, start_x + k + W, ... below start_x + count_x -
+    pool, then claims pool slots (its own XCD's counter first, then the others in turn, skipping
+    counters it found drained) until all are drained. Workgroups advance one tile at a time in a
+    seeded random interleaving (seed None: round robin)."""
+    import random
+
+    per, rem = tiles // 8, tiles % 8
+
+    def rng(x):
+        return x * per + min(x, rem), per + (1 if x < rem else 0)
+
+    grid = 8 * wg_per_xcd
+    claims = [0] * 8
+    state = {}
+    for bid in range(grid):
+        x, k = bid % 8, bid // 8
+        start, count = rng(x)
+        state[bid] = {"next": start + k, "end": start + count - pool, "j": 0}
+    taken, live = [], list(range(grid))
+    r = random.Random(seed)
+    while live:
+        bid = live[0] if seed is None else r.choice(live)
+        if seed is None:
+            live.append(live.pop(0))
+        st, x = state[bid], bid % 8
+        if st["next"] is not None and st["next"] < st["end"]:
+            taken.append(st["next"])
+            st["next"] += wg_per_xcd
+            continue
+        st["next"] = None
+        got = None
+        while st["j"] < 8:
+            y = (x + st["j"]) % 8
+            i = claims[y]
+            claims[y] += 1
+            if i < pool:
+                ys, yc = rng(y)
+                got = ys + yc - pool + i
+                break
+            st["j"] += 1
+        if got is None:
+            live.remove(bid)
+        else:
+            taken.append(got)
+    return taken
+
+
 @pytest.mark.parametrize("m,n,table", [(75600, 5120, False), (75600, 20480, True), (10496, 8408, False),
-                                       (8060, 4990, False), (75600, 28672, True)])
+                                       (8060, 4990, False), (75600, 28672, True), (75600, 15360, False)])
 def test_tile_queue_plan_covers_every_tile_once(lib, m, n, table):
     """With the launch plan's pool and grid, every tile is taken exactly once whatever order the
-    workgroups arrive in (here: dispatch order, reversed, and seeded shuffles)."""
+    workgroups arrive in (here: dispatch order, reversed, and seeded shuffles; for looping
+    workgroups, round robin and seeded random interleavings of their steps)."""
     import random
 
     from mx_qlinear import _lib
 
     plan = _lib.gemm_plan(m, n, 1024, table)
     assert plan["pool"] > 0 and plan["grid"] == 8 * plan["wg_per_xcd"]
+    if plan["persistent"]:
+        for seed in (None, 0, 1, 2):
+            got = _persistent_cover(plan["tiles"], plan["pool"], plan["wg_per_xcd"], seed)
+            assert sorted(got) == list(range(plan["tiles"]))
+        return
     orders = [list(range(plan["grid"])), list(range(plan["grid"]))[::-1]]
     for seed in range(3):
         o = list(range(plan["grid"]))

@@ -111,6 +111,9 @@ struct GemmArgs {
   int pool, wg_per_xcd, n_claim;
   unsigned* counters;
   int group_m;  // tile-rows per group of the tile order (tile_walk)
+  // Ping-pong kernel only: wg_per_xcd workgroups per XCD loop over the tiles, claiming them from
+  // the counters (pp_tiles); n_claim is then the grid.
+  int persistent;
 };
 
 // LDS operand layout: a tile row is 128 bytes = eight 16-byte chunks; chunk c of row r sits at
@@ -119,6 +122,14 @@ struct GemmArgs {
 // gives them sixteen distinct (r & 1, slot) pairs, i.e. all 64 banks once.
 MXQ_DEVICE int swz_f(int r) { return (r >> 1) & 7; }
 MXQ_DEVICE int swz(int r, int c) { return r * kBK + ((c ^ swz_f(r)) << 4); }
+
+// threadIdx.x read through an empty asm statement: what is computed from it cannot be hoisted
+// out of the ping-pong kernel's tile loop (lane addresses kept live across the main loop spilled).
+MXQ_DEVICE int tid_x() {
+  int t = threadIdx.x;
+  __asm__ volatile("" : "+v"(t));
+  return t;
+}
 
 // Zero source for the K tail of A (B's tail may hold anything: it meets zeros).
 static __device__ __attribute__((aligned(16))) uint8_t kZeroChunk[16];
@@ -167,15 +178,20 @@ struct Loader {
 
 template <int kL>
 MXQ_DEVICE void make_loader(Loader<kL>& L, const GemmArgs& p, int64_t m0, int64_t n0) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int w = tid_x() >> 6, lane = tid_x() & 63;
   L.wave = __builtin_amdgcn_readfirstlane(w);
+  // (the operand bases pass an empty asm statement too, so that their register copies are not
+  // hoisted out of the ping-pong kernel's tile loop either)
+  const int8_t* a = p.a;
+  const int8_t* b = p.b;
+  __asm__ volatile("" : "+s"(a), "+s"(b));
 #pragma unroll
   for (int t = 0; t < kL; ++t) {
     const int r = (w * kL + t) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ swz_f(r);  // depends on t only through t & 1
     if (t < 2) L.koff[t] = c * 16;
-    L.a[t] = p.a + min(m0 + r, p.M - 1) * p.K + c * 16;
-    L.b[t] = p.b + min(n0 + r, p.N - 1) * p.K;
+    L.a[t] = a + min(m0 + r, p.M - 1) * p.K + c * 16;
+    L.b[t] = b + min(n0 + r, p.N - 1) * p.K;
   }
 }
 
@@ -208,8 +224,8 @@ MXQ_DEVICE void issue_slot(const Loader<kL>& L, char* slot, int64_t k0, int64_t 
 // ks*2 + l/32. Every row a lane touches has the same swizzle f = ((l % 32) >> 1) & 7, so one base
 // address per operand serves all its blocks.
 template <class C>
-MXQ_DEVICE void load_frags(uint32_t slot_a, uint32_t slot_b, int wrow, int wcol, int ks, v4i fa[C::kBI], v4i fb[C::kBJ]) {
-  const int lane = threadIdx.x & 63;
+MXQ_DEVICE void load_frags(int lane, uint32_t slot_a, uint32_t slot_b, int wrow, int wcol, int ks, v4i fa[C::kBI],
+                           v4i fb[C::kBJ]) {
   const int lr = lane & 31;
   const uint32_t x = (uint32_t)(((ks * 2 + (lane >> 5)) ^ swz_f(lr)) << 4);
   const uint32_t ba = slot_a + (uint32_t)(wrow + lr) * kBK + x;
@@ -382,26 +398,36 @@ MXQ_DEVICE void wave_lds_sync() {
 }
 
 // The 8 bytes of half h of chunk c of row r.
+// The staging accesses are inline assembly (lds_write_*, lds_read_b128): the ping-pong kernel
+// runs its epilogue while the next tile's first operand loads land in other LDS slots.
 MXQ_DEVICE void stage_put8(char* buf, int r, int c, int h, uint32_t w0, uint32_t w1) {
-  *reinterpret_cast<v2u*>(stage_at(buf, r, c) + h * 8) = v2u{w0, w1};
+  lds_write_b64(lds_addr(stage_at(buf, r, c) + h * 8), v2u{w0, w1});
 }
 
 MXQ_DEVICE void stage_put16(char* buf, int r, int c, const uint32_t* w) {
-  *reinterpret_cast<v4u*>(stage_at(buf, r, c)) = v4u{w[0], w[1], w[2], w[3]};
+  lds_write_b128(lds_addr(stage_at(buf, r, c)), v4u{w[0], w[1], w[2], w[3]});
 }
 
-MXQ_DEVICE v4u stage_get(char* buf, int t) {
-  const int lane = threadIdx.x & 63;
-  return *reinterpret_cast<const v4u*>(stage_at(buf, t * 8 + (lane >> 3), lane & 7));
+// Row-order reads t = 0..3 of the staged piece; the caller waits for them (stage_wait).
+MXQ_DEVICE void stage_get4(char* buf, v4u (&v)[4]) {
+  const int lane = tid_x() & 63;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    v[t] = __builtin_bit_cast(v4u, lds_read_b128<0>(lds_addr(stage_at(buf, t * 8 + (lane >> 3), lane & 7))));
+}
+
+MXQ_DEVICE void stage_wait() {
+  wait_lgkm<0>();
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // Stores the staged piece as bytes [byte0, byte0 + 128) of rows row0 .. row0 + 31 of d.
 MXQ_DEVICE void stage_store(const GemmArgs& p, char* buf, int64_t row0, int64_t byte0, int64_t pitch) {
-  const int lane = threadIdx.x & 63;
+  const int lane = tid_x() & 63;
   wave_lds_sync();
   v4u v[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) v[t] = stage_get(buf, t);
+  stage_get4(buf, v);
+  stage_wait();
   char* base = reinterpret_cast<char*>(p.d) + (row0 + (lane >> 3)) * pitch + byte0 + (lane & 7) * 16;
 #pragma unroll
   for (int t = 0; t < 4; ++t) *reinterpret_cast<v4u*>(base + t * 8 * pitch) = v[t];
@@ -410,7 +436,7 @@ MXQ_DEVICE void stage_store(const GemmArgs& p, char* buf, int64_t row0, int64_t 
 // Two 32 x 32 blocks of 16-bit words (jj = 0, 1: 8 words each, as epi_run gives them), or one
 // block of 32-bit words, as one piece.
 MXQ_DEVICE void stage_blocks16(char* buf, const uint32_t (&w)[2][8]) {
-  const int lane = threadIdx.x & 63;
+  const int lane = tid_x() & 63;
   wave_lds_sync();  // the previous piece has been read
 #pragma unroll
   for (int jj = 0; jj < 2; ++jj)
@@ -419,7 +445,7 @@ MXQ_DEVICE void stage_blocks16(char* buf, const uint32_t (&w)[2][8]) {
 }
 
 MXQ_DEVICE void stage_block32(char* buf, const uint32_t* w) {
-  const int lane = threadIdx.x & 63;
+  const int lane = tid_x() & 63;
   wave_lds_sync();
 #pragma unroll
   for (int q = 0; q < 4; ++q) stage_put16(buf, lane & 31, q * 2 + (lane >> 5), w + q * 4);
@@ -431,7 +457,7 @@ MXQ_DEVICE void stage_block32(char* buf, const uint32_t* w) {
 // staging so that their latency overlaps it.
 MXQ_DEVICE void gated_lines(const GemmArgs& p, char* buf, int64_t row0, int64_t col0, const int64_t (&grow)[4],
                             const uint32_t (&w)[2][8]) {
-  const int lane = threadIdx.x & 63;
+  const int lane = tid_x() & 63;
   uint16_t* res = p.res + (row0 + (lane >> 3)) * p.ldr + col0 + (lane & 7) * 8;
   v4u r[4], g[4];
 #pragma unroll
@@ -441,9 +467,12 @@ MXQ_DEVICE void gated_lines(const GemmArgs& p, char* buf, int64_t row0, int64_t 
   }
   stage_blocks16(buf, w);
   wave_lds_sync();
+  v4u ys[4];
+  stage_get4(buf, ys);
+  stage_wait();
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    const v4u y = stage_get(buf, t);
+    const v4u y = ys[t];
     *reinterpret_cast<v4u*>(res + t * 8 * p.ldr) =
         v4u{gated_pair(r[t][0], y[0], g[t][0]), gated_pair(r[t][1], y[1], g[t][1]),
             gated_pair(r[t][2], y[2], g[t][2]), gated_pair(r[t][3], y[3], g[t][3])};
@@ -520,10 +549,10 @@ MXQ_DEVICE int pick_tile(const GemmArgs& p, int num, char* lds) {
 // load goes to a slot no wave reads any more; stage kt+1 is complete (each wave waited for its
 // own loads of it, vmcnt) before the barrier that opens P3, its first reader.
 template <class C>
-MXQ_DEVICE void pp_frags(uint32_t slot_a, uint32_t slot_b, int wrow, int wcol, int ks0, v4i (&fa)[2][C::kBI],
+MXQ_DEVICE void pp_frags(int lane, uint32_t slot_a, uint32_t slot_b, int wrow, int wcol, int ks0, v4i (&fa)[2][C::kBI],
                          v4i (&fb)[2][C::kBJ]) {
-  load_frags<C>(slot_a, slot_b, wrow, wcol, ks0, fa[0], fb[0]);
-  load_frags<C>(slot_a, slot_b, wrow, wcol, ks0 + 1, fa[1], fb[1]);
+  load_frags<C>(lane, slot_a, slot_b, wrow, wcol, ks0, fa[0], fb[0]);
+  load_frags<C>(lane, slot_a, slot_b, wrow, wcol, ks0 + 1, fa[1], fb[1]);
 }
 
 // The 16 MFMAs of a half stage; with kLoadsB > 0 one direct-to-LDS load (t = 0 .. kLoadsB-1 of a
@@ -558,27 +587,30 @@ MXQ_DEVICE void pp_barrier() {
 // One group's whole main loop (kG = 0: waves 0-3, 1: waves 4-7). The two groups run separate
 // straight-line code with the same barriers, so no accumulator or fragment value depends on a
 // branch (a branch per phase made the compiler copy and spill them).
-template <class C, int kG>
+// `before_tail` runs ahead of the last two or three iterations (the epilogue's factor reads, whose
+// latency then hides behind those iterations' MFMAs).
+template <class C, int kG, class BeforeTail>
 MXQ_DEVICE void pp_loop(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][C::kBJ], int wrow, int wcol,
-                        const Loader<C::kLoads>& ld) {
+                        const Loader<C::kLoads>& ld, BeforeTail&& before_tail) {
   constexpr int kSlotBytes = C::kSlotBytes, kSlots = C::kSlots, kL = C::kLoads;
   const int ktiles = (int)((p.K + kBK - 1) / kBK);
   const uint32_t lds_addr = (uint32_t)(uintptr_t)(lptr_t)lds;
   auto slot_addr = [&](int sl) { return lds_addr + (uint32_t)(sl * kSlotBytes); };
+  const int lane = tid_x() & 63;  // (once per tile: what the fragment reads derive from it stays out of the K loop)
 
-  // prologue: stages 0 and 1 into slots 0-3; stage 0 complete; group 0 reads (0, 0-1)
-  pp_issue<false, true>(ld, lds, 0, p.K, true);
-  pp_issue<true, true>(ld, lds + kSlotBytes, 0, p.K, true);
-  pp_issue<false, true>(ld, lds + 2 * kSlotBytes, kBK, p.K, ktiles > 1);
+  // prologue: A_0, B_0 and A_1 were issued into slots 0-2 before (pp_first_loads); B_1 goes to
+  // slot 3 once every wave is done with the previous tile's epilogue (factors in slot 3, staging
+  // in slot 4); then stage 0 is complete and group 0 reads (0, 0-1)
+  pp_barrier();
   pp_issue<true, true>(ld, lds + 3 * kSlotBytes, kBK, p.K, ktiles > 1);
   if (ktiles > 1)
-    wait_vmcnt<2 * kL>();
+    wait_vmcnt<kL>();
   else
     wait_vmcnt<0>();
   pp_barrier();
   v4i fa[2][C::kBI], fb[2][C::kBJ];
   if constexpr (kG == 0) {
-    pp_frags<C>(slot_addr(0), slot_addr(1), wrow, wcol, 0, fa, fb);
+    pp_frags<C>(lane, slot_addr(0), slot_addr(1), wrow, wcol, 0, fa, fb);
     wait_lgkm<0>();
   }
   pp_barrier();
@@ -598,19 +630,19 @@ MXQ_DEVICE void pp_loop(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][C::kBJ
     if constexpr (kG == 0) {
       pp_mma<C, 0, false>(fa, fb, acc, ld, nullptr, 0, 0, false);                       // P0
       pp_barrier();
-      pp_frags<C>(slot_addr(sa), slot_addr(sb), wrow, wcol, 2, fa, fb);                  // P1
+      pp_frags<C>(lane, slot_addr(sa), slot_addr(sb), wrow, wcol, 2, fa, fb);                  // P1
       pp_issue<false, !kSteady>(ld, slot_pa, k2, p.K, more2);
       wait_lgkm<0>();
       pp_barrier();
       pp_mma<C, 0, false>(fa, fb, acc, ld, nullptr, 0, 0, false);                       // P2
     } else {
-      pp_frags<C>(slot_addr(sa), slot_addr(sb), wrow, wcol, 0, fa, fb);                  // P0
+      pp_frags<C>(lane, slot_addr(sa), slot_addr(sb), wrow, wcol, 0, fa, fb);                  // P0
       pp_issue<false, !kSteady>(ld, slot_pa, k2, p.K, more2);
       wait_lgkm<0>();
       pp_barrier();
       pp_mma<C, 0, false>(fa, fb, acc, ld, nullptr, 0, 0, false);                       // P1
       pp_barrier();
-      pp_frags<C>(slot_addr(sa), slot_addr(sb), wrow, wcol, 2, fa, fb);                  // P2
+      pp_frags<C>(lane, slot_addr(sa), slot_addr(sb), wrow, wcol, 2, fa, fb);                  // P2
       wait_lgkm<0>();
     }
     // stage kt+1 has landed: only A_kt+2 (when it exists) was issued after it
@@ -621,7 +653,7 @@ MXQ_DEVICE void pp_loop(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][C::kBJ
     pp_barrier();
     if constexpr (kG == 0) {
       // P3 (at the last stage these reads fetch slots nobody uses; they keep the code branch-free)
-      pp_frags<C>(slot_addr(na), slot_addr(nb), wrow, wcol, 0, fa, fb);
+      pp_frags<C>(lane, slot_addr(na), slot_addr(nb), wrow, wcol, 0, fa, fb);
       pp_issue<true, !kSteady>(ld, slot_sa, k2, p.K, more2);
       wait_lgkm<0>();
     } else {
@@ -634,176 +666,88 @@ MXQ_DEVICE void pp_loop(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][C::kBJ
   const int steady = (int)max<int64_t>(p.K / kBK - 2, 0);
   int kt = 0;
   for (; kt < steady; ++kt) iteration(kt, std::true_type{});
+  before_tail();
   for (; kt < ktiles; ++kt) iteration(kt, std::false_type{});
-  // every load has completed and no wave reads the ring any more: the epilogue may reuse the LDS
-  wait_all();
-  pp_barrier();
+  // Leaves with every operand load complete (the last iteration waited for all of them) and
+  // every fragment read landed (each phase waits for its own), so the ring is idle; the caller
+  // ends the tile with a barrier.
 }
 
+// A tile's first operand chunks: A_0, B_0 and (when K has a second stage) A_1 into slots 0-2.
 template <class C>
-MXQ_DEVICE void pp_main_loop(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][C::kBJ], int wrow, int wcol,
-                             int64_t m0, int64_t n0) {
-  static_assert(C::kWaves == 8 && C::kSlots == 5 && C::kLoads == 4, "the ping-pong ring");
-  Loader<C::kLoads> ld;
-  make_loader(ld, p, m0, n0);
-  if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8)) == 0)
-    pp_loop<C, 0>(p, lds, acc, wrow, wcol, ld);
-  else
-    pp_loop<C, 1>(p, lds, acc, wrow, wcol, ld);
+MXQ_DEVICE void pp_first_loads(const GemmArgs& p, char* lds, const Loader<C::kLoads>& ld) {
+  pp_issue<false, true>(ld, lds, 0, p.K, true);
+  pp_issue<true, true>(ld, lds + C::kSlotBytes, 0, p.K, true);
+  pp_issue<false, true>(ld, lds + 2 * C::kSlotBytes, kBK, p.K, p.K > kBK);
 }
 
-template <int kEpi, int kOut, int kT, bool kDeep, bool kPP>
-__global__ __launch_bounds__((TileCfg<kT, kDeep, kPP>::kThreads), (TileCfg<kT, kDeep, kPP>::kPerCu)) void gemm_i8_kernel(GemmArgs p) {
-  typedef TileCfg<kT, kDeep, kPP> C;
-  constexpr int kBM = C::kBM, kBN = C::kBN, kWaveM = C::kWaveM, kWaveN = C::kWaveN;
-  constexpr int kBI = C::kBI, kBJ = C::kBJ, kSlotBytes = C::kSlotBytes, kLoads = C::kLoads;
-  constexpr int kSlots = C::kSlots, kAhead = C::kAhead;
-  static_assert(kT == 256 || (kEpi != kEpiGelu && kEpi != kEpiSwiGLU), "table epilogues need the 160 KB ring");
-  __shared__ __attribute__((aligned(16))) char lds[C::kLds];
+// The dequant epilogues' per-tile factors, read from global memory ahead of the epilogue: the
+// weight scale and the bias (raw, in the output type) of column n0 + t for thread t, and the
+// per-token scales of the lane's rows. Every read is unconditional (a missing bias reads the
+// first weight scale's bytes instead), so no branch waits for one.
+template <int kBI, int kOut>
+struct EpiFactors {
+  float ws;
+  typename OutT<kOut>::T bias_raw;
+  float xs[kBI];
+};
 
-  const int pos = pick_tile(p, p.tiles_m * p.tiles_n, lds);
-  if (pos < 0) return;
-  int tm, tn;
-  tile_walk(pos, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
-  const int64_t m0 = (int64_t)tm * kBM, n0 = (int64_t)tn * kBN;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  // The wave's first output row and column in the tile: a 2 x 2 grid of 128 x 128 quadrants;
-  // with kPP the two waves of a SIMD (w and w + 4) take the two 64-column halves of quadrant w.
-  const int wrow = ((wave & 3) >> 1) * kWaveM;
-  const int wcol = kPP ? (wave & 1) * 128 + (wave >> 2) * 64 : (wave & 1) * kWaveN;
-
-  v16i acc[kBI][kBJ];
+template <class C, int kEpi, int kOut>
+MXQ_DEVICE void load_epi_factors(const GemmArgs& p, int64_t m0, int64_t n0, int wrow, EpiFactors<C::kBI, kOut>& f) {
+  if constexpr (kEpi != kEpiI32) {
+    typedef typename OutT<kOut>::T BT;
+    const int t = tid_x(), lr = t & 31;
+    const int64_t col = min(n0 + t, p.N - 1);
+    f.ws = p.ws[p.ws_per_channel ? col : 0];
+    f.bias_raw = *(p.bias ? reinterpret_cast<const BT*>(p.bias) + col : reinterpret_cast<const BT*>(p.ws));
 #pragma unroll
-  for (int i = 0; i < kBI; ++i)
-#pragma unroll
-    for (int j = 0; j < kBJ; ++j) acc[i][j] = v16i{};
-
-  if constexpr (kPP) {
-    pp_main_loop<C>(p, lds, acc, wrow, wcol, m0, n0);
-  } else {
-    // Pipeline (D = kAhead stages ahead, a ring of S = 2D + 1 slots of one operand chunk each):
-    // the operand chunks arrive in the order A0 B0 A1 B1 A2 ..., chunk i (A_j = 2j, B_j = 2j + 1)
-    // into slot i % S; stage j (128 K-bytes) reads A_j and B_j. Entering iteration kt, A_kt and
-    // B_kt are complete and visible, stages kt+1 .. kt+D-1 are in flight and F0 holds the
-    // fragments of (stage kt, K-step 0). The iteration runs K-steps 0..3, each step's fragments
-    // read behind the previous step's MFMAs. A_kt+D goes into the slot of B_kt-1 (free since the
-    // previous barrier) with its loads spread over the MFMAs of K-steps 0 and 1; before the MFMAs
-    // of K-step 3 the wave waits for stage kt+1, passes the barrier that frees the slots of A_kt
-    // and B_kt, reads (kt+1, 0), and spreads the loads of B_kt+D over those MFMAs (into A_kt's
-    // slot). A chunk is thus requested D-1 to D stages before it is used, and no wave issues a
-    // burst of loads while its matrix pipe sits idle.
-    const int ktiles = (int)((p.K + kBK - 1) / kBK);
-    Loader<kLoads> ld;
-    make_loader(ld, p, m0, n0);
-    const int pre = min(ktiles, kAhead);  // stages requested before the loop
-    for (int s = 0; s < pre; ++s) {
-      issue_slot<false>(ld, lds + 2 * s * kSlotBytes, (int64_t)s * kBK, p.K);
-      issue_slot<true>(ld, lds + (2 * s + 1) * kSlotBytes, (int64_t)s * kBK, p.K);
-    }
-    // wait for stage 0: every load but those of stages 1 .. pre-1 has completed
-    static_for<kAhead>([&](auto P) {
-      constexpr int np = decltype(P)::value + 1;
-      if (pre == np) wait_vmcnt<2 * (np - 1) * kLoads>();
-    });
-    barrier_no_drain();
-
-    const uint32_t lds_addr = (uint32_t)(uintptr_t)(lptr_t)lds;
-    v4i f0a[kBI], f0b[kBJ], f1a[kBI], f1b[kBJ];
-    load_frags<C>(lds_addr, lds_addr + kSlotBytes, wrow, wcol, 0, f0a, f0b);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    __builtin_amdgcn_sched_barrier(0);
-    int sa = 0;  // slot of A_kt; B_kt is in (sa + 1) % 5
-    // One iteration. kSteady: stage kt+2 exists and lies wholly below K, so every load of the
-    // iteration is issued and none needs the K-tail check (no per-load compare, select or branch);
-    // the last two or three iterations take the general form.
-    auto iteration = [&](int kt, auto steady) {
-      constexpr bool kSteady = decltype(steady)::value;
-      const int sb = sa == kSlots - 1 ? 0 : sa + 1;
-      const int na = sb == kSlots - 1 ? 0 : sb + 1;  // A_kt+1
-      const int nb = na == kSlots - 1 ? 0 : na + 1;  // B_kt+1
-      const int pa = sa == 0 ? kSlots - 1 : sa - 1;  // A_kt+D (slot of B_kt-1)
-      const uint32_t cur_a = lds_addr + (uint32_t)(sa * kSlotBytes), cur_b = lds_addr + (uint32_t)(sb * kSlotBytes);
-      const bool more2 = kSteady || kt + kAhead < ktiles;  // stage kt+D exists
-      const bool more1 = kSteady || kt + 1 < ktiles;
-      const int64_t k2 = (int64_t)(kt + kAhead) * kBK;
-      load_frags<C>(cur_a, cur_b, wrow, wcol, 1, f1a, f1b);
-      wait_lgkm<kBI + kBJ>();
-      __builtin_amdgcn_sched_barrier(0);
-      mma_step_dma<C, false, 0, kLoads / 2, !kSteady>(f0a, f0b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
-      __builtin_amdgcn_sched_barrier(0);
-      load_frags<C>(cur_a, cur_b, wrow, wcol, 2, f0a, f0b);
-      wait_lgkm<kBI + kBJ>();
-      __builtin_amdgcn_sched_barrier(0);
-      mma_step_dma<C, false, kLoads / 2, kLoads / 2, !kSteady>(f1a, f1b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
-      __builtin_amdgcn_sched_barrier(0);
-      load_frags<C>(cur_a, cur_b, wrow, wcol, 3, f1a, f1b);
-      wait_lgkm<kBI + kBJ>();
-      __builtin_amdgcn_sched_barrier(0);
-      mma_step<C>(f0a, f0b, acc);
-      __builtin_amdgcn_sched_barrier(0);
-      // Stage kt+1 has landed when only the loads issued after B_kt+1 are outstanding: stages
-      // kt+2 .. kt+D-1 and A_kt+D where they exist (2 (r - 1) chunks when only r < D stages remain).
-      if (more2) {
-        wait_vm_lgkm0<(2 * kAhead - 3) * kLoads>();
-      } else if constexpr (kAhead > 2) {
-        const int r = ktiles - 1 - kt;
-        if (r == 3) {
-          wait_vm_lgkm0<4 * kLoads>();
-        } else if (r == 2) {
-          wait_vm_lgkm0<2 * kLoads>();
-        } else {
-          wait_all();
-        }
-      } else {
-        wait_all();
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      if (more1) {
-        barrier_no_drain();
-        load_frags<C>(lds_addr + (uint32_t)(na * kSlotBytes), lds_addr + (uint32_t)(nb * kSlotBytes), wrow, wcol, 0, f0a, f0b);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      mma_step_dma<C, true, 0, kLoads, !kSteady>(f1a, f1b, acc, ld, lds + sa * kSlotBytes, k2, p.K, more2 && more1);
-      __builtin_amdgcn_sched_barrier(0);
-      sa = na;
-    };
-    // steady < ktiles always (ktiles >= 1): written as do-while, the tail is seen to run at least
-    // once, so no path leaves the steady loop with fragment reads in flight straight into the
-    // epilogue (whose register copies would otherwise race those reads).
-    const int steady = (int)max<int64_t>(p.K / kBK - kAhead, 0);  // iterations whose stage kt+D is full
-    int kt = 0;
-    for (; kt < steady; ++kt) iteration(kt, std::true_type{});
-    do {
-      iteration(kt, std::false_type{});
-    } while (++kt < ktiles);
-    // Every wave is done reading the ring before the epilogue reuses it, and the last (unused)
-    // fragment reads have landed before their registers are reused.
-    wait_all();
-    __builtin_amdgcn_sched_barrier(0);
-    barrier_no_drain();
+    for (int i = 0; i < C::kBI; ++i) f.xs[i] = p.xs[min(m0 + wrow + i * 32 + lr, p.M - 1)];
   }
+}
 
+// The epilogue of one tile from its accumulators (lane l holds, for m-block i and n-block j, row
+// wrow + i*32 + l%32 and the four column runs j*32 + q*8 + (l/32)*4 + {0..3}, q = 0..3). The LDS
+// is free on entry (every wave is done with the operand ring): the per-column factors go to
+// C::kEpiLds, the output staging buffers to kStageBase (table epilogues: behind the factors).
+// `pre` runs once the factor reads are issued and before anything waits for them (the
+// ping-pong kernel issues the next tile's first operand loads there, into LDS the epilogue does
+// not touch; every LDS access below is inline assembly, so none of them waits for those loads).
+template <class C, int kEpi, int kOut, int kStageBase, int kFactorBase, class Pre>
+MXQ_DEVICE void gemm_epilogue(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][C::kBJ], int64_t m0, int64_t n0,
+                              int wrow, int wcol, const EpiFactors<C::kBI, kOut>& f, Pre&& pre) {
+  constexpr int kBM = C::kBM, kBN = C::kBN, kBI = C::kBI, kBJ = C::kBJ;
+  const int wave = tid_x() >> 6, lane = tid_x() & 63;
   // ---- epilogue ----
   // Lane l holds, for m-block i and n-block j, row wrow + i*32 + l%32 and the four column
   // runs j*32 + q*8 + (l/32)*4 + {0..3}, q = 0..3 (see mma_step). The main loop's last barrier
-  // left the LDS free: per-column factors go behind the four stage buffers and, for GELU, the
-  // 128 KB bf16 -> bf16 table is fetched into the buffers themselves while the dequant runs.
+  // left the LDS free: per-column factors go to kFactorBase and, for GELU, the 128 KB
+  // bf16 -> bf16 table is fetched into the ring's first slots while the dequant runs.
   constexpr int kElem = (kEpi == kEpiI32 || kOut == 0) ? 4 : 2;
   const int lr = lane & 31, lh = lane >> 5;
-  const int t = threadIdx.x;
-  float* s_ws = reinterpret_cast<float*>(lds + C::kEpiLds);
+  const int t = tid_x();
+  float* s_ws = reinterpret_cast<float*>(lds + kFactorBase);
   float* s_bias = s_ws + kBN;
   const uint16_t* s_gelu = reinterpret_cast<const uint16_t*>(lds);
   const bool has_b = p.bias != nullptr;
   float xsv[kBI] = {};
-  if (kEpi != kEpiI32) {
-    // Global reads of the factors are issued before the table fetch, so waiting for them
-    // leaves the fetch in flight.
-    const int64_t col = min(n0 + t, p.N - 1);
-    const float wsl = p.ws_per_channel ? p.ws[col] : p.ws[0];
-    const float bl = has_b ? OutT<kOut>::load(reinterpret_cast<const typename OutT<kOut>::T*>(p.bias) + col) : -0.0f;
+  if constexpr (kEpi == kEpiI32) {
+    pre();
+  } else {
+    const float bl = has_b ? OutT<kOut>::load(&f.bias_raw) : -0.0f;
+    if (t < kBN) {
+      lds_write_b32(lds_addr(s_ws + t), __float_as_uint(f.ws));
+      lds_write_b32(lds_addr(s_bias + t), __float_as_uint(bl));
+    }
+    // The factors are consumed here (the row scales through an empty asm statement), before any
+    // direct-to-LDS load is issued: with one of those in flight, the compiler's wait for a
+    // register load is a wait for every load (vmcnt(0)). The GELU / SiLU table fetch and `pre`
+    // then stay in flight through the dequant.
 #pragma unroll
-    for (int i = 0; i < kBI; ++i) xsv[i] = p.xs[min(m0 + wrow + i * 32 + lr, p.M - 1)];
+    for (int i = 0; i < kBI; ++i) {
+      xsv[i] = f.xs[i];
+      __asm__ volatile("" : "+v"(xsv[i]));
+    }
+    __builtin_amdgcn_sched_barrier(0);
     if (kEpi == kEpiGelu || kEpi == kEpiSwiGLU) {
       const char* src = reinterpret_cast<const char*>(kEpi == kEpiGelu ? (const void*)&kGeluFull : (const void*)&kSiluFull) +
                         lane * 16;
@@ -811,10 +755,8 @@ __global__ __launch_bounds__((TileCfg<kT, kDeep, kPP>::kThreads), (TileCfg<kT, k
       for (int q = wave; q < 128; q += C::kWaves)
         __builtin_amdgcn_global_load_lds((gptr_t)(src + q * 1024), (lptr_t)(lds + q * 1024), 16, 0, 0);
     }
-    if (t < kBN) {
-      s_ws[t] = wsl;
-      s_bias[t] = bl;
-    }
+    pre();
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt left open (max)
     barrier_no_drain();
   }
@@ -823,9 +765,11 @@ __global__ __launch_bounds__((TileCfg<kT, kDeep, kPP>::kThreads), (TileCfg<kT, k
   // staging buffers sit behind the per-column factors when a table fills the ring, else at 0.
   constexpr bool kTable = kEpi == kEpiGelu || kEpi == kEpiSwiGLU;
   const bool lines = full && p.line_store;
-  char* sbuf = lds + (kTable ? C::kEpiLds + 2 * kBN * 4 : 0) + wave * kStageBytes;
-  static_assert((kTable ? C::kEpiLds + 2 * kBN * 4 : 0) + C::kWaves * kStageBytes <= (kTable ? C::kLds : C::kEpiLds),
+  constexpr int kSB = kTable ? kFactorBase + 2 * kBN * 4 : kStageBase, kSE = kSB + C::kWaves * kStageBytes;
+  static_assert(kSE <= C::kLds && (kSE <= kFactorBase || kSB >= kFactorBase + 2 * kBN * 4) &&
+                    (!kTable || kSB >= 128 * 1024) && (!kTable || kFactorBase >= 128 * 1024),
                 "staging buffers overlap the table, the factors or the end of LDS");
+  char* sbuf = lds + kSB + wave * kStageBytes;
   const int64_t pitch = p.ldd * kElem;
   int64_t grow[kBI] = {};     // kEpiGatedRes: the gate row of each of this lane's rows
   int64_t grow_rm[kBI][4] = {};  // ... and of the rows it updates in the whole-line form
@@ -850,20 +794,27 @@ __global__ __launch_bounds__((TileCfg<kT, kDeep, kPP>::kThreads), (TileCfg<kT, k
     constexpr int jp = decltype(JP)::value;
     float wsv[2][16], bsv[2][16];
     if constexpr (kEpi != kEpiI32) {
+      // columns wcol + (2 jp + jj) * 32 + lh * 4 + q * 8 + {0..3}
+      const uint32_t a_ws = lds_addr(s_ws + wcol + 2 * jp * 32 + lh * 4), a_b = a_ws + kBN * 4;
+      v4i w4[2][4], b4[2][4];
+      static_for<2>([&](auto JJ) {
+        static_for<4>([&](auto Q) {
+          constexpr int kOff = decltype(JJ)::value * 128 + decltype(Q)::value * 32;
+          w4[decltype(JJ)::value][decltype(Q)::value] = lds_read_b128<kOff>(a_ws);
+          b4[decltype(JJ)::value][decltype(Q)::value] = lds_read_b128<kOff>(a_b);
+        });
+      });
+      wait_lgkm<0>();
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const int cl0 = wcol + (2 * jp + jj) * 32 + lh * 4;
+      for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const v4f w4 = *reinterpret_cast<const v4f*>(s_ws + cl0 + q * 8);
-          const v4f b4 = *reinterpret_cast<const v4f*>(s_bias + cl0 + q * 8);
+        for (int q = 0; q < 4; ++q)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            wsv[jj][q * 4 + e] = w4[e];
-            bsv[jj][q * 4 + e] = b4[e];
+            wsv[jj][q * 4 + e] = __int_as_float(w4[jj][q][e]);
+            bsv[jj][q * 4 + e] = __int_as_float(b4[jj][q][e]);
           }
-        }
-      }
     }
     static_for<kBI>([&](auto I) {
       constexpr int i = decltype(I)::value;
@@ -1020,6 +971,296 @@ __global__ __launch_bounds__((TileCfg<kT, kDeep, kPP>::kThreads), (TileCfg<kT, k
   }
 }
 
+// ---- persistent ping-pong workgroups ----
+// With the tile queue, the ping-pong kernel runs W = wg_per_xcd workgroups per XCD (one per CU)
+// that loop over tiles. XCD x's range splits as in pick_tile: its first count_x - pool positions
+// are static, its last `pool` are claimed at run time. Workgroup (x = bid % 8, k = bid / 8) takes
+// the static positions start_x + k, start_x + k + W, ... and then claims pool positions, from its
+// own XCD's counter first and then from the others in turn; a counter found drained is not asked
+// again (nothing refills it during a launch). Only the last eighth of the tiles thus waits for a
+// claim, and no claim is in flight across a main loop (the vmcnt waits there count operand loads
+// only). Wave 0 decides the next position (lane 0 claims, the wave reads the result as a scalar,
+// so the claim state costs no vector registers) and passes it to the workgroup through LDS. A
+// workgroup that finds every counter drained counts itself out (acquire-release); the last one
+// of the launch resets the counters for the next.
+MXQ_DEVICE int pp_claim(const GemmArgs& p, int num, int& j) {
+  const int x = blockIdx.x & 7;
+  const bool lane0 = (tid_x() & 63) == 0;
+  for (; j < 8; ++j) {
+    const int y = (x + j) & 7;
+    unsigned i = 0;
+    if (lane0) i = __hip_atomic_fetch_add(p.counters + y * 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    i = (unsigned)__builtin_amdgcn_readfirstlane((int)i);
+    if (i < (unsigned)p.pool) {
+      int ys, yc;
+      xcd_range(y, num, ys, yc);
+      return ys + yc - p.pool + (int)i;
+    }
+  }
+  // Release: this workgroup's claims are ordered before its count; acquire: the last one sees
+  // every claim of the launch (the counts form one release sequence) before it resets.
+  if (lane0) {
+    const unsigned done = __hip_atomic_fetch_add(p.counters + 8 * 32, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (done == (unsigned)p.n_claim - 1) {
+      for (int y = 0; y < 8; ++y) __hip_atomic_exchange(p.counters + y * 32, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_exchange(p.counters + 8 * 32, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  return -1;
+}
+
+// The ping-pong kernel: its tiles (one, or a sequence when p.persistent), each through the main
+// loop and the epilogue. LDS at tile boundaries: slots 0-2 take the next tile's first chunks while
+// the epilogue keeps its per-column factors in slot 3 and its output staging in slot 4; the next
+// position passes from wave 0 to the workgroup through a word of slot 3.
+template <class C, int kEpi, int kOut>
+MXQ_DEVICE void pp_tiles(const GemmArgs& p, char* lds) {
+  static_assert(C::kWaves == 8 && C::kSlots == 5 && C::kLoads == 4, "the ping-pong ring");
+  constexpr int kSlotBytes = C::kSlotBytes, kFactorBase = 3 * kSlotBytes, kStageBase = 4 * kSlotBytes;
+  static_assert(kFactorBase + 2 * C::kBN * 4 + 4 <= kStageBase, "slot 3 holds the factors and the next position");
+  const uint32_t next_word = lds_addr(lds + kFactorBase + 2 * C::kBN * 4);
+  const int num = p.tiles_m * p.tiles_n;
+  const bool wave0 = __builtin_amdgcn_readfirstlane(tid_x() >> 6) == 0;
+  // Wave 0's next position: the next static one while there is one, then claims; -1 at the end.
+  int static_next = -1, static_end = 0, claim_j = 0;
+  auto next_position = [&]() -> int {
+    if (!p.persistent) return -1;
+    if (static_next >= 0 && static_next < static_end) {
+      const int pos = static_next;
+      static_next += p.wg_per_xcd;
+      return pos;
+    }
+    static_next = -1;
+    return pp_claim(p, num, claim_j);
+  };
+  int pos;
+  if (p.persistent) {
+    int s, c;
+    xcd_range(blockIdx.x & 7, num, s, c);
+    static_next = s + (int)(blockIdx.x >> 3);
+    static_end = s + c - p.pool;
+    if (static_next < static_end) {
+      pos = static_next;
+      static_next += p.wg_per_xcd;
+    } else {  // more workgroups than static positions: the first tile is claimed too
+      if (wave0) {
+        const int got = next_position();
+        if ((tid_x() & 63) == 0) lds_write_b32(next_word, (uint32_t)got);
+      }
+      wait_all();
+      pp_barrier();
+      const uint32_t r = lds_read_b32(next_word);
+      wait_lgkm<0>();
+      __builtin_amdgcn_sched_barrier(0);
+      pos = __builtin_amdgcn_readfirstlane((int)r);
+      pp_barrier();  // read before the first loads land in slot 3's neighbourhood
+      if (pos < 0) return;
+    }
+  } else {
+    pos = pick_tile(p, num, lds);
+    if (pos < 0) return;
+  }
+  const int wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);  // scalar: so are wrow and wcol
+  // The wave's first output row and column in the tile: the two waves of a SIMD (w and w + 4)
+  // take the two 64-column halves of 128 x 128 quadrant w of the 2 x 2 grid.
+  const int wrow = ((wave & 3) >> 1) * C::kWaveM;
+  const int wcol = (wave & 1) * 128 + (wave >> 2) * 64;
+  const bool group0 = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8)) == 0;
+  int tm, tn;
+  tile_walk(pos, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+  int64_t m0 = (int64_t)tm * C::kBM, n0 = (int64_t)tn * C::kBN;
+  {
+    Loader<C::kLoads> first;
+    make_loader(first, p, m0, n0);
+    pp_first_loads<C>(p, lds, first);
+  }
+  for (;;) {
+    // (formed again per tile: the next tile's first loads use a copy of their own, so no loader
+    // stays live through the epilogue)
+    Loader<C::kLoads> ld;
+    make_loader(ld, p, m0, n0);
+    v16i acc[C::kBI][C::kBJ];
+#pragma unroll
+    for (int i = 0; i < C::kBI; ++i)
+#pragma unroll
+      for (int j = 0; j < C::kBJ; ++j) acc[i][j] = v16i{};
+    EpiFactors<C::kBI, kOut> f;
+    auto factors = [&] { load_epi_factors<C, kEpi, kOut>(p, m0, n0, wrow, f); };
+    if (group0)
+      pp_loop<C, 0>(p, lds, acc, wrow, wcol, ld, factors);
+    else
+      pp_loop<C, 1>(p, lds, acc, wrow, wcol, ld, factors);
+    // The ring is idle (pp_loop): slot 3 takes the next position before the barrier that ends
+    // the tile publishes it.
+    if (wave0) {
+      const int got = next_position();
+      if ((tid_x() & 63) == 0) lds_write_b32(next_word, (uint32_t)got);
+    }
+    wait_all();
+    pp_barrier();
+    const uint32_t next_read = lds_read_b32(next_word);
+    wait_lgkm<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    const int next = __builtin_amdgcn_readfirstlane((int)next_read);
+    int64_t nm0 = 0, nn0 = 0;
+    gemm_epilogue<C, kEpi, kOut, kStageBase, kFactorBase>(p, lds, acc, m0, n0, wrow, wcol, f, [&] {
+      if (next >= 0) {
+        int ntm, ntn;
+        tile_walk(next, p.tiles_m, p.tiles_n, p.group_m, ntm, ntn);
+        nm0 = (int64_t)ntm * C::kBM;
+        nn0 = (int64_t)ntn * C::kBN;
+        Loader<C::kLoads> next_ld;
+        make_loader(next_ld, p, nm0, nn0);
+        pp_first_loads<C>(p, lds, next_ld);
+      }
+    });
+    if (next < 0) break;
+    m0 = nm0;
+    n0 = nn0;
+  }
+}
+
+// The four-wave kernels: one tile per workgroup.
+template <class C, int kEpi, int kOut>
+MXQ_DEVICE void four_wave_tile(const GemmArgs& p, char* lds) {
+  constexpr int kBM = C::kBM, kBN = C::kBN, kWaveM = C::kWaveM, kWaveN = C::kWaveN;
+  constexpr int kBI = C::kBI, kBJ = C::kBJ, kSlotBytes = C::kSlotBytes, kLoads = C::kLoads;
+  constexpr int kSlots = C::kSlots, kAhead = C::kAhead;
+  const int pos = pick_tile(p, p.tiles_m * p.tiles_n, lds);
+  if (pos < 0) return;
+  int tm, tn;
+  tile_walk(pos, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+  const int64_t m0 = (int64_t)tm * kBM, n0 = (int64_t)tn * kBN;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // The wave's first output row and column in the tile: a 2 x 2 grid of quadrants.
+  const int wrow = (wave >> 1) * kWaveM;
+  const int wcol = (wave & 1) * kWaveN;
+
+  v16i acc[kBI][kBJ];
+#pragma unroll
+  for (int i = 0; i < kBI; ++i)
+#pragma unroll
+    for (int j = 0; j < kBJ; ++j) acc[i][j] = v16i{};
+
+  {
+    // Pipeline (D = kAhead stages ahead, a ring of S = 2D + 1 slots of one operand chunk each):
+    // the operand chunks arrive in the order A0 B0 A1 B1 A2 ..., chunk i (A_j = 2j, B_j = 2j + 1)
+    // into slot i % S; stage j (128 K-bytes) reads A_j and B_j. Entering iteration kt, A_kt and
+    // B_kt are complete and visible, stages kt+1 .. kt+D-1 are in flight and F0 holds the
+    // fragments of (stage kt, K-step 0). The iteration runs K-steps 0..3, each step's fragments
+    // read behind the previous step's MFMAs. A_kt+D goes into the slot of B_kt-1 (free since the
+    // previous barrier) with its loads spread over the MFMAs of K-steps 0 and 1; before the MFMAs
+    // of K-step 3 the wave waits for stage kt+1, passes the barrier that frees the slots of A_kt
+    // and B_kt, reads (kt+1, 0), and spreads the loads of B_kt+D over those MFMAs (into A_kt's
+    // slot). A chunk is thus requested D-1 to D stages before it is used, and no wave issues a
+    // burst of loads while its matrix pipe sits idle.
+    const int ktiles = (int)((p.K + kBK - 1) / kBK);
+    Loader<kLoads> ld;
+    make_loader(ld, p, m0, n0);
+    const int pre = min(ktiles, kAhead);  // stages requested before the loop
+    for (int s = 0; s < pre; ++s) {
+      issue_slot<false>(ld, lds + 2 * s * kSlotBytes, (int64_t)s * kBK, p.K);
+      issue_slot<true>(ld, lds + (2 * s + 1) * kSlotBytes, (int64_t)s * kBK, p.K);
+    }
+    // wait for stage 0: every load but those of stages 1 .. pre-1 has completed
+    static_for<kAhead>([&](auto P) {
+      constexpr int np = decltype(P)::value + 1;
+      if (pre == np) wait_vmcnt<2 * (np - 1) * kLoads>();
+    });
+    barrier_no_drain();
+
+    const uint32_t lds_addr = (uint32_t)(uintptr_t)(lptr_t)lds;
+    v4i f0a[kBI], f0b[kBJ], f1a[kBI], f1b[kBJ];
+    load_frags<C>(lane, lds_addr, lds_addr + kSlotBytes, wrow, wcol, 0, f0a, f0b);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_sched_barrier(0);
+    int sa = 0;  // slot of A_kt; B_kt is in (sa + 1) % 5
+    // One iteration. kSteady: stage kt+2 exists and lies wholly below K, so every load of the
+    // iteration is issued and none needs the K-tail check (no per-load compare, select or branch);
+    // the last two or three iterations take the general form.
+    auto iteration = [&](int kt, auto steady) {
+      constexpr bool kSteady = decltype(steady)::value;
+      const int sb = sa == kSlots - 1 ? 0 : sa + 1;
+      const int na = sb == kSlots - 1 ? 0 : sb + 1;  // A_kt+1
+      const int nb = na == kSlots - 1 ? 0 : na + 1;  // B_kt+1
+      const int pa = sa == 0 ? kSlots - 1 : sa - 1;  // A_kt+D (slot of B_kt-1)
+      const uint32_t cur_a = lds_addr + (uint32_t)(sa * kSlotBytes), cur_b = lds_addr + (uint32_t)(sb * kSlotBytes);
+      const bool more2 = kSteady || kt + kAhead < ktiles;  // stage kt+D exists
+      const bool more1 = kSteady || kt + 1 < ktiles;
+      const int64_t k2 = (int64_t)(kt + kAhead) * kBK;
+      load_frags<C>(lane, cur_a, cur_b, wrow, wcol, 1, f1a, f1b);
+      wait_lgkm<kBI + kBJ>();
+      __builtin_amdgcn_sched_barrier(0);
+      mma_step_dma<C, false, 0, kLoads / 2, !kSteady>(f0a, f0b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
+      __builtin_amdgcn_sched_barrier(0);
+      load_frags<C>(lane, cur_a, cur_b, wrow, wcol, 2, f0a, f0b);
+      wait_lgkm<kBI + kBJ>();
+      __builtin_amdgcn_sched_barrier(0);
+      mma_step_dma<C, false, kLoads / 2, kLoads / 2, !kSteady>(f1a, f1b, acc, ld, lds + pa * kSlotBytes, k2, p.K, more2);
+      __builtin_amdgcn_sched_barrier(0);
+      load_frags<C>(lane, cur_a, cur_b, wrow, wcol, 3, f1a, f1b);
+      wait_lgkm<kBI + kBJ>();
+      __builtin_amdgcn_sched_barrier(0);
+      mma_step<C>(f0a, f0b, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      // Stage kt+1 has landed when only the loads issued after B_kt+1 are outstanding: stages
+      // kt+2 .. kt+D-1 and A_kt+D where they exist (2 (r - 1) chunks when only r < D stages remain).
+      if (more2) {
+        wait_vm_lgkm0<(2 * kAhead - 3) * kLoads>();
+      } else if constexpr (kAhead > 2) {
+        const int r = ktiles - 1 - kt;
+        if (r == 3) {
+          wait_vm_lgkm0<4 * kLoads>();
+        } else if (r == 2) {
+          wait_vm_lgkm0<2 * kLoads>();
+        } else {
+          wait_all();
+        }
+      } else {
+        wait_all();
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (more1) {
+        barrier_no_drain();
+        load_frags<C>(lane, lds_addr + (uint32_t)(na * kSlotBytes), lds_addr + (uint32_t)(nb * kSlotBytes), wrow, wcol, 0, f0a, f0b);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      mma_step_dma<C, true, 0, kLoads, !kSteady>(f1a, f1b, acc, ld, lds + sa * kSlotBytes, k2, p.K, more2 && more1);
+      __builtin_amdgcn_sched_barrier(0);
+      sa = na;
+    };
+    // steady < ktiles always (ktiles >= 1): written as do-while, the tail is seen to run at least
+    // once, so no path leaves the steady loop with fragment reads in flight straight into the
+    // epilogue (whose register copies would otherwise race those reads).
+    const int steady = (int)max<int64_t>(p.K / kBK - kAhead, 0);  // iterations whose stage kt+D is full
+    int kt = 0;
+    for (; kt < steady; ++kt) iteration(kt, std::true_type{});
+    do {
+      iteration(kt, std::false_type{});
+    } while (++kt < ktiles);
+    // Every wave is done reading the ring before the epilogue reuses it, and the last (unused)
+    // fragment reads have landed before their registers are reused.
+    wait_all();
+    __builtin_amdgcn_sched_barrier(0);
+    barrier_no_drain();
+  }
+
+  EpiFactors<kBI, kOut> f;
+  load_epi_factors<C, kEpi, kOut>(p, m0, n0, wrow, f);
+  gemm_epilogue<C, kEpi, kOut, 0, C::kEpiLds>(p, lds, acc, m0, n0, wrow, wcol, f, [] {});
+}
+
+template <int kEpi, int kOut, int kT, bool kDeep, bool kPP>
+__global__ __launch_bounds__((TileCfg<kT, kDeep, kPP>::kThreads), (TileCfg<kT, kDeep, kPP>::kPerCu)) void gemm_i8_kernel(GemmArgs p) {
+  typedef TileCfg<kT, kDeep, kPP> C;
+  static_assert(kT == 256 || (kEpi != kEpiGelu && kEpi != kEpiSwiGLU), "table epilogues need the 160 KB ring");
+  __shared__ __attribute__((aligned(16))) char lds[C::kLds];
+  if constexpr (kPP)
+    pp_tiles<C, kEpi, kOut>(p, lds);
+  else
+    four_wave_tile<C, kEpi, kOut>(p, lds);
+}
+
 // Balanced tile queue (pick_tile): each XCD's pool is 1/kPoolDiv of its range and each XCD
 // gets as many extra workgroups as its pool holds tiles; problems of fewer than two rounds of
 // tiles keep the static order.
@@ -1035,6 +1276,7 @@ struct GemmPlan {
   int pool, wg_per_xcd, n_claim;
   int group_m;
   int64_t grid;
+  bool persistent;  // ping-pong workgroups that loop over their XCD's tiles (pp_tiles)
 };
 
 // Problems with fewer 256-tiles than CUs run 128-tiles (four times as many workgroups). Larger ones
@@ -1075,9 +1317,18 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, bool table, int64_t workspace_by
   if (workspace_bytes >= kTileQueueBytes && tiles >= 2 * slots && tiles <= INT32_MAX / 2) {
     const int64_t per = tiles / 8, rem = tiles % 8;
     g.pool = (int)((per + kPoolDiv - 1) / kPoolDiv);
-    g.wg_per_xcd = (int)(per + (rem ? 1 : 0) + g.pool);
-    g.grid = 8 * (int64_t)g.wg_per_xcd;
-    g.n_claim = (int)(g.grid - tiles + 8 * (int64_t)g.pool);
+    if (g.tile == 256 && !table) {
+      // Ping-pong tiles: one workgroup per CU, each looping over its XCD's static positions and
+      // then over claimed ones, so that a tile's epilogue overlaps the next tile's first loads.
+      g.persistent = true;
+      g.wg_per_xcd = std::max(1, mxq_cu_count() / 8);
+      g.grid = 8 * (int64_t)g.wg_per_xcd;
+      g.n_claim = (int)g.grid;
+    } else {
+      g.wg_per_xcd = (int)(per + (rem ? 1 : 0) + g.pool);
+      g.grid = 8 * (int64_t)g.wg_per_xcd;
+      g.n_claim = (int)(g.grid - tiles + 8 * (int64_t)g.pool);
+    }
   }
   return g;
 }
@@ -1094,6 +1345,7 @@ static int launch_gemm(const GemmArgs& args0, void* workspace, int64_t workspace
   args.n_claim = g.n_claim;
   args.counters = g.pool ? reinterpret_cast<unsigned*>(workspace) : nullptr;
   args.group_m = g.group_m;
+  args.persistent = g.persistent;
   const int elem = (kOut == 0 || kEpi == kEpiI32) ? 4 : 2;
   args.vec_store = ((uintptr_t)args.d % (4 * elem) == 0) && (args.ldd % 4 == 0);
   args.line_store = ((uintptr_t)args.d % 16 == 0) && ((args.ldd * elem) % 16 == 0);
@@ -1112,9 +1364,9 @@ static int launch_gemm(const GemmArgs& args0, void* workspace, int64_t workspace
     }
     // 256-tiles without a table epilogue: the ping-pong schedule (eight waves)
     gemm_i8_kernel<kEpi, kOut, 256, false, true><<<grid, TileCfg<256, false, true>::kThreads, 0, stream>>>(args);
-    return mxq_check_launch("gemm_i8_kernel");
+  } else {
+    gemm_i8_kernel<kEpi, kOut, 256, false, false><<<grid, kGemmThreads, 0, stream>>>(args);
   }
-  gemm_i8_kernel<kEpi, kOut, 256, false, false><<<grid, kGemmThreads, 0, stream>>>(args);
   return mxq_check_launch("gemm_i8_kernel");
 }
 
@@ -1153,6 +1405,7 @@ extern "C" int mxq_int8_gemm_plan(int64_t M, int64_t N, int64_t K, int table_epi
   plan[4] = g.wg_per_xcd;
   plan[5] = g.tile == 256 ? TileCfg<256>::kAhead : g.deep ? TileCfg<128, true>::kAhead : TileCfg<128>::kAhead;
   plan[6] = g.group_m;
+  plan[7] = g.persistent;
   return MXQ_OK;
 }
 

@@ -422,6 +422,27 @@ MXQ_DEVICE v4i lds_read_b128(uint32_t addr) {
   return r;
 }
 
+// LDS writes issued as inline assembly, for the same reason: code that runs while direct-to-LDS
+// loads are in flight (a tile's epilogue behind the next tile's first operand loads) would
+// otherwise wait for all of them before its first LDS access. The "memory" clobber keeps them in
+// program order with the other memory accesses; one wave's LDS instructions execute in order, so
+// a later read by the same wave sees them without a wait.
+MXQ_DEVICE void lds_write_b32(uint32_t addr, uint32_t v) {
+  __asm__ volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+MXQ_DEVICE void lds_write_b64(uint32_t addr, v2u v) {
+  __asm__ volatile("ds_write_b64 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+MXQ_DEVICE void lds_write_b128(uint32_t addr, v4u v) {
+  __asm__ volatile("ds_write_b128 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+MXQ_DEVICE uint32_t lds_read_b32(uint32_t addr) {
+  uint32_t r;
+  __asm__ volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+  return r;
+}
+MXQ_DEVICE uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(lptr_t)const_cast<void*>(p); }
+
 }  // namespace mxq
 
 // ---- host-side error plumbing (defined in capi.hip) -------------------------------
