@@ -52,7 +52,7 @@ int mxq_abi_version(void);
  * Per-row (per-token) symmetric INT8 quantization.
  *   x      [rows, cols] of x_dtype (bf16, fp16 or fp32), row-major, contiguous
  *   q      [rows, cols] int8 out;  scales [rows] fp32 out
- *   input_act  MXQ_ACT_NONE or MXQ_ACT_GELU_TANH (bf16 only): apply tanh-GELU to x first
+ *   input_act  MXQ_ACT_NONE or MXQ_ACT_GELU_TANH (bf16 or fp16): apply tanh-GELU to x first
  * Semantics: CK/backends/eager/quantization.py:857-875.
  * Replaces: launch_quantize_int8_rowwise_kernel, CK/backends/cuda/ops/int8_linear.cu:1035-1084
  * (stochastic rounding: mxq_quantize_int8_rowwise_stochastic).
@@ -276,8 +276,8 @@ int mxq_rms_adaln_quantize_int8(const void* x, const void* norm_weight, const vo
  *   r = a @ H_G per group of group_size columns, H_G = kron(h4, ..., h4) / sqrt(G), rounded once
  *       to x's dtype (the exact product; CK/tensor/int8_utils.py:11-74), skipped if group_size == 0
  *   q, scales = the row quantizer of r (CK/backends/eager/quantization.py:857-875).
- *   x_dtype: bf16 (any activation) or fp32 (no activation); cols % 16 == 0; group_size a power
- *   of 4 up to 1024 dividing cols (or 0).
+ *   x_dtype: bf16 or fp16 (any activation; fp16 activations as mxq_input_act_f16) or fp32 (no
+ *   activation); cols % 16 == 0; group_size a power of 4 up to 1024 dividing cols (or 0).
  * Replaces: launch_quantize_int8_rowwise_convrot{,64} (CK/backends/cuda/ops/int8_linear.cu:
  * 1086-1157, 1295-1409) and the eager rotation before quantize_int8_rowwise
  * (CK/backends/eager/quantization.py:1012-1025).
@@ -292,6 +292,14 @@ int mxq_quantize_int8_rowwise_convrot(const void* x, int x_dtype, int8_t* q, flo
  * Replaces: apply_input_act(x, "swiglu"), CK/backends/_activations.py:50-52.
  */
 int mxq_swiglu_bf16(const void* x, void* y, int64_t rows, int64_t cols, void* stream);
+
+/*
+ * The input activation on float16: input_act MXQ_ACT_GELU_TANH gives y[r, c] = gelu_tanh(x[r, c])
+ * for x [rows, cols]; MXQ_ACT_SWIGLU gives y[r, c] = fp16(fp16(silu(x[r, c])) * x[r, cols + c])
+ * for x [rows, 2*cols]. Bit-identical to torch's CPU routines on float16, NaN patterns included.
+ * Replaces: apply_input_act(x, input_act) on a float16 x, CK/backends/_activations.py:40-53.
+ */
+int mxq_input_act_f16(const void* x, void* y, int64_t rows, int64_t cols, int input_act, void* stream);
 
 /* p[0..n) = value on the stream (a kernel, so it is safe inside captured graphs). */
 int mxq_fill_f32(float* p, float value, int64_t n, void* stream);

@@ -150,6 +150,31 @@ def convrot_quantize_bf16(x_bits: np.ndarray, group_size: int, input_act: str | 
     return q, s, rot
 
 
+def round_f64_to_f16(x: np.ndarray) -> np.ndarray:
+    """float64 -> float16, one round-to-nearest-even rounding (numpy converts from the float64
+    bits directly; the device goes through a round-to-odd float32, which lands on the same side
+    of every float16 rounding boundary)."""
+    with np.errstate(over="ignore"):
+        return np.asarray(x, dtype=np.float64).astype(np.float16)
+
+
+def convrot_quantize_f16(x: np.ndarray, group_size: int, input_act: str | None = None):
+    """float16 activations [..., K] (or [..., 2K] for swiglu) -> (q int8, scale fp32 [..., 1],
+    rotated float16). The activation and the row quantizer are the reference's own torch CPU ops
+    in float16 (eager_torch: CK/backends/_activations.py:40-53, CK/backends/eager/
+    quantization.py:857-875); the rotation is the exact product rounded once to float16. group_size
+    0 skips the rotation."""
+    import torch
+
+    from . import eager_torch
+
+    a = eager_torch.apply_input_act(torch.from_numpy(np.asarray(x, dtype=np.float16)), input_act).numpy()
+    with np.errstate(invalid="ignore"):  # inf - inf in the rotation: NaN, as in the device's
+        rot = round_f64_to_f16(fht_f64(a.astype(np.float64), group_size)) if group_size else a
+    q, s = eager_torch.quantize_int8_rowwise(torch.from_numpy(rot))
+    return q.numpy(), s.numpy(), rot
+
+
 def convrot_quantize_f32(x: np.ndarray, group_size: int):
     """float32 activations [..., K] -> (q, scale, rotated float32)."""
     rot = fht_f64(np.asarray(x, dtype=F32).astype(np.float64), group_size).astype(F32)

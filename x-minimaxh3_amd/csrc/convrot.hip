@@ -32,7 +32,7 @@
 // modulation in the eager order: y = bf16(bf16(n * bf16(1 + scale[seg])) + shift[seg]).
 // y is optionally stored (the rms_adaln output) and then rotated and quantized as above.
 
-#include "act_rot.h"
+#include "act_f16.h"
 
 namespace mxq {
 
@@ -77,7 +77,8 @@ MXQ_DEVICE uint32_t half_of(const v4u* w, int i) {  // bf16 i of 16 packed in tw
 template <int kAct, int kDtype, int kMod, int kNW,
           int kOcc = (kDtype == MXQ_DTYPE_F32 || kNW > 4 || (kMod != kModNone && kNW > 3)) ? 2 : 3>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOcc))) void convrot_quant_kernel(CrArgs p) {
-  constexpr bool kF32 = kDtype == MXQ_DTYPE_F32;
+  constexpr bool kF32 = kDtype == MXQ_DTYPE_F32, kF16 = kDtype == MXQ_DTYPE_F16;
+  static_assert(kMod == kModNone || kDtype == MXQ_DTYPE_BF16, "the RMS adaLN front end takes bfloat16 rows");
   constexpr int kRawWords = kF32 ? 16 : (kAct == MXQ_ACT_SWIGLU ? 16 : 8);  // dwords per window
   constexpr int kKeepWords = kF32 ? 16 : 8;
   __shared__ uint32_t red_max[2][4];
@@ -175,15 +176,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOcc))) voi
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           uint32_t b = half_of(rw, i);
-          if constexpr (kAct == MXQ_ACT_GELU_TANH) b = gelu_bf16(b);
-          if constexpr (kAct == MXQ_ACT_SWIGLU) b = swiglu_bf16(b, half_of(rw + 2, i));
+          if constexpr (kAct == MXQ_ACT_GELU_TANH) b = kF16 ? gelu_f16(b) : gelu_bf16(b);
+          if constexpr (kAct == MXQ_ACT_SWIGLU) b = kF16 ? swiglu_f16(b, half_of(rw + 2, i)) : swiglu_bf16(b, half_of(rw + 2, i));
           if constexpr (kMod != kModNone) {
             const float t = round_bf16(1.0f + bf16_to_f32(half_of(sc, i)));
             const float n = round_bf16((bf16_to_f32(b) * rinv) * bf16_to_f32(half_of(nw, i)));
             b = f32_to_bf16_bits(round_bf16(n * t) + bf16_to_f32(half_of(sh, i)));
             if (i & 1) ybits[i >> 1] |= b << 16; else ybits[i >> 1] = b;
           }
-          v[i] = (double)bf16_to_f32(b);
+          v[i] = (double)(kF16 ? f16_to_f32(b) : bf16_to_f32(b));
         }
         if constexpr (kMod != kModNone) {
           if (p.y_out && on) {
@@ -205,7 +206,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOcc))) voi
       } else {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const uint32_t lo = f64_to_bf16_bits(v[2 * i] * inv), hi = f64_to_bf16_bits(v[2 * i + 1] * inv);
+          const uint32_t lo = kF16 ? f64_to_f16_bits(v[2 * i] * inv) : f64_to_bf16_bits(v[2 * i] * inv);
+          const uint32_t hi = kF16 ? f64_to_f16_bits(v[2 * i + 1] * inv) : f64_to_bf16_bits(v[2 * i + 1] * inv);
           keep[j][i] = lo | (hi << 16);
           if (on) amax = absmax_acc_bf16x2(amax, keep[j][i]);
         }
@@ -213,13 +215,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOcc))) voi
     }
     if constexpr (kMod == kModOnly) continue;
     // ---- row absmax across the row's waves, scale
-    const float wmax = wave_absmax(kF32 ? amax : absmax_bits_of_bf16x2(amax));
+    // (|float16| and |bfloat16| both order like their bit patterns, so one integer maximum serves both)
+    const uint32_t hmax = max(amax & 0xFFFFu, amax >> 16);
+    const float wmax = wave_absmax(kF32 ? amax : (kF16 ? __float_as_uint(f16_to_f32(hmax)) : hmax << 16));
     if (lane == 0) red_max[it][wave] = __float_as_uint(wmax);
     __syncthreads();
     uint32_t rmax = red_max[it][slot * wpr];
     for (int i = 1; i < wpr; ++i) rmax = rmax > red_max[it][slot * wpr + i] ? rmax : red_max[it][slot * wpr + i];
     const float s = row_scale_from_absmax(__uint_as_float(rmax));
     const float r = 1.0f / round_bf16(s);
+    // float16 rows divide by the scale rounded to float16 (torch.finfo(float16).tiny if that is 0),
+    // one fp32 division rounded to float16, as the generic quantizer does
+    float s16 = round_f16(s);
+    if (s16 == 0.0f) s16 = 6.103515625e-05f;
     // ---- quantize from registers, 16-byte stores
 #pragma unroll
     for (int j = 0; j < kNW; ++j) {
@@ -230,6 +238,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOcc))) voi
       for (int i = 0; i < 16; ++i) {
         if constexpr (kF32) {
           qv[i] = quant_round_clamp(__uint_as_float(keep[j][i]) / s);
+        } else if constexpr (kF16) {
+          const uint32_t h = (keep[j][i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+          qv[i] = quant_round_clamp(round_f16(f16_to_f32(h) / s16));
         } else {
           const uint32_t h = (keep[j][i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
           qv[i] = quant_round_clamp(round_bf16(bf16_to_f32(h) * r));
@@ -608,8 +619,8 @@ extern "C" int mxq_quantize_int8_rowwise_convrot(const void* x, int x_dtype, int
   }
   if (input_act < MXQ_ACT_NONE || input_act > MXQ_ACT_SWIGLU)
     return mxq_set_error(MXQ_ERR_INVALID, "unsupported input_act code %d", input_act);
-  if (x_dtype != MXQ_DTYPE_BF16 && !(x_dtype == MXQ_DTYPE_F32 && input_act == MXQ_ACT_NONE))
-    return mxq_set_error(MXQ_ERR_UNSUPPORTED, "rotation quantizer takes bfloat16 (or float32 without an activation)");
+  if (x_dtype != MXQ_DTYPE_BF16 && x_dtype != MXQ_DTYPE_F16 && !(x_dtype == MXQ_DTYPE_F32 && input_act == MXQ_ACT_NONE))
+    return mxq_set_error(MXQ_ERR_UNSUPPORTED, "rotation quantizer takes bfloat16 or float16 (or float32 without an activation)");
   if (rows == 0 || cols == 0) return MXQ_OK;
   if (!x || !q || !scales) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
   if (cols % 16) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "columns must be a multiple of 16");
@@ -621,6 +632,13 @@ extern "C" int mxq_quantize_int8_rowwise_convrot(const void* x, int x_dtype, int
   row_split(cols, a.wpr, nw);
   hipStream_t st = (hipStream_t)stream;
   if (x_dtype == MXQ_DTYPE_F32) return launch_convrot<MXQ_ACT_NONE, MXQ_DTYPE_F32, kModNone>(a, nw, st);
+  if (x_dtype == MXQ_DTYPE_F16) {
+    switch (input_act) {
+      case MXQ_ACT_NONE: return launch_convrot<MXQ_ACT_NONE, MXQ_DTYPE_F16, kModNone>(a, nw, st);
+      case MXQ_ACT_GELU_TANH: return launch_convrot<MXQ_ACT_GELU_TANH, MXQ_DTYPE_F16, kModNone>(a, nw, st);
+      default: return launch_convrot<MXQ_ACT_SWIGLU, MXQ_DTYPE_F16, kModNone>(a, nw, st);
+    }
+  }
   if (units_fit(cols, digits)) {
     switch (input_act) {
       case MXQ_ACT_NONE: return launch_units_digits<MXQ_ACT_NONE, kModNone>(a, st);

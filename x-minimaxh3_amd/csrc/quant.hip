@@ -14,7 +14,7 @@
 // 1 B written / element). The quantizer fed a known row absmax and the adaLN kernels below
 // describe their own layouts.
 
-#include "mxq_common.h"
+#include "act_f16.h"
 
 namespace mxq {
 
@@ -90,10 +90,10 @@ __global__ __launch_bounds__(kQuantBlock) void quant_rows_generic(
       if (kDtype == MXQ_DTYPE_F32) {
         f = reinterpret_cast<const float*>(xv)[row * cols + i];
       } else {
-        const uint16_t b = reinterpret_cast<const uint16_t*>(xv)[row * cols + i];
+        uint32_t b = reinterpret_cast<const uint16_t*>(xv)[row * cols + i];
+        if (kGelu) b = (kDtype == MXQ_DTYPE_BF16) ? gelu_bf16(b) : gelu_f16(b);
         f = (kDtype == MXQ_DTYPE_BF16) ? bf16_to_f32(b) : f16_to_f32(b);
       }
-      if (kGelu) f = bf16_to_f32(gelu_bf16(f32_to_bf16_bits(f)));
       return f;
     };
     uint32_t m = 0;
@@ -582,6 +582,22 @@ __global__ __launch_bounds__(256) void gelu_bf16_kernel(const uint16_t* __restri
   }
 }
 
+// The input activation on float16 rows: y[r, c] = gelu(x[r, c]) (x [rows, cols]) or
+// swiglu(x[r, c], x[r, cols + c]) (x [rows, 2 cols], the [gate | up] halves).
+template <int kAct>
+__global__ __launch_bounds__(256) void act_f16_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+                                                     int64_t rows, int64_t cols) {
+  const int64_t n = rows * cols;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    if constexpr (kAct == MXQ_ACT_GELU_TANH) {
+      y[i] = (uint16_t)gelu_f16(x[i]);
+    } else {
+      const int64_t r = i / cols, c = i - r * cols;
+      y[i] = (uint16_t)swiglu_f16(x[r * 2 * cols + c], x[r * 2 * cols + cols + c]);
+    }
+  }
+}
+
 __global__ void fill_f32_kernel(float* __restrict__ p, float value, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x)
@@ -688,8 +704,8 @@ extern "C" int mxq_quantize_int8_rowwise(const void* x, int x_dtype, int8_t* q, 
     return mxq_set_error(MXQ_ERR_UNSUPPORTED, "input dtype code %d", x_dtype);
   if (input_act != MXQ_ACT_NONE && input_act != MXQ_ACT_GELU_TANH)
     return mxq_set_error(MXQ_ERR_INVALID, "unsupported input_act code %d", input_act);
-  if (input_act == MXQ_ACT_GELU_TANH && x_dtype != MXQ_DTYPE_BF16)
-    return mxq_set_error(MXQ_ERR_UNSUPPORTED, "gelu_tanh input_act needs bf16 input");
+  if (input_act == MXQ_ACT_GELU_TANH && x_dtype == MXQ_DTYPE_F32)
+    return mxq_set_error(MXQ_ERR_UNSUPPORTED, "gelu_tanh input_act needs bf16 or fp16 input");
   hipStream_t st = (hipStream_t)stream;
   const bool gelu = input_act == MXQ_ACT_GELU_TANH;
   const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 8 == 0);
@@ -715,7 +731,10 @@ extern "C" int mxq_quantize_int8_rowwise(const void* x, int x_dtype, int8_t* q, 
     else
       quant_rows_generic<MXQ_DTYPE_BF16, false><<<row_grid(rows), kQuantBlock, 0, st>>>(x, q, scales, rows, cols);
   } else if (x_dtype == MXQ_DTYPE_F16) {
-    quant_rows_generic<MXQ_DTYPE_F16, false><<<row_grid(rows), kQuantBlock, 0, st>>>(x, q, scales, rows, cols);
+    if (gelu)
+      quant_rows_generic<MXQ_DTYPE_F16, true><<<row_grid(rows), kQuantBlock, 0, st>>>(x, q, scales, rows, cols);
+    else
+      quant_rows_generic<MXQ_DTYPE_F16, false><<<row_grid(rows), kQuantBlock, 0, st>>>(x, q, scales, rows, cols);
   } else {
     quant_rows_generic<MXQ_DTYPE_F32, false><<<row_grid(rows), kQuantBlock, 0, st>>>(x, q, scales, rows, cols);
   }
@@ -862,4 +881,20 @@ extern "C" int mxq_gelu_tanh_bf16(const void* x, void* y, int64_t n, void* strea
   if (blocks > 65536) blocks = 65536;
   gelu_bf16_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>((const uint16_t*)x, (uint16_t*)y, n, vec);
   return mxq_check_launch("gelu_bf16_kernel");
+}
+
+extern "C" int mxq_input_act_f16(const void* x, void* y, int64_t rows, int64_t cols, int input_act, void* stream) {
+  if (rows < 0 || cols < 0) return mxq_set_error(MXQ_ERR_INVALID, "negative shape");
+  if (input_act != MXQ_ACT_GELU_TANH && input_act != MXQ_ACT_SWIGLU)
+    return mxq_set_error(MXQ_ERR_INVALID, "unsupported input_act code %d", input_act);
+  if (rows == 0 || cols == 0) return MXQ_OK;
+  if (!x || !y) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  if (rows > INT64_MAX / 2 / cols) return mxq_set_error(MXQ_ERR_INVALID, "shape too large");
+  const int64_t blocks = std::min<int64_t>((rows * cols + 255) / 256, 65536);
+  hipStream_t st = (hipStream_t)stream;
+  if (input_act == MXQ_ACT_GELU_TANH)
+    act_f16_kernel<MXQ_ACT_GELU_TANH><<<(unsigned)blocks, 256, 0, st>>>((const uint16_t*)x, (uint16_t*)y, rows, cols);
+  else
+    act_f16_kernel<MXQ_ACT_SWIGLU><<<(unsigned)blocks, 256, 0, st>>>((const uint16_t*)x, (uint16_t*)y, rows, cols);
+  return mxq_check_launch("act_f16_kernel");
 }

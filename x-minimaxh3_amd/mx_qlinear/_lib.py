@@ -48,6 +48,7 @@ SIGNATURES: dict[str, list] = {
     "mxq_fill_f32": [_P, _F, _I64, _P],
     "mxq_quantize_int8_rowwise_convrot": [_P, _I, _P, _P, _I64, _I64, _I64, _I, _P],
     "mxq_swiglu_bf16": [_P, _P, _I64, _I64, _P],
+    "mxq_input_act_f16": [_P, _P, _I64, _I64, _I, _P],
     "mxq_int8_linear_m1": [_P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _P],
     "mxq_int8_gemv_dequant": [_P, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I, _P],
     "mxq_rms_adaln_quantize_int8": [_P, _P, _P, _P, _I64, _I64, _P, _F, _P, _P, _P, _I64, _I64, _I64, _P],

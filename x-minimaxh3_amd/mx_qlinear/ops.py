@@ -105,7 +105,7 @@ def quantize_int8_rowwise(x: torch.Tensor, stochastic_rounding: int | None = 0,
     > 0 is the reference's seed (quantization.py:803-826): the noise is ``torch.rand`` in x's
     dtype from a generator on x's device seeded with it, the same draws the reference makes, and
     the kernel adds it to the scaled value and floors. ``input_act`` ('gelu_tanh' or 'swiglu',
-    bf16 inputs; CK/backends/_activations.py:40-53) is applied first (not with stochastic
+    bf16 or fp16 inputs; CK/backends/_activations.py:40-53) is applied first (not with stochastic
     rounding); with 'swiglu' the input is ``[..., 2K]`` and the result ``[..., K]``.
     """
     act = _act_code(input_act)
@@ -118,8 +118,8 @@ def quantize_int8_rowwise(x: torch.Tensor, stochastic_rounding: int | None = 0,
     dev = _require_gpu(x)
     if x.dtype not in (torch.bfloat16, torch.float16, torch.float32):
         raise ValueError(f"unsupported input dtype {x.dtype}")
-    if act and x.dtype != torch.bfloat16:
-        raise NotImplementedError(f"input_act={input_act!r} is provided for bfloat16 inputs")
+    if act and x.dtype == torch.float32:
+        raise NotImplementedError(f"input_act={input_act!r} is provided for bfloat16 and float16 inputs")
     k = x.shape[-1]
     if k == 0:
         raise ValueError("quantize_int8_rowwise needs a non-empty last dimension")
@@ -161,15 +161,16 @@ def quantize_int8_rowwise_convrot(x: torch.Tensor, group_size: int = 256,
     CK/backends/eager/quantization.py:876-895 and 1012-1025): optional activation
     (CK/backends/_activations.py:40-53), then x @ H_G per group of ``group_size`` columns
     (CK/tensor/int8_utils.py:11-74, the exact product rounded once to x's dtype), then the row
-    quantizer. ``group_size=0`` skips the rotation. bf16 inputs (any activation) or fp32
-    inputs (no activation).
+    quantizer. ``group_size=0`` skips the rotation. bf16 or fp16 inputs (any activation) or
+    fp32 inputs (no activation).
     """
     act = _act_code(input_act)
     dev = _require_gpu(x)
     if group_size:
         _check_power_of_four(group_size)
-    if x.dtype not in (torch.bfloat16, torch.float32) or (act and x.dtype != torch.bfloat16):
-        raise NotImplementedError("the rotation quantizer takes bfloat16 inputs (or float32 without an activation)")
+    if x.dtype not in (torch.bfloat16, torch.float16, torch.float32) or (act and x.dtype == torch.float32):
+        raise NotImplementedError("the rotation quantizer takes bfloat16 or float16 inputs (or float32 without an "
+                                  "activation)")
     width = x.shape[-1]
     if width % _act_width(input_act):
         raise ValueError(f"{input_act} needs an even last dimension, got {width}")
@@ -202,18 +203,29 @@ def quantize_int8_convrot_weight(weight: torch.Tensor, group_size: int = 256) ->
 
 
 def apply_input_act(x: torch.Tensor, input_act: str | None) -> torch.Tensor:
-    """The pre-quantization activation (CK/backends/_activations.py:40-53) for bf16 inputs.
+    """The pre-quantization activation (CK/backends/_activations.py:40-53) for bf16 and fp16 inputs.
 
-    ``gelu_tanh`` is bit-identical to torch's CPU ``gelu(approximate='tanh')`` on bfloat16;
+    ``gelu_tanh`` is bit-identical to torch's CPU ``gelu(approximate='tanh')`` in the input's dtype;
     ``swiglu`` maps ``[..., 2K]`` to ``[..., K]`` as torch's ``silu(gate).mul_(up)``.
     """
     code = _act_code(input_act)
     if code == _lib.ACT_NONE:
         return x
     dev = _require_gpu(x)
-    if x.dtype != torch.bfloat16:
-        raise NotImplementedError(f"{input_act} is provided for bfloat16 tensors")
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise NotImplementedError(f"{input_act} is provided for bfloat16 and float16 tensors")
     xc = x.contiguous()
+    if x.dtype == torch.float16:
+        width = x.shape[-1]
+        if code == _lib.ACT_SWIGLU and width % 2:
+            raise ValueError(f"swiglu needs an even last dimension, got {width}")
+        k = width // 2 if code == _lib.ACT_SWIGLU else width
+        rows = xc.numel() // max(width, 1)
+        y = torch.empty((*x.shape[:-1], k), dtype=x.dtype, device=dev)
+        if y.numel():
+            with torch.cuda.device(dev):
+                call("mxq_input_act_f16", _p(xc), _p(y), rows, k, code, _stream(dev))
+        return y
     if code == _lib.ACT_SWIGLU:
         if x.shape[-1] % 2:
             raise ValueError(f"swiglu needs an even last dimension, got {x.shape[-1]}")
@@ -554,8 +566,8 @@ def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tenso
     dev = _require_gpu(x, weight)
     n = weight.shape[0]
     _weight_scale(weight_scale, n, dev)  # validate before launching anything
-    if act and x.dtype != torch.bfloat16:
-        raise NotImplementedError(f"input_act={input_act!r} needs a bfloat16 input")
+    if act and x.dtype == torch.float32:
+        raise NotImplementedError(f"input_act={input_act!r} needs a bfloat16 or float16 input")
     lead = x.shape[:-1]
     if x.numel() == 0:
         return torch.empty((*lead, n), dtype=out_dtype, device=dev)
@@ -759,8 +771,8 @@ def int8_linear_gated_residual_(residual: torch.Tensor, x: torch.Tensor, weight:
     width = x.shape[-1] // _act_width(input_act)
     if width != weight.shape[-1] or x.shape[-1] % _act_width(input_act):
         raise ValueError(f"Input and weight inner dimensions must match, got {width} and {weight.shape[-1]}")
-    if act and x.dtype != torch.bfloat16:
-        raise NotImplementedError(f"input_act={input_act!r} needs a bfloat16 input")
+    if act and x.dtype == torch.float32:
+        raise NotImplementedError(f"input_act={input_act!r} needs a bfloat16 or float16 input")
     x2 = x.reshape(-1, x.shape[-1])
     if convrot:
         _check_power_of_four(convrot_groupsize)
