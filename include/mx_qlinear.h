@@ -113,6 +113,18 @@ int mxq_adaln_quantize_int8(const void* x, const void* scale, const void* shift,
                             void* stream);
 
 /*
+ * adaLN on float16: y = f16(f16(f16(LN(x)) * f16(1 + scale)) + shift) with the LayerNorm
+ * statistics in fp32, the reference's adaln evaluated in float16 (CK/backends/eager/adaln.py:
+ * 11-14); scale/shift rows per group as mxq_adaln. y_out (float16 [rows, cols]) and q/scales (the
+ * row quantizer of y with the float16 rule, CK/backends/eager/quantization.py:857-875) are each
+ * optional (NULL), not both. Any cols.
+ * Replaces: the reference's adaln and, with q, the quantizer that consumes it, on float16 tensors.
+ */
+int mxq_adaln_quantize_int8_f16(const void* x, const void* scale, const void* shift, int64_t scale_group,
+                                int64_t shift_group, float eps, int8_t* q, float* scales, void* y_out,
+                                int64_t rows, int64_t cols, void* stream);
+
+/*
  * Tile-queue workspace of the INT8 GEMMs below (the `workspace, workspace_bytes` pair before the
  * stream). The hardware deals workgroups to the 8 XCDs round-robin, so a static tile order gives
  * every XCD 1/8 of the tiles, and the slowest XCD sets the GEMM's time. With a workspace, the
@@ -268,6 +280,18 @@ int mxq_rms_adaln_quantize_int8(const void* x, const void* norm_weight, const vo
                                 const int32_t* mod_rows, float eps, void* y_out, int8_t* q,
                                 float* scales, int64_t rows, int64_t cols, int64_t group_size,
                                 void* stream);
+
+/*
+ * The same on float16: x, norm_weight, scale, shift and y_out float16, every rounding above to
+ * float16 instead of bfloat16 (the reference's RMSNorm and modulation evaluated in float16), the
+ * rotated values rounded once to float16 and quantized with the float16 rule.
+ * Replaces: rms_adaln (kernels.py:7594-7640) and its quantizer on float16 tensors.
+ */
+int mxq_rms_adaln_quantize_int8_f16(const void* x, const void* norm_weight, const void* scale,
+                                    const void* shift, int64_t ld_mod, int64_t mod_count,
+                                    const int32_t* mod_rows, float eps, void* y_out, int8_t* q,
+                                    float* scales, int64_t rows, int64_t cols, int64_t group_size,
+                                    void* stream);
 
 /*
  * ConvRot rotation + per-row INT8 quantization, optionally after an activation:

@@ -121,3 +121,71 @@ def test_int8_linear_f16_inputs(dev, convrot, act):
     acc = eager_np.int8_matmul(q_ref, w.numpy())
     ref = eager_np.dequant_epilogue(acc, s_ref.reshape(-1), ws.numpy(), bf16_bits(b.float().numpy()), "bf16")
     assert np.array_equal(y.view(torch.int16).numpy().view(np.uint16), bf16_bits(ref))
+
+
+def _f16_ulp(v: np.ndarray) -> np.ndarray:
+    return np.spacing(np.abs(np.asarray(v, dtype=np.float32)).astype(np.float16)).astype(np.float64)
+
+
+# Fraction of float16 adaLN / RMS adaLN outputs that may differ from torch's CPU result by the
+# bounded amount: the statistics are reductions in another order than torch's, and float16 (eleven
+# significant bits) meets a rounding boundary more often than bfloat16. Measured on one MI355X:
+# adaLN 3.3e-5 to 1.2e-4, RMS adaLN 3.3e-5 to 4.3e-5 on the shapes below.
+F16_NORM_MISMATCH_BOUND = 5e-4
+
+
+@pytest.mark.parametrize("m,d,groups", [(64, 5120, 1), (33, 1000, 1), (40, 768, 4)])
+def test_adaln_f16(dev, m, d, groups):
+    """Modulated float16 within 2 ulp(n.t) + ulp(y) of torch's CPU adaln in float16; the int8
+    quantization of the kernel's own modulated rows bit-exact (torch's quantizer sequence)."""
+    x = (torch.randn(m, d, generator=gen(m + d)) * 2 + 0.3).to(torch.float16)
+    sc = (torch.randn(groups, d, generator=gen(5)) * 0.1).to(torch.float16)
+    sh = (torch.randn(groups, d, generator=gen(6)) * 0.1).to(torch.float16)
+    q, s, y = _mx().adaln_quantize_int8(x.to(dev), sc.to(dev), sh.to(dev), 1e-6, return_modulated=True)
+    rep = m // groups
+    scr, shr = sc.repeat_interleave(rep, 0), sh.repeat_interleave(rep, 0)
+    y_ref = eager_torch.adaln(x, scr, shr, 1e-6)
+    yv, rv = y.cpu().float().numpy(), y_ref.float().numpy()
+    x64 = x.double().numpy()
+    mu = x64.mean(-1, keepdims=True)
+    n64 = (x64 - mu) / np.sqrt(((x64 - mu) ** 2).mean(-1, keepdims=True) + 1e-6)
+    t = (1 + scr.float()).half().float().numpy()
+    tol = 2 * _f16_ulp(n64 * t) + _f16_ulp(np.maximum(np.abs(rv), np.abs(yv)))
+    assert np.all(np.abs(yv.astype(np.float64) - rv) <= tol)
+    rate = float(np.mean(_bits(y.cpu()) != _bits(y_ref)))
+    print(f"adaLN float16 mismatch rate vs torch CPU ({m}x{d}): {rate:.2e}", flush=True)
+    assert rate <= F16_NORM_MISMATCH_BOUND
+    q_ref, s_ref = eager_torch.quantize_int8_rowwise(y.cpu())
+    assert torch.equal(q.cpu(), q_ref) and torch.equal(s.cpu(), s_ref)
+    assert torch.equal(_mx().adaln(x.to(dev), sc.to(dev), sh.to(dev), 1e-6), y)
+
+
+@pytest.mark.parametrize("g", [0, 256])
+@pytest.mark.parametrize("m,d", [(48, 5376), (20, 3072)])
+def test_rms_adaln_f16(dev, m, d, g):
+    """RMS adaLN on float16 within 2 ulp(n.t) + ulp(y) of torch's CPU sequence in float16 (three
+    segments); q / scales bit-exact against the oracle's rotation and quantizer on the kernel's
+    own modulated rows."""
+    from mx_qlinear import ops
+
+    x = (torch.randn(m, d, generator=gen(m * 3 + d)) * 1.5).to(torch.float16)
+    w = (1 + 0.1 * torch.randn(d, generator=gen(7))).to(torch.float16)
+    sc = (torch.randn(3, d, generator=gen(8)) * 0.1).to(torch.float16)
+    sh = (torch.randn(3, d, generator=gen(9)) * 0.1).to(torch.float16)
+    segs = [(0, m // 3, 0), (m // 3, 2 * m // 3, 2), (2 * m // 3, m, 1)]
+    q, s, y = ops.rms_adaln_quantize_int8(x.to(dev), (w.to(dev), 1e-6), sh.to(dev), sc.to(dev), segs, g,
+                                          return_modulated=True)
+    y_ref = eager_torch.rms_adaln(x.clone(), w, 1e-6, sh, sc, segs)
+    yv, rv = y.cpu().float().numpy(), y_ref.float().numpy()
+    x64 = x.double().numpy()
+    n64 = x64 / np.sqrt((x64 * x64).mean(-1, keepdims=True) + 1e-6) * w.double().numpy()
+    rows = np.concatenate([np.full(b - a, r) for a, b, r in segs])
+    t = (1 + sc.float()).half().float().numpy()[rows]
+    tol = 2 * _f16_ulp(n64 * t) + _f16_ulp(np.maximum(np.abs(rv), np.abs(yv)))
+    assert np.all(np.abs(yv.astype(np.float64) - rv) <= tol)
+    rate = float(np.mean(_bits(y.cpu()) != _bits(y_ref)))
+    print(f"RMS adaLN float16 mismatch rate vs torch CPU ({m}x{d}, G={g}): {rate:.2e}", flush=True)
+    assert rate <= F16_NORM_MISMATCH_BOUND
+    q_ref, s_ref, _ = cr.convrot_quantize_f16(y.cpu().numpy(), g, None)
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    _same_scales(s.cpu().numpy(), s_ref)

@@ -78,7 +78,11 @@ template <int kAct, int kDtype, int kMod, int kNW,
           int kOcc = (kDtype == MXQ_DTYPE_F32 || kNW > 4 || (kMod != kModNone && kNW > 3)) ? 2 : 3>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOcc))) void convrot_quant_kernel(CrArgs p) {
   constexpr bool kF32 = kDtype == MXQ_DTYPE_F32, kF16 = kDtype == MXQ_DTYPE_F16;
-  static_assert(kMod == kModNone || kDtype == MXQ_DTYPE_BF16, "the RMS adaLN front end takes bfloat16 rows");
+  static_assert(kMod == kModNone || !kF32, "the RMS adaLN front end takes bfloat16 or float16 rows");
+  // the 16-bit row dtype's conversion and rounding (bfloat16 or float16)
+  auto cvt = [](uint32_t h) { return kF16 ? f16_to_f32(h) : bf16_to_f32(h); };
+  auto rnd = [](float f) { return kF16 ? round_f16(f) : round_bf16(f); };
+  auto to_bits = [](float f) { return kF16 ? f32_to_f16_bits(f) : f32_to_bf16_bits(f); };
   constexpr int kRawWords = kF32 ? 16 : (kAct == MXQ_ACT_SWIGLU ? 16 : 8);  // dwords per window
   constexpr int kKeepWords = kF32 ? 16 : 8;
   __shared__ uint32_t red_max[2][4];
@@ -128,10 +132,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOcc))) voi
       double ss = 0.0;
 #pragma unroll
       for (int j = 0; j < kNW; ++j) {
-        double acc = 0.0;  // squares of bf16 values are exact in float32; summed in float64
+        double acc = 0.0;  // squares of bf16 / fp16 values are exact in float32; summed in float64
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float lo = bf16_to_f32(raw[j][e] & 0xFFFFu), hi = bf16_to_f32(raw[j][e] >> 16);
+          const float lo = cvt(raw[j][e] & 0xFFFFu), hi = cvt(raw[j][e] >> 16);
           acc += (double)(lo * lo) + (double)(hi * hi);
         }
         ss += acc;
@@ -179,9 +183,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOcc))) voi
           if constexpr (kAct == MXQ_ACT_GELU_TANH) b = kF16 ? gelu_f16(b) : gelu_bf16(b);
           if constexpr (kAct == MXQ_ACT_SWIGLU) b = kF16 ? swiglu_f16(b, half_of(rw + 2, i)) : swiglu_bf16(b, half_of(rw + 2, i));
           if constexpr (kMod != kModNone) {
-            const float t = round_bf16(1.0f + bf16_to_f32(half_of(sc, i)));
-            const float n = round_bf16((bf16_to_f32(b) * rinv) * bf16_to_f32(half_of(nw, i)));
-            b = f32_to_bf16_bits(round_bf16(n * t) + bf16_to_f32(half_of(sh, i)));
+            const float t = rnd(1.0f + cvt(half_of(sc, i)));
+            const float n = rnd((cvt(b) * rinv) * cvt(half_of(nw, i)));
+            b = to_bits(rnd(n * t) + cvt(half_of(sh, i)));
             if (i & 1) ybits[i >> 1] |= b << 16; else ybits[i >> 1] = b;
           }
           v[i] = (double)(kF16 ? f16_to_f32(b) : bf16_to_f32(b));
@@ -663,11 +667,10 @@ extern "C" int mxq_swiglu_bf16(const void* x, void* y, int64_t rows, int64_t col
   return mxq_check_launch("swiglu_kernel");
 }
 
-extern "C" int mxq_rms_adaln_quantize_int8(const void* x, const void* norm_weight, const void* scale,
-                                           const void* shift, int64_t ld_mod, int64_t mod_count,
-                                           const int32_t* mod_rows, float eps, void* y_out, int8_t* q,
-                                           float* scales, int64_t rows, int64_t cols, int64_t group_size,
-                                           void* stream) {
+static int rms_adaln_launch(const void* x, const void* norm_weight, const void* scale, const void* shift,
+                            int64_t ld_mod, int64_t mod_count, const int32_t* mod_rows, float eps, void* y_out,
+                            int8_t* q, float* scales, int64_t rows, int64_t cols, int64_t group_size, bool f16,
+                            void* stream) {
   if (rows < 0 || cols < 0) return mxq_set_error(MXQ_ERR_INVALID, "negative shape");
   int digits = 0;
   if (q && group_size != 0) {
@@ -702,10 +705,32 @@ extern "C" int mxq_rms_adaln_quantize_int8(const void* x, const void* norm_weigh
   a.eps = eps;
   a.y_out = (uint16_t*)y_out;
   hipStream_t st = (hipStream_t)stream;
+  if (f16) {  // float16 rows: the window form
+    if (q) return launch_convrot<MXQ_ACT_NONE, MXQ_DTYPE_F16, kModQuant>(a, nw, st);
+    return launch_convrot<MXQ_ACT_NONE, MXQ_DTYPE_F16, kModOnly>(a, nw, st);
+  }
   if (units_fit(cols, digits)) {
     if (q) return launch_units_digits<MXQ_ACT_NONE, kModQuant>(a, st);
     return launch_units_digits<MXQ_ACT_NONE, kModOnly>(a, st);
   }
   if (q) return launch_convrot<MXQ_ACT_NONE, MXQ_DTYPE_BF16, kModQuant>(a, nw, st);
   return launch_convrot<MXQ_ACT_NONE, MXQ_DTYPE_BF16, kModOnly>(a, nw, st);
+}
+
+extern "C" int mxq_rms_adaln_quantize_int8(const void* x, const void* norm_weight, const void* scale,
+                                           const void* shift, int64_t ld_mod, int64_t mod_count,
+                                           const int32_t* mod_rows, float eps, void* y_out, int8_t* q,
+                                           float* scales, int64_t rows, int64_t cols, int64_t group_size,
+                                           void* stream) {
+  return rms_adaln_launch(x, norm_weight, scale, shift, ld_mod, mod_count, mod_rows, eps, y_out, q, scales, rows,
+                          cols, group_size, false, stream);
+}
+
+extern "C" int mxq_rms_adaln_quantize_int8_f16(const void* x, const void* norm_weight, const void* scale,
+                                               const void* shift, int64_t ld_mod, int64_t mod_count,
+                                               const int32_t* mod_rows, float eps, void* y_out, int8_t* q,
+                                               float* scales, int64_t rows, int64_t cols, int64_t group_size,
+                                               void* stream) {
+  return rms_adaln_launch(x, norm_weight, scale, shift, ld_mod, mod_count, mod_rows, eps, y_out, q, scales, rows,
+                          cols, group_size, true, stream);
 }

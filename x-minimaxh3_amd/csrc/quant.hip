@@ -598,6 +598,58 @@ __global__ __launch_bounds__(256) void act_f16_kernel(const uint16_t* __restrict
   }
 }
 
+// adaLN on float16 rows (the reference's layer_norm(x) * (1 + scale) + shift evaluated in
+// float16, CK/backends/eager/adaln.py:11-14): n = f16((x - mean) * rstd) with the statistics in
+// fp32 (mean = sum / cols, var = sum (x - mean)^2 / cols, rstd = 1 / sqrt(var + eps)),
+// y = f16(f16(n * f16(1 + scale)) + shift); optionally the row quantizer of y with the float16
+// rule (as quant_rows_generic). One wave per row, rows grid-stride; the row is read from global
+// memory once per pass (the later passes hit the caches). Each lane sums its columns in order and
+// the wave combines the lanes as wave_sum does.
+MXQ_DEVICE uint32_t adaln_f16_value(float xv, float mean, float rstd, uint32_t sc, uint32_t sh) {
+  const float n = round_f16((xv - mean) * rstd);
+  const float t = round_f16(1.0f + f16_to_f32(sc));
+  const float p = round_f16(n * t);
+  return f32_to_f16_bits(p + f16_to_f32(sh));
+}
+
+__global__ __launch_bounds__(kQuantBlock) void adaln_f16_rows(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ scale, const uint16_t* __restrict__ shift,
+    int64_t scale_group, int64_t shift_group, float eps, int8_t* __restrict__ q, float* __restrict__ scales,
+    uint16_t* __restrict__ y_out, int64_t rows, int64_t cols) {
+  const int lane = threadIdx.x % kWave;
+  for (int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave; row < rows;
+       row += (int64_t)gridDim.x * kRowsPerBlock) {
+    const uint16_t* xr = x + row * cols;
+    const uint16_t* sc = scale + (row / scale_group) * cols;
+    const uint16_t* sh = shift + (row / shift_group) * cols;
+    float sum = 0.0f;
+    for (int64_t i = lane; i < cols; i += kWave) sum += f16_to_f32(xr[i]);
+    const float mean = wave_sum(sum) / (float)cols;
+    float ss = 0.0f;
+    for (int64_t i = lane; i < cols; i += kWave) {
+      const float d = f16_to_f32(xr[i]) - mean;
+      ss = __builtin_fmaf(d, d, ss);
+    }
+    const float rstd = 1.0f / sqrtf(wave_sum(ss) / (float)cols + eps);
+    uint32_t m = 0;
+    for (int64_t i = lane; i < cols; i += kWave) {
+      const uint32_t y = adaln_f16_value(f16_to_f32(xr[i]), mean, rstd, sc[i], sh[i]);
+      if (y_out) y_out[row * cols + i] = (uint16_t)y;
+      m = max(m, abs_bits(f16_to_f32(y)));
+    }
+    if (q) {
+      const float s = row_scale_from_absmax(wave_absmax(m));
+      float s16 = round_f16(s);
+      if (s16 == 0.0f) s16 = 6.103515625e-05f;  // torch.finfo(float16).tiny
+      for (int64_t i = lane; i < cols; i += kWave) {
+        const uint32_t y = adaln_f16_value(f16_to_f32(xr[i]), mean, rstd, sc[i], sh[i]);
+        q[row * cols + i] = (int8_t)quant_round_clamp(round_f16(f16_to_f32(y) / s16));
+      }
+      if (lane == 0) scales[row] = s;
+    }
+  }
+}
+
 __global__ void fill_f32_kernel(float* __restrict__ p, float value, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x)
@@ -897,4 +949,19 @@ extern "C" int mxq_input_act_f16(const void* x, void* y, int64_t rows, int64_t c
   else
     act_f16_kernel<MXQ_ACT_SWIGLU><<<(unsigned)blocks, 256, 0, st>>>((const uint16_t*)x, (uint16_t*)y, rows, cols);
   return mxq_check_launch("act_f16_kernel");
+}
+
+extern "C" int mxq_adaln_quantize_int8_f16(const void* x, const void* scale, const void* shift,
+                                           int64_t scale_group, int64_t shift_group, float eps, int8_t* q,
+                                           float* scales, void* y_out, int64_t rows, int64_t cols, void* stream) {
+  if (rows < 0 || cols <= 0) return mxq_set_error(MXQ_ERR_INVALID, "bad shape");
+  if (rows == 0) return MXQ_OK;
+  if (!x || !scale || !shift) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
+  if (scale_group <= 0 || shift_group <= 0) return mxq_set_error(MXQ_ERR_INVALID, "modulation groups must be positive");
+  if (!q != !scales) return mxq_set_error(MXQ_ERR_INVALID, "q and scales go together");
+  if (!q && !y_out) return mxq_set_error(MXQ_ERR_INVALID, "neither a modulated output nor a quantized output");
+  adaln_f16_rows<<<row_grid(rows), kQuantBlock, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)x, (const uint16_t*)scale, (const uint16_t*)shift, scale_group, shift_group, eps, q, scales,
+      (uint16_t*)y_out, rows, cols);
+  return mxq_check_launch("adaln_f16_rows");
 }

@@ -49,9 +49,11 @@ SIGNATURES: dict[str, list] = {
     "mxq_quantize_int8_rowwise_convrot": [_P, _I, _P, _P, _I64, _I64, _I64, _I, _P],
     "mxq_swiglu_bf16": [_P, _P, _I64, _I64, _P],
     "mxq_input_act_f16": [_P, _P, _I64, _I64, _I, _P],
+    "mxq_adaln_quantize_int8_f16": [_P, _P, _P, _I64, _I64, _F, _P, _P, _P, _I64, _I64, _P],
     "mxq_int8_linear_m1": [_P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _P],
     "mxq_int8_gemv_dequant": [_P, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I, _P],
     "mxq_rms_adaln_quantize_int8": [_P, _P, _P, _P, _I64, _I64, _P, _F, _P, _P, _P, _I64, _I64, _I64, _P],
+    "mxq_rms_adaln_quantize_int8_f16": [_P, _P, _P, _P, _I64, _I64, _P, _F, _P, _P, _P, _I64, _I64, _I64, _P],
     "mxq_gelu_tanh_bf16": [_P, _P, _I64, _P],
     "mxq_dequant_int4_grouped_to_int8": [_P, _P, _I, _P, _P, _I64, _I64, _I64, _P],
     "mxq_w4a8_codebook_gemm": [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P, _I64,

@@ -241,8 +241,8 @@ def apply_input_act(x: torch.Tensor, input_act: str | None) -> torch.Tensor:
     return y
 
 
-def _modulation(t: torch.Tensor, rows: int, cols: int, dev, name: str):
-    t = t.to(device=dev, dtype=torch.bfloat16)
+def _modulation(t: torch.Tensor, rows: int, cols: int, dev, name: str, dtype=torch.bfloat16):
+    t = t.to(device=dev, dtype=dtype)
     if t.shape[-1] != cols:
         raise ValueError(f"{name} last dimension {t.shape[-1]} != {cols}")
     t2 = t.reshape(-1, cols).contiguous()
@@ -253,25 +253,30 @@ def _modulation(t: torch.Tensor, rows: int, cols: int, dev, name: str):
 
 
 def adaln(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
-    """``layer_norm(x) * (1 + scale) + shift`` in bf16 (CK/__init__.py:110-127, eager adaln.py:11-14).
+    """``layer_norm(x) * (1 + scale) + shift`` in x's dtype, bf16 or fp16 (CK/__init__.py:110-127,
+    eager adaln.py:11-14).
 
     ``scale`` / ``shift`` are ``[D]`` or one row per consecutive group of x rows
     (``[G, D]`` with G dividing the number of rows), as the reference's CUDA launcher's
     scale_group / shift_group (CK/backends/cuda/ops/adaln.cu:256-313).
     """
     dev = _require_gpu(x)
-    if x.dtype != torch.bfloat16:
-        raise NotImplementedError("mx_qlinear.adaln supports bfloat16 inputs")
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise NotImplementedError("mx_qlinear.adaln supports bfloat16 and float16 inputs")
     d = x.shape[-1]
     x2 = x.reshape(-1, d).contiguous()
     rows = x2.shape[0]
     out = torch.empty_like(x2)
     if rows == 0:
         return out.reshape(x.shape)
-    sc, sg = _modulation(scale, rows, d, dev, "scale")
-    sh, hg = _modulation(shift, rows, d, dev, "shift")
+    sc, sg = _modulation(scale, rows, d, dev, "scale", x.dtype)
+    sh, hg = _modulation(shift, rows, d, dev, "shift", x.dtype)
     with torch.cuda.device(dev):
-        call("mxq_adaln", _p(x2), _p(sc), _p(sh), _p(out), rows, d, sg, hg, float(eps), _stream(dev))
+        if x.dtype == torch.float16:
+            call("mxq_adaln_quantize_int8_f16", _p(x2), _p(sc), _p(sh), sg, hg, float(eps), None, None, _p(out), rows,
+                 d, _stream(dev))
+        else:
+            call("mxq_adaln", _p(x2), _p(sc), _p(sh), _p(out), rows, d, sg, hg, float(eps), _stream(dev))
     return out.reshape(x.shape)
 
 
@@ -282,8 +287,8 @@ def adaln_quantize_int8(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tenso
     Returns ``(q, x_scale)`` or ``(q, x_scale, modulated_bf16)`` when ``return_modulated``.
     """
     dev = _require_gpu(x)
-    if x.dtype != torch.bfloat16:
-        raise NotImplementedError("adaln_quantize_int8 supports bfloat16 inputs")
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise NotImplementedError("adaln_quantize_int8 supports bfloat16 and float16 inputs")
     d = x.shape[-1]
     x2 = x.reshape(-1, d).contiguous()
     rows = x2.shape[0]
@@ -291,32 +296,32 @@ def adaln_quantize_int8(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tenso
     s = torch.empty((rows, 1), dtype=torch.float32, device=dev)
     y = torch.empty_like(x2) if return_modulated else None
     if rows:
-        sc, sg = _modulation(scale, rows, d, dev, "scale")
-        sh, hg = _modulation(shift, rows, d, dev, "shift")
+        sc, sg = _modulation(scale, rows, d, dev, "scale", x.dtype)
+        sh, hg = _modulation(shift, rows, d, dev, "shift", x.dtype)
+        entry = "mxq_adaln_quantize_int8_f16" if x.dtype == torch.float16 else "mxq_adaln_quantize_int8"
         with torch.cuda.device(dev):
-            call("mxq_adaln_quantize_int8", _p(x2), _p(sc), _p(sh), sg, hg, float(eps), _p(q), _p(s),
-                 _p(y), rows, d, _stream(dev))
+            call(entry, _p(x2), _p(sc), _p(sh), sg, hg, float(eps), _p(q), _p(s), _p(y), rows, d, _stream(dev))
     out = (q.reshape(x.shape), s.reshape(*x.shape[:-1], 1))
     return out + (y.reshape(x.shape),) if return_modulated else out
 
 
-def _norm_parts(norm, d: int, dev) -> tuple[torch.Tensor, float]:
+def _norm_parts(norm, d: int, dev, dtype=torch.bfloat16) -> tuple[torch.Tensor, float]:
     """An RMSNorm module (``.weight`` [d], ``.eps``) or a ``(weight, eps)`` pair ->
-    (bf16 weight on ``dev``, eps); the weight is cast like ``weight.to(x.dtype)``."""
+    (weight on ``dev`` in x's dtype, eps); the weight is cast like ``weight.to(x.dtype)``."""
     weight, eps = (norm.weight, norm.eps) if hasattr(norm, "weight") else norm
-    w = weight.detach().to(device=dev, dtype=torch.bfloat16).reshape(-1).contiguous()
+    w = weight.detach().to(device=dev, dtype=dtype).reshape(-1).contiguous()
     if w.numel() != d:
         raise ValueError(f"RMSNorm weight has {w.numel()} entries, expected {d}")
     return w, float(eps)
 
 
-def _segment_table(t: torch.Tensor, d: int, dev, name: str) -> torch.Tensor:
+def _segment_table(t: torch.Tensor, d: int, dev, name: str, dtype=torch.bfloat16) -> torch.Tensor:
     t = t.detach()
     if t.dim() == 1:
         t = t.reshape(1, -1)
     if t.dim() != 2 or t.shape[1] != d:
         raise ValueError(f"{name} must be [rows, {d}], got {tuple(t.shape)}")
-    return t.to(device=dev, dtype=torch.bfloat16).contiguous()
+    return t.to(device=dev, dtype=dtype).contiguous()
 
 
 def rms_adaln_quantize_int8(value: torch.Tensor, norm, shift: torch.Tensor, scale: torch.Tensor,
@@ -341,17 +346,17 @@ def rms_adaln(value: torch.Tensor, norm, shift: torch.Tensor, scale: torch.Tenso
 def _rms_adaln_call(value, norm, shift, scale, segments, quant: bool, group: int, want_y: bool):
     if value.dim() != 2:
         raise ValueError("rms_adaln expects a 2-D [tokens, hidden] tensor")
-    if value.dtype != torch.bfloat16:
-        raise NotImplementedError("rms_adaln supports bfloat16 inputs")
+    if value.dtype not in (torch.bfloat16, torch.float16):
+        raise NotImplementedError("rms_adaln supports bfloat16 and float16 inputs")
     dev = _require_gpu(value)
     rows, d = value.shape
     if quant and group:
         _check_power_of_four(group)
         if d % group:
             raise ValueError(f"ConvRot group size {group} does not divide input features {d}")
-    w, eps = _norm_parts(norm, d, dev)
-    sc = _segment_table(scale, d, dev, "scale")
-    sh = _segment_table(shift, d, dev, "shift")
+    w, eps = _norm_parts(norm, d, dev, value.dtype)
+    sc = _segment_table(scale, d, dev, "scale", value.dtype)
+    sh = _segment_table(shift, d, dev, "shift", value.dtype)
     if sc.shape[0] != sh.shape[0]:
         raise ValueError("scale and shift must have the same number of rows")
     if isinstance(segments, torch.Tensor):
@@ -366,8 +371,9 @@ def _rms_adaln_call(value, norm, shift, scale, segments, quant: bool, group: int
     s = torch.empty((rows, 1), dtype=torch.float32, device=dev) if quant else None
     if rows and d:
         with torch.cuda.device(dev):
-            call("mxq_rms_adaln_quantize_int8", _p(x), _p(w), _p(sc), _p(sh), sc.stride(0), sc.shape[0], _p(mr),
-                 eps, _p(y), _p(q), _p(s), rows, d, group if quant else 0, _stream(dev))
+            entry = "mxq_rms_adaln_quantize_int8_f16" if x.dtype == torch.float16 else "mxq_rms_adaln_quantize_int8"
+            call(entry, _p(x), _p(w), _p(sc), _p(sh), sc.stride(0), sc.shape[0], _p(mr), eps, _p(y), _p(q), _p(s),
+                 rows, d, group if quant else 0, _stream(dev))
     if not quant:
         return y
     return (q, s, y) if want_y else (q, s)
