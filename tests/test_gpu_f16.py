@@ -189,3 +189,20 @@ def test_rms_adaln_f16(dev, m, d, g):
     q_ref, s_ref, _ = cr.convrot_quantize_f16(y.cpu().numpy(), g, None)
     assert np.array_equal(q.cpu().numpy(), q_ref)
     _same_scales(s.cpu().numpy(), s_ref)
+
+
+def test_int8_ffn_gelu_f16_input(dev):
+    """The fused FFN chain on a float16 input equals the two-call composition (int8_linear with
+    bf16 output, then int8_linear with input_act='gelu_tanh'), bit for bit."""
+    m, k, h, n = 96, 512, 1024, 384
+    x = (torch.randn(m, k, generator=gen(61)) * 2).to(torch.float16).to(dev)
+    w1 = torch.randint(-127, 128, (h, k), generator=gen(62), dtype=torch.int8).to(dev)
+    w2 = torch.randint(-127, 128, (n, h), generator=gen(63), dtype=torch.int8).to(dev)
+    s1 = (torch.rand(h, generator=gen(64)) * 0.01 + 1e-3).to(dev)
+    s2 = (torch.rand(n, generator=gen(65)) * 0.01 + 1e-3).to(dev)
+    b1 = (torch.randn(h, generator=gen(66)) * 0.1).to(torch.bfloat16).to(dev)
+    b2 = (torch.randn(n, generator=gen(67)) * 0.1).to(torch.bfloat16).to(dev)
+    mx = _mx()
+    y = mx.int8_ffn_gelu(x, w1, s1, b1, w2, s2, b2)
+    ref = mx.int8_linear(mx.int8_linear(x, w1, s1, b1), w2, s2, b2, input_act="gelu_tanh")
+    assert torch.equal(y.view(torch.int16), ref.view(torch.int16))

@@ -632,10 +632,11 @@ def int8_ffn_gelu(x: torch.Tensor, fc1_weight: torch.Tensor, fc1_scale: torch.Te
     CU, its lookups hidden under that pass's HBM traffic); with ``return_hidden`` the same pass
     writes the GELU output over fc1's. Hidden widths beyond that pass's register budget (32768)
     apply GELU and the row absmax in fc1's epilogue instead. Results are identical to the
-    two-call composition. bf16 in and out.
+    two-call composition. x bf16, fp16 or fp32 (the first quantizer reads it in its dtype; fc1's
+    output and everything after are bf16, the composition's default out_dtype); bf16 out.
     """
-    if x.dtype != torch.bfloat16:
-        raise NotImplementedError("int8_ffn_gelu takes a bfloat16 input")
+    if x.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise NotImplementedError("int8_ffn_gelu takes a bfloat16, float16 or float32 input")
     dev = _require_gpu(x, fc1_weight, fc2_weight)
     k = x.shape[-1]
     hidden, n = fc1_weight.shape[0], fc2_weight.shape[0]
@@ -659,7 +660,7 @@ def int8_ffn_gelu(x: torch.Tensor, fc1_weight: torch.Tensor, fc1_scale: torch.Te
     st = _stream(dev)
     gws = _gemm_ws(dev)
     with torch.cuda.device(dev):
-        call("mxq_quantize_int8_rowwise", _p(x2), _lib.DTYPE_BF16, _p(ws.xq), _p(ws.xs), m, k,
+        call("mxq_quantize_int8_rowwise", _p(x2), _OUT_CODES[x.dtype], _p(ws.xq), _p(ws.xs), m, k,
              _lib.ACT_NONE, st)
         if hidden <= _GELU_QUANT_MAX_COLS:
             call("mxq_int8_gemm_dequant", _p(ws.xq), _p(w1), _p(ws.xs), _p(s1), s1.numel(), _p(b1),
