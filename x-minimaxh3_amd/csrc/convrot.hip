@@ -374,19 +374,22 @@ __global__ __launch_bounds__(kUnitMaxWaves * 64) void convrot_units_kernel(CrArg
   const int64_t xstride = kAct == MXQ_ACT_SWIGLU ? 2 * (int64_t)p.K : p.K;
   double* tb = tbuf + wave * kTWave;
   int it = 0;
-  // Raw loads of every unit of this group for the batch starting at r (zeros for units past
-  // the row and rows past the end).
+  // Raw loads of every unit of this group for the batch starting at r, through one raw buffer
+  // over rows r .. (the batch's rows span at most 16 * 2 * 2^16 bytes): units past the row and
+  // rows past the end pass an offset beyond the buffer and read zeros, without a branch.
   auto load_batch = [&](int64_t r, uint32_t (&raw)[kNU][kRawWords]) {
     const int64_t row = r + slot;
     const bool row_on = slot < rpb && row < p.rows;
+    const char* base = reinterpret_cast<const char*>(p.x) + r * xstride * 2;
+    const int bytes = (int)std::min<int64_t>((p.rows - r) * xstride * 2, 0x7FFFFFF0);
 #pragma unroll
     for (int k = 0; k < kNU; ++k) {
       const int u = gi + k * gr;
       const bool on = row_on && u < units;
-      const uint16_t* xr = reinterpret_cast<const uint16_t*>(p.x) + (on ? row * xstride + u * 256 + gl * 16 : 0);
+      const uint32_t off = on ? (uint32_t)((slot * xstride + u * 256 + gl * 16) * 2) : kBufferOff;
 #pragma unroll
       for (int c = 0; c < kRawWords / 4; ++c) {
-        const v4u w = on ? *reinterpret_cast<const v4u*>(xr + (c < 2 ? 0 : p.K) + 8 * (c & 1)) : v4u{0, 0, 0, 0};
+        const v4u w = buffer_load_x4(base, bytes, off + (c < 2 ? 0u : (uint32_t)p.K * 2u) + 16u * (c & 1));
 #pragma unroll
         for (int e = 0; e < 4; ++e) raw[k][4 * c + e] = w[e];
       }
@@ -401,7 +404,9 @@ __global__ __launch_bounds__(kUnitMaxWaves * 64) void convrot_units_kernel(CrArg
     // the first kPreMod units, requested with the raw loads so that their latency overlaps the
     // row sum instead of following it; the other units' words are requested one unit ahead of
     // their use. (All units up front: 144 -> 188 VGPRs at three units, and at the occupancy that
-    // leaves, 0.71 -> 0.83 ms for [75600, 5376]; the first unit alone: 0.70 ms.)
+    // leaves, 0.71 -> 0.83 ms for [75600, 5376]; the first unit alone: 0.70 ms.) The loads are
+    // unconditional: a unit past the row reads columns 0 .. 15 of a valid row, and its values
+    // are left out of the row's absmax and never stored.
     v4u nw[kMod != kModNone ? kNU : 1][2], sc[kMod != kModNone ? kNU : 1][2], sh[kMod != kModNone ? kNU : 1][2];
     const uint16_t* msc = nullptr;
     const uint16_t* msh = nullptr;
@@ -411,9 +416,9 @@ __global__ __launch_bounds__(kUnitMaxWaves * 64) void convrot_units_kernel(CrArg
       const int e0 = on ? u * 256 + gl * 16 : 0;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        nw[k][c] = on ? reinterpret_cast<const v4u*>(p.norm_w + e0)[c] : v4u{0, 0, 0, 0};
-        sc[k][c] = on ? reinterpret_cast<const v4u*>(msc + e0)[c] : v4u{0, 0, 0, 0};
-        sh[k][c] = on ? reinterpret_cast<const v4u*>(msh + e0)[c] : v4u{0, 0, 0, 0};
+        nw[k][c] = reinterpret_cast<const v4u*>(p.norm_w + e0)[c];
+        sc[k][c] = reinterpret_cast<const v4u*>(msc + e0)[c];
+        sh[k][c] = reinterpret_cast<const v4u*>(msh + e0)[c];
       }
     };
     if constexpr (kMod != kModNone) {
@@ -464,13 +469,16 @@ __global__ __launch_bounds__(kUnitMaxWaves * 64) void convrot_units_kernel(CrArg
         for (int i = 0; i < 8; ++i) {
           const uint32_t xw = rw[i >> 2][i & 3], ww = nw[k][i >> 2][i & 3];
           const uint32_t sw = sc[k][i >> 2][i & 3], hw = sh[k][i >> 2][i & 3];
-          // t = bf16(1 + scale), n = bf16((x * r) * w), y = bf16(bf16(n * t) + shift), in pairs
-          const uint32_t t = pack_bf16x2(1.0f + bf16_lo(sw), 1.0f + bf16_hi(sw));
-          const uint32_t n = pack_bf16x2((bf16_lo(xw) * rinv) * bf16_lo(ww), (bf16_hi(xw) * rinv) * bf16_hi(ww));
-          const uint32_t nt = pack_bf16x2(bf16_lo(n) * bf16_lo(t), bf16_hi(n) * bf16_hi(t));
-          ybits[i] = pack_bf16x2(bf16_lo(nt) + bf16_lo(hw), bf16_hi(nt) + bf16_hi(hw));
-          v[2 * i] = (double)bf16_lo(ybits[i]);
-          v[2 * i + 1] = (double)bf16_hi(ybits[i]);
+          // t = bf16(1 + scale), n = bf16((x * r) * w), y = bf16(bf16(n * t) + shift), each
+          // rounding kept in fp32 form (round_bf16), the pair packed only for the y store
+          const float tl = round_bf16(1.0f + bf16_lo(sw)), th = round_bf16(1.0f + bf16_hi(sw));
+          const float nl = round_bf16((bf16_lo(xw) * rinv) * bf16_lo(ww));
+          const float nh = round_bf16((bf16_hi(xw) * rinv) * bf16_hi(ww));
+          const float yl = round_bf16(round_bf16(nl * tl) + bf16_lo(hw));
+          const float yh = round_bf16(round_bf16(nh * th) + bf16_hi(hw));
+          ybits[i] = pair_of_rounded(yl, yh);
+          v[2 * i] = (double)yl;
+          v[2 * i + 1] = (double)yh;
         }
         if (p.y_out && on) {
           v4u* dst = reinterpret_cast<v4u*>(p.y_out + row * p.K + e0);
@@ -500,8 +508,10 @@ __global__ __launch_bounds__(kUnitMaxWaves * 64) void convrot_units_kernel(CrArg
         for (int i = 0; i < 8; ++i)
           keep[k][i] = f64_to_bf16_bits(v[2 * i] * kInv) | (f64_to_bf16_bits(v[2 * i + 1] * kInv) << 16);
       }
+      uint32_t ua = 0;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) amax = absmax_acc_bf16x2(amax, keep[k][i]);
+      for (int i = 0; i < 8; ++i) ua = absmax_acc_bf16x2(ua, keep[k][i]);
+      amax = on ? absmax_acc_bf16x2(amax, ua) : amax;
       if constexpr (kDigits >= 3) unit_back16(keep[k], tb);
     }
     if constexpr (kMod == kModOnly) continue;

@@ -290,10 +290,9 @@ MXQ_DEVICE void epi_run(const v16i& acc, int q, float xs, const float* w, const 
   } else {
     float y[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) y[e] = (float)acc[q * 4 + e] * (xs * w[e]);
-    const uint32_t p0 = pack_bf16x2(y[0], y[1]), p1 = pack_bf16x2(y[2], y[3]);
-    out[0] = pack_bf16x2(__uint_as_float(p0 << 16) + bias[0], __uint_as_float(p0 & 0xFFFF0000u) + bias[1]);
-    out[1] = pack_bf16x2(__uint_as_float(p1 << 16) + bias[2], __uint_as_float(p1 & 0xFFFF0000u) + bias[3]);
+    for (int e = 0; e < 4; ++e) y[e] = round_bf16((float)acc[q * 4 + e] * (xs * w[e])) + bias[e];
+    out[0] = pack_bf16x2(y[0], y[1]);
+    out[1] = pack_bf16x2(y[2], y[3]);
   }
 }
 

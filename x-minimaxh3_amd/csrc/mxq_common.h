@@ -66,7 +66,21 @@ MXQ_DEVICE uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2));
 }
 
-MXQ_DEVICE float round_bf16(float f) { return bf16_to_f32(f32_to_bf16_bits(f)); }
+// f rounded to bfloat16 (round-to-nearest-even), as an fp32 value: one v_cvt_pk_bf16_f32 with the
+// value in the high half and zero in the low half, so the word already is the fp32 form (no
+// unpacking shift). Rounding each value of a pair this way costs two instructions where a packed
+// conversion and the two unpacks cost three.
+MXQ_DEVICE float round_bf16(float f) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  const f2 v = {0.0f, fp32_barrier(f)};
+  return __builtin_bit_cast(float, __builtin_convertvector(v, bf2));
+}
+
+// Two bf16-valued fp32 numbers (low 16 bits zero) as one packed pair, lo in bits 0..15.
+MXQ_DEVICE uint32_t pair_of_rounded(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
 
 MXQ_DEVICE float f16_to_f32(uint32_t bits16) {
   _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits16);
@@ -151,9 +165,10 @@ MXQ_DEVICE v2u quant8_bf16(v4u w, float r) {
 // bytes are the two's complement int8 values.
 typedef short mxq_s2 __attribute__((ext_vector_type(2)));
 
-MXQ_DEVICE uint32_t quant_pair_finite(uint32_t p) {
+// (flo, fhi: the two values already rounded to bf16, as fp32)
+MXQ_DEVICE uint32_t quant_pair_finite(float flo, float fhi) {
   constexpr float kRound = 12582912.0f;
-  const uint32_t lo = __float_as_uint(bf16_lo(p) + kRound), hi = __float_as_uint(bf16_hi(p) + kRound);
+  const uint32_t lo = __float_as_uint(flo + kRound), hi = __float_as_uint(fhi + kRound);
   const mxq_s2 n = __builtin_bit_cast(mxq_s2, __builtin_amdgcn_perm(hi, lo, 0x05040100u));
   return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(n, mxq_s2{127, 127}));
 }
@@ -161,7 +176,7 @@ MXQ_DEVICE uint32_t quant_pair_finite(uint32_t p) {
 MXQ_DEVICE v2u quant8_bf16_finite(v4u w, float r) {
   uint32_t n[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) n[i] = quant_pair_finite(pack_bf16x2(bf16_lo(w[i]) * r, bf16_hi(w[i]) * r));
+  for (int i = 0; i < 4; ++i) n[i] = quant_pair_finite(round_bf16(bf16_lo(w[i]) * r), round_bf16(bf16_hi(w[i]) * r));
   v2u o;
   o[0] = __builtin_amdgcn_perm(n[1], n[0], 0x06040200u);
   o[1] = __builtin_amdgcn_perm(n[3], n[2], 0x06040200u);
@@ -377,6 +392,15 @@ MXQ_DEVICE void buffer_load_lds16(const void* base, int bytes, lptr_t dst, uint3
       __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, kRawBufferWord3), dst, 16, (int)voff,
       soff, 0, 0);
 }
+
+// 16-byte buffer load into registers from a raw buffer of `bytes` bytes at `base` (wave-uniform):
+// an offset at or beyond `bytes` reads zeros, so a lane with nothing to read passes such an offset
+// instead of branching around the load and zeroing its registers.
+MXQ_DEVICE v4u buffer_load_x4(const void* base, int bytes, uint32_t voff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, kRawBufferWord3), (int)voff, 0, 0);
+}
+constexpr uint32_t kBufferOff = 0x80000000u;  // an offset beyond every buffer these kernels form
 
 // s_waitcnt with vmcnt <= n (lgkmcnt and expcnt left alone); n is a compile-time constant.
 template <int n> MXQ_DEVICE void wait_vmcnt() {

@@ -511,9 +511,8 @@ __global__ __launch_bounds__(kQuantBlock) __attribute__((amdgpu_waves_per_eu(kEx
           const float hl = i < 2 ? h0[2 * i] : h1[2 * i - 4], hh = i < 2 ? h0[2 * i + 1] : h1[2 * i - 3];
           float xl, xh;
           unpack_fresh(v[j][i], xl, xh);
-          const uint32_t n = pack_bf16x2((xl - mean) * rstd, (xh - mean) * rstd);
-          const uint32_t p = pack_bf16x2(bf16_lo(n) * tl, bf16_hi(n) * th);
-          v[j][i] = pack_bf16x2(bf16_lo(p) + hl, bf16_hi(p) + hh);
+          const float nl = round_bf16((xl - mean) * rstd), nh = round_bf16((xh - mean) * rstd);
+          v[j][i] = pack_bf16x2(round_bf16(nl * tl) + hl, round_bf16(nh * th) + hh);
           m = ok ? absmax_acc_bf16x2(m, v[j][i]) : m;
         }
         if (y_out != nullptr && ok) __builtin_nontemporal_store(v[j], reinterpret_cast<v4u*>(y_out + r * cols) + c);
