@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MXQ_ABI_VERSION 3
+#define MXQ_ABI_VERSION 4
 
 /* Return codes. */
 #define MXQ_OK 0
@@ -141,13 +141,14 @@ int mxq_adaln_quantize_int8_f16(const void* x, const void* scale, const void* sh
 /*
  * Launch plan the INT8 GEMMs below choose for an M x N x K problem (table_epilogue: 1 for the
  * GELU and SwiGLU epilogues, 0 otherwise) given workspace_bytes of tile-queue workspace (0:
- * none): plan[0] tile edge (256 or 128), plan[1] workgroups, plan[2] tiles, plan[3] tiles per
+ * none): plan[0] tile rows (256 or 128), plan[1] workgroups, plan[2] tiles, plan[3] tiles per
  * XCD claimed at run time (0: static order), plan[4] workgroups per XCD, plan[5] stages of
  * operands requested ahead of the MFMAs (4 when the 128-tiles all fit on the CUs at once, one
  * workgroup per CU; else 2), plan[6] tile-rows per group of the tile order, plan[7] 1 when
  * the workgroups loop over tiles (one per CU: plan[4] per XCD each take the static positions
  * start + k, start + k + plan[4], ... of their XCD's range, then claim pool positions) and 0 when
- * each runs one tile. plan holds 8 entries. Host only; no
+ * each runs one tile, plan[8] tile columns (the tile rows, or 96: 128 x 96 tiles when those
+ * still fit on the CUs at once and use more of them). plan holds 9 entries. Host only; no
  * reference counterpart (CUTLASS's Gemm::get_workspace_size is the nearest,
  * CK/backends/cuda/ops/cutlass_gemm_int8.cu:318); tests and tuning read it.
  */

@@ -61,7 +61,7 @@ def test_library_exports_every_declared_symbol(lib):
 def test_abi_version_and_error_string(lib):
     from mx_qlinear import _lib
 
-    assert lib.mxq_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.mxq_abi_version() == _lib.ABI_VERSION == 4
     lib.mxq_last_error.restype = ctypes.c_char_p
     assert isinstance(lib.mxq_last_error(), bytes)
     # a rejected call leaves a message naming the problem
@@ -148,7 +148,7 @@ def test_gemm_plan_queues_large_problems(lib, m, n, k, table, tile, queued):
 
     plan = _lib.gemm_plan(m, n, k, table)
     assert plan["tile"] == tile
-    tiles = -(-m // tile) * -(-n // tile)
+    tiles = -(-m // tile) * -(-n // plan["tile_n"])
     assert plan["tiles"] == tiles
     if queued:
         per = tiles // 8
@@ -168,21 +168,23 @@ def test_gemm_plan_queues_large_problems(lib, m, n, k, table, tile, queued):
 
 
 @pytest.mark.parametrize(
-    "m,n,table,tile,ahead",
+    "m,n,table,tile,tile_n,ahead",
     [
-        (1024, 3072, False, 128, 4),    # 192 tiles of 128: one workgroup per CU, deep ring
-        (1100, 1800, False, 128, 4),    # 135 tiles of 128, both edges partial
-        (2048, 2048, False, 128, 4),    # exactly 256 tiles of 128
-        (2050, 2056, False, 128, 2),    # 289 tiles of 128: two workgroups per CU
-        (75600, 5120, False, 256, 2),
-        (1024, 3072, True, 256, 2),     # table epilogues always take 256-tiles
+        (1024, 3072, False, 128, 96, 4),    # 192 tiles of 128 -> 256 of 128 x 96, one per CU, deep ring
+        (1100, 1800, False, 128, 96, 4),    # 135 tiles of 128 -> 171 of 128 x 96, both edges partial
+        (2048, 2048, False, 128, 128, 4),   # exactly 256 tiles of 128 (352 of 128 x 96 would not fit)
+        (1100, 192, False, 128, 128, 4),    # 18 tiles either way: the square tiles stay
+        (2050, 2056, False, 128, 128, 2),   # 289 tiles of 128: two workgroups per CU
+        (75600, 5120, False, 256, 256, 2),
+        (1024, 3072, True, 256, 256, 2),    # table epilogues always take 256-tiles
     ],
 )
-def test_gemm_plan_ring_depth(lib, m, n, table, tile, ahead):
+def test_gemm_plan_ring_depth(lib, m, n, table, tile, tile_n, ahead):
     from mx_qlinear import _lib
 
     plan = _lib.gemm_plan(m, n, 1024, table)
-    assert (plan["tile"], plan["ahead"]) == (tile, ahead)
+    assert (plan["tile"], plan["tile_n"], plan["ahead"]) == (tile, tile_n, ahead)
+    assert plan["tiles"] == -(-m // tile) * -(-n // tile_n)
 
 
 def _tile_walk(t, tiles_m, tiles_n, group_m):
@@ -205,7 +207,7 @@ def test_tile_order_visits_every_tile_once(lib, m, n, group_m):
     plan = _lib.gemm_plan(m, n, 1024)
     if group_m is not None:
         assert plan["group_m"] == group_m
-    tm, tn = -(-m // plan["tile"]), -(-n // plan["tile"])
+    tm, tn = -(-m // plan["tile"]), -(-n // plan["tile_n"])
     seen = {_tile_walk(t, tm, tn, plan["group_m"]) for t in range(tm * tn)}
     assert seen == {(i, j) for i in range(tm) for j in range(tn)}
     if plan["ahead"] == 4:

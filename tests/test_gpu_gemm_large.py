@@ -126,57 +126,85 @@ def test_gated_residual_256_tiles(dev):
     assert np.array_equal(bits(out), want)
 
 
-# ---- the deep-ring 128-tile configuration: at most 256 tiles of 128, one workgroup per CU with
-# four stages in flight. K covers one partial stage (16), one full (128), the loop's tail with
-# three, two and one stages left after a partial last stage (144 .. 656), steady iterations
-# (1024) and a long loop ending in a partial stage (3088).
+# ---- the deep-ring configurations: at most 256 tiles, one workgroup per CU with four stages in
+# flight, as 128 x 128 tiles or, where more of them then fit on the CUs at once, 128 x 96 tiles
+# (four 32-row strips of three blocks per wave; 12 KB B chunks). K covers one partial stage (16),
+# one full (128), the loop's tail with three, two and one stages left after a partial last stage
+# (144 .. 656), steady iterations (1024) and a long loop ending in a partial stage (3088).
 
-MD, ND = 1100, 1800  # 9 x 15 = 135 tiles of 128, both edges partial
+DEEP = {
+    "square": (1900, 2000, 128),  # 15 x 16 = 240 tiles of 128 (315 of 128 x 96 would not fit)
+    "128x96": (1100, 1800, 96),   # 9 x 19 = 171 tiles of 128 x 96 (135 of 128), both edges partial
+}
 
 
-def _assert_deep(m, n, k):
+def _assert_deep(m, n, k, tile_n):
     import mx_qlinear._lib as L
 
     plan = L.gemm_plan(m, n, k)
-    assert (plan["tile"], plan["ahead"]) == (128, 4), plan
+    assert (plan["tile"], plan["tile_n"], plan["ahead"]) == (128, tile_n, 4), plan
 
 
+@pytest.mark.parametrize("form", list(DEEP))
 @pytest.mark.parametrize("k", [16, 128, 144, 400, 528, 656, 1024, 3088])
-def test_gemm_i32_deep_ring(dev, k):
-    _assert_deep(MD, ND, k)
-    print(f"gemm i32 deep-ring m={MD} n={ND} k={k}", flush=True)
-    a, w = _i8((MD, k), 240 + k), _i8((ND, k), 241 + k)
+def test_gemm_i32_deep_ring(dev, k, form):
+    md, nd, tile_n = DEEP[form]
+    _assert_deep(md, nd, k, tile_n)
+    print(f"gemm i32 deep-ring {form} m={md} n={nd} k={k}", flush=True)
+    a, w = _i8((md, k), 240 + k), _i8((nd, k), 241 + k)
     c = _mx().mm_int8(a.to(dev), w.to(dev).t())
     assert np.array_equal(c.cpu().numpy(), eager_np.int8_matmul(a.numpy(), w.numpy()))
 
 
-@pytest.mark.parametrize("k,bias", [(400, True), (3072, False)])
-def test_int8_linear_deep_ring(dev, k, bias):
-    _assert_deep(1024, 3072, k)
-    print(f"int8_linear deep-ring m=1024 n=3072 k={k} bias={bias}", flush=True)
-    x = activations(1024, k, 250 + k)
-    w, ws = int8_weight(3072, k, 251 + k)
-    b = bf16_vec(3072, 252, 0.01) if bias else None
+@pytest.mark.parametrize("m,n,tile_n,k,bias", [(1024, 3072, 96, 400, True), (1024, 3072, 96, 3072, False),
+                                               (1900, 2000, 128, 400, True)])
+def test_int8_linear_deep_ring(dev, m, n, tile_n, k, bias):
+    _assert_deep(m, n, k, tile_n)
+    print(f"int8_linear deep-ring m={m} n={n} k={k} bias={bias}", flush=True)
+    x = activations(m, k, 250 + k)
+    w, ws = int8_weight(n, k, 251 + k)
+    b = bf16_vec(n, 252, 0.01) if bias else None
     y = _mx().int8_linear(x.to(dev), w.to(dev), ws.to(dev), None if b is None else b.to(dev))
     ref = eager_np.int8_linear(bits(x), w.numpy(), ws.numpy(), None if b is None else bits(b), "bf16")
     assert np.array_equal(bits(y), bf16_bits(ref))
 
 
-def test_gated_residual_deep_ring(dev):
+@pytest.mark.parametrize("out", ["fp32", "fp16"])
+def test_dequant_deep_ring_128x96_wide_outputs(dev, out):
+    """fp32 outputs leave the odd third block through the staged 128-byte lines, fp16 ones by runs."""
+    md, nd, tile_n = DEEP["128x96"]
     k = 528
-    _assert_deep(MD, ND, k)
-    print(f"gated residual deep-ring m={MD} n={ND} k={k}", flush=True)
-    x = activations(MD, k, 260)
-    w, ws = int8_weight(ND, k, 261)
-    b = bf16_vec(ND, 262, 0.02)
-    gate = torch.randn(2, ND, generator=gen(263)).to(torch.bfloat16)
-    res = activations(MD, ND, 264) * 3
-    segs = ((0, 600, 1), (600, MD, 0))
+    _assert_deep(md, nd, k, tile_n)
+    print(f"dequant deep-ring 128x96 m={md} n={nd} k={k} out={out}", flush=True)
+    dt = torch.float32 if out == "fp32" else torch.float16
+    a, w = _i8((md, k), 255), _i8((nd, k), 256)
+    xs = torch.rand(md, generator=gen(257)) * 1e-3
+    ws = torch.rand(nd, generator=gen(258)) * 1e-2
+    b = (torch.randn(nd, generator=gen(259)) * 0.5).to(dt)
+    y = _mx().int8_linear_prequantized(a.to(dev), xs.to(dev), w.to(dev), ws.to(dev), b.to(dev), out_dtype=dt)
+    ref = eager_np.dequant_epilogue(eager_np.int8_matmul(a.numpy(), w.numpy()), xs.numpy(), ws.numpy(),
+                                    b.float().numpy(), out, bias_dtype="f32")
+    want = ref.astype(np.float32 if out == "fp32" else np.float16)
+    assert np.array_equal(y.cpu().numpy().view(want.dtype.str.replace("f", "u")), want.view(want.dtype.str.replace("f", "u")))
+
+
+@pytest.mark.parametrize("form", list(DEEP))
+def test_gated_residual_deep_ring(dev, form):
+    md, nd, tile_n = DEEP[form]
+    k = 528
+    _assert_deep(md, nd, k, tile_n)
+    print(f"gated residual deep-ring {form} m={md} n={nd} k={k}", flush=True)
+    x = activations(md, k, 260)
+    w, ws = int8_weight(nd, k, 261)
+    b = bf16_vec(nd, 262, 0.02)
+    gate = torch.randn(2, nd, generator=gen(263)).to(torch.bfloat16)
+    res = activations(md, nd, 264) * 3
+    segs = ((0, 600, 1), (600, md, 0))
     out = res.to(dev)
     _mx().int8_linear_gated_residual_(out, x.to(dev), w.to(dev), ws.to(dev), b.to(dev), gate.to(dev), segs)
     q, s = eager_np.quantize_int8_rowwise(bits(x))
     y = eager_np.dequant_epilogue(eager_np.int8_matmul(q, w.numpy()), s, ws.numpy(), bits(b), "bf16")
-    want = eager_np.gated_residual_bf16(bits(res), bf16_bits(y), bits(gate), eager_np.segment_row_map(MD, segs))
+    want = eager_np.gated_residual_bf16(bits(res), bf16_bits(y), bits(gate), eager_np.segment_row_map(md, segs))
     assert np.array_equal(bits(out), want)
 
 

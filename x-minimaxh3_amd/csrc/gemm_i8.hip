@@ -55,25 +55,32 @@ constexpr int kGemmThreads = 256;                       // 4 waves as 2 x 2
 // one workgroup per CU with a 144 KB ring that holds four stages in flight instead of two, for
 // problems whose 128-tiles all fit on the CUs at once (one workgroup per CU then leaves the
 // main loop waiting on operand latency, not on other workgroups).
-template <int kT, bool kDeep = false, bool kPP = false>
+// kTN = 96 (deep ring only): 128 x 96 tiles, the four waves stacked as 32-row strips of 1 x 3
+// blocks, for problems that fill more CUs that way (1024 x 3072: 256 tiles instead of 192 of 128).
+// A B chunk is then 12 KB in a 16 KB slot, and the ring carries 28 KB per stage instead of 32.
+template <int kT, bool kDeep = false, bool kPP = false, int kTN = kT>
 struct TileCfg {
   static_assert(kT == 128 || !kDeep, "the deep ring exists for 128-tiles only");
   static_assert(kT == 256 || !kPP, "the ping-pong schedule exists for 256-tiles only");
+  static_assert(kTN == kT || (kDeep && kTN == 96), "128 x 96 tiles run the deep ring only");
   static constexpr bool kPingPong = kPP;
   static constexpr int kWaves = kPP ? 8 : 4;                    // two per SIMD with kPP
   static constexpr int kThreads = kWaves * 64;
-  static constexpr int kBM = kT, kBN = kT;
-  static constexpr int kWaveM = kT / 2, kWaveN = kPP ? kT / 4 : kT / 2;
+  static constexpr int kBM = kT, kBN = kTN;
+  static constexpr int kWavesN = kPP ? 4 : (kTN == kT ? 2 : 1);  // waves across the tile's columns
+  static constexpr int kWaveM = kPP ? kT / 2 : kT / (kWaves / kWavesN), kWaveN = kTN / kWavesN;
   static constexpr int kBI = kWaveM / 32, kBJ = kWaveN / 32;
-  static constexpr int kSlotBytes = kT * kBK;                  // one operand chunk of a stage
-  static constexpr int kLoads = kSlotBytes / 1024 / kWaves;     // direct-to-LDS loads per wave per slot
+  static constexpr int kSlotBytes = kT * kBK;                  // one operand chunk of a stage (slot size)
+  static constexpr int kLoads = kSlotBytes / 1024 / kWaves;     // direct-to-LDS loads per wave per A slot
+  static constexpr int kLoadsB = kTN * kBK / 1024 / kWaves;     // ... per B slot
   static constexpr int kAhead = kDeep ? 4 : 2;                  // stages requested ahead of the MFMAs
   static constexpr int kSlots = 2 * kAhead + 1;                 // LDS ring of operand chunks
   static constexpr int kLds = kSlots * kSlotBytes;
   static constexpr int kEpiLds = kT == 256 ? 131072 : 4 * kSlotBytes;  // per-column factors
   static constexpr int kPerCu = kT == 256 || kDeep ? 1 : 2;     // workgroups per CU
   static_assert(kLds <= 160 * 1024, "the ring exceeds the CU's LDS");
-  static_assert(2 * kAhead * kLoads < 64, "loads in flight exceed the vmcnt counter");
+  static_assert(kAhead * (kLoads + kLoadsB) < 64, "loads in flight exceed the vmcnt counter");
+  static_assert(kWaveM % 32 == 0 && kWaveN % 32 == 0 && kTN % (8 * kWaves) == 0, "tile split");
 };
 // Tile-rows per group for problems of several rounds: with 2, the ~32 tiles an XCD runs at once are
 // 2 tile-rows x 16 tile-columns, so an activation panel is read from HBM once and then served
@@ -168,16 +175,21 @@ MXQ_DEVICE void xcd_range(int x, int num, int& start, int& count) {
 // (i % 8) ^ f(row) of that row, and eight lanes read one whole 128-byte line of the row-major
 // operand (half lines, as 64-byte steps would read, halve the L2 -> CU throughput). Wave w
 // loads blocks b = kL w .. kL w + kL - 1 of each A and B slot.
-template <int kL>
+template <int kL, int kLB = kL>
 struct Loader {
   const int8_t* a[kL];
-  const int8_t* b[kL];
-  int koff[2];   // logical chunk offset (bytes) of this lane's piece, for even and odd t
+  const int8_t* b[kLB];
+  int koff[2];   // logical chunk offset (bytes) of this lane's piece in 8-row block 2i and 2i + 1
   int wave;      // the wave's index, as a scalar: LDS destinations (M0) are then scalar arithmetic
 };
 
+// A load's 8-row block b = wave * (loads per slot) + t: the chunk swizzle of its rows depends on
+// b only through b & 1 (swz_f(8 b + l / 8) = 4 (b & 1) + l / 16).
 template <int kL>
-MXQ_DEVICE void make_loader(Loader<kL>& L, const GemmArgs& p, int64_t m0, int64_t n0) {
+MXQ_DEVICE int load_parity(int wave, int t) { return (wave * kL + t) & 1; }
+
+template <int kL, int kLB>
+MXQ_DEVICE void make_loader(Loader<kL, kLB>& L, const GemmArgs& p, int64_t m0, int64_t n0) {
   const int w = tid_x() >> 6, lane = tid_x() & 63;
   L.wave = __builtin_amdgcn_readfirstlane(w);
   // (the operand bases pass an empty asm statement too, so that their register copies are not
@@ -186,11 +198,15 @@ MXQ_DEVICE void make_loader(Loader<kL>& L, const GemmArgs& p, int64_t m0, int64_
   const int8_t* b = p.b;
   __asm__ volatile("" : "+s"(a), "+s"(b));
 #pragma unroll
+  for (int par = 0; par < 2; ++par) L.koff[par] = ((lane & 7) ^ swz_f(par * 8 + (lane >> 3))) * 16;
+#pragma unroll
   for (int t = 0; t < kL; ++t) {
     const int r = (w * kL + t) * 8 + (lane >> 3);
-    const int c = (lane & 7) ^ swz_f(r);  // depends on t only through t & 1
-    if (t < 2) L.koff[t] = c * 16;
-    L.a[t] = a + min(m0 + r, p.M - 1) * p.K + c * 16;
+    L.a[t] = a + min(m0 + r, p.M - 1) * p.K + ((lane & 7) ^ swz_f(r)) * 16;
+  }
+#pragma unroll
+  for (int t = 0; t < kLB; ++t) {
+    const int r = (w * kLB + t) * 8 + (lane >> 3);
     L.b[t] = b + min(n0 + r, p.N - 1) * p.K;
   }
 }
@@ -198,10 +214,12 @@ MXQ_DEVICE void make_loader(Loader<kL>& L, const GemmArgs& p, int64_t m0, int64_
 // Load t of this wave's share of an A (kB = false) or B slot. With kCheck a chunk past K reads
 // zeros (A) or any valid bytes (B: their products with A's zeros vanish); without it the caller
 // guarantees the whole stage lies below K.
-template <bool kB, bool kCheck, int kL>
-MXQ_DEVICE void issue_one(const Loader<kL>& L, char* slot, int64_t k0, int64_t K, int t) {
+template <bool kB, bool kCheck, int kL, int kLB>
+MXQ_DEVICE void issue_one(const Loader<kL, kLB>& L, char* slot, int64_t k0, int64_t K, int t) {
+  constexpr int kN = kB ? kLB : kL;
   const int w = L.wave;
-  const int koff = L.koff[t & 1];
+  // (a select, not an index: a run-time index would put the pair in scratch memory)
+  const int koff = load_parity<kN>(w, t) ? L.koff[1] : L.koff[0];
   const void* src;
   if constexpr (kCheck) {
     const bool kin = k0 + koff < K;
@@ -210,13 +228,13 @@ MXQ_DEVICE void issue_one(const Loader<kL>& L, char* slot, int64_t k0, int64_t K
   } else {
     src = kB ? (const void*)(L.b[t] + k0 + koff) : (const void*)(L.a[t] + k0);
   }
-  __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)(slot + (w * kL + t) * 1024), 16, 0, 0);
+  __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)(slot + (w * kN + t) * 1024), 16, 0, 0);
 }
 
-template <bool kB, int kL>
-MXQ_DEVICE void issue_slot(const Loader<kL>& L, char* slot, int64_t k0, int64_t K) {
+template <bool kB, int kL, int kLB>
+MXQ_DEVICE void issue_slot(const Loader<kL, kLB>& L, char* slot, int64_t k0, int64_t K) {
 #pragma unroll
-  for (int t = 0; t < kL; ++t) issue_one<kB, true>(L, slot, k0, K, t);
+  for (int t = 0; t < (kB ? kLB : kL); ++t) issue_one<kB, true>(L, slot, k0, K, t);
 }
 
 // Fragments of K-step ks (32 K-bytes) of a stage: A rows wrow + i*32 + l%32 and B rows
@@ -252,7 +270,7 @@ MXQ_DEVICE void mma_step(const v4i fa[C::kBI], const v4i fb[C::kBJ], v16i acc[C:
 // run, rather than after the last of them.
 template <class C, bool kB, int kFirst, int kCount, bool kCheck>
 MXQ_DEVICE void mma_step_dma(const v4i fa[C::kBI], const v4i fb[C::kBJ], v16i acc[C::kBI][C::kBJ],
-                             const Loader<C::kLoads>& L, char* slot, int64_t k0, int64_t K, bool on) {
+                             const Loader<C::kLoads, C::kLoadsB>& L, char* slot, int64_t k0, int64_t K, bool on) {
   static_assert(kCount <= C::kBI * C::kBJ, "more loads than MFMAs to spread them over");
 #pragma unroll
   for (int q = 0; q < C::kBI * C::kBJ; ++q) {
@@ -786,17 +804,20 @@ MXQ_DEVICE void gemm_epilogue(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][
     }
   }
 
-  // The blocks go by pairs of 32-column blocks (jp), the factors of a pair held in registers.
+  // The blocks go by pairs of 32-column blocks (jp), the factors of a pair held in registers; an
+  // odd last block (128 x 96 tiles: three blocks per wave) goes alone, with run stores.
   // GELU / SwiGLU: pre-activation bf16 pairs, kept until the table has landed.
+  static_assert(!kTable || kBJ % 2 == 0, "the table epilogues take pairs of blocks");
   uint32_t yp[kTable ? kBI : 1][kTable ? kBJ : 1][8];
-  static_for<kBJ / 2>([&](auto JP) {
+  static_for<(kBJ + 1) / 2>([&](auto JP) {
     constexpr int jp = decltype(JP)::value;
+    constexpr int kJJ = 2 * jp + 2 <= kBJ ? 2 : 1;  // blocks in this group
     float wsv[2][16], bsv[2][16];
     if constexpr (kEpi != kEpiI32) {
       // columns wcol + (2 jp + jj) * 32 + lh * 4 + q * 8 + {0..3}
       const uint32_t a_ws = lds_addr(s_ws + wcol + 2 * jp * 32 + lh * 4), a_b = a_ws + kBN * 4;
       v4i w4[2][4], b4[2][4];
-      static_for<2>([&](auto JJ) {
+      static_for<kJJ>([&](auto JJ) {
         static_for<4>([&](auto Q) {
           constexpr int kOff = decltype(JJ)::value * 128 + decltype(Q)::value * 32;
           w4[decltype(JJ)::value][decltype(Q)::value] = lds_read_b128<kOff>(a_ws);
@@ -806,7 +827,7 @@ MXQ_DEVICE void gemm_epilogue(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][
       wait_lgkm<0>();
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj)
+      for (int jj = 0; jj < kJJ; ++jj)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
@@ -823,7 +844,7 @@ MXQ_DEVICE void gemm_epilogue(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][
       uint32_t w[2][8];
       uint32_t w32[2][16];
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj)
+      for (int jj = 0; jj < kJJ; ++jj)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           if constexpr (kElem == 4)
@@ -837,30 +858,30 @@ MXQ_DEVICE void gemm_epilogue(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][
 #pragma unroll
           for (int r = 0; r < 8; ++r) yp[i][2 * jp + jj][r] = w[jj][r];
       } else if constexpr (kEpi == kEpiGatedRes) {
-        if (lines) {
+        if (lines && kJJ == 2) {
           gated_lines(p, sbuf, row0, col0, grow_rm[i], w);
         } else {
 #pragma unroll
-          for (int jj = 0; jj < 2; ++jj) gated_block_row(p, full, row0 + lr, grow[i], col0 + jj * 32 + lh * 4, w[jj]);
+          for (int jj = 0; jj < kJJ; ++jj) gated_block_row(p, full, row0 + lr, grow[i], col0 + jj * 32 + lh * 4, w[jj]);
         }
       } else if constexpr (kElem == 4) {
         if (lines) {
 #pragma unroll
-          for (int jj = 0; jj < 2; ++jj) {
+          for (int jj = 0; jj < kJJ; ++jj) {
             stage_block32(sbuf, w32[jj]);
             stage_store(p, sbuf, row0, (col0 + jj * 32) * 4, pitch);
           }
         } else {
 #pragma unroll
-          for (int jj = 0; jj < 2; ++jj) store_block_row<4>(p, full, row0 + lr, col0 + jj * 32 + lh * 4, w32[jj]);
+          for (int jj = 0; jj < kJJ; ++jj) store_block_row<4>(p, full, row0 + lr, col0 + jj * 32 + lh * 4, w32[jj]);
         }
       } else {
-        if (lines) {
+        if (lines && kJJ == 2) {
           stage_blocks16(sbuf, w);
           stage_store(p, sbuf, row0, col0 * 2, pitch);
         } else {
 #pragma unroll
-          for (int jj = 0; jj < 2; ++jj) store_block_row<2>(p, full, row0 + lr, col0 + jj * 32 + lh * 4, w[jj]);
+          for (int jj = 0; jj < kJJ; ++jj) store_block_row<2>(p, full, row0 + lr, col0 + jj * 32 + lh * 4, w[jj]);
         }
       }
     });
@@ -1125,15 +1146,17 @@ MXQ_DEVICE void four_wave_tile(const GemmArgs& p, char* lds) {
   constexpr int kBM = C::kBM, kBN = C::kBN, kWaveM = C::kWaveM, kWaveN = C::kWaveN;
   constexpr int kBI = C::kBI, kBJ = C::kBJ, kSlotBytes = C::kSlotBytes, kLoads = C::kLoads;
   constexpr int kSlots = C::kSlots, kAhead = C::kAhead;
+  constexpr int kStageLoads = C::kLoads + C::kLoadsB;  // loads per wave per stage (A and B chunks)
   const int pos = pick_tile(p, p.tiles_m * p.tiles_n, lds);
   if (pos < 0) return;
   int tm, tn;
   tile_walk(pos, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
   const int64_t m0 = (int64_t)tm * kBM, n0 = (int64_t)tn * kBN;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  // The wave's first output row and column in the tile: a 2 x 2 grid of quadrants.
-  const int wrow = (wave >> 1) * kWaveM;
-  const int wcol = (wave & 1) * kWaveN;
+  // The wave's first output row and column in the tile: a 2 x 2 grid of quadrants (128 x 96
+  // tiles: four 32-row strips).
+  const int wrow = (wave / C::kWavesN) * kWaveM;
+  const int wcol = (wave % C::kWavesN) * kWaveN;
 
   v16i acc[kBI][kBJ];
 #pragma unroll
@@ -1154,7 +1177,7 @@ MXQ_DEVICE void four_wave_tile(const GemmArgs& p, char* lds) {
     // slot). A chunk is thus requested D-1 to D stages before it is used, and no wave issues a
     // burst of loads while its matrix pipe sits idle.
     const int ktiles = (int)((p.K + kBK - 1) / kBK);
-    Loader<kLoads> ld;
+    Loader<kLoads, C::kLoadsB> ld;
     make_loader(ld, p, m0, n0);
     const int pre = min(ktiles, kAhead);  // stages requested before the loop
     for (int s = 0; s < pre; ++s) {
@@ -1164,7 +1187,7 @@ MXQ_DEVICE void four_wave_tile(const GemmArgs& p, char* lds) {
     // wait for stage 0: every load but those of stages 1 .. pre-1 has completed
     static_for<kAhead>([&](auto P) {
       constexpr int np = decltype(P)::value + 1;
-      if (pre == np) wait_vmcnt<2 * (np - 1) * kLoads>();
+      if (pre == np) wait_vmcnt<(np - 1) * kStageLoads>();
     });
     barrier_no_drain();
 
@@ -1205,13 +1228,13 @@ MXQ_DEVICE void four_wave_tile(const GemmArgs& p, char* lds) {
       // Stage kt+1 has landed when only the loads issued after B_kt+1 are outstanding: stages
       // kt+2 .. kt+D-1 and A_kt+D where they exist (2 (r - 1) chunks when only r < D stages remain).
       if (more2) {
-        wait_vm_lgkm0<(2 * kAhead - 3) * kLoads>();
+        wait_vm_lgkm0<(kAhead - 2) * kStageLoads + kLoads>();
       } else if constexpr (kAhead > 2) {
         const int r = ktiles - 1 - kt;
         if (r == 3) {
-          wait_vm_lgkm0<4 * kLoads>();
+          wait_vm_lgkm0<2 * kStageLoads>();
         } else if (r == 2) {
-          wait_vm_lgkm0<2 * kLoads>();
+          wait_vm_lgkm0<kStageLoads>();
         } else {
           wait_all();
         }
@@ -1224,7 +1247,7 @@ MXQ_DEVICE void four_wave_tile(const GemmArgs& p, char* lds) {
         load_frags<C>(lane, lds_addr + (uint32_t)(na * kSlotBytes), lds_addr + (uint32_t)(nb * kSlotBytes), wrow, wcol, 0, f0a, f0b);
       }
       __builtin_amdgcn_sched_barrier(0);
-      mma_step_dma<C, true, 0, kLoads, !kSteady>(f1a, f1b, acc, ld, lds + sa * kSlotBytes, k2, p.K, more2 && more1);
+      mma_step_dma<C, true, 0, C::kLoadsB, !kSteady>(f1a, f1b, acc, ld, lds + sa * kSlotBytes, k2, p.K, more2 && more1);
       __builtin_amdgcn_sched_barrier(0);
       sa = na;
     };
@@ -1249,9 +1272,9 @@ MXQ_DEVICE void four_wave_tile(const GemmArgs& p, char* lds) {
   gemm_epilogue<C, kEpi, kOut, 0, C::kEpiLds>(p, lds, acc, m0, n0, wrow, wcol, f, [] {});
 }
 
-template <int kEpi, int kOut, int kT, bool kDeep, bool kPP>
-__global__ __launch_bounds__((TileCfg<kT, kDeep, kPP>::kThreads), (TileCfg<kT, kDeep, kPP>::kPerCu)) void gemm_i8_kernel(GemmArgs p) {
-  typedef TileCfg<kT, kDeep, kPP> C;
+template <int kEpi, int kOut, int kT, bool kDeep, bool kPP, int kTN = kT>
+__global__ __launch_bounds__((TileCfg<kT, kDeep, kPP, kTN>::kThreads), (TileCfg<kT, kDeep, kPP, kTN>::kPerCu)) void gemm_i8_kernel(GemmArgs p) {
+  typedef TileCfg<kT, kDeep, kPP, kTN> C;
   static_assert(kT == 256 || (kEpi != kEpiGelu && kEpi != kEpiSwiGLU), "table epilogues need the 160 KB ring");
   __shared__ __attribute__((aligned(16))) char lds[C::kLds];
   if constexpr (kPP)
@@ -1269,7 +1292,8 @@ static_assert(MXQ_GEMM_WORKSPACE_BYTES >= kTileQueueBytes, "workspace holds the 
 
 // Launch plan of one GEMM: tile size, tile queue and grid.
 struct GemmPlan {
-  int tile;  // 256 or 128
+  int tile;  // 256 or 128 (rows of a tile)
+  int tile_n;  // columns of a tile: the tile size, or 96 (128 x 96 deep-ring tiles)
   bool deep;  // 128-tiles with the deep ring: every tile on its own CU at once
   int tiles_m, tiles_n;
   int pool, wg_per_xcd, n_claim;
@@ -1291,10 +1315,14 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, bool table, int64_t workspace_by
   const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
   const bool prefer128 = big_tiles < 256 || ((tiles128 + 511) / 512) * 11 < ((big_tiles + 255) / 256) * 20;
   g.tile = !table && prefer128 ? 128 : 256;
+  g.deep = g.tile == 128 && tiles128 <= 256;
+  // Deep-ring problems whose 128 x 96 tiles still fit on the CUs at once take those: more CUs,
+  // each with three quarters of the work (1024 x 3072: 256 tiles instead of 192).
+  const int64_t tiles96 = ((M + 127) / 128) * ((N + 95) / 96);
+  g.tile_n = g.deep && tiles96 > tiles128 && tiles96 <= std::min(mxq_cu_count(), 256) ? 96 : g.tile;
   g.tiles_m = (int)std::min<int64_t>((M + g.tile - 1) / g.tile, INT32_MAX);
-  g.tiles_n = (int)std::min<int64_t>((N + g.tile - 1) / g.tile, INT32_MAX);
+  g.tiles_n = (int)std::min<int64_t>((N + g.tile_n - 1) / g.tile_n, INT32_MAX);
   const int64_t tiles = (int64_t)g.tiles_m * g.tiles_n;
-  g.deep = g.tile == 128 && tiles <= 256;
   g.grid = tiles;
   // Deep-ring problems run every tile at once, one per CU: each XCD fetches the A and B panels
   // of its range once, so the range is made as square as the groups allow (1024 x 3072, 24
@@ -1355,7 +1383,9 @@ static int launch_gemm(const GemmArgs& args0, void* workspace, int64_t workspace
   const unsigned grid = (unsigned)g.grid;
   if constexpr (kEpi != kEpiGelu && kEpi != kEpiSwiGLU) {
     if (g.tile == 128) {
-      if (g.deep)
+      if (g.deep && g.tile_n == 96)
+        gemm_i8_kernel<kEpi, kOut, 128, true, false, 96><<<grid, kGemmThreads, 0, stream>>>(args);
+      else if (g.deep)
         gemm_i8_kernel<kEpi, kOut, 128, true, false><<<grid, kGemmThreads, 0, stream>>>(args);
       else
         gemm_i8_kernel<kEpi, kOut, 128, false, false><<<grid, kGemmThreads, 0, stream>>>(args);
@@ -1405,6 +1435,7 @@ extern "C" int mxq_int8_gemm_plan(int64_t M, int64_t N, int64_t K, int table_epi
   plan[5] = g.tile == 256 ? TileCfg<256>::kAhead : g.deep ? TileCfg<128, true>::kAhead : TileCfg<128>::kAhead;
   plan[6] = g.group_m;
   plan[7] = g.persistent;
+  plan[8] = g.tile_n;
   return MXQ_OK;
 }
 

@@ -19,7 +19,7 @@ MXQ_ERR_UNSUPPORTED = -2
 MXQ_ERR_HIP = -3
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_E4M3 = 0, 1, 2, 5
-ABI_VERSION = 3
+ABI_VERSION = 4
 # MXQ_GEMM_WORKSPACE_BYTES: the INT8 GEMMs' tile-queue workspace (counters)
 GEMM_WORKSPACE_BYTES = 4096
 ACT_NONE, ACT_GELU_TANH, ACT_SWIGLU = 0, 1, 2
@@ -102,13 +102,13 @@ def load() -> ctypes.CDLL:
 
 
 def gemm_plan(m: int, n: int, k: int, table: bool = False, workspace_bytes: int = GEMM_WORKSPACE_BYTES) -> dict:
-    """The INT8 GEMM launch plan (mxq_int8_gemm_plan): tile edge, workgroups, tiles, tiles per XCD
+    """The INT8 GEMM launch plan (mxq_int8_gemm_plan): tile rows, workgroups, tiles, tiles per XCD
     claimed at run time (0: static order), workgroups per XCD, operand stages requested ahead,
-    tile-rows per group of the tile order, and whether the workgroups loop over tiles."""
-    out = (ctypes.c_int64 * 8)()
+    tile-rows per group of the tile order, whether the workgroups loop over tiles, tile columns."""
+    out = (ctypes.c_int64 * 9)()
     call("mxq_int8_gemm_plan", m, n, k, int(table), workspace_bytes, out)
     return {"tile": out[0], "grid": out[1], "tiles": out[2], "pool": out[3], "wg_per_xcd": out[4],
-            "ahead": out[5], "group_m": out[6], "persistent": bool(out[7])}
+            "ahead": out[5], "group_m": out[6], "persistent": bool(out[7]), "tile_n": out[8]}
 
 
 def call(name: str, *args) -> None:
