@@ -365,7 +365,11 @@ int mxq_w4a8_codebook_gemm(const int8_t* xq, const int8_t* qdata, const void* s_
  * hipMalloc). Same arguments and results (bit for bit) as mxq_w4a8_codebook_gemm, less
  * `workspace` and the GEMM workspace (a second static array, 4 KiB, holds the tile-queue
  * counters); min(chunk_cols, N) * K must not exceed 32 MiB (MXQ_ERR_INVALID otherwise).
- * Calls share the GPU's arrays: two calls that overlap on one GPU (different streams) race.
+ * Calls share the GPU's arrays. Each call makes its stream wait for the previous call on the same
+ * GPU (an event the library creates with its first call per device and records after every
+ * call), so calls on different streams do not overlap. Under graph capture the wait and the
+ * record are left out: a replayed graph that runs beside another call on the same GPU races
+ * with it on the arrays.
  */
 int mxq_w4a8_codebook_gemm_noalloc(const int8_t* xq, const int8_t* qdata, const void* s_rel,
                                    int s_rel_dtype, const float* codebook, const float* s_channel,

@@ -1,8 +1,9 @@
 """GPU parity of the allocation-free W4A8 entry point (mxq_w4a8_codebook_gemm_noalloc) against
 the entry point it varies (mxq_w4a8_codebook_gemm with a caller workspace), called through the
 C ABI: two calls in a row, the second smaller, then a chunk too large for the static workspace;
-and two calls whose chunk GEMMs are large enough to claim tiles at run time (the workspace entry
-with a per-stream tile-queue workspace, the allocation-free one with its static counters).
+two calls whose chunk GEMMs are large enough to claim tiles at run time (the workspace entry
+with a per-stream tile-queue workspace, the allocation-free one with its static counters); and
+two calls on two streams with no host wait between them (ordered by the entry point's event).
 
 Bar: outputs bit-identical to the workspace entry point's on every call.
 """
@@ -15,16 +16,11 @@ from _util import activations, bf16_vec, gen, packed_int4
 pytestmark = pytest.mark.gpu
 
 
-def _call_pair(dev, m, n, k, g, e4m3, codebook, bias, chunk, seed, queued=False):
+def _problem(dev, m, n, k, g, e4m3, codebook, bias, seed):
+    """Inputs of one W4A8 codebook GEMM as the C entry points take them."""
     import mx_qlinear
     from mx_qlinear import _lib
-    from mx_qlinear.ops import _gemm_ws, _p, _stream
 
-    if queued:  # each chunk GEMM claims tiles at run time
-        plan = _lib.gemm_plan(m, min(chunk, n), k)
-        assert plan["pool"] > 0, plan
-
-    print(f"no-alloc w4a8 m={m} n={n} k={k} g={g} e4m3={e4m3} codebook={codebook} chunk={chunk}", flush=True)
     x = activations(m, k, seed).to(dev)
     xq, xs = mx_qlinear.quantize_int8_rowwise(x)
     qd = packed_int4(n, k, seed + 1).to(dev)
@@ -36,15 +32,46 @@ def _call_pair(dev, m, n, k, g, e4m3, codebook, bias, chunk, seed, queued=False)
     cb = (torch.randn(16, generator=gen(seed + 3)) * 4).to(dev) if codebook else None
     sch = (torch.rand(n, generator=gen(seed + 4)) * 0.5 + 0.5).to(dev) * (0.06 / 127)
     b = bf16_vec(n, seed + 5, 0.01).to(dev) if bias else None
-    want = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=dev)
-    got = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=dev)
-    work = torch.empty((min(chunk, n), k), dtype=torch.int8, device=dev)
-    st = _stream(dev)
+    return dict(m=m, n=n, k=k, g=g, xq=xq, xs=xs, qd=qd, sr=sr, code=code, cb=cb, sch=sch, b=b)
+
+
+def _workspace_entry(dev, pb, chunk, queued, st):
+    from mx_qlinear import _lib
+    from mx_qlinear.ops import _gemm_ws, _p
+
+    want = torch.full((pb["m"], pb["n"]), float("nan"), dtype=torch.bfloat16, device=dev)
+    work = torch.empty((min(chunk, pb["n"]), pb["k"]), dtype=torch.int8, device=dev)
     gws = _gemm_ws(dev) if queued else (None, 0)
-    _lib.call("mxq_w4a8_codebook_gemm", _p(xq), _p(qd), _p(sr), code, _p(cb), _p(sch), _p(xs), _p(b), _p(work),
-              _p(want), m, n, k, g, chunk, _lib.DTYPE_BF16, *gws, st)
-    _lib.call("mxq_w4a8_codebook_gemm_noalloc", _p(xq), _p(qd), _p(sr), code, _p(cb), _p(sch), _p(xs), _p(b),
-              _p(got), m, n, k, g, chunk, _lib.DTYPE_BF16, st)
+    _lib.call("mxq_w4a8_codebook_gemm", _p(pb["xq"]), _p(pb["qd"]), _p(pb["sr"]), pb["code"], _p(pb["cb"]),
+              _p(pb["sch"]), _p(pb["xs"]), _p(pb["b"]), _p(work), _p(want), pb["m"], pb["n"], pb["k"], pb["g"], chunk,
+              _lib.DTYPE_BF16, *gws, st)
+    return want
+
+
+def _noalloc_entry(dev, pb, chunk, st):
+    from mx_qlinear import _lib
+    from mx_qlinear.ops import _p
+
+    got = torch.full((pb["m"], pb["n"]), float("nan"), dtype=torch.bfloat16, device=dev)
+    _lib.call("mxq_w4a8_codebook_gemm_noalloc", _p(pb["xq"]), _p(pb["qd"]), _p(pb["sr"]), pb["code"], _p(pb["cb"]),
+              _p(pb["sch"]), _p(pb["xs"]), _p(pb["b"]), _p(got), pb["m"], pb["n"], pb["k"], pb["g"], chunk,
+              _lib.DTYPE_BF16, st)
+    return got
+
+
+def _call_pair(dev, m, n, k, g, e4m3, codebook, bias, chunk, seed, queued=False):
+    from mx_qlinear import _lib
+    from mx_qlinear.ops import _stream
+
+    if queued:  # each chunk GEMM claims tiles at run time
+        plan = _lib.gemm_plan(m, min(chunk, n), k)
+        assert plan["pool"] > 0, plan
+
+    print(f"no-alloc w4a8 m={m} n={n} k={k} g={g} e4m3={e4m3} codebook={codebook} chunk={chunk}", flush=True)
+    pb = _problem(dev, m, n, k, g, e4m3, codebook, bias, seed)
+    st = _stream(dev)
+    want = _workspace_entry(dev, pb, chunk, queued, st)
+    got = _noalloc_entry(dev, pb, chunk, st)
     torch.cuda.synchronize()
     assert not bool(torch.isnan(want).any())
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
@@ -80,3 +107,29 @@ def test_noalloc_rejects_a_chunk_beyond_the_static_workspace(dev):
     with pytest.raises(ValueError, match="static workspace"):
         _lib.call("mxq_w4a8_codebook_gemm_noalloc", _p(xq), _p(qd), _p(sr), _lib.DTYPE_F32, None, _p(sch), _p(xs),
                   None, _p(out), m, n, k, g, 4097, _lib.DTYPE_BF16, _stream(dev))
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(dev):
+    """Two calls on two streams issued back to back with no host wait between them: the second
+    call's stream waits for the first call (the entry point's order event), so neither call's
+    decode overwrites the static array while the other's GEMMs read it. Both outputs equal the
+    workspace entry's, computed beforehand on the current stream."""
+    from mx_qlinear.ops import _stream
+
+    print("no-alloc w4a8 two streams", flush=True)
+    a = _problem(dev, 2048, 8192, 1024, 16, True, True, True, 7201)
+    b = _problem(dev, 1024, 6000, 1024, 16, False, True, False, 7202)
+    want_a = _workspace_entry(dev, a, 4096, False, _stream(dev))
+    want_b = _workspace_entry(dev, b, 3000, False, _stream(dev))
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(dev), torch.cuda.Stream(dev)
+    got_a = torch.empty(0, device=dev)
+    got_b = torch.empty(0, device=dev)
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            got_a = _noalloc_entry(dev, a, 4096, s1.cuda_stream)
+        with torch.cuda.stream(s2):
+            got_b = _noalloc_entry(dev, b, 3000, s2.cuda_stream)
+        torch.cuda.synchronize()
+        assert torch.equal(got_a.view(torch.int16), want_a.view(torch.int16))
+        assert torch.equal(got_b.view(torch.int16), want_b.view(torch.int16))

@@ -358,8 +358,11 @@ extern "C" int mxq_w4a8_codebook_gemm(const int8_t* xq, const int8_t* qdata, con
 // never passes `scratch` itself to a kernel (in host code the name is a host-side stand-in, not a
 // device address): the device address is looked up once per device with hipGetSymbolAddress and
 // kept in g_scratch_ptr. Every call on one GPU reuses that GPU's array; the decode overwrites
-// every byte a GEMM reads, so nothing needs clearing between calls, and two calls that overlap on
-// one GPU (two streams) race on it. The chunk GEMMs' tile-queue counters are a second, small
+// every byte a GEMM reads, so nothing needs clearing between calls. Every call first makes its
+// stream wait for the previous call on the same GPU (an event recorded after every call, created
+// with the address lookup), so calls from two streams do not overlap. Under graph capture neither the wait nor the record is made (the
+// graph's own edges order its calls), so a replayed graph that runs beside another call on the
+// same GPU races with it on the array. The chunk GEMMs' tile-queue counters are a second, small
 // array of the same kind (zero when the library loads; every GEMM leaves them zero).
 constexpr int64_t kNoAllocScratchBytes = int64_t(32) << 20;
 static __device__ __attribute__((aligned(256))) int8_t scratch[kNoAllocScratchBytes];
@@ -370,17 +373,17 @@ constexpr int kMaxScratchDevices = 64;
 std::mutex g_scratch_mutex;
 int8_t* g_scratch_ptr[kMaxScratchDevices] = {};
 void* g_queue_ptr[kMaxScratchDevices] = {};
+hipEvent_t g_last_call[kMaxScratchDevices] = {};  // recorded after each call on the device
 
-// Device addresses of the current device's scratch and queue arrays (looked up on the first call
-// per device).
-int current_device_scratch(int8_t** ptr, void** queue) {
+// Device addresses of the current device's scratch and queue arrays and its call-order event
+// (looked up and created on the first call per device). The caller holds g_scratch_mutex.
+int current_device_scratch(int* device, int8_t** ptr, void** queue) {
   int dev = -1;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return mxq_set_error(MXQ_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(err));
   if (dev < 0 || dev >= kMaxScratchDevices)
     return mxq_set_error(MXQ_ERR_UNSUPPORTED, "device ordinal %d outside the %d the library tracks", dev,
                          kMaxScratchDevices);
-  std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (g_scratch_ptr[dev] == nullptr) {
     void* p = nullptr;
     err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
@@ -392,9 +395,15 @@ int current_device_scratch(int8_t** ptr, void** queue) {
     if (err != hipSuccess || qp == nullptr)
       return mxq_set_error(MXQ_ERR_HIP, "hipGetSymbolAddress(queue_scratch) failed on device %d: %s", dev,
                            hipGetErrorString(err));
+    hipEvent_t ev = nullptr;
+    err = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (err != hipSuccess)
+      return mxq_set_error(MXQ_ERR_HIP, "hipEventCreateWithFlags failed on device %d: %s", dev, hipGetErrorString(err));
     g_scratch_ptr[dev] = static_cast<int8_t*>(p);
     g_queue_ptr[dev] = qp;
+    g_last_call[dev] = ev;
   }
+  *device = dev;
   *ptr = g_scratch_ptr[dev];
   *queue = g_queue_ptr[dev];
   return MXQ_OK;
@@ -417,10 +426,29 @@ extern "C" int mxq_w4a8_codebook_gemm_noalloc(const int8_t* xq, const int8_t* qd
                          (long long)(kNoAllocScratchBytes / K));
   int8_t* ws = nullptr;
   void* queue = nullptr;
-  rc = current_device_scratch(&ws, &queue);
+  int dev = -1;
+  hipStream_t st = (hipStream_t)stream;
+  // Host threads take turns: the order wait, the launches and the order record happen under the
+  // lock, so no other call's launches come between them.
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  rc = current_device_scratch(&dev, &ws, &queue);
   if (rc) return rc;
-  return codebook_gemm_chunks(xq, qdata, s_rel, s_rel_dtype, codebook, s_channel, xs, bias, ws, out, M, N, K,
-                              group_size, chunk_cols, out_dtype, queue, MXQ_GEMM_WORKSPACE_BYTES, stream);
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  hipError_t err = hipStreamIsCapturing(st, &capture);
+  if (err != hipSuccess) return mxq_set_error(MXQ_ERR_HIP, "hipStreamIsCapturing failed: %s", hipGetErrorString(err));
+  const bool order = capture == hipStreamCaptureStatusNone;
+  if (order) {  // (also on the same stream, where it orders nothing new: a stream handle can be reused)
+    err = hipStreamWaitEvent(st, g_last_call[dev], 0);
+    if (err != hipSuccess) return mxq_set_error(MXQ_ERR_HIP, "hipStreamWaitEvent failed: %s", hipGetErrorString(err));
+  }
+  rc = codebook_gemm_chunks(xq, qdata, s_rel, s_rel_dtype, codebook, s_channel, xs, bias, ws, out, M, N, K,
+                            group_size, chunk_cols, out_dtype, queue, MXQ_GEMM_WORKSPACE_BYTES, stream);
+  if (rc) return rc;
+  if (order) {
+    err = hipEventRecord(g_last_call[dev], st);
+    if (err != hipSuccess) return mxq_set_error(MXQ_ERR_HIP, "hipEventRecord failed: %s", hipGetErrorString(err));
+  }
+  return MXQ_OK;
 }
 
 static int check_grouped(const int8_t* a, const float* xs, const int8_t* qdata, const uint16_t* group_scale,
