@@ -90,11 +90,16 @@ def test_gemm_i32_strided_output(dev):
     assert np.all(c[:, n:] == 7)
 
 
+@pytest.mark.parametrize("m,n,tile_n", [(260, 520, 96), (1000, 192, 128)])  # both deep-ring tile forms
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("with_bias", [False, True])
 @pytest.mark.parametrize("per_channel", [False, True])
-def test_dequant_epilogue_matches_oracle(dev, out_dtype, with_bias, per_channel):
-    m, n, k = 260, 520, 1024
+def test_dequant_epilogue_matches_oracle(dev, out_dtype, with_bias, per_channel, m, n, tile_n):
+    from mx_qlinear import _lib
+
+    k = 1024
+    assert _lib.gemm_plan(m, n, k)["tile_n"] == tile_n
+    print(f"dequant epilogue m={m} n={n} out={out_dtype} bias={with_bias} per_channel={per_channel}", flush=True)
     x = activations(m, k, 41)
     w, ws = int8_weight(n, k, 42)
     if not per_channel:
