@@ -698,6 +698,14 @@ MXQ_DEVICE void pp_first_loads(const GemmArgs& p, char* lds, const Loader<C::kLo
   pp_issue<false, true>(ld, lds + 2 * C::kSlotBytes, kBK, p.K, p.K > kBK);
 }
 
+// One of those three chunks: A_0 (part 0), B_0 (1), A_1 (2).
+template <class C>
+MXQ_DEVICE void pp_first_load_part(const GemmArgs& p, char* lds, const Loader<C::kLoads>& ld, int part) {
+  if (part == 0) pp_issue<false, true>(ld, lds, 0, p.K, true);
+  if (part == 1) pp_issue<true, true>(ld, lds + C::kSlotBytes, 0, p.K, true);
+  if (part == 2) pp_issue<false, true>(ld, lds + 2 * C::kSlotBytes, kBK, p.K, p.K > kBK);
+}
+
 // The dequant epilogues' per-tile factors, read from global memory ahead of the epilogue: the
 // weight scale and the bias (raw, in the output type) of column n0 + t for thread t, and the
 // per-token scales of the lane's rows. Every read is unconditional (a missing bias reads the
@@ -726,9 +734,13 @@ MXQ_DEVICE void load_epi_factors(const GemmArgs& p, int64_t m0, int64_t n0, int 
 // wrow + i*32 + l%32 and the four column runs j*32 + q*8 + (l/32)*4 + {0..3}, q = 0..3). The LDS
 // is free on entry (every wave is done with the operand ring): the per-column factors go to
 // C::kEpiLds, the output staging buffers to kStageBase (table epilogues: behind the factors).
-// `pre` runs once the factor reads are issued and before anything waits for them (the
-// ping-pong kernel issues the next tile's first operand loads there, into LDS the epilogue does
-// not touch; every LDS access below is inline assembly, so none of them waits for those loads).
+// `pre(part)`, part = 0, 1, 2 (or -1: all), issues work that must not wait for anything the epilogue does: the
+// ping-pong kernel issues the next tile's first three operand chunks there, into LDS the epilogue
+// does not touch (every LDS access below is inline assembly, so none of them waits for those
+// loads). The parts come one before each of the first three block rows of the dequant, so that
+// a wave held up issuing loads into a full memory pipeline leaves its SIMD to the other wave's
+// dequant work; the gated residual epilogue, whose residual reads would wait for the loads,
+// issues all three up front.
 template <class C, int kEpi, int kOut, int kStageBase, int kFactorBase, class Pre>
 MXQ_DEVICE void gemm_epilogue(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][C::kBJ], int64_t m0, int64_t n0,
                               int wrow, int wcol, const EpiFactors<C::kBI, kOut>& f, Pre&& pre) {
@@ -748,7 +760,6 @@ MXQ_DEVICE void gemm_epilogue(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][
   const bool has_b = p.bias != nullptr;
   float xsv[kBI] = {};
   if constexpr (kEpi == kEpiI32) {
-    pre();
   } else {
     const float bl = has_b ? OutT<kOut>::load(&f.bias_raw) : -0.0f;
     if (t < kBN) {
@@ -772,7 +783,7 @@ MXQ_DEVICE void gemm_epilogue(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][
       for (int q = wave; q < 128; q += C::kWaves)
         __builtin_amdgcn_global_load_lds((gptr_t)(src + q * 1024), (lptr_t)(lds + q * 1024), 16, 0, 0);
     }
-    pre();
+    if constexpr (kEpi == kEpiGatedRes) pre(-1);  // all three parts
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt left open (max)
     barrier_no_drain();
@@ -838,6 +849,11 @@ MXQ_DEVICE void gemm_epilogue(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][
     }
     static_for<kBI>([&](auto I) {
       constexpr int i = decltype(I)::value;
+      if constexpr (kEpi != kEpiGatedRes && jp == 0 && i < 3) {
+        __builtin_amdgcn_sched_barrier(0);
+        pre(i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       constexpr int kWords = kElem == 4 ? 4 : 2;
       const int64_t row0 = m0 + wrow + i * 32;  // the block row's first row
       const int64_t col0 = n0 + wcol + jp * 64;  // the pair's first column
@@ -1123,15 +1139,21 @@ MXQ_DEVICE void pp_tiles(const GemmArgs& p, char* lds) {
     __builtin_amdgcn_sched_barrier(0);
     const int next = __builtin_amdgcn_readfirstlane((int)next_read);
     int64_t nm0 = 0, nn0 = 0;
-    gemm_epilogue<C, kEpi, kOut, kStageBase, kFactorBase>(p, lds, acc, m0, n0, wrow, wcol, f, [&] {
+    gemm_epilogue<C, kEpi, kOut, kStageBase, kFactorBase>(p, lds, acc, m0, n0, wrow, wcol, f, [&](int part) {
       if (next >= 0) {
-        int ntm, ntn;
-        tile_walk(next, p.tiles_m, p.tiles_n, p.group_m, ntm, ntn);
-        nm0 = (int64_t)ntm * C::kBM;
-        nn0 = (int64_t)ntn * C::kBN;
+        if (part <= 0) {  // the first call
+          int ntm, ntn;
+          tile_walk(next, p.tiles_m, p.tiles_n, p.group_m, ntm, ntn);
+          nm0 = (int64_t)ntm * C::kBM;
+          nn0 = (int64_t)ntn * C::kBN;
+        }
+        // (a loader formed per part: one kept live through the epilogue would take registers)
         Loader<C::kLoads> next_ld;
         make_loader(next_ld, p, nm0, nn0);
-        pp_first_loads<C>(p, lds, next_ld);
+        if (part < 0)
+          pp_first_loads<C>(p, lds, next_ld);
+        else
+          pp_first_load_part<C>(p, lds, next_ld, part);
       }
     });
     if (next < 0) break;
@@ -1269,7 +1291,7 @@ MXQ_DEVICE void four_wave_tile(const GemmArgs& p, char* lds) {
 
   EpiFactors<kBI, kOut> f;
   load_epi_factors<C, kEpi, kOut>(p, m0, n0, wrow, f);
-  gemm_epilogue<C, kEpi, kOut, 0, C::kEpiLds>(p, lds, acc, m0, n0, wrow, wcol, f, [] {});
+  gemm_epilogue<C, kEpi, kOut, 0, C::kEpiLds>(p, lds, acc, m0, n0, wrow, wcol, f, [](int) {});
 }
 
 template <int kEpi, int kOut, int kT, bool kDeep, bool kPP, int kTN = kT>
