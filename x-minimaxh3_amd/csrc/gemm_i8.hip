@@ -89,7 +89,9 @@ struct TileCfg {
 // 32 on the FFN and QKV shapes at 720p, 2 was fastest (fc1 -2.8 %, fc2 -3.2 %, QKV -2 % against
 // 8). The ping-pong kernel (a third more LDS traffic per MFMA, so a lower clock under the board's
 // power limit) does better with the fewer L2 fills of 4-row groups (QKV -1 to -2 %, FFN -0.3 %
-// against 2; 1, 6 and 8 slower). Problems of one round choose their own (plan_gemm).
+// against 2; 1, 6 and 8 slower), also as looping workgroups (against 4: 3 the same on the FFN
+// chain and 0.4 % slower on QKV, 5 +0.7 %, 6 +1.3 %, 8 +3 %). Problems of one round choose their
+// own (plan_gemm).
 constexpr int kGroupM = 2, kGroupMPingPong = 4;
 
 enum { kEpiI32 = 0, kEpiDequant = 1, kEpiGelu = 2, kEpiGatedRes = 3, kEpiSwiGLU = 4 };
