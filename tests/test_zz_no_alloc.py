@@ -3,7 +3,8 @@ the entry point it varies (mxq_w4a8_codebook_gemm with a caller workspace), call
 C ABI: two calls in a row, the second smaller, then a chunk too large for the static workspace;
 two calls whose chunk GEMMs are large enough to claim tiles at run time (the workspace entry
 with a per-stream tile-queue workspace, the allocation-free one with its static counters); and
-two calls on two streams with no host wait between them (ordered by the entry point's event).
+two calls on two streams with no host wait between them (ordered by the entry point's event);
+and a call captured in a HIP graph, replayed between eager calls of another problem.
 
 Bar: outputs bit-identical to the workspace entry point's on every call.
 """
@@ -133,3 +134,35 @@ def test_noalloc_calls_on_two_streams_are_ordered(dev):
         torch.cuda.synchronize()
         assert torch.equal(got_a.view(torch.int16), want_a.view(torch.int16))
         assert torch.equal(got_b.view(torch.int16), want_b.view(torch.int16))
+
+
+def test_noalloc_call_replays_in_a_graph(dev):
+    """Captured in a HIP graph (where the entry point makes no order wait or record), the call
+    replays to the workspace entry's result; between replays an eager call of another problem
+    overwrites the static array, and the next replay decodes its own chunks again."""
+    from mx_qlinear.ops import _stream
+
+    print("no-alloc w4a8 graph replay", flush=True)
+    a = _problem(dev, 1024, 6000, 1024, 16, True, True, True, 7301)
+    other = _problem(dev, 512, 8192, 1024, 16, False, False, True, 7302)
+    want = _workspace_entry(dev, a, 4096, False, _stream(dev))
+    want_other = _workspace_entry(dev, other, 4096, False, _stream(dev))
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):  # the first call per device looks up the arrays outside the capture
+        _noalloc_entry(dev, a, 4096, side.cuda_stream)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = _noalloc_entry(dev, a, 4096, _stream(dev))
+    for r in range(3):
+        eager = _noalloc_entry(dev, other, 4096, _stream(dev))  # overwrites the static array
+        torch.cuda.synchronize()
+        assert torch.equal(eager.view(torch.int16), want_other.view(torch.int16))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"replay {r} differs"
+    del graph
+
