@@ -20,7 +20,8 @@
 //    the operand loads interleaved one per MFMA.
 // Problems with fewer 256-tiles than CUs run the four-wave code on 128 x 128 tiles: two
 // workgroups per CU, or, when all the 128-tiles fit on the CUs at once, one per CU with a
-// nine-slot ring four stages deep.
+// nine-slot ring four stages deep -- as 128 x 96 tiles (four 32-row wave strips) when those
+// still fit and are more numerous, so that more CUs share the work.
 //
 // Epilogue: the MFMAs run with the weights as first operand, so each lane's accumulators are
 // one output row in four runs of four consecutive columns. Every output type is converted in
