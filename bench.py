@@ -461,7 +461,8 @@ def _clip_segments(segments, rows):
 
 
 class _H3Modulation:
-    """RMSNorm weight, adaLN scale/shift/gate tables [3, D] and the segment row map."""
+    """RMSNorm weight, adaLN scale/shift/gate tables [3, D], the segment row map and the
+    modulation workspace of the rms_adaln launches."""
 
     def __init__(self, dev, m, d, seed):
         self.norm_w = (1 + 0.1 * torch.randn(d, generator=_gen(dev, seed), device=dev)).to(torch.bfloat16)
@@ -471,6 +472,8 @@ class _H3Modulation:
         self.segments = h3_segments(m)
         self.rows = mx_qlinear.segment_row_map(m, self.segments, dev)
         self.eps = 1e-6
+        # room for bf16(1 + scale) of the three modulation rows, formed once per rms_adaln call
+        self.ws = torch.empty(3 * d * 2, dtype=torch.uint8, device=dev)
 
 
 class H3MlpWorkload:
@@ -501,7 +504,8 @@ class H3MlpWorkload:
         m, d, f, mod = self.m, self.d, self.inner, self.mod
         with t("rms_adaln_quant"):
             _lib.call("mxq_rms_adaln_quantize_int8", _p(self.res), _p(mod.norm_w), _p(mod.scale), _p(mod.shift), d, 3,
-                      _p(mod.rows), mod.eps, None, _p(self.q1), _p(self.xs1), m, d, 256, st)
+                      _p(mod.rows), mod.eps, None, _p(self.q1), _p(self.xs1), m, d, 256,
+                      _p(mod.ws), mod.ws.numel(), st)
         with t("fc1_swiglu_gemm"):
             _lib.call("mxq_int8_gemm_dequant_swiglu", _p(self.q1), _p(self.fc1.qweight), _p(self.xs1),
                       _p(self.fc1.scale), 2 * f, _p(self.fc1.bias), _p(self.h), m, 2 * f, d, f, *_gemm_ws(self.dev), st)
@@ -575,7 +579,8 @@ class H3QkvWorkload:
         m, d, n, mod = self.m, self.d, self.n, self.mod
         with t("rms_adaln_quant"):
             _lib.call("mxq_rms_adaln_quantize_int8", _p(self.x), _p(mod.norm_w), _p(mod.scale), _p(mod.shift), d, 3,
-                      _p(mod.rows), mod.eps, None, _p(self.q), _p(self.xs), m, d, 256, st)
+                      _p(mod.rows), mod.eps, None, _p(self.q), _p(self.xs), m, d, 256,
+                      _p(mod.ws), mod.ws.numel(), st)
         with t("qkv_gemm"):
             _lib.call("mxq_int8_gemm_dequant", _p(self.q), _p(self.w), _p(self.xs), _p(self.s), n, _p(self.b),
                       _p(self.out), m, n, d, n, _lib.DTYPE_BF16, *_gemm_ws(self.dev), st)

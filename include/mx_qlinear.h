@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MXQ_ABI_VERSION 4
+#define MXQ_ABI_VERSION 5
 
 /* Return codes. */
 #define MXQ_OK 0
@@ -270,6 +270,11 @@ int mxq_gelu_tanh_bf16(const void* x, void* y, int64_t n, void* stream);
  *   x bf16 [rows, cols]; norm_weight bf16 [cols]; scale, shift bf16 [mod_count, ld_mod];
  *   mod_rows int32 [rows] (clamped into [0, mod_count)). y_out (bf16 [rows, cols]) and q/scales
  *   are each optional (NULL), not both. cols % 16 == 0, ld_mod % 8 == 0, 16-byte aligned tensors.
+ *   workspace (optional, 16-byte aligned): with q set and at least mod_count * ld_mod * 2 bytes,
+ *   bf16(1 + scale) of every modulation row is formed there once per call (one small kernel on
+ *   the stream before the main one) and read by the main kernel in place of scale; otherwise each
+ *   element forms it. The outputs are the same either way. Calls that share a workspace on two
+ *   streams race.
  * Semantics: rms_adaln, h3serve/native_engine/model/kernels.py:7594-7640 (eager branch) with
  * RMSNorm = F.rms_norm(x, weight.to(x.dtype), eps) (h3serve/native_engine/model/layers.py:33-48).
  * Replaces: segmented_rms_adaln / native_rms_one_pass_adaln
@@ -280,7 +285,7 @@ int mxq_rms_adaln_quantize_int8(const void* x, const void* norm_weight, const vo
                                 const void* shift, int64_t ld_mod, int64_t mod_count,
                                 const int32_t* mod_rows, float eps, void* y_out, int8_t* q,
                                 float* scales, int64_t rows, int64_t cols, int64_t group_size,
-                                void* stream);
+                                void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * The same on float16: x, norm_weight, scale, shift and y_out float16, every rounding above to

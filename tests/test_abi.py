@@ -61,7 +61,7 @@ def test_library_exports_every_declared_symbol(lib):
 def test_abi_version_and_error_string(lib):
     from mx_qlinear import _lib
 
-    assert lib.mxq_abi_version() == _lib.ABI_VERSION == 4
+    assert lib.mxq_abi_version() == _lib.ABI_VERSION == 5
     lib.mxq_last_error.restype = ctypes.c_char_p
     assert isinstance(lib.mxq_last_error(), bytes)
     # a rejected call leaves a message naming the problem

@@ -235,3 +235,36 @@ def test_rms_adaln_quantize_h3_width_many_rows(dev, mapping):
     assert np.array_equal(q.cpu().numpy(), qr) and np.array_equal(s.cpu().numpy(), sr)
     y2 = _mx().rms_adaln(x.to(dev), (w.to(dev), eps), shift.to(dev), scale.to(dev), segs)
     assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("ld_pad", [0, 40])
+def test_rms_adaln_modulation_workspace_changes_nothing(dev, ld_pad):
+    """Through the C-ABI: the same call with the modulation workspace (bf16(1 + scale) formed
+    once per call), with one 16 bytes too small and with none gives identical q, scales and y,
+    also for scale / shift rows strided beyond the hidden size."""
+    from mx_qlinear import _lib
+    from mx_qlinear.ops import _p, _stream
+
+    m, d, eps, mods = 777, 5376, 1e-6, 5
+    print(f"rms_adaln workspace m={m} d={d} ld_pad={ld_pad}", flush=True)
+    x, w, _, _ = _rms_inputs(m, d, 91 + ld_pad)
+    ld = d + ld_pad
+    scale = (0.1 * torch.randn(mods, ld, generator=gen(92))).to(torch.bfloat16).to(dev)
+    shift = (0.1 * torch.randn(mods, ld, generator=gen(93))).to(torch.bfloat16).to(dev)
+    rows = torch.randint(0, mods, (m,), generator=gen(94), dtype=torch.int32).to(dev)
+    x, w = x.to(dev), w.to(dev)
+    outs = []
+    for ws_bytes in (mods * ld * 2, mods * ld * 2 - 16, 0):
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        q = torch.empty((m, d), dtype=torch.int8, device=dev)
+        s = torch.empty((m, 1), dtype=torch.float32, device=dev)
+        y = torch.empty((m, d), dtype=torch.bfloat16, device=dev)
+        _lib.call("mxq_rms_adaln_quantize_int8", _p(x), _p(w), _p(scale), _p(shift), ld, mods, _p(rows), eps, _p(y),
+                  _p(q), _p(s), m, d, 256, _p(ws) if ws_bytes else None, ws_bytes, _stream(dev))
+        torch.cuda.synchronize()
+        outs.append((q, s, y))
+    for q, s, y in outs[1:]:
+        assert torch.equal(q, outs[0][0]) and torch.equal(s, outs[0][1]) and torch.equal(y, outs[0][2])
+    # and the modulated rows are the oracle's within the stated bound
+    _check_rms_adaln_bound(outs[0][2].cpu(), x.cpu(), w.cpu(), scale[:, :d].contiguous().cpu(), shift[:, :d].contiguous().cpu(),
+                           rows.cpu().numpy(), eps)

@@ -360,7 +360,7 @@ MXQ_DEVICE void unit_back16(uint32_t (&w)[8], double* tb) {
   wave_lds_fence();  // read before the region's next writes
 }
 
-template <int kAct, int kMod, int kDigits, int kNU, int kPreMod = 1>
+template <int kAct, int kMod, int kDigits, int kNU, bool kTab = false, int kPreMod = 1>
 __global__ __launch_bounds__(kUnitMaxWaves * 64) void convrot_units_kernel(CrArgs p, int gr, int rpb) {
   constexpr int kRawWords = kAct == MXQ_ACT_SWIGLU ? 16 : 8;  // dwords per unit and lane
   constexpr double kInv = 1.0 / (double)(1 << kDigits);     // 1/sqrt(G), exact
@@ -471,7 +471,9 @@ __global__ __launch_bounds__(kUnitMaxWaves * 64) void convrot_units_kernel(CrArg
           const uint32_t sw = sc[k][i >> 2][i & 3], hw = sh[k][i >> 2][i & 3];
           // t = bf16(1 + scale), n = bf16((x * r) * w), y = bf16(bf16(n * t) + shift), each
           // rounding kept in fp32 form (round_bf16), the pair packed only for the y store
-          const float tl = round_bf16(1.0f + bf16_lo(sw)), th = round_bf16(1.0f + bf16_hi(sw));
+          // (with kTab the words are already bf16(1 + scale), built once per call)
+          const float tl = kTab ? bf16_lo(sw) : round_bf16(1.0f + bf16_lo(sw));
+          const float th = kTab ? bf16_hi(sw) : round_bf16(1.0f + bf16_hi(sw));
           const float nl = round_bf16((bf16_lo(xw) * rinv) * bf16_lo(ww));
           const float nh = round_bf16((bf16_hi(xw) * rinv) * bf16_hi(ww));
           const float yl = round_bf16(round_bf16(nl * tl) + bf16_lo(hw));
@@ -572,7 +574,7 @@ UnitSplit unit_split(int units) {
   return best;
 }
 
-template <int kAct, int kMod, int kDigits>
+template <int kAct, int kMod, int kDigits, bool kTab = false>
 int launch_units(const CrArgs& a, const UnitSplit& u, hipStream_t st) {
   // One row batch per block (measured faster at 720p than persistent blocks that prefetch the
   // next batch); small blocks, many resident per CU, hide the load latency instead.
@@ -580,23 +582,23 @@ int launch_units(const CrArgs& a, const UnitSplit& u, hipStream_t st) {
   const unsigned threads = (unsigned)(u.waves * 64);
   const size_t lds = (size_t)u.waves * kTWave * sizeof(double);
   switch (u.nu) {
-    case 1: convrot_units_kernel<kAct, kMod, kDigits, 1><<<grid, threads, lds, st>>>(a, u.gr, u.rpb); break;
-    case 2: convrot_units_kernel<kAct, kMod, kDigits, 2><<<grid, threads, lds, st>>>(a, u.gr, u.rpb); break;
-    case 3: convrot_units_kernel<kAct, kMod, kDigits, 3><<<grid, threads, lds, st>>>(a, u.gr, u.rpb); break;
-    default: convrot_units_kernel<kAct, kMod, kDigits, 4><<<grid, threads, lds, st>>>(a, u.gr, u.rpb); break;
+    case 1: convrot_units_kernel<kAct, kMod, kDigits, 1, kTab><<<grid, threads, lds, st>>>(a, u.gr, u.rpb); break;
+    case 2: convrot_units_kernel<kAct, kMod, kDigits, 2, kTab><<<grid, threads, lds, st>>>(a, u.gr, u.rpb); break;
+    case 3: convrot_units_kernel<kAct, kMod, kDigits, 3, kTab><<<grid, threads, lds, st>>>(a, u.gr, u.rpb); break;
+    default: convrot_units_kernel<kAct, kMod, kDigits, 4, kTab><<<grid, threads, lds, st>>>(a, u.gr, u.rpb); break;
   }
   return mxq_check_launch("convrot_units_kernel");
 }
 
-template <int kAct, int kMod>
+template <int kAct, int kMod, bool kTab = false>
 int launch_units_digits(const CrArgs& a, hipStream_t st) {
   const UnitSplit u = unit_split(a.K >> 8);
   switch (a.digits) {
-    case 0: return launch_units<kAct, kMod, 0>(a, u, st);
-    case 1: return launch_units<kAct, kMod, 1>(a, u, st);
-    case 2: return launch_units<kAct, kMod, 2>(a, u, st);
-    case 3: return launch_units<kAct, kMod, 3>(a, u, st);
-    default: return launch_units<kAct, kMod, 4>(a, u, st);
+    case 0: return launch_units<kAct, kMod, 0, kTab>(a, u, st);
+    case 1: return launch_units<kAct, kMod, 1, kTab>(a, u, st);
+    case 2: return launch_units<kAct, kMod, 2, kTab>(a, u, st);
+    case 3: return launch_units<kAct, kMod, 3, kTab>(a, u, st);
+    default: return launch_units<kAct, kMod, 4, kTab>(a, u, st);
   }
 }
 
@@ -677,10 +679,27 @@ extern "C" int mxq_swiglu_bf16(const void* x, void* y, int64_t rows, int64_t col
   return mxq_check_launch("swiglu_kernel");
 }
 
+// t[m, c] = bf16(1 + scale[m, c]) for the modulation rows (c < cols, row stride ld): the factor
+// every token of segment m multiplies its normalized value by, formed once per call instead of
+// once per token and element. Eight columns (16 bytes) per thread.
+__global__ __launch_bounds__(256) void one_plus_rows_kernel(const uint16_t* __restrict__ scale, uint16_t* __restrict__ t,
+                                                            int64_t ld, int64_t mod_count, int64_t cols) {
+  const int64_t per_row = cols / 8, n = mod_count * per_row;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t m = i / per_row, c = (i - m * per_row) * 8;
+    const v4u w = *reinterpret_cast<const v4u*>(scale + m * ld + c);
+    v4u o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = pack_bf16x2(1.0f + bf16_lo(w[e]), 1.0f + bf16_hi(w[e]));
+    *reinterpret_cast<v4u*>(t + m * ld + c) = o;
+  }
+}
+
 static int rms_adaln_launch(const void* x, const void* norm_weight, const void* scale, const void* shift,
                             int64_t ld_mod, int64_t mod_count, const int32_t* mod_rows, float eps, void* y_out,
                             int8_t* q, float* scales, int64_t rows, int64_t cols, int64_t group_size, bool f16,
-                            void* stream) {
+                            void* workspace, int64_t workspace_bytes, void* stream) {
   if (rows < 0 || cols < 0) return mxq_set_error(MXQ_ERR_INVALID, "negative shape");
   int digits = 0;
   if (q && group_size != 0) {
@@ -720,6 +739,16 @@ static int rms_adaln_launch(const void* x, const void* norm_weight, const void* 
     return launch_convrot<MXQ_ACT_NONE, MXQ_DTYPE_F16, kModOnly>(a, nw, st);
   }
   if (units_fit(cols, digits)) {
+    if (q && workspace && workspace_bytes >= mod_count * ld_mod * 2 && (uintptr_t)workspace % 16 == 0) {
+      // bf16(1 + scale) of every modulation row into the workspace, then the kernel reads it there
+      uint16_t* t = (uint16_t*)workspace;
+      const int64_t n = mod_count * (cols / 8);
+      one_plus_rows_kernel<<<(unsigned)std::min<int64_t>((n + 255) / 256, 4096), 256, 0, st>>>(
+          (const uint16_t*)scale, t, ld_mod, mod_count, cols);
+      if (int rc = mxq_check_launch("one_plus_rows_kernel")) return rc;
+      a.mscale = t;
+      return launch_units_digits<MXQ_ACT_NONE, kModQuant, true>(a, st);
+    }
     if (q) return launch_units_digits<MXQ_ACT_NONE, kModQuant>(a, st);
     return launch_units_digits<MXQ_ACT_NONE, kModOnly>(a, st);
   }
@@ -731,9 +760,10 @@ extern "C" int mxq_rms_adaln_quantize_int8(const void* x, const void* norm_weigh
                                            const void* shift, int64_t ld_mod, int64_t mod_count,
                                            const int32_t* mod_rows, float eps, void* y_out, int8_t* q,
                                            float* scales, int64_t rows, int64_t cols, int64_t group_size,
-                                           void* stream) {
+                                           void* workspace, int64_t workspace_bytes, void* stream) {
+  if (workspace_bytes < 0) return mxq_set_error(MXQ_ERR_INVALID, "negative workspace size");
   return rms_adaln_launch(x, norm_weight, scale, shift, ld_mod, mod_count, mod_rows, eps, y_out, q, scales, rows,
-                          cols, group_size, false, stream);
+                          cols, group_size, false, workspace, workspace_bytes, stream);
 }
 
 extern "C" int mxq_rms_adaln_quantize_int8_f16(const void* x, const void* norm_weight, const void* scale,
@@ -742,5 +772,5 @@ extern "C" int mxq_rms_adaln_quantize_int8_f16(const void* x, const void* norm_w
                                                float* scales, int64_t rows, int64_t cols, int64_t group_size,
                                                void* stream) {
   return rms_adaln_launch(x, norm_weight, scale, shift, ld_mod, mod_count, mod_rows, eps, y_out, q, scales, rows,
-                          cols, group_size, true, stream);
+                          cols, group_size, true, nullptr, 0, stream);
 }

@@ -19,7 +19,7 @@ MXQ_ERR_UNSUPPORTED = -2
 MXQ_ERR_HIP = -3
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_E4M3 = 0, 1, 2, 5
-ABI_VERSION = 4
+ABI_VERSION = 5
 # MXQ_GEMM_WORKSPACE_BYTES: the INT8 GEMMs' tile-queue workspace (counters)
 GEMM_WORKSPACE_BYTES = 4096
 ACT_NONE, ACT_GELU_TANH, ACT_SWIGLU = 0, 1, 2
@@ -52,7 +52,7 @@ SIGNATURES: dict[str, list] = {
     "mxq_adaln_quantize_int8_f16": [_P, _P, _P, _I64, _I64, _F, _P, _P, _P, _I64, _I64, _P],
     "mxq_int8_linear_m1": [_P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _P],
     "mxq_int8_gemv_dequant": [_P, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I, _P],
-    "mxq_rms_adaln_quantize_int8": [_P, _P, _P, _P, _I64, _I64, _P, _F, _P, _P, _P, _I64, _I64, _I64, _P],
+    "mxq_rms_adaln_quantize_int8": [_P, _P, _P, _P, _I64, _I64, _P, _F, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _P],
     "mxq_rms_adaln_quantize_int8_f16": [_P, _P, _P, _P, _I64, _I64, _P, _F, _P, _P, _P, _I64, _I64, _I64, _P],
     "mxq_gelu_tanh_bf16": [_P, _P, _I64, _P],
     "mxq_dequant_int4_grouped_to_int8": [_P, _P, _I, _P, _P, _I64, _I64, _I64, _P],

@@ -371,9 +371,15 @@ def _rms_adaln_call(value, norm, shift, scale, segments, quant: bool, group: int
     s = torch.empty((rows, 1), dtype=torch.float32, device=dev) if quant else None
     if rows and d:
         with torch.cuda.device(dev):
-            entry = "mxq_rms_adaln_quantize_int8_f16" if x.dtype == torch.float16 else "mxq_rms_adaln_quantize_int8"
-            call(entry, _p(x), _p(w), _p(sc), _p(sh), sc.stride(0), sc.shape[0], _p(mr), eps, _p(y), _p(q), _p(s),
-                 rows, d, group if quant else 0, _stream(dev))
+            if x.dtype == torch.float16:
+                call("mxq_rms_adaln_quantize_int8_f16", _p(x), _p(w), _p(sc), _p(sh), sc.stride(0), sc.shape[0],
+                     _p(mr), eps, _p(y), _p(q), _p(s), rows, d, group if quant else 0, _stream(dev))
+            else:
+                # room for bf16(1 + scale) of each modulation row, formed once per call
+                ws = torch.empty(sc.shape[0] * sc.stride(0) * 2 if quant else 0, dtype=torch.uint8, device=dev)
+                call("mxq_rms_adaln_quantize_int8", _p(x), _p(w), _p(sc), _p(sh), sc.stride(0), sc.shape[0],
+                     _p(mr), eps, _p(y), _p(q), _p(s), rows, d, group if quant else 0, _p(ws), ws.numel(),
+                     _stream(dev))
     if not quant:
         return y
     return (q, s, y) if want_y else (q, s)
