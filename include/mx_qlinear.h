@@ -140,7 +140,7 @@ int mxq_adaln_quantize_int8_f16(const void* x, const void* scale, const void* sh
 
 /*
  * Launch plan the INT8 GEMMs below choose for an M x N x K problem (table_epilogue: 1 for the
- * GELU and SwiGLU epilogues, 0 otherwise) given workspace_bytes of tile-queue workspace (0:
+ * GELU epilogue, 2 for the SwiGLU one, 0 otherwise) given workspace_bytes of tile-queue workspace (0:
  * none): plan[0] tile rows (256 or 128), plan[1] workgroups, plan[2] tiles, plan[3] tiles per
  * XCD claimed at run time (0: static order), plan[4] workgroups per XCD, plan[5] stages of
  * operands requested ahead of the MFMAs (4 when the 128-tiles all fit on the CUs at once, one

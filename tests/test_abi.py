@@ -137,7 +137,8 @@ def test_python_maps_codes_to_the_reference_exceptions(lib):
     "m,n,k,table,tile,queued",
     [
         (75600, 5120, 20480, False, 256, True),   # FFN fc2 at 720p
-        (75600, 20480, 5120, True, 256, True),    # FFN fc1 (planned as a table epilogue)
+        (75600, 20480, 5120, True, 256, True),    # FFN fc1 (planned as a GELU table epilogue)
+        (75600, 28672, 5376, 2, 256, True),       # H3 fc1 with the SwiGLU epilogue (compact table)
         (75600, 15360, 5120, False, 256, True),   # QKV at 720p
         (8192, 5120, 5120, False, 128, True),     # 2.5 rounds of 128-tiles
         (1024, 3072, 3072, False, 128, False),    # under two rounds: static order
@@ -153,9 +154,9 @@ def test_gemm_plan_queues_large_problems(lib, m, n, k, table, tile, queued):
     if queued:
         per = tiles // 8
         assert plan["pool"] == -(-per // 8)
-        # 256-tiles without a table epilogue: one looping workgroup per CU (this host has no GPU,
-        # so the library plans for 256 CUs); otherwise one workgroup per tile plus claimers
-        assert plan["persistent"] == (tile == 256 and not table)
+        # 256-tiles without the GELU table epilogue: one looping workgroup per CU (this host has
+        # no GPU, so the library plans for 256 CUs); otherwise one workgroup per tile plus claimers
+        assert plan["persistent"] == (tile == 256 and table != 1)
         if plan["persistent"]:
             assert plan["wg_per_xcd"] == 256 // 8
         else:
@@ -177,6 +178,7 @@ def test_gemm_plan_queues_large_problems(lib, m, n, k, table, tile, queued):
         (2050, 2056, False, 128, 128, 2),   # 289 tiles of 128: two workgroups per CU
         (75600, 5120, False, 256, 256, 2),
         (1024, 3072, True, 256, 256, 2),    # table epilogues always take 256-tiles
+        (1024, 3072, 2, 256, 256, 2),
     ],
 )
 def test_gemm_plan_ring_depth(lib, m, n, table, tile, tile_n, ahead):

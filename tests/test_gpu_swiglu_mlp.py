@@ -38,6 +38,49 @@ def test_swiglu_fc1_matches_oracle(dev, m, f, k, bias, per_channel):
     assert np.array_equal(bits(h), cr.swiglu_bf16(bf16_bits(y)))
 
 
+def test_swiglu_fc1_every_gate_pattern(dev):
+    """All 65,536 bf16 gate patterns (NaN, infinities, zeros, subnormals, both signs) through the
+    GEMM epilogue's SiLU: zero activations make every fc1 output its bias, so the gate half of the
+    bias runs over every pattern and the up half over random values. 512 tiles of 256 on two
+    rounds: the looping workgroups' epilogues run beside the next tile's first loads."""
+    m, f, k = 40, 65536, 16
+    print(f"swiglu fc1 every gate pattern m={m} f={f}", flush=True)
+    gate_bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    up = torch.randn(f, generator=gen(31)).to(torch.bfloat16)
+    b = torch.cat([gate_bits.view(torch.bfloat16), up])
+    w, ws = int8_weight(2 * f, k, 32)
+    q = np.zeros((m, k), dtype=np.int8)
+    s = np.full((m, 1), 0.5, dtype=np.float32)
+    fc1 = _mx().prepare_swiglu_fc1(w.to(dev), ws.to(dev), b.to(dev))
+    from mx_qlinear import _lib
+
+    plan = _lib.gemm_plan(m, 2 * f, k, 2)
+    assert plan["persistent"] and plan["tiles"] == 512, plan
+    h = _mx().int8_swiglu_fc1(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), fc1)
+    y = eager_np.dequant_epilogue(np.zeros((m, 2 * f), dtype=np.int32), s, ws.numpy(), bits(b), "bf16")
+    assert np.array_equal(bits(h), cr.swiglu_bf16(bf16_bits(y)))
+
+
+@pytest.mark.parametrize("m,f,k", [(4096, 4096, 512), (4100, 4112, 400)])
+def test_swiglu_fc1_multi_round_matches_oracle(dev, m, f, k):
+    """Looping ping-pong workgroups over 512+ tiles (ragged edges in the second case): sampled
+    rows against the oracle, bit for bit."""
+    print(f"swiglu fc1 multi-round m={m} f={f} k={k}", flush=True)
+    from mx_qlinear import _lib
+
+    assert _lib.gemm_plan(m, 2 * f, k, 2)["persistent"]
+    x = activations(m, k, m + 3)
+    w, ws = int8_weight(2 * f, k, f + 4)
+    b = bf16_vec(2 * f, 5, 0.05)
+    q, s = eager_np.quantize_int8_rowwise(bits(x))
+    fc1 = _mx().prepare_swiglu_fc1(w.to(dev), ws.to(dev), b.to(dev))
+    h = _mx().int8_swiglu_fc1(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), fc1).cpu()
+    rows = np.unique(np.concatenate([[0, m - 1], np.random.default_rng(m).choice(m, 30, replace=False)]))
+    acc = (q[rows].astype(np.float64) @ w.numpy().astype(np.float64).T).astype(np.int64).astype(np.int32)
+    y = eager_np.dequant_epilogue(acc, s[rows], ws.numpy(), bits(b), "bf16")
+    assert np.array_equal(bits(h[rows]), cr.swiglu_bf16(bf16_bits(y)))
+
+
 def test_swiglu_fc1_equals_linear_then_swiglu_on_device(dev):
     m, f, k = 200, 768, 512
     x = activations(m, k, 5).to(dev)

@@ -210,6 +210,30 @@ def test_device_silu_table_matches_golden():
     assert np.array_equal(dev, golden)
 
 
+def test_compact_silu_lookup_matches_golden():
+    """The SwiGLU GEMM epilogue's form: the table entry at (b >> 15) * span + (b & 0x7FFF) - E_LO * 128
+    (offset clamped into the table) when E_LO <= exponent < E_NEG, the closed-form rules (x / 2,
+    inf / NaN, x, -0) otherwise -- silu_compact_offset / silu_compact_in / silu_rule_out."""
+    inc = (CSRC / "silu_bf16_table.inc").read_text()
+    defs = dict(line.split()[1:3] for line in inc.splitlines() if line.startswith("#define"))
+    e_lo, e_neg = int(defs["MXQ_SILU_E_LO"]), int(defs["MXQ_SILU_E_NEG"])
+    nan = int(defs["MXQ_SILU_NAN"].rstrip("u"), 16)
+    body = inc[inc.index("{") + 1:inc.rindex("}")]
+    table = np.array([int(v, 16) for v in body.replace("\n", "").split(",") if v.strip()], np.uint32)
+    golden = np.load(GOLDEN / "silu_bf16.npy").astype(np.uint32)
+    lo, span = e_lo << 7, (e_neg - e_lo) << 7
+    b = np.arange(65536, dtype=np.uint32)
+    sign, mag, e = b & 0x8000, b & 0x7FFF, (b >> 7) & 0xFF
+    off = (mag - np.uint32(lo)) & np.uint32(0xFFFFFFFF)  # 32-bit wrap below the range
+    inside = off < span
+    idx = (b >> 15) * span + np.minimum(off, span - 1)
+    assert idx.max() < table.size == 2 * span
+    v = mag & 0xFF
+    half = sign | np.where(e >= 2, mag - 0x80, (v >> 1) + ((v & 1) & ((v >> 1) & 1)))
+    out = np.where(e < e_lo, half, np.where(e == 255, np.where(b == 0x7F80, 0x7F80, nan), np.where(sign != 0, 0x8000, b)))
+    assert np.array_equal(np.where(inside, table[idx], out), golden)
+
+
 def test_swiglu_oracle_matches_torch():
     x = activations(32, 2 * 768, 21, outlier_frac=0.0) * 3
     gate, up = x.chunk(2, dim=-1)

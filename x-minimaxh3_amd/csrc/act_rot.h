@@ -38,6 +38,40 @@ static __device__ __attribute__((aligned(16))) const SiluFullTable kSiluFull = m
 
 MXQ_DEVICE uint32_t silu_bf16(uint32_t b) { return kSiluFull.v[b & 0xFFFFu]; }
 
+// The compact form, for kernels with 8 KB of LDS to spare rather than 128 KB: the 3840 entries
+// of biased exponents [E_LO, E_NEG), both signs (entry (b >> 15) * span + (b & 0x7FFF) - E_LO * 128),
+// padded to 8 KB. silu_compact_offset(b) is the byte offset of b's entry when silu_compact_in(b),
+// else some offset inside the table; silu_rule_out(b) is the value of every b outside the range
+// (silu_rule_c's other rules). Checked against all 65,536 torch outputs by the GPU tests of the
+// SwiGLU epilogue and, on the CPU, by tests/test_oracle_convrot.py.
+constexpr uint32_t kSiluLoMag = (uint32_t)MXQ_SILU_E_LO << 7;
+constexpr uint32_t kSiluSpan = (uint32_t)(MXQ_SILU_E_NEG - MXQ_SILU_E_LO) << 7;
+struct SiluCompactTable {
+  uint16_t v[4096];
+};
+constexpr SiluCompactTable make_silu_compact() {
+  SiluCompactTable t{};
+  for (uint32_t i = 0; i < 2u * kSiluSpan; ++i) t.v[i] = kSiluTableC[i];
+  return t;
+}
+static_assert(2u * kSiluSpan == MXQ_SILU_TABLE_SIZE && MXQ_SILU_TABLE_SIZE <= 4096, "compact SiLU table layout");
+static __device__ __attribute__((aligned(16))) const SiluCompactTable kSiluCompact = make_silu_compact();
+
+MXQ_DEVICE bool silu_compact_in(uint32_t b) { return (b & 0x7FFFu) - kSiluLoMag < kSiluSpan; }
+MXQ_DEVICE uint32_t silu_compact_offset(uint32_t b) {
+  const uint32_t off = min((b & 0x7FFFu) - kSiluLoMag, kSiluSpan - 1u);  // below the range: wraps, clamped
+  return ((b >> 15) * kSiluSpan + off) * 2u;
+}
+MXQ_DEVICE uint32_t silu_rule_out(uint32_t b) {
+  const uint32_t e = (b >> 7) & 0xFFu, sign = b & 0x8000u, mag = b & 0x7FFFu;
+  if (e < MXQ_SILU_E_LO) {
+    const uint32_t v = mag & 0xFFu;
+    return sign | (e >= 2 ? mag - 0x80u : (v >> 1) + ((v & 1u) & ((v >> 1) & 1u)));
+  }
+  if (e == 255u) return b == 0x7F80u ? 0x7F80u : MXQ_SILU_NAN;
+  return sign ? 0x8000u : b;  // e >= E_NEG: x (positive) or -0.0
+}
+
 // SwiGLU of one bf16 pair: bf16(bf16(silu(gate)) * up) -- the product of two bf16 is exact in
 // fp32, so this is torch's bf16 mul_ (one rounding); a NaN product becomes 0x7FC0, the pattern
 // torch's float -> bfloat16 conversion gives every NaN.

@@ -96,6 +96,9 @@ struct TileCfg {
 constexpr int kGroupM = 2, kGroupMPingPong = 4;
 
 enum { kEpiI32 = 0, kEpiDequant = 1, kEpiGelu = 2, kEpiGatedRes = 3, kEpiSwiGLU = 4 };
+// Table epilogues as plan_gemm sees them: GELU keeps the whole 128 KB table in LDS (four-wave
+// 256-tiles), SwiGLU the 8 KB compact SiLU table (ping-pong 256-tiles).
+enum { kTableGelu = 1, kTableSwiGLU = 2 };
 
 struct GemmArgs {
   const int8_t* a;
@@ -453,6 +456,22 @@ MXQ_DEVICE void stage_store(const GemmArgs& p, char* buf, int64_t row0, int64_t 
   for (int t = 0; t < 4; ++t) *reinterpret_cast<v4u*>(base + t * 8 * pitch) = v[t];
 }
 
+// The same for a piece of 64 bytes per row (chunks 0-3): rows row0 .. row0 + 31 of d, bytes
+// [byte0, byte0 + 64), two 16-byte stores per lane. (Pairing two ping-pong waves' halves into
+// whole lines behind a workgroup barrier measured 0.7 % slower on the SwiGLU fc1.)
+MXQ_DEVICE void stage_store64(const GemmArgs& p, char* buf, int64_t row0, int64_t byte0, int64_t pitch) {
+  const int lane = tid_x() & 63;
+  wave_lds_sync();
+  v4u v[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+    v[t] = __builtin_bit_cast(v4u, lds_read_b128<0>(lds_addr(stage_at(buf, t * 16 + (lane >> 2), lane & 3))));
+  stage_wait();
+  char* base = reinterpret_cast<char*>(p.d) + (row0 + (lane >> 2)) * pitch + byte0 + (lane & 3) * 16;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) *reinterpret_cast<v4u*>(base + t * 16 * pitch) = v[t];
+}
+
 // Two 32 x 32 blocks of 16-bit words (jj = 0, 1: 8 words each, as epi_run gives them), or one
 // block of 32-bit words, as one piece.
 MXQ_DEVICE void stage_blocks16(char* buf, const uint32_t (&w)[2][8]) {
@@ -746,7 +765,7 @@ MXQ_DEVICE void load_epi_factors(const GemmArgs& p, int64_t m0, int64_t n0, int 
 // issues all three up front.
 template <class C, int kEpi, int kOut, int kStageBase, int kFactorBase, class Pre>
 MXQ_DEVICE void gemm_epilogue(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][C::kBJ], int64_t m0, int64_t n0,
-                              int wrow, int wcol, const EpiFactors<C::kBI, kOut>& f, Pre&& pre) {
+                              int wrow, int wcol, const EpiFactors<C::kBI, kOut>& f, Pre&& pre, int pre_loads = 0) {
   constexpr int kBM = C::kBM, kBN = C::kBN, kBI = C::kBI, kBJ = C::kBJ;
   const int wave = tid_x() >> 6, lane = tid_x() & 63;
   // ---- epilogue ----
@@ -760,6 +779,10 @@ MXQ_DEVICE void gemm_epilogue(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][
   float* s_ws = reinterpret_cast<float*>(lds + kFactorBase);
   float* s_bias = s_ws + kBN;
   const uint16_t* s_gelu = reinterpret_cast<const uint16_t*>(lds);
+  // SwiGLU: the compact SiLU table, behind the factors and the ping-pong kernel's position word
+  constexpr int kSiluTabBase = kFactorBase + 2 * kBN * 4 + 2048;
+  static_assert(kEpi != kEpiSwiGLU || (C::kPingPong && kSiluTabBase + 8192 <= kStageBase),
+                "the SwiGLU epilogue runs in the ping-pong kernel, its table in the factors' slot");
   const bool has_b = p.bias != nullptr;
   float xsv[kBI] = {};
   if constexpr (kEpi == kEpiI32) {
@@ -779,12 +802,16 @@ MXQ_DEVICE void gemm_epilogue(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][
       __asm__ volatile("" : "+v"(xsv[i]));
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (kEpi == kEpiGelu || kEpi == kEpiSwiGLU) {
-      const char* src = reinterpret_cast<const char*>(kEpi == kEpiGelu ? (const void*)&kGeluFull : (const void*)&kSiluFull) +
-                        lane * 16;
+    if constexpr (kEpi == kEpiGelu) {
+      const char* src = reinterpret_cast<const char*>(&kGeluFull) + lane * 16;
 #pragma unroll 4
       for (int q = wave; q < 128; q += C::kWaves)
         __builtin_amdgcn_global_load_lds((gptr_t)(src + q * 1024), (lptr_t)(lds + q * 1024), 16, 0, 0);
+    } else if constexpr (kEpi == kEpiSwiGLU) {
+      // the compact SiLU table (8 KB, one kilobyte per wave) behind the factors
+      static_assert(C::kWaves == 8, "one kilobyte of the compact table per wave");
+      const char* src = reinterpret_cast<const char*>(&kSiluCompact) + wave * 1024 + lane * 16;
+      __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)(lds + kSiluTabBase + wave * 1024), 16, 0, 0);
     }
     if constexpr (kEpi == kEpiGatedRes) pre(-1);  // all three parts
     __builtin_amdgcn_sched_barrier(0);
@@ -796,9 +823,10 @@ MXQ_DEVICE void gemm_epilogue(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][
   // staging buffers sit behind the per-column factors when a table fills the ring, else at 0.
   constexpr bool kTable = kEpi == kEpiGelu || kEpi == kEpiSwiGLU;
   const bool lines = full && p.line_store;
-  constexpr int kSB = kTable ? kFactorBase + 2 * kBN * 4 : kStageBase, kSE = kSB + C::kWaves * kStageBytes;
+  constexpr int kSB = kEpi == kEpiGelu ? kFactorBase + 2 * kBN * 4 : kStageBase, kSE = kSB + C::kWaves * kStageBytes;
   static_assert(kSE <= C::kLds && (kSE <= kFactorBase || kSB >= kFactorBase + 2 * kBN * 4) &&
-                    (!kTable || kSB >= 128 * 1024) && (!kTable || kFactorBase >= 128 * 1024),
+                    (kEpi != kEpiSwiGLU || kSB >= kSiluTabBase + 8192) &&
+                    (kEpi != kEpiGelu || (kSB >= 128 * 1024 && kFactorBase >= 128 * 1024)),
                 "staging buffers overlap the table, the factors or the end of LDS");
   char* sbuf = lds + kSB + wave * kStageBytes;
   const int64_t pitch = p.ldd * kElem;
@@ -966,12 +994,22 @@ MXQ_DEVICE void gemm_epilogue(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][
     }
   }
   if constexpr (kEpi == kEpiSwiGLU) {
-    wait_vmcnt<0>();
-    barrier_no_drain();  // every wave's part of the SiLU table has landed
+    // Every wave's kilobyte of the SiLU table has landed: only the `pre_loads` loads of the next
+    // tile, issued after it, may stay in flight (a wait for more than those is still correct).
+    if (pre_loads >= 3 * C::kLoads)
+      wait_vmcnt<3 * C::kLoads>();
+    else if (pre_loads >= 2 * C::kLoads)
+      wait_vmcnt<2 * C::kLoads>();
+    else if (pre_loads >= C::kLoads)
+      wait_vmcnt<C::kLoads>();
+    else
+      wait_vmcnt<0>();
+    barrier_no_drain();
     // Runs 0, 1 of a 32 x 32 block are gate columns, runs 2, 3 the matching up columns; output
-    // channel c of block b (tile column t0 = b * 32) is h column t0 / 2 + c. A wave's four
-    // blocks of a block row give 64 h columns: one 128-byte piece for the whole-line form.
-    const uint16_t* s_silu = reinterpret_cast<const uint16_t*>(lds);
+    // channel c of block b (tile column t0 = b * 32) is h column t0 / 2 + c. A wave's blocks of a
+    // block row give 16 h columns each: a 64-byte piece per row (two blocks) for the whole-line
+    // form, or a 128-byte one (four).
+    const uint32_t tab = lds_addr(lds + kSiluTabBase);
     const int64_t nh = p.N / 2;
     const bool hfull = p.vec_store && m0 + kBM <= p.M && (n0 + kBN) / 2 <= nh;
     const bool hlines = hfull && p.line_store;
@@ -979,13 +1017,29 @@ MXQ_DEVICE void gemm_epilogue(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][
       constexpr int i = decltype(I)::value;
       const int64_t row = m0 + wrow + i * 32 + lr;
       uint32_t hw[kBJ][4];
+      // silu of the row's gate values from the compact table (LDS reads as inline assembly: the
+      // next tile's operand loads stay in flight), then the rules for values outside its range
+      uint32_t sg[kBJ][4][2];
+#pragma unroll
+      for (int j = 0; j < kBJ; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t g = yp[i][j][r];
+          sg[j][r][0] = lds_read_u16_at(tab + silu_compact_offset(g & 0xFFFFu));
+          sg[j][r][1] = lds_read_u16_at(tab + silu_compact_offset(g >> 16));
+        }
+      wait_lgkm<0>();
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < kBJ; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const uint32_t g = yp[i][j][r], u = yp[i][j][r + 4];
-          const float plo = bf16_to_f32(s_silu[g & 0xFFFFu]) * bf16_to_f32(u & 0xFFFFu);
-          const float phi = bf16_to_f32(s_silu[g >> 16]) * bf16_to_f32(u >> 16);
+          const uint32_t glo = g & 0xFFFFu, ghi = g >> 16;
+          const uint32_t slo = silu_compact_in(glo) ? sg[j][r][0] : silu_rule_out(glo);
+          const uint32_t shi = silu_compact_in(ghi) ? sg[j][r][1] : silu_rule_out(ghi);
+          const float plo = bf16_to_f32(slo) * bf16_to_f32(u & 0xFFFFu);
+          const float phi = bf16_to_f32(shi) * bf16_to_f32(u >> 16);
           hw[j][r] = (plo != plo ? 0x7FC0u : f32_to_bf16_bits(plo)) | ((phi != phi ? 0x7FC0u : f32_to_bf16_bits(phi)) << 16);
         }
       if (hlines) {
@@ -995,7 +1049,10 @@ MXQ_DEVICE void gemm_epilogue(const GemmArgs& p, char* lds, v16i (&acc)[C::kBI][
           stage_put8(sbuf, lr, j * 2, lh, hw[j][0], hw[j][1]);
           stage_put8(sbuf, lr, j * 2 + 1, lh, hw[j][2], hw[j][3]);
         }
-        stage_store(p, sbuf, m0 + wrow + i * 32, (n0 + wcol) / 2 * 2, pitch);
+        if constexpr (kBJ == 4)
+          stage_store(p, sbuf, m0 + wrow + i * 32, (n0 + wcol) / 2 * 2, pitch);
+        else
+          stage_store64(p, sbuf, m0 + wrow + i * 32, (n0 + wcol) / 2 * 2, pitch);
       } else {
 #pragma unroll
         for (int j = 0; j < kBJ; ++j) {
@@ -1158,7 +1215,7 @@ MXQ_DEVICE void pp_tiles(const GemmArgs& p, char* lds) {
         else
           pp_first_load_part<C>(p, lds, next_ld, part);
       }
-    });
+    }, next >= 0 ? (p.K > kBK ? 3 : 2) * C::kLoads : 0);
     if (next < 0) break;
     m0 = nm0;
     n0 = nn0;
@@ -1334,7 +1391,7 @@ struct GemmPlan {
 // (4096 x 5120: 1.25 rounds, 0.147 -> 0.117 ms) and a full one is not. The table epilogues (GELU,
 // SwiGLU) need the 256-tile ring. With a workspace, problems of two rounds or more balance their
 // tiles over the XCDs at run time (pick_tile).
-static GemmPlan plan_gemm(int64_t M, int64_t N, bool table, int64_t workspace_bytes) {
+static GemmPlan plan_gemm(int64_t M, int64_t N, int table, int64_t workspace_bytes) {
   GemmPlan g{};
   const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256);
   const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
@@ -1353,7 +1410,7 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, bool table, int64_t workspace_by
   // of its range once, so the range is made as square as the groups allow (1024 x 3072, 24
   // tiles per XCD: 4 x 6 tiles read 10 panels where 2 x 12 read 14; 17.8 against 18.5 us per
   // launch with operands from HBM). Two workgroups per CU measured no better this way.
-  g.group_m = g.tile == 256 && !table ? kGroupMPingPong : kGroupM;
+  g.group_m = g.tile == 256 && table != kTableGelu ? kGroupMPingPong : kGroupM;
   const int64_t slots = g.tile == 256 ? 256 : 512;
   if (g.deep) {
     const int64_t per = (tiles + 7) / 8;
@@ -1369,7 +1426,7 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, bool table, int64_t workspace_by
   if (workspace_bytes >= kTileQueueBytes && tiles >= 2 * slots && tiles <= INT32_MAX / 2) {
     const int64_t per = tiles / 8, rem = tiles % 8;
     g.pool = (int)((per + kPoolDiv - 1) / kPoolDiv);
-    if (g.tile == 256 && !table) {
+    if (g.tile == 256 && table != kTableGelu) {
       // Ping-pong tiles: one workgroup per CU, each looping over its XCD's static positions and
       // then over claimed ones, so that a tile's epilogue overlaps the next tile's first loads.
       g.persistent = true;
@@ -1388,7 +1445,8 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, bool table, int64_t workspace_by
 template <int kEpi, int kOut>
 static int launch_gemm(const GemmArgs& args0, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   GemmArgs args = args0;
-  const GemmPlan g = plan_gemm(args.M, args.N, kEpi == kEpiGelu || kEpi == kEpiSwiGLU, workspace ? workspace_bytes : 0);
+  const GemmPlan g = plan_gemm(args.M, args.N, kEpi == kEpiGelu ? kTableGelu : kEpi == kEpiSwiGLU ? kTableSwiGLU : 0,
+                               workspace ? workspace_bytes : 0);
   if ((int64_t)g.tiles_m * g.tiles_n > INT32_MAX / 2) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "too many tiles");
   args.tiles_m = g.tiles_m;
   args.tiles_n = g.tiles_n;
@@ -1406,7 +1464,10 @@ static int launch_gemm(const GemmArgs& args0, void* workspace, int64_t workspace
     args.line_store = args.line_store && ((uintptr_t)args.gate % 16 == 0) && (args.ldg % 8 == 0);
   }
   const unsigned grid = (unsigned)g.grid;
-  if constexpr (kEpi != kEpiGelu && kEpi != kEpiSwiGLU) {
+  if constexpr (kEpi == kEpiSwiGLU) {
+    // 256-tiles on the ping-pong schedule, the compact SiLU table in the epilogue
+    gemm_i8_kernel<kEpi, kOut, 256, false, true><<<grid, TileCfg<256, false, true>::kThreads, 0, stream>>>(args);
+  } else if constexpr (kEpi != kEpiGelu) {
     if (g.tile == 128) {
       if (g.deep && g.tile_n == 96)
         gemm_i8_kernel<kEpi, kOut, 128, true, false, 96><<<grid, kGemmThreads, 0, stream>>>(args);
@@ -1451,7 +1512,8 @@ using namespace mxq;
 extern "C" int mxq_int8_gemm_plan(int64_t M, int64_t N, int64_t K, int table_epilogue,
                                   int64_t workspace_bytes, int64_t* plan) {
   if (M <= 0 || N <= 0 || K <= 0 || !plan) return mxq_set_error(MXQ_ERR_INVALID, "GEMM plan needs a positive shape and an output");
-  const GemmPlan g = plan_gemm(M, N, table_epilogue != 0, workspace_bytes);
+  if (table_epilogue < 0 || table_epilogue > kTableSwiGLU) return mxq_set_error(MXQ_ERR_INVALID, "table_epilogue must be 0, 1 or 2");
+  const GemmPlan g = plan_gemm(M, N, table_epilogue, workspace_bytes);
   plan[0] = g.tile;
   plan[1] = g.grid;
   plan[2] = (int64_t)g.tiles_m * g.tiles_n;

@@ -465,6 +465,11 @@ MXQ_DEVICE uint32_t lds_read_b32(uint32_t addr) {
   __asm__ volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(addr) : "memory");
   return r;
 }
+MXQ_DEVICE uint32_t lds_read_u16_at(uint32_t addr) {  // zero-extended
+  uint32_t r;
+  __asm__ volatile("ds_read_u16 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+  return r;
+}
 MXQ_DEVICE uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(lptr_t)const_cast<void*>(p); }
 
 }  // namespace mxq

@@ -101,10 +101,11 @@ def load() -> ctypes.CDLL:
     return _lib
 
 
-def gemm_plan(m: int, n: int, k: int, table: bool = False, workspace_bytes: int = GEMM_WORKSPACE_BYTES) -> dict:
+def gemm_plan(m: int, n: int, k: int, table: int = 0, workspace_bytes: int = GEMM_WORKSPACE_BYTES) -> dict:
     """The INT8 GEMM launch plan (mxq_int8_gemm_plan): tile rows, workgroups, tiles, tiles per XCD
     claimed at run time (0: static order), workgroups per XCD, operand stages requested ahead,
-    tile-rows per group of the tile order, whether the workgroups loop over tiles, tile columns."""
+    tile-rows per group of the tile order, whether the workgroups loop over tiles, tile columns.
+    ``table``: 0 plain epilogues, 1 (or True) the GELU epilogue, 2 the SwiGLU one."""
     out = (ctypes.c_int64 * 9)()
     call("mxq_int8_gemm_plan", m, n, k, int(table), workspace_bytes, out)
     return {"tile": out[0], "grid": out[1], "tiles": out[2], "pool": out[3], "wg_per_xcd": out[4],
