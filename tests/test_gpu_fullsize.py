@@ -193,3 +193,59 @@ def test_c4_w4a8_skinny_full_width(dev, prepared):
     yr = _rows(y, rows)
     a, xs = eager_np.quantize_int8_rowwise(bits(_rows(x, rows)))
     _w4a8_check(yr, a, xs.reshape(-1), qd.cpu().numpy(), gs.cpu().numpy(), k)
+
+
+def test_h3_mlp_full_size(dev):
+    """The H3 block's MLP half at 720p (hidden 5376, SwiGLU 2 x 14336, ConvRot 256, three
+    modulation segments), run whole (h3_mlp_) and by its parts, checked at each boundary on the
+    sampled rows: the RMS adaLN rows within the stated bound of the oracle; q1 / scales bit-exact
+    from the kernel's own modulated rows; fc1 + SwiGLU (looping ping-pong workgroups, compact SiLU
+    table) bit-exact from q1; the re-quant bit-exact from h; the gated residual update bit-exact
+    from q2; and the whole chain identical to its parts on every row."""
+    from oracle import convrot as cr
+
+    d, f, eps = 5376, 14336, 1e-6
+    print(f"H3 MLP half m={M} d={d} f={f}", flush=True)
+    res0 = (_activations(M, d, dev, 40).float() * 2).to(torch.bfloat16)
+    nw = (1 + 0.1 * torch.randn(d, generator=_gen(dev, 41), device=dev)).to(torch.bfloat16)
+    sc, sh, gate = ((0.1 * torch.randn(3, d, generator=_gen(dev, 42 + i), device=dev)).to(torch.bfloat16) for i in range(3))
+    segs = ((0, 25200, 0), (25200, 50400, 1), (50400, M, 2))
+    w1, s1 = _int8_weight(2 * f, d, dev, 45)
+    w2, s2 = _int8_weight(d, f, dev, 46)
+    b1, b2 = _bias(2 * f, dev, 47), _bias(d, dev, 48)
+    fc1 = _mx().prepare_swiglu_fc1(w1, s1, b1)
+    # the parts
+    q1, x1s, y = _mx().rms_adaln_quantize_int8(res0, (nw, eps), sh, sc, segs, convrot_groupsize=256,
+                                               return_modulated=True)
+    h = _mx().int8_swiglu_fc1(q1, x1s, fc1)
+    q2, x2s = _mx().quantize_int8_rowwise_convrot(h, 256)
+    res_parts = res0.clone()
+    _mx().swiglu_mlp_gated_residual_(res_parts, q1, x1s, fc1, w2, s2, b2, gate, segs)
+    # the whole chain
+    res_whole = res0.clone()
+    _mx().h3_mlp_(res_whole, (nw, eps), sh, sc, gate, segs, fc1, w2, s2, b2)
+    assert torch.equal(res_whole, res_parts)
+    rows = _sample_rows(M)
+    r0, yr, q1r, s1r, hr, q2r, s2r, outr = (_rows(t, rows) for t in (res0, y, q1, x1s, h, q2, x2s, res_parts))
+    del h, q2, res_whole
+    rmap = eager_np.segment_row_map(M, segs)[rows]
+    # 1. RMS adaLN rows within the bound and rate of the RMS adaLN tests
+    from test_gpu_residual import _check_rms_adaln_bound
+
+    _check_rms_adaln_bound(yr, r0, nw.cpu(), sc.cpu(), sh.cpu(), rmap, eps)
+    # 2. ConvRot quantizer of the kernel's own modulated rows
+    q1o, s1o, _ = cr.convrot_quantize_bf16(bits(yr), 256)
+    assert np.array_equal(q1r.numpy(), q1o) and np.array_equal(s1r.numpy(), s1o)
+    # 3. fc1 + SwiGLU from q1
+    y1 = eager_np.dequant_epilogue(eager_np.int8_matmul(q1o, w1.cpu().numpy()), s1o, s1.cpu().numpy(),
+                                   bits(b1.cpu()), "bf16")
+    h_ref = cr.swiglu_bf16(bf16_bits(y1))
+    assert np.array_equal(bits(hr), h_ref)
+    # 4. the re-quant of h
+    q2o, s2o, _ = cr.convrot_quantize_bf16(h_ref, 256)
+    assert np.array_equal(q2r.numpy(), q2o) and np.array_equal(s2r.numpy(), s2o)
+    # 5. fc2 + gated residual from q2
+    y2 = eager_np.dequant_epilogue(eager_np.int8_matmul(q2o, w2.cpu().numpy()), s2o, s2.cpu().numpy(),
+                                   bits(b2.cpu()), "bf16")
+    want = eager_np.gated_residual_bf16(bits(r0), bf16_bits(y2), bits(gate.cpu()), rmap)
+    assert np.array_equal(bits(outr), want)

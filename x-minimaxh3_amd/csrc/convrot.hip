@@ -614,6 +614,23 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict_
   }
 }
 
+// t[m, c] = bf16(1 + scale[m, c]) for the modulation rows (c < cols, row stride ld): the factor
+// every token of segment m multiplies its normalized value by, formed once per call instead of
+// once per token and element. Eight columns (16 bytes) per thread.
+__global__ __launch_bounds__(256) void one_plus_rows_kernel(const uint16_t* __restrict__ scale, uint16_t* __restrict__ t,
+                                                            int64_t ld, int64_t mod_count, int64_t cols) {
+  const int64_t per_row = cols / 8, n = mod_count * per_row;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t m = i / per_row, c = (i - m * per_row) * 8;
+    const v4u w = *reinterpret_cast<const v4u*>(scale + m * ld + c);
+    v4u o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = pack_bf16x2(1.0f + bf16_lo(w[e]), 1.0f + bf16_hi(w[e]));
+    *reinterpret_cast<v4u*>(t + m * ld + c) = o;
+  }
+}
+
 }  // namespace
 }  // namespace mxq
 
@@ -677,23 +694,6 @@ extern "C" int mxq_swiglu_bf16(const void* x, void* y, int64_t rows, int64_t col
   const int64_t blocks = std::min<int64_t>((n + 255) / 256, 65536);
   swiglu_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>((const uint16_t*)x, (uint16_t*)y, rows, cols);
   return mxq_check_launch("swiglu_kernel");
-}
-
-// t[m, c] = bf16(1 + scale[m, c]) for the modulation rows (c < cols, row stride ld): the factor
-// every token of segment m multiplies its normalized value by, formed once per call instead of
-// once per token and element. Eight columns (16 bytes) per thread.
-__global__ __launch_bounds__(256) void one_plus_rows_kernel(const uint16_t* __restrict__ scale, uint16_t* __restrict__ t,
-                                                            int64_t ld, int64_t mod_count, int64_t cols) {
-  const int64_t per_row = cols / 8, n = mod_count * per_row;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t m = i / per_row, c = (i - m * per_row) * 8;
-    const v4u w = *reinterpret_cast<const v4u*>(scale + m * ld + c);
-    v4u o;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      o[e] = pack_bf16x2(1.0f + bf16_lo(w[e]), 1.0f + bf16_hi(w[e]));
-    *reinterpret_cast<v4u*>(t + m * ld + c) = o;
-  }
 }
 
 static int rms_adaln_launch(const void* x, const void* norm_weight, const void* scale, const void* shift,
