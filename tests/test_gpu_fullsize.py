@@ -28,6 +28,8 @@ tile: 75600 = 295 x 256 + 80) and 64 drawn at random.
       tile form at its full width, on the prepared and on the checkpoint layout.
   Sampled rows bit-exact against the oracle's restatement of the summation order, and within
   1 ulp + the float32 accumulation bound of the float64 value.
+* The H3 block's MLP half (hidden 5376, SwiGLU 2 x 14336, ConvRot 256): each stage checked at its
+  boundary as for the adaLN chain above, and the whole chain identical to its parts.
 """
 
 import numpy as np
