@@ -625,16 +625,18 @@ class W4A8RefQkvWorkload:
     """The reference's own W4A8 format on the H3 QKV projection at 720p (ConvRotW4A8Linear,
     h3serve/native_engine/model/quantization.py:416-586): ConvRot-256 quant of x [75600, 5376],
     then int4 codes [21504, 5376] with e4m3 relative scales per 16 weights and fp32 channel scales,
-    decoded to the int8 grid chunk by chunk (3584 columns, within the reference's 4096-column
-    workspace bound) and multiplied (mxq_w4a8_codebook_gemm). The timed steps call that entry;
-    the event pass issues the same launches through its two parts (decode, dequant GEMM into the
-    output's column slice), so that kernel_ms and the roofline are per GEMM launch (one chunk)."""
+    decoded to the int8 grid and multiplied (mxq_w4a8_codebook_gemm) in the chunks the library's
+    caller picks (mx_qlinear.ops.w4a8_decode_chunk: here one chunk of all 21504 columns, 115 MB,
+    which stays in the last-level cache; the reference bounds its chunk to 4096 columns for 8 GB
+    boards). The timed steps call that entry; the event pass issues the same launches through its
+    two parts (decode, dequant GEMM into the output's column slice), so that kernel_ms and the
+    roofline are per GEMM launch (one chunk)."""
 
     name = "w4a8_ref_h3_qkv_720p"
-    chunk = 3584
 
     def __init__(self, dev, m=75600, d=H3_D, n=3 * H3_ATTN, g=16):
         self.m, self.d, self.n, self.g = m, d, n, g
+        self.chunk = mx_qlinear.ops.w4a8_decode_chunk(n, d)
         self.x = make_activations(m, d, dev, 60)
         # W4A8 storage made the way the reference makes it: an N(0, 0.02) bf16 weight rotated and
         # quantized by quantize_w4a8_int8_weight (group 16, the 16-level codebook, e4m3 s_rel)

@@ -60,7 +60,6 @@ def _format_r_storage(n, k, g, use_codebook, source):
     return qd, s_rel, s_ch, torch.linspace(-7.5, 7.5, 16) if use_codebook else None
 
 
-# N = 4232 decodes in two chunks (4096 + 136 columns) into the GEMM's output column slices.
 @pytest.mark.parametrize("source", ["random", "prepared"])
 @pytest.mark.parametrize("m,n,k,use_codebook", [(200, 300, 1024, True), (64, 4232, 256, False)])
 def test_w4a8_reference_format_linear(dev, m, n, k, use_codebook, source):
@@ -74,6 +73,30 @@ def test_w4a8_reference_format_linear(dev, m, n, k, use_codebook, source):
     ref = eager_np.w4a8_reference_linear(bits(x), qd.numpy(), s_rel.view(torch.uint8).numpy(), s_ch.numpy(),
                                          None if cb is None else cb.numpy(), g, bits(bias), "bf16", s_rel_is_e4m3=True)
     assert np.array_equal(bits(y), bf16_bits(ref))
+
+
+def test_w4a8_reference_format_chunking_changes_nothing(dev):
+    """Through the C-ABI: the decode-then-GEMM over column chunks of 4232 (one chunk, as
+    w4a8_decode_chunk picks here), 4096 + 136, 1000 and 136 columns gives the same output bit for
+    bit, each chunk's GEMM writing its output column slice."""
+    from mx_qlinear import _lib
+    from mx_qlinear.ops import _gemm_ws, _p, _stream
+
+    m, n, k, g = 64, 4232, 256, 16
+    assert _mx().ops.w4a8_decode_chunk(n, k) == n
+    qd, s_rel, s_ch, cb = (t.to(dev) for t in _format_r_storage(n, k, g, True, "random"))
+    xq = torch.randint(-127, 128, (m, k), generator=gen(36), dtype=torch.int8).to(dev)
+    xs = (torch.rand(m, generator=gen(37)) * 1e-2).to(dev)
+    bias = bf16_vec(n, 38, 0.01).to(dev)
+    outs = []
+    for chunk in (n, 4096, 1000, 136):
+        work = torch.empty((chunk, k), dtype=torch.int8, device=dev)
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        _lib.call("mxq_w4a8_codebook_gemm", _p(xq), _p(qd), _p(s_rel), _lib.DTYPE_E4M3, _p(cb), _p(s_ch), _p(xs),
+                  _p(bias), _p(work), _p(out), m, n, k, g, chunk, _lib.DTYPE_BF16, *_gemm_ws(dev), _stream(dev))
+        outs.append(out)
+    for out in outs[1:]:
+        assert torch.equal(out, outs[0])
 
 
 def _int_input(m, k, seed):
