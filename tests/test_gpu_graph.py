@@ -74,3 +74,28 @@ def test_h3_qkv_chain_in_a_graph(dev):
     qd = _mx().prepare_w4a8_grouped(packed_int4(n, d, 17).to(dev))
     gs = group_scales(d, n, 128, 18).to(dev)
     _replays_match(dev, lambda: _mx().w4a8_grouped_linear(x, qd, gs, 128), _mx().w4a8_grouped_linear(x, qd, gs, 128))
+
+
+def test_h3_mlp_chain_in_a_graph(dev):
+    """rms_adaln + ConvRot quant -> fc1 with the SwiGLU epilogue (ping-pong kernel, compact SiLU
+    table) -> ConvRot re-quant -> fc2 with the gated residual update, in place on a residual that
+    the graph first restores from a saved copy."""
+    m, d, f = 300, 512, 768
+    w1, s1 = int8_weight(2 * f, d, 41)
+    w2, s2 = int8_weight(d, f, 42)
+    b1, b2 = bf16_vec(2 * f, 43, 0.02).to(dev), bf16_vec(d, 44, 0.02).to(dev)
+    w1, s1, w2, s2 = w1.to(dev), s1.to(dev), w2.to(dev), s2.to(dev)
+    norm_w = (1 + 0.1 * torch.randn(d, generator=gen(45))).to(torch.bfloat16).to(dev)
+    scale, shift, gate = ((0.1 * torch.randn(3, d, generator=gen(46 + i))).to(torch.bfloat16).to(dev) for i in range(3))
+    segs = ((0, 100, 0), (100, 200, 1), (200, 300, 2))
+    fc1 = _mx().prepare_swiglu_fc1(w1, s1, b1)
+    res0 = (activations(m, d, 49) * 2).to(dev)
+    ref = res0.clone()
+    _mx().h3_mlp_(ref, (norm_w, 1e-6), shift, scale, gate, segs, fc1, w2, s2, b2)
+    res = torch.empty_like(res0)
+
+    def chain():
+        res.copy_(res0)
+        return _mx().h3_mlp_(res, (norm_w, 1e-6), shift, scale, gate, segs, fc1, w2, s2, b2)
+
+    _replays_match(dev, chain, ref)
