@@ -30,6 +30,20 @@ def test_convrot_quantizer_matches_oracle(dev, m, k, g):
     assert np.array_equal(s.cpu().numpy(), sr)
 
 
+@pytest.mark.parametrize("m,k,g", [(1, 5376, 256), (2, 4352, 64), (8, 6144, 256), (1, 6400, 256), (3, 8192, 16),
+                                   (9, 5376, 256), (1, 4096, 64), (1, 256, 256)])
+def test_convrot_quantizer_few_rows_matches_oracle(dev, m, k, g):
+    """Launches of at most 8 rows take one unit (256 columns) per 16-lane group, in blocks of up to
+    six waves (17-24 units), or the fewest units per group that fit four waves (25+ units); 9 rows
+    take the throughput split. All bit-exact."""
+    print(f"convrot quant few rows m={m} k={k} g={g}", flush=True)
+    x = activations(m, k, 300 + m + k + g)
+    q, s = _mx().quantize_int8_rowwise_convrot(x.to(dev), g)
+    qr, sr, _ = cr.convrot_quantize_bf16(bits(x), g)
+    assert np.array_equal(q.cpu().numpy(), qr)
+    assert np.array_equal(s.cpu().numpy(), sr)
+
+
 @pytest.mark.parametrize("act", ["gelu_tanh", "swiglu"])
 @pytest.mark.parametrize("g", [256, 0])
 def test_convrot_quantizer_with_input_act(dev, act, g):

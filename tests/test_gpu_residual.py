@@ -237,15 +237,16 @@ def test_rms_adaln_quantize_h3_width_many_rows(dev, mapping):
     assert torch.equal(y, y2)
 
 
-@pytest.mark.parametrize("ld_pad", [0, 40])
-def test_rms_adaln_modulation_workspace_changes_nothing(dev, ld_pad):
+@pytest.mark.parametrize("m,ld_pad", [(777, 0), (777, 40), (3, 40)])
+def test_rms_adaln_modulation_workspace_changes_nothing(dev, m, ld_pad):
     """Through the C-ABI: the same call with the modulation workspace (bf16(1 + scale) formed
     once per call), with one 16 bytes too small and with none gives identical q, scales and y,
-    also for scale / shift rows strided beyond the hidden size."""
+    also for scale / shift rows strided beyond the hidden size, and in a three-row launch (one
+    unit of 256 columns per 16-lane group); the quantizer of the modulated rows is bit-exact."""
     from mx_qlinear import _lib
     from mx_qlinear.ops import _p, _stream
 
-    m, d, eps, mods = 777, 5376, 1e-6, 5
+    d, eps, mods = 5376, 1e-6, 5
     print(f"rms_adaln workspace m={m} d={d} ld_pad={ld_pad}", flush=True)
     x, w, _, _ = _rms_inputs(m, d, 91 + ld_pad)
     ld = d + ld_pad
@@ -265,6 +266,8 @@ def test_rms_adaln_modulation_workspace_changes_nothing(dev, ld_pad):
         outs.append((q, s, y))
     for q, s, y in outs[1:]:
         assert torch.equal(q, outs[0][0]) and torch.equal(s, outs[0][1]) and torch.equal(y, outs[0][2])
+    qr, sr, _ = cr.convrot_quantize_bf16(bits(outs[0][2].cpu()), 256)
+    assert np.array_equal(outs[0][0].cpu().numpy(), qr) and np.array_equal(outs[0][1].cpu().numpy().reshape(-1), sr.reshape(-1))
     # and the modulated rows are the oracle's within the stated bound
     _check_rms_adaln_bound(outs[0][2].cpu(), x.cpu(), w.cpu(), scale[:, :d].contiguous().cpu(), shift[:, :d].contiguous().cpu(),
                            rows.cpu().numpy(), eps)

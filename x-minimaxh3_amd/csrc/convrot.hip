@@ -296,7 +296,12 @@ int launch_convrot(const CrArgs& a, int nw, hipStream_t st) {
 // the float64 -> bfloat16 rounding done in pairs (the midpoint correction of f64_to_bf16_bits
 // runs only for a unit where some float32 value lands on a bfloat16 midpoint) and rows whose
 // absmax is finite quantized by the finite-row path.
+// A launch of at most 8 rows (one token's row: the M = 1 linear, decode) is bound by the latency
+// of one row's work, not by throughput: it takes the fewest units per group, one unit a group in
+// blocks of up to kUnitLatWaves waves (K = 5376: 21 groups in 6 waves; the kernel 5.4 -> 3.8 us,
+// near the ~3.4 us of an empty launch, against 3 units a group in 2 waves).
 constexpr int kUnitMaxWaves = 4;
+constexpr int kUnitLatWaves = 6;
 
 // The rotation of one unit up to the transposed layout: digits 0 and 1 in the lane; for
 // kDigits >= 3 each 16-lane group transposes its 16 x 16 float64 values through its LDS region
@@ -360,12 +365,12 @@ MXQ_DEVICE void unit_back16(uint32_t (&w)[8], double* tb) {
   wave_lds_fence();  // read before the region's next writes
 }
 
-template <int kAct, int kMod, int kDigits, int kNU, bool kTab = false, int kPreMod = 1>
-__global__ __launch_bounds__(kUnitMaxWaves * 64) void convrot_units_kernel(CrArgs p, int gr, int rpb) {
+template <int kAct, int kMod, int kDigits, int kNU, bool kTab = false, int kPreMod = 1, int kWaves = kUnitMaxWaves>
+__global__ __launch_bounds__(kWaves * 64) void convrot_units_kernel(CrArgs p, int gr, int rpb) {
   constexpr int kRawWords = kAct == MXQ_ACT_SWIGLU ? 16 : 8;  // dwords per unit and lane
   constexpr double kInv = 1.0 / (double)(1 << kDigits);     // 1/sqrt(G), exact
-  __shared__ uint32_t red_max[2][4 * kUnitMaxWaves];
-  __shared__ double red_ss[2][4 * kUnitMaxWaves];
+  __shared__ uint32_t red_max[2][4 * kWaves];
+  __shared__ double red_ss[2][4 * kWaves];
   extern __shared__ __attribute__((aligned(16))) double tbuf[];  // kTWave per wave of the block
   const int wave = threadIdx.x >> 6;
   const int grp = threadIdx.x >> 4, gl = threadIdx.x & 15;
@@ -447,7 +452,8 @@ __global__ __launch_bounds__(kUnitMaxWaves * 64) void convrot_units_kernel(CrArg
       __syncthreads();
       // lane i of each group takes partials i and i + 16 of its row, then the 16 lanes combine
       double tot = 0.0;
-      for (int i = gl; i < gr; i += 16) tot += red_ss[it][slot * gr + i];
+      if (slot < rpb)  // groups past the block's rows read no partials
+        for (int i = gl; i < gr; i += 16) tot += red_ss[it][slot * gr + i];
       tot = row16_sum_f64(tot);
       const float mean = (float)tot / (float)p.K;
       rinv = 1.0f / sqrtf(mean + p.eps);
@@ -522,7 +528,8 @@ __global__ __launch_bounds__(kUnitMaxWaves * 64) void convrot_units_kernel(CrArg
     if (gl == 0) red_max[it][grp] = bits;
     __syncthreads();
     uint32_t rmax = 0;
-    for (int i = gl; i < gr; i += 16) rmax = max(rmax, red_max[it][slot * gr + i]);
+    if (slot < rpb)
+      for (int i = gl; i < gr; i += 16) rmax = max(rmax, red_max[it][slot * gr + i]);
     rmax = row16_max_u32(rmax);
     const float amaxf = __uint_as_float(rmax);
     const float s = row_scale_from_absmax(amaxf);
@@ -581,6 +588,10 @@ int launch_units(const CrArgs& a, const UnitSplit& u, hipStream_t st) {
   const unsigned grid = (unsigned)std::min<int64_t>((a.rows + u.rpb - 1) / u.rpb, 1 << 20);
   const unsigned threads = (unsigned)(u.waves * 64);
   const size_t lds = (size_t)u.waves * kTWave * sizeof(double);
+  if (u.waves > kUnitMaxWaves) {  // the few-row split: one unit a group
+    convrot_units_kernel<kAct, kMod, kDigits, 1, kTab, 1, kUnitLatWaves><<<grid, threads, lds, st>>>(a, u.gr, u.rpb);
+    return mxq_check_launch("convrot_units_kernel");
+  }
   switch (u.nu) {
     case 1: convrot_units_kernel<kAct, kMod, kDigits, 1, kTab><<<grid, threads, lds, st>>>(a, u.gr, u.rpb); break;
     case 2: convrot_units_kernel<kAct, kMod, kDigits, 2, kTab><<<grid, threads, lds, st>>>(a, u.gr, u.rpb); break;
@@ -592,7 +603,18 @@ int launch_units(const CrArgs& a, const UnitSplit& u, hipStream_t st) {
 
 template <int kAct, int kMod, bool kTab = false>
 int launch_units_digits(const CrArgs& a, hipStream_t st) {
-  const UnitSplit u = unit_split(a.K >> 8);
+  UnitSplit u = unit_split(a.K >> 8);
+  if (a.rows <= 8) {  // latency-bound: fewest units per group, one row a block
+    const int units = (int)(a.K >> 8);
+    if (units <= 4 * kUnitLatWaves) {
+      u = UnitSplit{1, units, 1, (units + 3) / 4};
+    } else {
+      for (int nu = 1; nu <= 4; ++nu) {
+        const int gr = (units + nu - 1) / nu;
+        if (gr <= 4 * kUnitMaxWaves) { u = UnitSplit{nu, gr, 1, (gr + 3) / 4}; break; }
+      }
+    }
+  }
   switch (a.digits) {
     case 0: return launch_units<kAct, kMod, 0, kTab>(a, u, st);
     case 1: return launch_units<kAct, kMod, 1, kTab>(a, u, st);
