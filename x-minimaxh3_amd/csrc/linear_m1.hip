@@ -12,10 +12,11 @@
 // The quantizer is the row kernel of mxq_quantize_int8_rowwise_convrot (one row: a single
 // workgroup). The GEMV is bound by streaming the [N, K] weights once: each wave owns kCols
 // output columns, issues all their 16-byte loads (lane l takes chunks l, l + 64, ... of a row,
-// so every load instruction reads 1 KB of contiguous weights) before the first use, forms the
-// dot products with v_dot4 against the quantized row (read once per wave, L2-resident), reduces
-// them across the wave and applies the epilogue. A launch is sized by K (chunks per lane) and
-// N (columns per wave) so that each CU keeps several 10-20 KB weight panels in flight.
+// so every load instruction reads 1 KB of contiguous weights; nontemporal, as the weights are
+// read once per token: 5376 x 21504 cycled through four layers 20.9 -> 19.3 us) before the
+// first use, forms the dot products with v_dot4 against the quantized row (read once per wave,
+// L2-resident), reduces them across the wave and applies the epilogue. A launch is sized by K (chunks per lane) and
+// N (one or two columns per wave), so that many waves each keep a few KB of weights in flight.
 
 #include "mxq_common.h"
 
@@ -55,7 +56,8 @@ __global__ __launch_bounds__(kGvThreads) void gemv_i8_kernel(GvArgs p) {
 #pragma unroll
     for (int j = 0; j < kChunks; ++j) {
       const int ch = j * kWave + lane;
-      wv[c][j] = (col_on && ch < chunks) ? *reinterpret_cast<const v4i*>(wr + (int64_t)ch * 16) : v4i{0, 0, 0, 0};
+      wv[c][j] = (col_on && ch < chunks) ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wr + (int64_t)ch * 16))
+                                         : v4i{0, 0, 0, 0};
     }
   }
   v4i xv[kChunks];
@@ -86,8 +88,11 @@ __global__ __launch_bounds__(kGvThreads) void gemv_i8_kernel(GvArgs p) {
 
 template <int kOut, int kChunks>
 int launch_gemv_c(const GvArgs& a, hipStream_t st) {
-  // Columns per wave: about 16 KB of weights in flight per wave.
-  constexpr int kCols = kChunks <= 2 ? 8 : (kChunks <= 4 ? 4 : (kChunks <= 8 ? 2 : 1));
+  // Columns per wave: many small waves rather than ~16 KB of weights in flight per wave (measured
+  // on [N, K] weights cycled from HBM, 16-byte nontemporal loads: 21504 x 5376 19.3 -> 19.1 us,
+  // 10240 x 8192 15.1 -> 14.6, 16384 x 4096 12.8 -> 12.0, 6144 x 2048 5.5 -> 4.6-5.0,
+  // 8192 x 1024 4.6 -> 4.0-4.1 against 2, 2, 4, 8 and 8 columns a wave).
+  constexpr int kCols = kChunks <= 4 ? 2 : 1;
   const int64_t per_block = (int64_t)kGvWaves * kCols;
   const int64_t blocks = (a.N + per_block - 1) / per_block;
   if (blocks > 0x7FFFFFFF) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "N too large");
