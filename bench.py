@@ -995,14 +995,9 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     # A second pass of the same steps with HIP events around each launch gives the per-kernel
-    # durations (kernel_ms, roofline). Every 50 steps a device-side wait of a few ms (a bounded
-    # clock spin) lets the host queue the next launches and events ahead of the device, so that
-    # a span times its kernel rather than the host's launch gap when the host issues launches
-    # and events more slowly than the device runs them (the one-token GEMV: ~19 us).
+    # durations (kernel_ms, roofline).
     timer = Timer()
-    for i in range(args.steps):
-        if i % 50 == 0:
-            torch.cuda._sleep(10_000_000)
+    for _ in range(args.steps):
         wl.step(timer)
     torch.cuda.synchronize()
     ms = wall * 1e3 / args.steps

@@ -322,15 +322,18 @@ MXQ_DEVICE void epi_run(const v16i& acc, int q, float xs, const float* w, const 
 
 // Store one run (words as produced by epi_run) of row `row` from column `col`. `fast`: the
 // caller has established that the four columns are inside the output and the run aligned.
+// The epilogue's vector stores are nontemporal: the output is not read again by this launch,
+// and keeping it out of the L2 leaves that to the operand panels the tiles share (FFN chain at
+// 720p: fc1 6.54 -> 6.46 ms, the chain 13.45 -> 13.35 ms on one box).
 template <int kElem>
 MXQ_DEVICE void store_run(void* d, int64_t ldd, int64_t row, int64_t col, int64_t N, bool fast,
                           const uint32_t* w) {
   char* base = reinterpret_cast<char*>(d) + (row * ldd + col) * kElem;
   if (fast) {
     if constexpr (kElem == 4)
-      *reinterpret_cast<v4u*>(base) = v4u{w[0], w[1], w[2], w[3]};
+      __builtin_nontemporal_store(v4u{w[0], w[1], w[2], w[3]}, reinterpret_cast<v4u*>(base));
     else
-      *reinterpret_cast<v2u*>(base) = v2u{w[0], w[1]};
+      __builtin_nontemporal_store(v2u{w[0], w[1]}, reinterpret_cast<v2u*>(base));
   } else {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -453,7 +456,7 @@ MXQ_DEVICE void stage_store(const GemmArgs& p, char* buf, int64_t row0, int64_t 
   stage_wait();
   char* base = reinterpret_cast<char*>(p.d) + (row0 + (lane >> 3)) * pitch + byte0 + (lane & 7) * 16;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) *reinterpret_cast<v4u*>(base + t * 8 * pitch) = v[t];
+  for (int t = 0; t < 4; ++t) __builtin_nontemporal_store(v[t], reinterpret_cast<v4u*>(base + t * 8 * pitch));
 }
 
 // The same for a piece of 64 bytes per row (chunks 0-3): rows row0 .. row0 + 31 of d, bytes
@@ -469,7 +472,7 @@ MXQ_DEVICE void stage_store64(const GemmArgs& p, char* buf, int64_t row0, int64_
   stage_wait();
   char* base = reinterpret_cast<char*>(p.d) + (row0 + (lane >> 2)) * pitch + byte0 + (lane & 3) * 16;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) *reinterpret_cast<v4u*>(base + t * 16 * pitch) = v[t];
+  for (int t = 0; t < 2; ++t) __builtin_nontemporal_store(v[t], reinterpret_cast<v4u*>(base + t * 16 * pitch));
 }
 
 // Two 32 x 32 blocks of 16-bit words (jj = 0, 1: 8 words each, as epi_run gives them), or one
@@ -512,9 +515,10 @@ MXQ_DEVICE void gated_lines(const GemmArgs& p, char* buf, int64_t row0, int64_t 
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const v4u y = ys[t];
-    *reinterpret_cast<v4u*>(res + t * 8 * p.ldr) =
+    __builtin_nontemporal_store(
         v4u{gated_pair(r[t][0], y[0], g[t][0]), gated_pair(r[t][1], y[1], g[t][1]),
-            gated_pair(r[t][2], y[2], g[t][2]), gated_pair(r[t][3], y[3], g[t][3])};
+            gated_pair(r[t][2], y[2], g[t][2]), gated_pair(r[t][3], y[3], g[t][3])},
+        reinterpret_cast<v4u*>(res + t * 8 * p.ldr));
   }
 }
 
