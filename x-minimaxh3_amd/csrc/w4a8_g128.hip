@@ -308,8 +308,8 @@ __global__ __launch_bounds__(kThreads, W4Cfg<kTileM>::kOcc) void w4a8_g128_kerne
     if (grow >= p.M) continue;
     const v4u v = *reinterpret_cast<const v4u*>(s_out + row * kPitch + ch * 16);
     char* dst = D + (grow * p.ldd + gcol) * kE;
-    if (vec && gcol + kPerElem <= p.N) {
-      *reinterpret_cast<v4u*>(dst) = v;
+    if (vec && gcol + kPerElem <= p.N) {  // nontemporal: 8192 x 5120 x 5120 0.252 -> 0.250 ms
+      __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(dst));
     } else {
       // Element by element from the register words (taking the address of v would place it in
       // memory, and the compiler then moves such per-thread arrays into LDS).
