@@ -22,11 +22,13 @@ def _mx():
     return mx_qlinear
 
 
-@pytest.mark.parametrize("g", [4, 16, 32, 128])
+@pytest.mark.parametrize("g", [4, 8, 16, 32, 48, 128])
 @pytest.mark.parametrize("e4m3", [False, True])
 @pytest.mark.parametrize("codebook", [False, True])
 def test_decode_matches_oracle(dev, g, e4m3, codebook):
-    n, k = 96, 512
+    """Every group size form of the decode: 4 and 8 (four and two scales per 16 weights), 16 and
+    its multiples, a power of two or not (one scale per 16 weights)."""
+    n, k = 96, 480 if g == 48 else 512
     qd = packed_int4(n, k, 7 + g)
     s = torch.rand(n, k // g, generator=gen(g)) * 30
     if e4m3:

@@ -50,28 +50,36 @@ template <bool kE4M3>
 __global__ __launch_bounds__(256) void decode_int4_grouped_kernel(
     const uint8_t* __restrict__ qdata, const void* __restrict__ s_rel,
     const float* __restrict__ codebook, int8_t* __restrict__ out, int64_t total_vec,
-    int64_t k_half, int64_t groups, int group_size) {
+    int64_t k_half, int64_t groups, int group_size, int gshift) {
   __shared__ float s_cb[16];
   if (threadIdx.x < 16) s_cb[threadIdx.x] = codebook ? codebook[threadIdx.x] : (float)threadIdx.x - 8.0f;
   __syncthreads();
   for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < total_vec;
        v += (int64_t)gridDim.x * blockDim.x) {
     // 8 packed bytes -> 16 weights of one row (K % 16 == 0 keeps them in one row).
+    // The vector's 16 weights lie in 16 / G groups (G = 4, 8) or in one (G a multiple of 16):
+    // their scales are read once per vector, and weight i takes scale i >> gshift (gshift =
+    // log2 G, or 4 for G >= 16), so no division runs per weight.
     const int64_t byte0 = v * 8;
     const int64_t n = byte0 / k_half;
-    const int64_t k0 = (byte0 - n * k_half) * 2;
+    const int k0 = (int)((byte0 - n * k_half) * 2);
+    const int64_t g0 = n * groups + k0 / group_size;
     const v2u w = *reinterpret_cast<const v2u*>(qdata + byte0);
+    const int ng = group_size >= 16 ? 1 : 16 / group_size;
+    float sv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t gi = g0 + (j < ng ? j : 0);
+      sv[j] = kE4M3 ? e4m3fn_to_f32(reinterpret_cast<const uint8_t*>(s_rel)[gi])
+                    : reinterpret_cast<const float*>(s_rel)[gi];
+    }
     uint32_t o[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const uint32_t byte = (w[i >> 3] >> (8 * ((i >> 1) & 3))) & 0xFFu;
       const uint32_t c = (i & 1) ? (byte >> 4) : (byte & 0xFu);
-      const int64_t g = (k0 + i) / group_size;
-      float s;
-      if (kE4M3)
-        s = e4m3fn_to_f32(reinterpret_cast<const uint8_t*>(s_rel)[n * groups + g]);
-      else
-        s = reinterpret_cast<const float*>(s_rel)[n * groups + g];
+      const int j = i >> gshift;
+      const float s = j == 0 ? sv[0] : (j == 1 ? sv[1] : (j == 2 ? sv[2] : sv[3]));
       float r = __builtin_rintf(s_cb[c] * s);
       r = fminf(fmaxf(r, -127.0f), 127.0f);
       const int q = (r != r) ? 0 : (int)r;
@@ -88,12 +96,13 @@ static int decode_launch(const int8_t* qdata, const void* s_rel, int s_rel_dtype
   int64_t blocks = (total_vec + 255) / 256;
   if (blocks > 65536) blocks = 65536;
   if (total_vec == 0) return MXQ_OK;
+  const int gshift = group_size == 4 ? 2 : (group_size == 8 ? 3 : 4);  // G = 4, 8 or 16 * j
   if (s_rel_dtype == MXQ_DTYPE_E4M3)
     decode_int4_grouped_kernel<true><<<(unsigned)blocks, 256, 0, st>>>(
-        (const uint8_t*)qdata, s_rel, codebook, out, total_vec, k_half, groups, (int)group_size);
+        (const uint8_t*)qdata, s_rel, codebook, out, total_vec, k_half, groups, (int)group_size, gshift);
   else
     decode_int4_grouped_kernel<false><<<(unsigned)blocks, 256, 0, st>>>(
-        (const uint8_t*)qdata, s_rel, codebook, out, total_vec, k_half, groups, (int)group_size);
+        (const uint8_t*)qdata, s_rel, codebook, out, total_vec, k_half, groups, (int)group_size, gshift);
   return mxq_check_launch("decode_int4_grouped_kernel");
 }
 
@@ -109,6 +118,7 @@ static int check_decode_args(const int8_t* qdata, const void* s_rel, int s_rel_d
     return mxq_set_error(MXQ_ERR_UNSUPPORTED, "s_rel dtype code %d", s_rel_dtype);
   if (N > 0 && K > 0 && (!qdata || !s_rel)) return mxq_set_error(MXQ_ERR_INVALID, "null pointer");
   if ((uintptr_t)qdata % 8) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "qdata must be 8-byte aligned");
+  if (K > (int64_t{1} << 30)) return mxq_set_error(MXQ_ERR_UNSUPPORTED, "K=%lld too large", (long long)K);
   return MXQ_OK;
 }
 
