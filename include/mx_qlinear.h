@@ -339,7 +339,8 @@ int mxq_fill_f32(float* p, float value, int64_t n, void* stream);
  *   w8[n, k] = clamp(rne(v * s_rel[n, k / G]), -127, 127), v = codebook[c] or c - 8,
  *   c = low nibble of qdata[n, k/2] for even k, high nibble for odd k.
  *   qdata [N, K/2] int8; s_rel [N, K/G] fp32 (s_rel_dtype 0) or float8_e4m3fn bits (5);
- *   codebook [16] fp32 or NULL; out [N, K] int8.
+ *   codebook [16] fp32 or NULL; out [N, K] int8. K a multiple of 16 and of G, at most 2^30;
+ *   G = 4, 8, or a multiple of 16; qdata 8-byte aligned (MXQ_ERR_INVALID / _UNSUPPORTED else).
  * Semantics: CK/backends/eager/w4a8_int8.py:344-363.
  * Replaces: launch_dequant_int4_grouped_to_int8 / _e4m3, CK/backends/cuda/ops/w4a8_gemm.cu:93-121.
  */
